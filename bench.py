@@ -1,0 +1,283 @@
+"""Benchmark: batched speculative decoding at the 8B shape on one MI355X.
+
+Workload (the reference's largest single-GPU configuration): target = LLaMA-style decoder with 32 layers,
+d_model 4096, 32 query / 8 KV heads, head_dim 128, SwiGLU ffn 14336, vocab 128256, bf16, weights
+N(0, 0.02) from a seed; draft = the target's embedding, head and first 4 layers. 64 running sequences,
+k = 6, contexts uniform in [2048, 8192] held in a paged pool with block_size 16. The contexts' keys and
+values are synthetic N(0, 1) bf16 written straight into the pools (no prefill), then `--steps` decode
+rounds are timed: k draft decode steps, one target verify pass over k+1 tokens, one fused acceptance.
+
+One "step" = one speculative round for the whole batch. `value` = committed tokens per second
+(accepted proposals + one target token per sequence per round), inputs resident in HBM.
+`roofline` = the paged verify attention (split-KV kernel + its combine), timed with HIP events on the
+launching stream around every verify-attention launch of the timed rounds, against 8 TB/s.
+`cpu_baseline` = the CPU oracle (oracle/reference_cpu.py) timed on this host on one target layer's
+verify pass, one draft layer's decode step, the LM head and the acceptance at the same shapes,
+scaled to a round.
+
+    python bench.py [--gpus 1] [--steps 128] [--warmup 4]
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+CFG = dict(vocab_size=128256, d_model=4096, n_layers=32, n_heads=32, n_kv_heads=8, ffn_dim=14336,
+           max_seq_len=10240)
+DRAFT_LAYERS = 4
+BATCH, K, BLOCK = 64, 6, 16
+CTX_LO, CTX_HI = 2048, 8192
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_models(torch, fa):
+    cfg = fa.ModelConfig(**CFG)
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device("cuda"):
+            target = fa.ForgeModel(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    draft = fa.early_exit_draft(target, DRAFT_LAYERS)
+    return target, draft
+
+
+def attn_bytes(ctxs, t, h, hkv, d, bs):
+    kv = sum(ctxs) * hkv * d * 2 * 2
+    qo = len(ctxs) * t * h * d * 2 * 2
+    tables = 4 * sum(-(-c // bs) for c in ctxs)
+    return kv + qo + tables + 4 * len(ctxs) * t
+
+
+def accept_bytes(b, k, v, s_logit=2):
+    return s_logit * b * v * (2 * k + 1) + 4 * b * v + 4 * b * k * 2 + 4 * b * (k + 2)
+
+
+def run_rounds(torch, fa, ops, sb, n_rounds, timer=None):
+    committed = 0
+    for _ in range(n_rounds):
+        committed += sb.round()
+    return committed
+
+
+def cpu_baseline(torch, committed_per_round):
+    """Time the CPU oracle on one layer of each kind at the benchmark shapes; scale to one round."""
+    from oracle import reference_cpu as orc
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    s = orc.Shape(CFG["vocab_size"], CFG["d_model"], 1, CFG["n_heads"], CFG["n_kv_heads"], CFG["ffn_dim"],
+                  CFG["max_seq_len"])
+    w = {}
+    for name, shape in orc.param_names(s):
+        if name == "tok_emb.weight":
+            continue
+        w[name] = torch.randn(shape, generator=g) * 0.02 if len(shape) > 1 else torch.ones(shape)
+    rope = orc.rope_tables(s)
+    ctxs = torch.randint(CTX_LO, CTX_HI + 1, (BATCH,), generator=torch.Generator().manual_seed(1)).tolist()
+    hd, hkv = s.head_dim, s.n_kv_heads
+
+    def layer(t):
+        """One decoder layer (model.py:104-106) for BATCH rows of t new tokens over their contexts."""
+        x = torch.randn(BATCH, t, s.d_model, generator=g) * 0.5
+        p = "layers.0."
+        h = orc.rms_norm(x, w[p + "attn_norm.weight"], s.norm_eps)
+        q = (h @ w[p + "attn.wq.weight"].T).view(BATCH, t, s.n_heads, hd).transpose(1, 2)
+        k = (h @ w[p + "attn.wk.weight"].T).view(BATCH, t, hkv, hd).transpose(1, 2)
+        v = (h @ w[p + "attn.wv.weight"].T).view(BATCH, t, hkv, hd).transpose(1, 2)
+        outs = []
+        for b in range(BATCH):          # one row at a time keeps the gathered context in memory
+            pos = torch.arange(ctxs[b] - t, ctxs[b])[None]
+            qb, kb = orc.rotate(q[b:b + 1], *rope, pos), orc.rotate(k[b:b + 1], *rope, pos)
+            kc = torch.randn(1, hkv, ctxs[b] - t, hd, generator=g)
+            vc = torch.randn(1, hkv, ctxs[b] - t, hd, generator=g)
+            outs.append(orc.attention_math(qb, torch.cat([kc, kb], 2), torch.cat([vc, v[b:b + 1]], 2), pos,
+                                           s.n_heads // hkv))
+        o = torch.cat(outs, 0)
+        x = x + o.transpose(1, 2).reshape(BATCH, t, -1) @ w[p + "attn.wo.weight"].T
+        h = orc.rms_norm(x, w[p + "mlp_norm.weight"], s.norm_eps)
+        return x + (torch.nn.functional.silu(h @ w[p + "mlp.w_gate.weight"].T) * (h @ w[p + "mlp.w_up.weight"].T)) \
+            @ w[p + "mlp.w_down.weight"].T
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    # the context-generation cost of the synthetic KV is excluded by timing it separately
+    t_verify = timed(lambda: layer(K + 1))
+    t_decode = timed(lambda: layer(1))
+    head = torch.randn(CFG["vocab_size"], CFG["d_model"], generator=g) * 0.02
+    t_head_v = timed(lambda: torch.randn(BATCH * (K + 1), CFG["d_model"]) @ head.T)
+    t_head_d = timed(lambda: torch.randn(BATCH, CFG["d_model"]) @ head.T)
+    logits_t = torch.randn(BATCH, K + 1, CFG["vocab_size"], generator=g) * 2
+    logits_d = logits_t[:, :K] + torch.randn(BATCH, K, CFG["vocab_size"], generator=g) * 0.5
+
+    def accept():
+        for b in range(BATCH):
+            p = orc.probs_from_logits(logits_t[b], 1.0)
+            q = orc.probs_from_logits(logits_d[b], 1.0)
+            xs = [int(q[i].argmax()) for i in range(K)]
+            orc.verify_with_noise(p, q, xs, torch.rand(K), torch.empty(CFG["vocab_size"]).exponential_())
+
+    t_acc = timed(accept)
+    n_t, n_d = CFG["n_layers"], DRAFT_LAYERS
+    round_s = n_t * t_verify + K * n_d * t_decode + t_head_v + K * t_head_d + t_acc
+    return {
+        "value": committed_per_round / round_s,
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"CPU oracle at the bench shapes: 1 target layer verify (B={BATCH}, T={K + 1}, per-row "
+                   f"contexts U[{CTX_LO},{CTX_HI}]) {t_verify:.2f}s, 1 draft layer decode {t_decode:.2f}s, "
+                   f"LM head {t_head_v:.2f}s/{t_head_d:.2f}s, acceptance {t_acc:.2f}s; scaled to one round "
+                   f"({n_t} verify layers + {K}x{n_d} draft layers + heads) = {round_s:.1f}s for "
+                   f"{committed_per_round:.1f} committed tokens"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--temperature", type=float, default=0.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import forgeserve_amd as fa
+    from forgeserve_amd import ops
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    t0 = time.time()
+    target, draft = build_models(torch, fa)
+    log(f"models built in {time.time() - t0:.1f}s")
+
+    g = torch.Generator().manual_seed(args.seed)
+    ctxs = torch.randint(CTX_LO, CTX_HI + 1, (BATCH,), generator=g).tolist()
+    rounds = args.warmup + args.steps
+    per_seq = [-(-(c + 2 + rounds * (K + 1) + K) // BLOCK) for c in ctxs]
+    nblocks = sum(per_seq) + 8
+    sb = fa.SpeculativeBatch(target, draft, nblocks, BLOCK, K,
+                             generator=torch.Generator(device="cuda").manual_seed(args.seed))
+    for store in (sb.pool_t.k_store, sb.pool_t.v_store, sb.pool_d.k_store, sb.pool_d.v_store):
+        store.normal_()
+    for c in ctxs:
+        toks = torch.randint(0, CFG["vocab_size"], (c + 1,), generator=g).tolist()
+        sb.add(toks, max_new_tokens=10 ** 9, temperature=args.temperature, prefill=False)
+    torch.cuda.synchronize()
+    log(f"pools: target {sb.pool_t.k_store.numel() * 4 / 1e9:.1f} GB, draft {sb.pool_d.k_store.numel() * 4 / 1e9:.1f} GB;"
+        f" setup {time.time() - t0:.1f}s")
+
+    for i in range(args.warmup):
+        sb.round()
+        log(f"warmup round {i} done")
+    torch.cuda.synchronize()
+
+    # verify-attention launches of the timed rounds are bracketed by events on the launching stream
+    events = []
+    ops.ATTN_EVENTS = events
+    ops.ATTN_EVENT_T = K + 1
+    ctx_log = []
+    acc0 = dict(sb.stats)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    committed = 0
+    for i in range(args.steps):
+        ctx_log.append([len(s.tokens) for s in sb.active()])
+        committed += sb.round()
+        if (i + 1) % 32 == 0:
+            log(f"round {i + 1}/{args.steps}: {committed} tokens committed")
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    ops.ATTN_EVENTS = None
+
+    # each round's verify pass runs n_layers attention launches over contexts len(tokens) - 1 + k + 1
+    layers = CFG["n_layers"]
+    assert len(events) == layers * args.steps, (len(events), layers * args.steps)
+    durs = [a.elapsed_time(b) * 1e-3 for a, b in events]
+    bytes_total = 0
+    for lens in ctx_log:
+        bytes_total += layers * attn_bytes([n + K for n in lens], K + 1, CFG["n_heads"], CFG["n_kv_heads"], 128, BLOCK)
+    attn_avg = sum(durs) / len(durs)
+    attn_gbs = bytes_total / sum(durs) / 1e9
+    attn_traffic = bytes_total / len(durs)
+
+    proposed = sb.stats["proposed"] - acc0["proposed"]
+    accepted = sb.stats["accepted"] - acc0["accepted"]
+    value = committed / elapsed
+
+    # the acceptance kernel alone at the benchmark shape (bf16 logits, V = 128256)
+    v = CFG["vocab_size"]
+    tl = torch.randn(BATCH, K + 1, v, device="cuda").mul_(2).bfloat16()
+    dl = (tl[:, :K].float() + torch.randn(BATCH, K, v, device="cuda") * 0.5).bfloat16()
+    xs = dl.float().argmax(-1).int()
+    temps = torch.ones(BATCH, device="cuda")
+    u = torch.rand(BATCH, K, device="cuda")
+    e = torch.empty(BATCH, v, device="cuda").exponential_()
+    for _ in range(3):
+        ops.spec_accept(tl, dl, xs, None, temps, u, e)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
+    for a, b in ev:
+        a.record()
+        ops.spec_accept(tl, dl, xs, None, temps, u, e)
+        b.record()
+    torch.cuda.synchronize()
+    acc_avg = sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e-3
+    acc_gbs = accept_bytes(BATCH, K, v) / acc_avg / 1e9
+
+    result = {
+        "metric": "accepted tok/s (8B-shape, k=6, bs=64); verify-attn HBM GB/s vs peak",
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights; synthetic N(0,1) bf16 context KV)",
+        "config": {"workload": "8B-shape speculative decode: 32L d4096 32/8 heads hd128 ffn14336 V128256 bf16, "
+                               "early-exit draft 4 layers, batch 64, k=6, contexts U[2048,8192], block 16",
+                   "global_batch": BATCH, "k": K, "temperature": args.temperature, "parallelism": "none (1 GPU)"},
+        "acceptance": {"proposed": proposed, "accepted": accepted,
+                       "rate": round(accepted / max(proposed, 1), 4),
+                       "committed_per_round": round(committed / args.steps, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "paged_attention verify (attn_mfma_bf16_kernel<128> + attn_combine_kernel)",
+                     "avg_launch_us": round(attn_avg * 1e6, 2),
+                     "algorithmic_bytes_per_launch": int(attn_traffic)},
+        "accept_kernel": {"avg_us": round(acc_avg * 1e6, 2), "achieved_GBs": round(acc_gbs, 1),
+                          "algorithmic_bytes": accept_bytes(BATCH, K, v)},
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline ...")
+        result["cpu_baseline"] = cpu_baseline(torch, committed / args.steps)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,101 @@
+// Shared device/host helpers for the forgeserve_amd gfx950 kernels.
+//
+// Numeric conventions (they decide bit-level parity with the PyTorch CPU reference):
+//   * bf16 <-> f32 conversions are round-to-nearest-even, as c10::BFloat16 does.
+//   * Every elementwise op that the reference performs in the tensor dtype is rounded to that dtype
+//     after the op (torch's CPU kernels compute bf16 ops in f32 and round each result).
+//   * The library is compiled with -ffp-contract=off: a*b - c*d stays two roundings, as in torch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/forgeserve_amd.h"
+
+#define FS_DEVICE __device__ __forceinline__
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short short4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float float4_t;
+
+// ------------------------------------------------------------------------------------------------
+// scalar conversions
+// ------------------------------------------------------------------------------------------------
+FS_DEVICE float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+FS_DEVICE uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+FS_DEVICE float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+FS_DEVICE uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }  // RNE
+
+// Storage-type traits: load/store one element as f32, and round an f32 to what the dtype can hold.
+template <int DT> struct Elem;
+template <> struct Elem<FS_F32> {
+  typedef float T;
+  static FS_DEVICE float load(const T* p, int64_t i) { return p[i]; }
+  static FS_DEVICE void store(T* p, int64_t i, float v) { p[i] = v; }
+  static FS_DEVICE float round(float v) { return v; }
+  static FS_DEVICE float to_f32(T v) { return v; }
+};
+template <> struct Elem<FS_BF16> {
+  typedef uint16_t T;
+  static FS_DEVICE float load(const T* p, int64_t i) { return bf16_to_f32(p[i]); }
+  static FS_DEVICE void store(T* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+  static FS_DEVICE float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+  static FS_DEVICE float to_f32(T v) { return bf16_to_f32(v); }
+};
+template <> struct Elem<FS_F16> {
+  typedef uint16_t T;
+  static FS_DEVICE float load(const T* p, int64_t i) { return f16_to_f32(p[i]); }
+  static FS_DEVICE void store(T* p, int64_t i, float v) { p[i] = f32_to_f16(v); }
+  static FS_DEVICE float round(float v) { return f16_to_f32(f32_to_f16(v)); }
+  static FS_DEVICE float to_f32(T v) { return f16_to_f32(v); }
+};
+
+// ------------------------------------------------------------------------------------------------
+// wavefront (64-lane) reductions
+// ------------------------------------------------------------------------------------------------
+FS_DEVICE float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+FS_DEVICE float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// (value, index) argmax where the larger value wins and equal values keep the lower index: the
+// first-occurrence rule of torch.argmax.
+FS_DEVICE void argmax_merge(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+FS_DEVICE void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(v, o, 64);
+    int oi = __shfl_xor(i, o, 64);
+    argmax_merge(v, i, ov, oi);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// host side: error reporting shared by every entry point
+// ------------------------------------------------------------------------------------------------
+namespace fs {
+void set_error(const char* fmt, ...);
+int arg_error(const char* fmt, ...);           // sets the message, returns FS_ERR_ARG
+int launch_status(const char* what);           // hipGetLastError after a launch -> 0 or >0
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+}  // namespace fs
+
+#define FS_CHECK_ARG(cond, ...) \
+  do {                           \
+    if (!(cond)) return fs::arg_error(__VA_ARGS__); \
+  } while (0)

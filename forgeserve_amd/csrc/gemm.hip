@@ -1,0 +1,238 @@
+// Dense projections: C[M,N] = A[M,K] . B[N,K]^T (+ R), the nn.Linear of model.py:57-60, 88-90, 119
+// (tied head) with the residual add of model.py:105-106 fused into the epilogue.
+//
+// bf16 path: v_mfma_f32_16x16x32_bf16 tiles, LDS double buffering, f32 accumulation, one rounding.
+// Every output element accumulates its K products in increasing k, 32 at a time, in one MFMA
+// accumulator, whatever the tile shape or M: a row's result does not depend on the batch it is in
+// (the draft step, the verify pass and prefill give identical rows for identical inputs).
+// f32 (and unaligned bf16) path: LDS-tiled VALU kernel, one fmaf chain per output in increasing k.
+#include "common.h"
+
+namespace {
+
+// ------------------------------------------------------------------------------------------------
+// bf16 MFMA kernel
+// ------------------------------------------------------------------------------------------------
+constexpr int BK = 64;
+constexpr int LDS_PITCH = BK + 8;  // bf16 elements per LDS row (16 B pad against bank conflicts)
+
+template <int BM, int BN>
+__global__ void __launch_bounds__(256) gemm_bf16_kernel(const uint16_t* __restrict__ A, int64_t lda,
+                                                        const uint16_t* __restrict__ B, int64_t ldb,
+                                                        uint16_t* __restrict__ C, int64_t ldc,
+                                                        const uint16_t* __restrict__ R, int64_t ldr, int64_t M,
+                                                        int64_t N, int64_t K, int tiles_n) {
+  constexpr int WM = BM / 2, WN = BN / 2;           // 2x2 waves
+  constexpr int TM = WM / 16, TN = WN / 16;         // MFMA tiles per wave
+  constexpr int A_CHUNKS = BM * BK / 8 / 256;       // 16-byte chunks per thread per stage
+  constexpr int B_CHUNKS = BN * BK / 8 / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDS_PITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LDS_PITCH];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tile = blockIdx.x;
+  const int64_t m0 = (int64_t)(tile / tiles_n) * BM;
+  const int64_t n0 = (int64_t)(tile % tiles_n) * BN;
+
+  typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+  u32x4 ra[A_CHUNKS], rb[B_CHUNKS];
+
+  auto gload = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / (BK / 8), kc = (c % (BK / 8)) * 8;
+      int64_t gr = m0 + row;
+      gr = gr < M ? gr : M - 1;
+      const int64_t gk = k0 + kc;
+      if (gk < K)
+        ra[i] = *reinterpret_cast<const u32x4*>(A + gr * lda + gk);
+      else
+        ra[i] = u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < B_CHUNKS; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / (BK / 8), kc = (c % (BK / 8)) * 8;
+      int64_t gr = n0 + row;
+      gr = gr < N ? gr : N - 1;
+      const int64_t gk = k0 + kc;
+      if (gk < K)
+        rb[i] = *reinterpret_cast<const u32x4*>(B + gr * ldb + gk);
+      else
+        rb[i] = u32x4{0, 0, 0, 0};
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / (BK / 8), kc = (c % (BK / 8)) * 8;
+      *reinterpret_cast<u32x4*>(&As[buf][row * LDS_PITCH + kc]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_CHUNKS; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / (BK / 8), kc = (c % (BK / 8)) * 8;
+      *reinterpret_cast<u32x4*>(&Bs[buf][row * LDS_PITCH + kc]) = rb[i];
+    }
+  };
+
+  float4_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (int)((K + BK - 1) / BK);
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload((int64_t)(kt + 1) * BK);
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      bf16x8_t af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8_t*>(&As[cur][(wm * WM + 16 * i + l16) * LDS_PITCH + 32 * ks + 8 * g]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[cur][(wn * WN + 16 * j + l16) * LDS_PITCH + 32 * ks + 8 * g]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) {
+      sstore(cur ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // acc[i][j] (A = B-tile, B = A-tile) holds C^T: lane (l16, g) has columns n = 16j + 4g + r, row m = 16i + l16
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t row = m0 + wm * WM + 16 * i + l16;
+    if (row >= M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col0 = n0 + wn * WN + 16 * j + 4 * g;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t col = col0 + r;
+        if (col >= N) continue;
+        float v = Elem<FS_BF16>::round(acc[i][j][r]);
+        if (R) v = v + bf16_to_f32(R[row * ldr + col]);
+        C[row * ldc + col] = f32_to_bf16(v);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// VALU kernel (f32 / f16 / unaligned bf16): 64x64 tile, 16-deep k stages, 4x4 outputs per thread
+// ------------------------------------------------------------------------------------------------
+template <int DT>
+__global__ void __launch_bounds__(256) gemm_valu_kernel(const typename Elem<DT>::T* __restrict__ A, int64_t lda,
+                                                        const typename Elem<DT>::T* __restrict__ B, int64_t ldb,
+                                                        typename Elem<DT>::T* __restrict__ C, int64_t ldc,
+                                                        const typename Elem<DT>::T* __restrict__ R, int64_t ldr,
+                                                        int64_t M, int64_t N, int64_t K, int tiles_n) {
+  typedef Elem<DT> E;
+  constexpr int T = 64, KB = 16;
+  __shared__ float As[KB][T + 4];
+  __shared__ float Bs[KB][T + 4];
+  const int tid = threadIdx.x;
+  const int tile = blockIdx.x;
+  const int64_t m0 = (int64_t)(tile / tiles_n) * T;
+  const int64_t n0 = (int64_t)(tile % tiles_n) * T;
+  const int tx = tid & 15, ty = tid >> 4;
+  float acc[4][4] = {};
+  for (int64_t k0 = 0; k0 < K; k0 += KB) {
+    for (int c = tid; c < T * KB; c += 256) {
+      const int r = c / KB, kk = c % KB;
+      const int64_t gk = k0 + kk;
+      const int64_t am = m0 + r, bn = n0 + r;
+      As[kk][r] = (am < M && gk < K) ? E::load(A, am * lda + gk) : 0.f;
+      Bs[kk][r] = (bn < N && gk < K) ? E::load(B, bn * ldb + gk) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < KB; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = m0 + ty * 4 + i;
+    if (row >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = n0 + tx * 4 + j;
+      if (col >= N) continue;
+      float v = E::round(acc[i][j]);
+      if (R) v = v + E::load(R, row * ldr + col);
+      E::store(C, row * ldc + col, v);
+    }
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+extern "C" int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, const void* R,
+                       int64_t ldr, int64_t M, int64_t N, int64_t K, int32_t dtype, void* stream) {
+  FS_CHECK_ARG(A && B && C, "gemm: null pointer");
+  FS_CHECK_ARG(dtype == FS_F32 || dtype == FS_BF16 || dtype == FS_F16, "gemm: dtype %d", dtype);
+  FS_CHECK_ARG(M >= 0 && N > 0 && K > 0, "gemm: M %lld N %lld K %lld", (long long)M, (long long)N, (long long)K);
+  FS_CHECK_ARG(lda >= K && ldb >= K && ldc >= N && (!R || ldr >= N), "gemm: leading dimensions");
+  if (M == 0) return 0;
+  hipStream_t s = fs::as_stream(stream);
+  const bool mfma = dtype == FS_BF16 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B);
+  if (mfma) {
+    const uint16_t* a = (const uint16_t*)A;
+    const uint16_t* b = (const uint16_t*)B;
+    if (M > 64) {
+      const int tm = (int)((M + 127) / 128), tn = (int)((N + 127) / 128);
+      gemm_bf16_kernel<128, 128><<<dim3((unsigned)(tm * tn)), 256, 0, s>>>(a, lda, b, ldb, (uint16_t*)C, ldc,
+                                                                           (const uint16_t*)R, ldr, M, N, K, tn);
+    } else {
+      const int tm = (int)((M + 63) / 64), tn = (int)((N + 63) / 64);
+      gemm_bf16_kernel<64, 64><<<dim3((unsigned)(tm * tn)), 256, 0, s>>>(a, lda, b, ldb, (uint16_t*)C, ldc,
+                                                                         (const uint16_t*)R, ldr, M, N, K, tn);
+    }
+    return fs::launch_status("gemm_bf16");
+  }
+  const int tm = (int)((M + 63) / 64), tn = (int)((N + 63) / 64);
+  dim3 grid((unsigned)(tm * tn));
+  switch (dtype) {
+    case FS_F32:
+      gemm_valu_kernel<FS_F32><<<grid, 256, 0, s>>>((const float*)A, lda, (const float*)B, ldb, (float*)C, ldc,
+                                                   (const float*)R, ldr, M, N, K, tn);
+      break;
+    case FS_BF16:
+      gemm_valu_kernel<FS_BF16><<<grid, 256, 0, s>>>((const uint16_t*)A, lda, (const uint16_t*)B, ldb, (uint16_t*)C,
+                                                    ldc, (const uint16_t*)R, ldr, M, N, K, tn);
+      break;
+    default:
+      gemm_valu_kernel<FS_F16><<<grid, 256, 0, s>>>((const uint16_t*)A, lda, (const uint16_t*)B, ldb, (uint16_t*)C,
+                                                   ldc, (const uint16_t*)R, ldr, M, N, K, tn);
+      break;
+  }
+  return fs::launch_status("gemm_valu");
+}

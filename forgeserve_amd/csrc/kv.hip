@@ -1,0 +1,231 @@
+// Paged KV cache kernels: fused rotary + KV write, plain KV write, and the compatibility gather.
+//
+// Reference: paged.py:71-82 (PagedLayerView.update) and model.py:40-45 (apply_rope).
+// Pool layout is described by fs_kv_layout; one (block, kv-head) tile of keys is block_size*head_dim
+// contiguous elements, and values are stored dim-major so the attention kernel reads 16 keys of one
+// dim as one contiguous run.
+#include "common.h"
+
+namespace {
+
+// Rotary half-split rotation of one pair (x[i], x[i + D/2]) at table row `pos`, in dtype DT:
+//   out[i]       = x1*c - x2*s,   out[i + D/2] = x2*c + x1*s        (model.py:44-45)
+// with c, s rounded to DT first (model.py:42-43) and every product and sum rounded to DT.
+template <int DT>
+FS_DEVICE void rope_pair(float x1, float x2, float c, float s, float& o1, float& o2) {
+  typedef Elem<DT> E;
+  c = E::round(c);
+  s = E::round(s);
+  float a = E::round(x1 * c), b = E::round(x2 * s);
+  float d = E::round(x2 * c), e = E::round(x1 * s);
+  o1 = E::round(a - b);
+  o2 = E::round(d + e);
+}
+
+FS_DEVICE bool slot_of(int pos, const int32_t* table, int64_t table_stride, int b, int max_blocks,
+                       const fs_kv_layout& kv, int64_t& blk, int& slot) {
+  if (pos < 0) return false;
+  int bi = pos / kv.block_size;
+  if (bi >= max_blocks) return false;
+  blk = table[(int64_t)b * table_stride + bi];
+  if (blk < 0 || blk >= kv.num_blocks) return false;
+  slot = pos - bi * kv.block_size;
+  return true;
+}
+
+// One workgroup per token. Threads cover (q heads + kv heads) * D/2 rotation pairs, then the values.
+template <int DT>
+__global__ void __launch_bounds__(256) qkv_rope_write_kernel(
+    const typename Elem<DT>::T* __restrict__ qkv, int64_t qkv_stride, int32_t T, int32_t H,
+    const int32_t* __restrict__ positions, const int32_t* __restrict__ slots, const float* __restrict__ rope_cos,
+    const float* __restrict__ rope_sin, int32_t rope_len, const int32_t* __restrict__ table,
+    int64_t table_stride, int32_t max_blocks, fs_kv_layout kv, typename Elem<DT>::T* __restrict__ q_out,
+    int64_t q_stride) {
+  typedef Elem<DT> E;
+  typedef typename E::T T_;
+  const int64_t m = blockIdx.x;
+  const int b = (int)(m / T);
+  const int D = kv.head_dim, half = D / 2, Hkv = kv.n_kv_heads;
+  const int pos = positions[m];
+  const bool rot_ok = pos >= 0 && pos < rope_len;
+  int64_t blk = 0;
+  int slot = 0;
+  const int wpos = slots ? slots[m] : pos;
+  const bool write_ok = rot_ok && slot_of(wpos, table, table_stride, b, max_blocks, kv, blk, slot);
+  const T_* row = qkv + m * qkv_stride;
+  T_* kp = reinterpret_cast<T_*>(kv.k);
+  T_* vp = reinterpret_cast<T_*>(kv.v);
+
+  const int n_pairs = (H + Hkv) * half;
+  for (int i = threadIdx.x; i < n_pairs; i += blockDim.x) {
+    const int head = i / half, p = i - head * half;
+    const float x1 = E::load(row, (int64_t)head * D + p);
+    const float x2 = E::load(row, (int64_t)head * D + p + half);
+    float o1 = 0.f, o2 = 0.f;
+    if (rot_ok) rope_pair<DT>(x1, x2, rope_cos[(int64_t)pos * half + p], rope_sin[(int64_t)pos * half + p], o1, o2);
+    if (head < H) {
+      T_* qo = q_out + m * q_stride + (int64_t)head * D;
+      E::store(qo, p, o1);
+      E::store(qo, p + half, o2);
+    } else if (write_ok) {
+      const int h = head - H;
+      const int64_t base = blk * kv.k_block + h * kv.k_head + slot * kv.k_slot;
+      E::store(kp, base + p * kv.k_dim, o1);
+      E::store(kp, base + (p + half) * kv.k_dim, o2);
+    }
+  }
+  if (write_ok) {
+    const int n_v = Hkv * D;
+    const T_* vrow = row + (int64_t)(H + Hkv) * D;
+    for (int i = threadIdx.x; i < n_v; i += blockDim.x) {
+      const int h = i / D, d = i - h * D;
+      vp[blk * kv.v_block + h * kv.v_head + slot * kv.v_slot + d * kv.v_dim] = vrow[i];
+    }
+  }
+}
+
+// One workgroup per (b, t): scatter k_new[b, :, t, :] and v_new[b, :, t, :].
+template <int DT>
+__global__ void __launch_bounds__(256) kv_write_kernel(const typename Elem<DT>::T* __restrict__ k_new,
+                                                       const typename Elem<DT>::T* __restrict__ v_new,
+                                                       int64_t s_b, int64_t s_h, int64_t s_t, int32_t T,
+                                                       const int32_t* __restrict__ positions,
+                                                       const int32_t* __restrict__ table, int64_t table_stride,
+                                                       int32_t max_blocks, fs_kv_layout kv) {
+  typedef typename Elem<DT>::T T_;
+  const int bt = blockIdx.x;
+  const int b = bt / T, t = bt - b * T;
+  int64_t blk = 0;
+  int slot = 0;
+  if (!slot_of(positions[bt], table, table_stride, b, max_blocks, kv, blk, slot)) return;
+  const int D = kv.head_dim, n = kv.n_kv_heads * D;
+  T_* kp = reinterpret_cast<T_*>(kv.k);
+  T_* vp = reinterpret_cast<T_*>(kv.v);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int h = i / D, d = i - h * D;
+    const int64_t src = (int64_t)b * s_b + (int64_t)h * s_h + (int64_t)t * s_t + d;
+    kp[blk * kv.k_block + h * kv.k_head + slot * kv.k_slot + d * kv.k_dim] = k_new[src];
+    vp[blk * kv.v_block + h * kv.v_head + slot * kv.v_slot + d * kv.v_dim] = v_new[src];
+  }
+}
+
+// out[b, h, j, d] for j < max_blocks*block_size; invalid block ids read as zeros.
+template <int DT>
+__global__ void __launch_bounds__(256) gather_kernel(fs_kv_layout kv, const int32_t* __restrict__ table,
+                                                     int64_t table_stride, int32_t max_blocks,
+                                                     typename Elem<DT>::T* __restrict__ k_out,
+                                                     typename Elem<DT>::T* __restrict__ v_out, int64_t total) {
+  typedef typename Elem<DT>::T T_;
+  const T_* kp = reinterpret_cast<const T_*>(kv.k);
+  const T_* vp = reinterpret_cast<const T_*>(kv.v);
+  const int D = kv.head_dim, BS = kv.block_size, Hkv = kv.n_kv_heads;
+  const int64_t S = (int64_t)max_blocks * BS;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int d = (int)(i % D);
+    int64_t r = i / D;
+    const int64_t j = r % S;
+    r /= S;
+    const int h = (int)(r % Hkv);
+    const int b = (int)(r / Hkv);
+    const int64_t blk = table[(int64_t)b * table_stride + j / BS];
+    const int slot = (int)(j % BS);
+    T_ kv_k = T_(0), kv_v = T_(0);
+    if (blk >= 0 && blk < kv.num_blocks) {
+      kv_k = kp[blk * kv.k_block + h * kv.k_head + slot * kv.k_slot + d * kv.k_dim];
+      kv_v = vp[blk * kv.v_block + h * kv.v_head + slot * kv.v_slot + d * kv.v_dim];
+    }
+    k_out[i] = kv_k;
+    v_out[i] = kv_v;
+  }
+}
+
+int check_layout(const fs_kv_layout* kv) {
+  FS_CHECK_ARG(kv != nullptr && kv->k != nullptr && kv->v != nullptr, "kv layout: null pool");
+  FS_CHECK_ARG(kv->dtype == FS_F32 || kv->dtype == FS_BF16 || kv->dtype == FS_F16, "kv layout: bad dtype %d",
+               kv->dtype);
+  FS_CHECK_ARG(kv->block_size > 0 && kv->n_kv_heads > 0 && kv->head_dim > 0 && kv->head_dim % 2 == 0,
+               "kv layout: block_size %d, n_kv_heads %d, head_dim %d", kv->block_size, kv->n_kv_heads,
+               kv->head_dim);
+  FS_CHECK_ARG(kv->num_blocks > 0, "kv layout: num_blocks %lld", (long long)kv->num_blocks);
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int fs_qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_t T, int32_t n_heads,
+                                 const int32_t* positions, const int32_t* slots, const float* rope_cos,
+                                 const float* rope_sin,
+                                 int32_t rope_len, const int32_t* block_tables, int64_t table_stride,
+                                 int32_t max_blocks, const fs_kv_layout* kv, void* q_out, int64_t q_stride,
+                                 void* stream) {
+  if (int e = check_layout(kv)) return e;
+  FS_CHECK_ARG(qkv && positions && rope_cos && rope_sin && block_tables && q_out, "qkv_rope_write: null pointer");
+  FS_CHECK_ARG(T > 0 && n_tokens >= 0 && n_tokens % T == 0, "qkv_rope_write: n_tokens %lld not a multiple of T %d",
+               (long long)n_tokens, T);
+  FS_CHECK_ARG(n_heads > 0 && n_heads % kv->n_kv_heads == 0, "qkv_rope_write: n_heads %d vs n_kv_heads %d", n_heads,
+               kv->n_kv_heads);
+  FS_CHECK_ARG(max_blocks > 0 && table_stride >= max_blocks, "qkv_rope_write: table %d/%lld", max_blocks,
+               (long long)table_stride);
+  FS_CHECK_ARG(qkv_stride >= (int64_t)(n_heads + 2 * kv->n_kv_heads) * kv->head_dim, "qkv_rope_write: qkv stride");
+  if (n_tokens == 0) return 0;
+  hipStream_t s = fs::as_stream(stream);
+  dim3 grid((unsigned)n_tokens);
+#define FS_LAUNCH(DT)                                                                                        \
+  qkv_rope_write_kernel<DT><<<grid, 256, 0, s>>>(                                                          \
+      (const typename Elem<DT>::T*)qkv, qkv_stride, T, n_heads, positions, slots, rope_cos, rope_sin, rope_len, \
+      block_tables, table_stride, max_blocks, *kv, (typename Elem<DT>::T*)q_out, q_stride)
+  switch (kv->dtype) {
+    case FS_F32: FS_LAUNCH(FS_F32); break;
+    case FS_BF16: FS_LAUNCH(FS_BF16); break;
+    default: FS_LAUNCH(FS_F16); break;
+  }
+#undef FS_LAUNCH
+  return fs::launch_status("qkv_rope_write");
+}
+
+extern "C" int fs_paged_kv_write(const void* k_new, const void* v_new, int64_t s_b, int64_t s_h, int64_t s_t,
+                                 int32_t B, int32_t T, const int32_t* positions, const int32_t* block_tables,
+                                 int64_t table_stride, int32_t max_blocks, const fs_kv_layout* kv, void* stream) {
+  if (int e = check_layout(kv)) return e;
+  FS_CHECK_ARG(k_new && v_new && positions && block_tables, "paged_kv_write: null pointer");
+  FS_CHECK_ARG(B >= 0 && T >= 0, "paged_kv_write: B %d T %d", B, T);
+  FS_CHECK_ARG(max_blocks > 0 && table_stride >= max_blocks, "paged_kv_write: table %d/%lld", max_blocks,
+               (long long)table_stride);
+  if (B == 0 || T == 0) return 0;
+  hipStream_t s = fs::as_stream(stream);
+  dim3 grid((unsigned)(B * T));
+#define FS_LAUNCH(DT)                                                                                            \
+  kv_write_kernel<DT><<<grid, 256, 0, s>>>((const typename Elem<DT>::T*)k_new, (const typename Elem<DT>::T*)v_new, \
+                                           s_b, s_h, s_t, T, positions, block_tables, table_stride, max_blocks, *kv)
+  switch (kv->dtype) {
+    case FS_F32: FS_LAUNCH(FS_F32); break;
+    case FS_BF16: FS_LAUNCH(FS_BF16); break;
+    default: FS_LAUNCH(FS_F16); break;
+  }
+#undef FS_LAUNCH
+  return fs::launch_status("paged_kv_write");
+}
+
+extern "C" int fs_paged_gather(const fs_kv_layout* kv, const int32_t* block_tables, int64_t table_stride, int32_t B,
+                               int32_t max_blocks, void* k_out, void* v_out, void* stream) {
+  if (int e = check_layout(kv)) return e;
+  FS_CHECK_ARG(block_tables && k_out && v_out, "paged_gather: null pointer");
+  FS_CHECK_ARG(B >= 0 && max_blocks >= 0 && table_stride >= max_blocks, "paged_gather: B %d max_blocks %d", B,
+               max_blocks);
+  const int64_t total = (int64_t)B * kv->n_kv_heads * max_blocks * kv->block_size * kv->head_dim;
+  if (total == 0) return 0;
+  hipStream_t s = fs::as_stream(stream);
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  dim3 grid((unsigned)blocks);
+#define FS_LAUNCH(DT)                                                                                 \
+  gather_kernel<DT><<<grid, 256, 0, s>>>(*kv, block_tables, table_stride, max_blocks,               \
+                                         (typename Elem<DT>::T*)k_out, (typename Elem<DT>::T*)v_out, total)
+  switch (kv->dtype) {
+    case FS_F32: FS_LAUNCH(FS_F32); break;
+    case FS_BF16: FS_LAUNCH(FS_BF16); break;
+    default: FS_LAUNCH(FS_F16); break;
+  }
+#undef FS_LAUNCH
+  return fs::launch_status("paged_gather");
+}

@@ -1,0 +1,675 @@
+// Sampling and speculative acceptance over vocab-wide rows, with no host round trip.
+//
+// Reference: sampling.py:9-21 (probs_from_logits, sample), speculative.py:20-33 (verify_draft) and the
+// rollback arithmetic of speculative.py:77.
+//
+// Every row of V logits is cut into chunks of CH columns. Launch 1 reduces each (row, chunk) to
+// (max of x/T, sum of exp(x/T - max), first argmax of x). Later launches merge a row's chunk partials
+// in increasing chunk order, so every workgroup that needs a row's softmax gets bit-identical
+// (M, S) and therefore bit-identical probabilities p_v = exp(x_v/T - M) / S.
+//
+// torch.multinomial(w, 1) draws argmax_v(w_v / E_v) with E ~ Exp(1) (first index on ties); the
+// caller supplies E, so the draw is a deterministic function of (logits, E) and can be compared
+// bit for bit with the CPU reference on the same noise.
+#include <math.h>
+
+#include "common.h"
+
+namespace {
+
+constexpr int THREADS = 256;
+constexpr int VEC = 8;                       // consecutive columns per thread group
+constexpr int UNROLL = 2;                    // groups per thread per chunk
+constexpr int CH = THREADS * VEC * UNROLL;   // 4096 columns per chunk
+
+struct Stat {
+  float m;    // max of x/T (T > 0) or of x (T == 0)
+  float s;    // sum of exp(x/T - m) (T > 0)
+  float av;   // argmax value (of x)
+  int ai;     // argmax index (first occurrence)
+};
+
+// Rows of a batch of sequences: for sequence b, rows 0..n0-1 come from base0 (row i at
+// base0 + b*sb0 + i*si0) and rows n0..n0+n1-1 from base1.
+struct RowSet {
+  const void* base0;
+  int64_t sb0, si0;
+  int32_t n0;
+  const void* base1;
+  int64_t sb1, si1;
+  int32_t n1;
+};
+
+template <int DT>
+FS_DEVICE const typename Elem<DT>::T* row_ptr(const RowSet& rs, int b, int i) {
+  typedef typename Elem<DT>::T T_;
+  if (i < rs.n0) return reinterpret_cast<const T_*>(rs.base0) + b * rs.sb0 + i * rs.si0;
+  return reinterpret_cast<const T_*>(rs.base1) + b * rs.sb1 + (i - rs.n0) * rs.si1;
+}
+
+// Load 8 consecutive columns starting at v (a multiple of 8) as f32; columns >= V read as `fill`.
+template <int DT>
+FS_DEVICE void load8(const typename Elem<DT>::T* row, int64_t v, int64_t V, bool vec_ok, float fill, float (&x)[8]) {
+  if (vec_ok && v + 8 <= V) {
+    if (DT == FS_F32) {
+      const float4_t a = *reinterpret_cast<const float4_t*>(reinterpret_cast<const float*>(row) + v);
+      const float4_t c = *reinterpret_cast<const float4_t*>(reinterpret_cast<const float*>(row) + v + 4);
+      x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+      x[4] = c[0]; x[5] = c[1]; x[6] = c[2]; x[7] = c[3];
+    } else {
+      typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+      const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(row) + v);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[2 * j] = Elem<DT>::to_f32((uint16_t)(w[j] & 0xffffu));
+        x[2 * j + 1] = Elem<DT>::to_f32((uint16_t)(w[j] >> 16));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = (v + j < V) ? Elem<DT>::load(row, v + j) : fill;
+  }
+}
+
+FS_DEVICE void load8_f32(const float* row, int64_t v, int64_t V, bool vec_ok, float (&x)[8]) {
+  if (vec_ok && v + 8 <= V) {
+    const float4_t a = *reinterpret_cast<const float4_t*>(row + v);
+    const float4_t c = *reinterpret_cast<const float4_t*>(row + v + 4);
+    x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+    x[4] = c[0]; x[5] = c[1]; x[6] = c[2]; x[7] = c[3];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = (v + j < V) ? row[v + j] : 1.f;
+  }
+}
+
+// Workgroup reductions in a fixed order (lane butterfly, then waves in index order).
+FS_DEVICE float block_max(float v, float* sh) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = sh[0];
+#pragma unroll
+  for (int i = 1; i < THREADS / 64; ++i) r = fmaxf(r, sh[i]);
+  return r;
+}
+FS_DEVICE float block_sum(float v, float* sh) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = sh[0];
+#pragma unroll
+  for (int i = 1; i < THREADS / 64; ++i) r += sh[i];
+  return r;
+}
+FS_DEVICE void block_argmax(float& v, int& i, float* shv, int* shi) {
+  wave_argmax(v, i);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    shv[threadIdx.x >> 6] = v;
+    shi[threadIdx.x >> 6] = i;
+  }
+  __syncthreads();
+  v = shv[0];
+  i = shi[0];
+#pragma unroll
+  for (int w = 1; w < THREADS / 64; ++w) argmax_merge(v, i, shv[w], shi[w]);
+}
+
+// Merge the chunk partials of one row (increasing chunk order).
+FS_DEVICE Stat merge_row(const Stat* st, int nch) {
+  Stat r = st[0];
+  float M = r.m;
+  for (int c = 1; c < nch; ++c) M = fmaxf(M, st[c].m);
+  float S = 0.f;
+  for (int c = 0; c < nch; ++c) {
+    const float mc = st[c].m;
+    S += (mc == -INFINITY) ? 0.f : st[c].s * expf(mc - M);
+  }
+  for (int c = 1; c < nch; ++c) argmax_merge(r.av, r.ai, st[c].av, st[c].ai);
+  r.m = M;
+  r.s = S;
+  return r;
+}
+
+// p_v of a row from logits and merged stats (T > 0): softmax(f32(x) / T) (sampling.py:13).
+FS_DEVICE float softmax_at(float x, float T, const Stat& st) { return expf(x / T - st.m) / st.s; }
+
+// ------------------------------------------------------------------------------------------------
+// launch 1: per-(row, chunk) statistics
+// ------------------------------------------------------------------------------------------------
+template <int DT>
+__global__ void __launch_bounds__(THREADS) stats_kernel(RowSet rs, int64_t V, int nch, const float* __restrict__ temps,
+                                                        float t_all, const int32_t* __restrict__ k_eff,
+                                                        Stat* __restrict__ out) {
+  __shared__ float shf[THREADS / 64];
+  __shared__ int shi[THREADS / 64];
+  const int c = blockIdx.x;
+  const int rho = blockIdx.y;
+  const int per = rs.n0 + rs.n1;
+  const int b = rho / per, i = rho - b * per;
+  if (k_eff) {  // rows a sequence does not use: target rows > k_eff, draft rows >= k_eff
+    const int ke = min(max(k_eff[b], 0), rs.n1);
+    if (i < rs.n0 ? i > ke : (i - rs.n0) >= ke) return;
+  }
+  const float T = temps ? temps[b] : t_all;
+  const auto* row = row_ptr<DT>(rs, b, i);
+  const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
+  float x[UNROLL][8];
+  float lmax = -INFINITY, amv = -INFINITY;
+  int ami = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+    load8<DT>(row, v0, V, vec_ok, -INFINITY, x[u]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (v0 + j < V) argmax_merge(amv, ami, x[u][j], (int)(v0 + j));
+    }
+  }
+  block_argmax(amv, ami, shf, shi);
+  Stat st;
+  st.av = amv;
+  st.ai = ami;
+  if (T > 0.f) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        x[u][j] = x[u][j] / T;  // -inf padding stays -inf
+        lmax = fmaxf(lmax, x[u][j]);
+      }
+    const float m = block_max(lmax, shf);
+    float ls = 0.f;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ls += (x[u][j] == -INFINITY) ? 0.f : expf(x[u][j] - m);
+    st.m = m;
+    st.s = block_sum(ls, shf);
+  } else {
+    st.m = amv;
+    st.s = 0.f;
+  }
+  if (threadIdx.x == 0) out[(int64_t)rho * nch + c] = st;
+}
+
+// ------------------------------------------------------------------------------------------------
+// sampling: argmax over a chunk of p_v / E_v, then a per-row finalize
+// ------------------------------------------------------------------------------------------------
+template <int DT>
+__global__ void __launch_bounds__(THREADS) sample_argmax_kernel(RowSet rs, int64_t V, int nch,
+                                                                const float* __restrict__ temps, float t_all,
+                                                                const Stat* __restrict__ stats,
+                                                                const float* __restrict__ E, int64_t ldE,
+                                                                float* __restrict__ pv, int* __restrict__ pi) {
+  __shared__ float shf[THREADS / 64];
+  __shared__ int shi[THREADS / 64];
+  __shared__ Stat shs;
+  const int c = blockIdx.x, r = blockIdx.y;
+  const float T = temps ? temps[r] : t_all;
+  if (T <= 0.f) return;
+  if (threadIdx.x == 0) shs = merge_row(stats + (int64_t)r * nch, nch);
+  __syncthreads();
+  const Stat st = shs;
+  const auto* row = row_ptr<DT>(rs, r, 0);
+  const float* er = E + (int64_t)r * ldE;
+  const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(er) & 15) == 0);
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+    float x[8], e[8];
+    load8<DT>(row, v0, V, vec_ok, -INFINITY, x);
+    load8_f32(er, v0, V, vec_ok, e);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (v0 + j < V) argmax_merge(bv, bi, softmax_at(x[j], T, st) / e[j], (int)(v0 + j));
+    }
+  }
+  block_argmax(bv, bi, shf, shi);
+  if (threadIdx.x == 0) {
+    pv[(int64_t)r * nch + c] = bv;
+    pi[(int64_t)r * nch + c] = bi;
+  }
+}
+
+__global__ void sample_final_kernel(int R, int nch, const float* __restrict__ temps, float t_all, bool greedy_only,
+                                    const Stat* __restrict__ stats, const float* __restrict__ pv,
+                                    const int* __restrict__ pi, int64_t* __restrict__ tok, int32_t* __restrict__ tok32,
+                                    int64_t ld32) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= R) return;
+  int best;
+  const float T = temps ? temps[r] : t_all;
+  if (greedy_only || T <= 0.f) {
+    best = merge_row(stats + (int64_t)r * nch, nch).ai;
+  } else {
+    float v = pv[(int64_t)r * nch];
+    best = pi[(int64_t)r * nch];
+    for (int c = 1; c < nch; ++c) argmax_merge(v, best, pv[(int64_t)r * nch + c], pi[(int64_t)r * nch + c]);
+  }
+  tok[r] = best;
+  if (tok32) tok32[(int64_t)r * ld32] = best;
+}
+
+// ------------------------------------------------------------------------------------------------
+// acceptance
+// ------------------------------------------------------------------------------------------------
+struct AcceptArgs {
+  RowSet rs;          // n0 = K+1 target rows, n1 = K draft rows
+  int32_t K;
+  int64_t V;
+  int nch;
+  const int32_t* draft;  // [B, K]
+  const int32_t* k_eff;  // [B] or null (= K)
+  const float* temps;    // [B] (ignored for probabilities)
+  const float* u;        // [B, K]
+  const float* E;        // [B, V]
+  int64_t ldE;
+  const Stat* stats;     // [B*(2K+1)][nch] (logits mode)
+  float* resid;          // [B][nch]
+  float* pv;             // [B][nch]
+  int* pi;               // [B][nch]
+  int* jpos;             // [B]
+};
+
+// Value of p (row i < n0) or q (row >= n0) at column v, and the row's merged stats.
+template <int DT, bool PROBS>
+struct Dist {
+  const typename Elem<DT>::T* row;
+  Stat st;
+  float T;
+  FS_DEVICE float at_x(float x) const { return PROBS ? x : softmax_at(x, T, st); }
+};
+
+// First rejected proposal (or k_eff when every proposal is accepted): speculative.py:25-29.
+template <int DT, bool PROBS>
+FS_DEVICE int decide(const AcceptArgs& A, int b, int ke, float T) {
+  const int per = A.rs.n0 + A.rs.n1;
+  for (int i = 0; i < ke; ++i) {
+    const int x = A.draft[(int64_t)b * A.K + i];
+    if (x < 0 || x >= A.V) return i;  // an invalid proposal can never be accepted
+    float px, qx;
+    const auto* pr = row_ptr<DT>(A.rs, b, i);
+    const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + i);
+    if (PROBS) {
+      px = Elem<DT>::load(pr, x);
+      qx = Elem<DT>::load(qr, x);
+    } else if (T > 0.f) {
+      const Stat sp = merge_row(A.stats + ((int64_t)b * per + i) * A.nch, A.nch);
+      const Stat sq = merge_row(A.stats + ((int64_t)b * per + A.rs.n0 + i) * A.nch, A.nch);
+      px = softmax_at(Elem<DT>::load(pr, x), T, sp);
+      qx = softmax_at(Elem<DT>::load(qr, x), T, sq);
+    } else {  // one-hot rows of the first argmax (sampling.py:11-12)
+      px = merge_row(A.stats + ((int64_t)b * per + i) * A.nch, A.nch).ai == x ? 1.f : 0.f;
+      qx = merge_row(A.stats + ((int64_t)b * per + A.rs.n0 + i) * A.nch, A.nch).ai == x ? 1.f : 0.f;
+    }
+    const float ratio = qx > 0.f ? Elem<DT>::round(px / qx) : 1.0f;
+    if (!(A.u[(int64_t)b * A.K + i] < fminf(1.0f, ratio))) return i;
+  }
+  return ke;
+}
+
+// launch 2: decision (recomputed by every chunk workgroup) + residual partial sums of the rejected row
+template <int DT, bool PROBS>
+__global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) {
+  __shared__ float shf[THREADS / 64];
+  __shared__ int shj;
+  __shared__ Stat shp, shq;
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int ke = A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K;
+  const float T = PROBS ? 1.f : A.temps[b];
+  const int per = A.rs.n0 + A.rs.n1;
+  if (threadIdx.x == 0) {
+    const int j = decide<DT, PROBS>(A, b, ke, T);
+    shj = j;
+    if (c == 0) A.jpos[b] = j;
+    if (!PROBS && j < ke && T > 0.f) {
+      shp = merge_row(A.stats + ((int64_t)b * per + j) * A.nch, A.nch);
+      shq = merge_row(A.stats + ((int64_t)b * per + A.rs.n0 + j) * A.nch, A.nch);
+    }
+  }
+  __syncthreads();
+  const int j = shj;
+  if (j >= ke || (!PROBS && T <= 0.f)) return;  // bonus token or greedy: no residual
+  const Stat sp = shp, sq = shq;
+  const auto* pr = row_ptr<DT>(A.rs, b, j);
+  const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + j);
+  const bool vec_ok = (A.V % VEC) == 0 && (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr)) & 15) == 0);
+  float ls = 0.f;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+    float xp[8], xq[8];
+    load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp);
+    load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      if (v0 + jj >= A.V) continue;
+      const float p = PROBS ? xp[jj] : softmax_at(xp[jj], T, sp);
+      const float q = PROBS ? xq[jj] : softmax_at(xq[jj], T, sq);
+      ls += fmaxf(Elem<DT>::round(p - q), 0.f);  // (p - q).clamp(min=0), speculative.py:30
+    }
+  }
+  const float tot = block_sum(ls, shf);
+  if (threadIdx.x == 0) A.resid[(int64_t)b * A.nch + c] = tot;
+}
+
+// launch 3: argmax over a chunk of w_v / E_v with w the normalised residual or the bonus row
+template <int DT, bool PROBS>
+__global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
+  __shared__ float shf[THREADS / 64];
+  __shared__ int shi[THREADS / 64];
+  __shared__ Stat shp, shq;
+  __shared__ float shs;
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int ke = A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K;
+  const float T = PROBS ? 1.f : A.temps[b];
+  if (!PROBS && T <= 0.f) return;
+  const int per = A.rs.n0 + A.rs.n1;
+  const int j = A.jpos[b];
+  const bool bonus = j >= ke;
+  if (threadIdx.x == 0) {
+    if (!PROBS) {
+      shp = merge_row(A.stats + ((int64_t)b * per + j) * A.nch, A.nch);
+      if (!bonus) shq = merge_row(A.stats + ((int64_t)b * per + A.rs.n0 + j) * A.nch, A.nch);
+    }
+    float s = 0.f;
+    if (!bonus)
+      for (int cc = 0; cc < A.nch; ++cc) s += A.resid[(int64_t)b * A.nch + cc];
+    shs = Elem<DT>::round(s);
+  }
+  __syncthreads();
+  const Stat sp = shp, sq = shq;
+  const float s = shs;
+  const auto* pr = row_ptr<DT>(A.rs, b, j);
+  const auto* qr = bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j);
+  const float* er = A.E + (int64_t)b * A.ldE;
+  const bool vec_ok = (A.V % VEC) == 0 &&
+                      (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr) |
+                         reinterpret_cast<uintptr_t>(er)) & 15) == 0);
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+    float xp[8], xq[8], e[8];
+    load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp);
+    if (!bonus) load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq);
+    load8_f32(er, v0, A.V, vec_ok, e);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      if (v0 + jj >= A.V) continue;
+      const float p = PROBS ? xp[jj] : softmax_at(xp[jj], T, sp);
+      float w;
+      if (bonus) {
+        w = p;  // speculative.py:33
+      } else {
+        const float q = PROBS ? xq[jj] : softmax_at(xq[jj], T, sq);
+        const float r = fmaxf(Elem<DT>::round(p - q), 0.f);
+        w = s > 0.f ? Elem<DT>::round(r / s) : p;  // speculative.py:31
+      }
+      argmax_merge(bv, bi, w / e[jj], (int)(v0 + jj));
+    }
+  }
+  block_argmax(bv, bi, shf, shi);
+  if (threadIdx.x == 0) {
+    A.pv[(int64_t)b * A.nch + c] = bv;
+    A.pi[(int64_t)b * A.nch + c] = bi;
+  }
+}
+
+// launch 4: outputs and the device-side rollback (one thread per sequence)
+template <int DT, bool PROBS>
+__global__ void accept_final_kernel(AcceptArgs A, int B, int32_t* __restrict__ out_tokens,
+                                    int32_t* __restrict__ n_acc, int32_t* __restrict__ seq_len) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int ke = A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K;
+  const float T = PROBS ? 1.f : A.temps[b];
+  const int per = A.rs.n0 + A.rs.n1;
+  const int j = A.jpos[b];
+  int extra;
+  if (!PROBS && T <= 0.f) {
+    extra = merge_row(A.stats + ((int64_t)b * per + j) * A.nch, A.nch).ai;  // argmax of target row j
+  } else {
+    float v = A.pv[(int64_t)b * A.nch];
+    extra = A.pi[(int64_t)b * A.nch];
+    for (int c = 1; c < A.nch; ++c) argmax_merge(v, extra, A.pv[(int64_t)b * A.nch + c], A.pi[(int64_t)b * A.nch + c]);
+  }
+  int32_t* o = out_tokens + (int64_t)b * (A.K + 1);
+  for (int i = 0; i < j; ++i) o[i] = A.draft[(int64_t)b * A.K + i];
+  o[j] = extra;
+  for (int i = j + 1; i <= A.K; ++i) o[i] = -1;
+  n_acc[b] = j;
+  if (seq_len) seq_len[b] = seq_len[b] + 1 + j;  // want = cached + 1 + len(accepted)
+}
+
+// ------------------------------------------------------------------------------------------------
+// probs_from_logits
+// ------------------------------------------------------------------------------------------------
+template <int DT>
+__global__ void __launch_bounds__(THREADS) probs_kernel(RowSet rs, int64_t V, int nch, float T,
+                                                        const Stat* __restrict__ stats, void* __restrict__ out,
+                                                        int64_t ldo) {
+  __shared__ Stat shs;
+  const int c = blockIdx.x, r = blockIdx.y;
+  if (threadIdx.x == 0) shs = merge_row(stats + (int64_t)r * nch, nch);
+  __syncthreads();
+  const Stat st = shs;
+  const auto* row = row_ptr<DT>(rs, r, 0);
+  for (int u = 0; u < UNROLL * VEC; ++u) {
+    const int64_t v = (int64_t)c * CH + (int64_t)u * THREADS + threadIdx.x;
+    if (v >= V) break;
+    if (T > 0.f) {
+      reinterpret_cast<float*>(out)[(int64_t)r * ldo + v] = softmax_at(Elem<DT>::load(row, v), T, st);
+    } else {
+      Elem<DT>::store(reinterpret_cast<typename Elem<DT>::T*>(out), (int64_t)r * ldo + v, v == st.ai ? 1.f : 0.f);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// workspace carving
+// ------------------------------------------------------------------------------------------------
+struct Carve {
+  char* p;
+  int64_t used = 0;
+  template <typename T>
+  T* take(int64_t n) {
+    T* r = reinterpret_cast<T*>(p + used);
+    used += ((n * (int64_t)sizeof(T) + 255) / 256) * 256;
+    return r;
+  }
+};
+
+int64_t nchunks(int64_t V) { return (V + CH - 1) / CH; }
+
+int64_t accept_ws(int64_t B, int64_t K, int64_t V) {
+  const int64_t nch = nchunks(V);
+  auto r = [](int64_t n) { return ((n + 255) / 256) * 256; };
+  return r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) + 3 * r(B * nch * 4) + r(B * 4) + r(4);
+}
+
+bool dtype_ok(int32_t dt) { return dt == FS_F32 || dt == FS_BF16 || dt == FS_F16; }
+
+template <int DT>
+int launch_accept(const AcceptArgs& A, int B, bool probs, int32_t* out_tokens, int32_t* n_acc, int32_t* seq_len,
+                  hipStream_t s) {
+  const int per = A.rs.n0 + A.rs.n1;
+  if (!probs) {
+    stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(B * per)), THREADS, 0, s>>>(A.rs, A.V, A.nch, A.temps, 0.f,
+                                                                                  A.k_eff, const_cast<Stat*>(A.stats));
+    accept_residual_kernel<DT, false><<<dim3((unsigned)A.nch, (unsigned)B), THREADS, 0, s>>>(A);
+    accept_argmax_kernel<DT, false><<<dim3((unsigned)A.nch, (unsigned)B), THREADS, 0, s>>>(A);
+    accept_final_kernel<DT, false><<<dim3((unsigned)((B + 63) / 64)), 64, 0, s>>>(A, B, out_tokens, n_acc, seq_len);
+  } else {
+    accept_residual_kernel<DT, true><<<dim3((unsigned)A.nch, (unsigned)B), THREADS, 0, s>>>(A);
+    accept_argmax_kernel<DT, true><<<dim3((unsigned)A.nch, (unsigned)B), THREADS, 0, s>>>(A);
+    accept_final_kernel<DT, true><<<dim3((unsigned)((B + 63) / 64)), 64, 0, s>>>(A, B, out_tokens, n_acc, seq_len);
+  }
+  return fs::launch_status("spec_accept");
+}
+
+}  // namespace
+
+extern "C" int64_t fs_sampling_workspace_size(int64_t R, int64_t V) {
+  if (R <= 0 || V <= 0) return 0;
+  const int64_t nch = nchunks(V);
+  auto r = [](int64_t n) { return ((n + 255) / 256) * 256; };
+  return r(R * nch * (int64_t)sizeof(Stat)) + 2 * r(R * nch * 4) + r(4);
+}
+
+extern "C" int64_t fs_spec_accept_workspace_size(int32_t B, int32_t K, int64_t V) {
+  if (B <= 0 || K < 0 || V <= 0) return 0;
+  return accept_ws(B, K, V);
+}
+
+extern "C" int fs_sample_logits(const void* logits, int64_t ld, int64_t R, int64_t V, const float* temperature,
+                                float temperature_all, const float* E, int64_t ldE, int32_t dtype, int64_t* tokens_out,
+                                int32_t* tokens_out32, int64_t ld_tok32, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  FS_CHECK_ARG(logits && tokens_out && workspace, "sample_logits: null pointer");
+  FS_CHECK_ARG(dtype_ok(dtype), "sample_logits: dtype %d", dtype);
+  FS_CHECK_ARG(R >= 0 && V > 0 && V < 0x7fffffff && ld >= V, "sample_logits: R %lld V %lld", (long long)R,
+               (long long)V);
+  FS_CHECK_ARG(temperature || temperature_all >= 0.f, "sample_logits: temperature %f", (double)temperature_all);
+  FS_CHECK_ARG(!E || ldE >= V, "sample_logits: ldE %lld < V", (long long)ldE);
+  FS_CHECK_ARG(workspace_bytes >= fs_sampling_workspace_size(R, V), "sample_logits: workspace too small");
+  FS_CHECK_ARG(R <= 65535, "sample_logits: at most 65535 rows per call");
+  if (R == 0) return 0;
+  const int nch = (int)nchunks(V);
+  Carve cv{reinterpret_cast<char*>(workspace)};
+  Stat* st = cv.take<Stat>(R * nch);
+  float* pv = cv.take<float>(R * nch);
+  int* pi = cv.take<int>(R * nch);
+  RowSet rs{logits, ld, 0, 1, nullptr, 0, 0, 0};
+  hipStream_t s = fs::as_stream(stream);
+  const bool greedy_only = E == nullptr;
+  // with no noise every row takes the argmax; the statistics pass then only needs the argmax
+  const float t_stats = greedy_only ? 0.f : temperature_all;
+  const float* t_ptr = greedy_only ? nullptr : temperature;
+#define FS_LAUNCH(DT)                                                                                                  \
+  stats_kernel<DT><<<dim3((unsigned)nch, (unsigned)R), THREADS, 0, s>>>(rs, V, nch, t_ptr, t_stats, nullptr, st);     \
+  if (!greedy_only)                                                                                                    \
+    sample_argmax_kernel<DT><<<dim3((unsigned)nch, (unsigned)R), THREADS, 0, s>>>(rs, V, nch, temperature,             \
+                                                                                 temperature_all, st, E, ldE, pv, pi);
+  switch (dtype) {
+    case FS_F32: FS_LAUNCH(FS_F32); break;
+    case FS_BF16: FS_LAUNCH(FS_BF16); break;
+    default: FS_LAUNCH(FS_F16); break;
+  }
+#undef FS_LAUNCH
+  sample_final_kernel<<<dim3((unsigned)((R + 63) / 64)), 64, 0, s>>>((int)R, nch, temperature, temperature_all,
+                                                                     greedy_only, st, pv, pi, tokens_out, tokens_out32,
+                                                                     ld_tok32);
+  return fs::launch_status("sample_logits");
+}
+
+extern "C" int fs_probs_from_logits(const void* logits, int64_t ld, int64_t R, int64_t V, float temperature,
+                                    int32_t dtype, void* out, int64_t ldo, int32_t out_dtype, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+  FS_CHECK_ARG(logits && out && workspace, "probs_from_logits: null pointer");
+  FS_CHECK_ARG(dtype_ok(dtype), "probs_from_logits: dtype %d", dtype);
+  FS_CHECK_ARG(temperature >= 0.f, "probs_from_logits: temperature %f", (double)temperature);
+  FS_CHECK_ARG(temperature > 0.f ? out_dtype == FS_F32 : out_dtype == dtype,
+               "probs_from_logits: out dtype must be f32 (T > 0) or the logits dtype (T == 0)");
+  FS_CHECK_ARG(R >= 0 && R <= 65535 && V > 0 && V < 0x7fffffff && ld >= V && ldo >= V, "probs_from_logits: shapes");
+  FS_CHECK_ARG(workspace_bytes >= fs_sampling_workspace_size(R, V), "probs_from_logits: workspace too small");
+  if (R == 0) return 0;
+  const int nch = (int)nchunks(V);
+  Carve cv{reinterpret_cast<char*>(workspace)};
+  Stat* st = cv.take<Stat>(R * nch);
+  RowSet rs{logits, ld, 0, 1, nullptr, 0, 0, 0};
+  hipStream_t s = fs::as_stream(stream);
+  dim3 grid((unsigned)nch, (unsigned)R);
+#define FS_LAUNCH(DT)                                                                           \
+  stats_kernel<DT><<<grid, THREADS, 0, s>>>(rs, V, nch, nullptr, temperature, nullptr, st);  \
+  probs_kernel<DT><<<grid, THREADS, 0, s>>>(rs, V, nch, temperature, st, out, ldo);
+  switch (dtype) {
+    case FS_F32: FS_LAUNCH(FS_F32); break;
+    case FS_BF16: FS_LAUNCH(FS_BF16); break;
+    default: FS_LAUNCH(FS_F16); break;
+  }
+#undef FS_LAUNCH
+  return fs::launch_status("probs_from_logits");
+}
+
+extern "C" int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
+                              int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype,
+                              const int32_t* draft_tokens, const int32_t* k_eff, const float* temperature,
+                              const float* u, const float* E, int64_t ldE, int32_t* out_tokens, int32_t* n_accepted,
+                              int32_t* seq_len, void* workspace, int64_t workspace_bytes, void* stream) {
+  FS_CHECK_ARG(tgt && temperature && out_tokens && n_accepted && workspace, "spec_accept: null pointer");
+  FS_CHECK_ARG(K == 0 || (dft && draft_tokens && u), "spec_accept: null draft inputs");
+  FS_CHECK_ARG(E != nullptr, "spec_accept: E (Exp(1) noise) is required");
+  FS_CHECK_ARG(dtype_ok(dtype), "spec_accept: dtype %d", dtype);
+  FS_CHECK_ARG(B > 0 && B <= 65535 && K >= 0 && V > 0 && V < 0x7fffffff, "spec_accept: B %d K %d V %lld", B, K,
+               (long long)V);
+  FS_CHECK_ARG(workspace_bytes >= accept_ws(B, K, V), "spec_accept: workspace %lld < %lld", (long long)workspace_bytes,
+               (long long)accept_ws(B, K, V));
+  const int nch = (int)nchunks(V);
+  Carve cv{reinterpret_cast<char*>(workspace)};
+  AcceptArgs A;
+  A.rs = RowSet{tgt, tgt_sb, tgt_si, K + 1, dft ? dft : tgt, dft_sb, dft_si, K};
+  A.K = K;
+  A.V = V;
+  A.nch = nch;
+  A.draft = draft_tokens;
+  A.k_eff = k_eff;
+  A.temps = temperature;
+  A.u = u;
+  A.E = E;
+  A.ldE = ldE;
+  A.stats = cv.take<Stat>((int64_t)B * (2 * K + 1) * nch);
+  A.resid = cv.take<float>((int64_t)B * nch);
+  A.pv = cv.take<float>((int64_t)B * nch);
+  A.pi = cv.take<int>((int64_t)B * nch);
+  A.jpos = cv.take<int>(B);
+  hipStream_t s = fs::as_stream(stream);
+  switch (dtype) {
+    case FS_F32: return launch_accept<FS_F32>(A, B, false, out_tokens, n_accepted, seq_len, s);
+    case FS_BF16: return launch_accept<FS_BF16>(A, B, false, out_tokens, n_accepted, seq_len, s);
+    default: return launch_accept<FS_F16>(A, B, false, out_tokens, n_accepted, seq_len, s);
+  }
+}
+
+extern "C" int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_t ldq, int32_t K, int64_t V,
+                               int32_t dtype, const int32_t* draft_tokens, const float* u, const float* E,
+                               int32_t* out_tokens, int32_t* n_accepted, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
+  FS_CHECK_ARG(p && E && out_tokens && n_accepted && workspace, "verify_probs: null pointer");
+  FS_CHECK_ARG(K == 0 || (q && draft_tokens && u), "verify_probs: null draft inputs");
+  FS_CHECK_ARG(dtype_ok(dtype), "verify_probs: dtype %d", dtype);
+  FS_CHECK_ARG(K >= 0 && V > 0 && V < 0x7fffffff, "verify_probs: K %d V %lld", K, (long long)V);
+  FS_CHECK_ARG(workspace_bytes >= accept_ws(1, K, V), "verify_probs: workspace too small");
+  const int nch = (int)nchunks(V);
+  Carve cv{reinterpret_cast<char*>(workspace)};
+  AcceptArgs A;
+  A.rs = RowSet{p, 0, ldp, K + 1, q ? q : p, 0, ldq, K};
+  A.K = K;
+  A.V = V;
+  A.nch = nch;
+  A.draft = draft_tokens;
+  A.k_eff = nullptr;
+  A.temps = nullptr;
+  A.u = u;
+  A.E = E;
+  A.ldE = V;
+  A.stats = cv.take<Stat>((int64_t)(2 * K + 1) * nch);
+  A.resid = cv.take<float>(nch);
+  A.pv = cv.take<float>(nch);
+  A.pi = cv.take<int>(nch);
+  A.jpos = cv.take<int>(1);
+  hipStream_t s = fs::as_stream(stream);
+  switch (dtype) {
+    case FS_F32: return launch_accept<FS_F32>(A, 1, true, out_tokens, n_accepted, nullptr, s);
+    case FS_BF16: return launch_accept<FS_BF16>(A, 1, true, out_tokens, n_accepted, nullptr, s);
+    default: return launch_accept<FS_F16>(A, 1, true, out_tokens, n_accepted, nullptr, s);
+  }
+}

@@ -1,0 +1,231 @@
+"""LLaMA-style decoder on gfx950 kernels (model.py:23-159 in the reference).
+
+Same modules, parameter names and state_dict keys as the reference (RMSNorm, Attention with GQA and
+half-split rotary, SwiGLU, pre-norm blocks, tied embedding/head), so weights load interchangeably.
+The forward runs on the GPU only, as one chain of HIP kernels per layer:
+
+    add_rmsnorm -> gemm(qkv) -> qkv_rope_write (rotary + KV write) -> paged_attention
+      -> gemm(wo, + residual) -> add_rmsnorm -> gemm(gate|up) -> silu_mul -> gemm(w_down, + residual)
+
+q/k/v and gate/up use one fused weight each; the per-projection parameters are re-pointed at slices
+of the fused buffer, so no weight is stored twice.
+"""
+
+import math
+from typing import List, Optional
+
+import torch
+import torch.nn as nn
+
+from . import ops
+from .config import ModelConfig
+from .parallel import SINGLE, TPContext
+
+
+def precompute_rope(head_dim: int, max_len: int, theta: float):
+    """cos/sin tables (max_len, head_dim/2) in f32 (model.py:34-37)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2).float() / head_dim))
+    angles = torch.outer(torch.arange(max_len).float(), inv_freq)
+    return angles.cos(), angles.sin()
+
+
+def _fused_weight(params: List[nn.Parameter]) -> torch.Tensor:
+    """One (sum of rows, cols) weight whose row slices are `params`; re-points them if needed."""
+    first = params[0].data
+    rows = sum(p.shape[0] for p in params)
+    cols = first.shape[1]
+    ok = all(p.data.is_contiguous() and p.dtype == first.dtype and p.device == first.device and p.shape[1] == cols
+             for p in params)
+    if ok:
+        off = first.data_ptr()
+        for p in params:
+            if p.data.data_ptr() != off or p.data.untyped_storage().data_ptr() != first.untyped_storage().data_ptr():
+                ok = False
+                break
+            off += p.numel() * p.element_size()
+    if ok:
+        return first.new_empty(0).set_(first.untyped_storage(), first.storage_offset(), (rows, cols), (cols, 1))
+    buf = torch.cat([p.data for p in params], 0).contiguous()
+    r = 0
+    for p in params:
+        n = p.shape[0]
+        p.data = buf[r: r + n]
+        r += n
+    return buf
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float = 1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x):
+        shape = x.shape
+        y = ops.add_rmsnorm(x.reshape(-1, shape[-1]), self.weight, self.eps)
+        return y.reshape(shape)
+
+
+class Attention(nn.Module):
+    """GQA attention: query head h reads KV head h // (n_heads // n_kv_heads) (model.py:48-78)."""
+
+    def __init__(self, cfg: ModelConfig, tp: TPContext):
+        super().__init__()
+        self.tp = tp
+        self.hd = cfg.head_dim
+        self.nh, self.nkv = cfg.n_heads // tp.size, cfg.n_kv_heads // tp.size
+        self.rep = cfg.n_heads // cfg.n_kv_heads
+        self.wq = nn.Linear(cfg.d_model, self.nh * self.hd, bias=False)
+        self.wk = nn.Linear(cfg.d_model, self.nkv * self.hd, bias=False)
+        self.wv = nn.Linear(cfg.d_model, self.nkv * self.hd, bias=False)
+        self.wo = nn.Linear(self.nh * self.hd, cfg.d_model, bias=False)
+
+    def qkv_weight(self) -> torch.Tensor:
+        return _fused_weight([self.wq.weight, self.wk.weight, self.wv.weight])
+
+    def attend(self, h: torch.Tensor, b: int, t: int, pos32: torch.Tensor, view, rope) -> torch.Tensor:
+        """h (B*T, d) normed input -> attention output (B*T, n_heads*head_dim), before wo."""
+        qkv = ops.gemm(h, self.qkv_weight())
+        layout, tables, slots, mask = view.prepare(b, t, self.nkv, self.hd, h.dtype, h.device, pos32)
+        q = ops.qkv_rope_write(qkv, pos32.reshape(-1), t, self.nh, rope[0], rope[1], tables, layout, slots=slots)
+        o = ops.paged_attention(q.view(b, t, self.nh, self.hd), layout, tables, mask, 1.0 / math.sqrt(self.hd))
+        view.commit(t)
+        return o.view(b * t, self.nh * self.hd)
+
+
+class SwiGLU(nn.Module):
+    def __init__(self, cfg: ModelConfig, tp: TPContext):
+        super().__init__()
+        self.tp = tp
+        hidden = cfg.ffn_dim // tp.size
+        self.w_gate = nn.Linear(cfg.d_model, hidden, bias=False)
+        self.w_up = nn.Linear(cfg.d_model, hidden, bias=False)
+        self.w_down = nn.Linear(hidden, cfg.d_model, bias=False)
+
+    def gate_up_weight(self) -> torch.Tensor:
+        return _fused_weight([self.w_gate.weight, self.w_up.weight])
+
+    def forward(self, x, residual: Optional[torch.Tensor] = None):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        h = ops.silu_mul(ops.gemm(x2, self.gate_up_weight()))
+        r = None if residual is None else residual.reshape(-1, shape[-1])
+        return ops.gemm(h, self.w_down.weight, residual=r).reshape(shape)
+
+
+class Block(nn.Module):
+    def __init__(self, cfg: ModelConfig, tp: TPContext):
+        super().__init__()
+        self.attn_norm = RMSNorm(cfg.d_model, cfg.norm_eps)
+        self.attn = Attention(cfg, tp)
+        self.mlp_norm = RMSNorm(cfg.d_model, cfg.norm_eps)
+        self.mlp = SwiGLU(cfg, tp)
+
+    def step(self, x: torch.Tensor, b: int, t: int, pos32: torch.Tensor, view, rope) -> torch.Tensor:
+        """x (B*T, d) -> x + attn(norm(x)), then + mlp(norm(.)) (model.py:104-106)."""
+        h = ops.add_rmsnorm(x, self.attn_norm.weight, self.attn_norm.eps)
+        a = self.attn.attend(h, b, t, pos32, view, rope)
+        x1 = ops.gemm(a, self.attn.wo.weight, residual=x)
+        h2 = ops.add_rmsnorm(x1, self.mlp_norm.weight, self.mlp_norm.eps)
+        return self.mlp(h2, residual=x1)
+
+
+class ForgeModel(nn.Module):
+    """Embedding and head are shared (tied), as in model.py:109-159."""
+
+    def __init__(self, cfg: ModelConfig, tp: TPContext = SINGLE):
+        super().__init__()
+        cfg.check_tensor_parallel(tp.size)
+        self.cfg, self.tp = cfg, tp
+        self.tok_emb = nn.Embedding(cfg.vocab_size, cfg.d_model)
+        self.layers = nn.ModuleList(Block(cfg, tp) for _ in range(cfg.n_layers))
+        self.norm = RMSNorm(cfg.d_model, cfg.norm_eps)
+        self.lm_head = nn.Linear(cfg.d_model, cfg.vocab_size, bias=False)
+        self.lm_head.weight = self.tok_emb.weight
+        cos, sin = precompute_rope(cfg.head_dim, cfg.max_seq_len, cfg.rope_theta)
+        self.register_buffer("rope_cos", cos, persistent=False)
+        self.register_buffer("rope_sin", sin, persistent=False)
+        self._rope_cache = None
+        self.apply(self._init_weights)
+
+    @staticmethod
+    def _init_weights(m):
+        if isinstance(m, (nn.Linear, nn.Embedding)):
+            nn.init.normal_(m.weight, mean=0.0, std=0.02)
+
+    def num_params(self) -> int:
+        return sum(p.numel() for p in self.parameters())
+
+    @property
+    def device(self) -> torch.device:
+        return self.tok_emb.weight.device
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.tok_emb.weight.dtype
+
+    def _rope(self):
+        """f32 copies of the rotary tables on the model's device (a bf16 model rounds them once)."""
+        c, s = self.rope_cos, self.rope_sin
+        key = (c.data_ptr(), s.data_ptr(), c.dtype, c.device)
+        if self._rope_cache is None or self._rope_cache[0] != key:
+            self._rope_cache = (key, (c.float().contiguous(), s.float().contiguous()))
+        return self._rope_cache[1]
+
+    def embed(self, idx):
+        return ops.embedding(idx.to(self.device), self.tok_emb.weight).reshape(*idx.shape, self.cfg.d_model)
+
+    def head(self, x):
+        shape = x.shape
+        y = ops.add_rmsnorm(x.reshape(-1, shape[-1]), self.norm.weight, self.norm.eps)
+        return ops.gemm(y, self.lm_head.weight).reshape(*shape[:-1], self.cfg.vocab_size)
+
+    @torch.no_grad()
+    def forward(self, idx, positions: Optional[torch.Tensor] = None, kv: Optional[List] = None,
+                last_only: bool = False):
+        """idx (B, T) token ids -> logits (B, T, vocab) (model.py:141-159).
+
+        positions (B, T): absolute positions; default continues after what `kv` holds.
+        kv: one cache view per layer (ContiguousKV or PagedLayerView); None uses a fresh cache.
+        last_only: return only the logits of the last position, (B, 1, vocab)."""
+        dev = self.device
+        if dev.type != "cuda":
+            raise RuntimeError("ForgeModel runs on the GPU: move it with .to('cuda') first")
+        b, t = idx.shape
+        if kv is None:
+            from .kv import new_contiguous_cache
+            kv = new_contiguous_cache(self.cfg.n_layers)
+        if positions is None:
+            start = kv[0].length
+            positions = (start + torch.arange(t))[None, :].expand(b, t)
+        pmax = int(positions.max())
+        if pmax >= self.cfg.max_seq_len:
+            raise ValueError(f"position {pmax} exceeds max_seq_len {self.cfg.max_seq_len}")
+        pos32 = positions.to(device=dev, dtype=torch.int32).reshape(b, t).contiguous()
+        rope = self._rope()
+        x = ops.embedding(idx.to(dev), self.tok_emb.weight)
+        for layer, view in zip(self.layers, kv):
+            x = layer.step(x, b, t, pos32, view, rope)
+        if last_only:
+            x = x.view(b, t, -1)[:, -1].contiguous()
+            return self.head(x).view(b, 1, -1)
+        return self.head(x).view(b, t, -1)
+
+
+def early_exit_draft(target: ForgeModel, n_layers: int) -> ForgeModel:
+    """A draft that is the target's embedding, first n_layers blocks, final norm and head, sharing the
+    target's weight tensors (no copy). Its KV cache is separate from the target's."""
+    from dataclasses import replace
+
+    cfg = replace(target.cfg, n_layers=n_layers)
+    d = ForgeModel.__new__(ForgeModel)
+    nn.Module.__init__(d)
+    d.cfg, d.tp = cfg, target.tp
+    d.tok_emb = target.tok_emb
+    d.layers = nn.ModuleList(list(target.layers)[:n_layers])
+    d.norm = target.norm
+    d.lm_head = target.lm_head
+    d.register_buffer("rope_cos", target.rope_cos, persistent=False)
+    d.register_buffer("rope_sin", target.rope_sin, persistent=False)
+    d._rope_cache = None
+    return d

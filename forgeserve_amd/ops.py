@@ -1,0 +1,325 @@
+"""Tensor-level wrappers of the gfx950 kernels (C ABI in include/forgeserve_amd.h).
+
+Each function checks shapes on the host, allocates outputs and workspace with torch's caching
+allocator, and launches on torch's current stream. Inputs must already be on the GPU; nothing here
+computes on the CPU.
+"""
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import DTYPE_CODE, KVLayout, check, ptr, require_device, stream_ptr
+
+I32 = torch.int32
+
+# Optional timing hook for benchmarks: when ATTN_EVENTS is a list, every paged_attention launch with
+# T == ATTN_EVENT_T appends a (start, end) pair of events recorded on the launching stream.
+ATTN_EVENTS = None
+ATTN_EVENT_T = None
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype} (float32, bfloat16, float16)") from None
+
+
+def _ws(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def _rows(t: torch.Tensor) -> Tuple[int, int]:
+    """(rows, row stride) of a 2-D tensor whose last dim is contiguous."""
+    if t.dim() != 2 or (t.stride(1) != 1 and t.shape[1] > 1):
+        raise ValueError(f"expected a 2-D tensor with a contiguous last dim, got {tuple(t.shape)} {t.stride()}")
+    return t.shape[0], t.stride(0)
+
+
+# ------------------------------------------------------------------------------------------------
+# KV pool layout
+# ------------------------------------------------------------------------------------------------
+def kv_layout(k: torch.Tensor, v: torch.Tensor) -> KVLayout:
+    """Layout of one layer: k, v are (num_blocks, n_kv_heads, block_size, head_dim) views (any strides)."""
+    if k.shape != v.shape or k.dim() != 4 or k.dtype != v.dtype:
+        raise ValueError(f"k/v pool views must match: {tuple(k.shape)} vs {tuple(v.shape)}")
+    nb, h, bs, d = k.shape
+    return KVLayout(k.data_ptr(), v.data_ptr(), *k.stride(), *v.stride(), bs, h, d, _dt(k), nb)
+
+
+# ------------------------------------------------------------------------------------------------
+# dense ops
+# ------------------------------------------------------------------------------------------------
+def gemm(a: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
+         residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = a @ w.T (+ residual): nn.Linear (model.py:57-60, 88-90, 119) with the residual add fused."""
+    require_device(a, w)
+    m, lda = _rows(a)
+    n, ldb = _rows(w)
+    k = a.shape[1]
+    if w.shape[1] != k or a.dtype != w.dtype:
+        raise ValueError(f"gemm: {tuple(a.shape)} {a.dtype} x {tuple(w.shape)} {w.dtype}")
+    if out is None:
+        out = torch.empty((m, n), dtype=a.dtype, device=a.device)
+    _, ldc = _rows(out)
+    ldr = 0
+    if residual is not None:
+        _, ldr = _rows(residual)
+        if residual.shape != out.shape or residual.dtype != a.dtype:
+            raise ValueError("gemm: residual shape/dtype")
+    check(_lib.load().fs_gemm(ptr(a), lda, ptr(w), ldb, ptr(out), ldc, ptr(residual), ldr, m, n, k, _dt(a),
+                              stream_ptr()), "gemm")
+    return out
+
+
+def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, delta: Optional[torch.Tensor] = None,
+                x_out: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = RMSNorm(x [+ delta]) (model.py:29-31); with delta, x + delta is also written to x_out."""
+    require_device(x, weight)
+    m, ldx = _rows(x)
+    n = x.shape[1]
+    if weight.shape != (n,) or weight.dtype != x.dtype:
+        raise ValueError("add_rmsnorm: weight shape/dtype")
+    ldd = ldxo = 0
+    if delta is not None:
+        _, ldd = _rows(delta)
+        if x_out is None:
+            raise ValueError("add_rmsnorm: delta needs x_out")
+        _, ldxo = _rows(x_out)
+    if y is None:
+        y = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    _, ldy = _rows(y)
+    check(_lib.load().fs_add_rmsnorm(ptr(x), ldx, ptr(delta), ldd, ptr(x_out), ldxo, ptr(weight), ptr(y), ldy, m, n,
+                                     float(eps), _dt(x), stream_ptr()), "add_rmsnorm")
+    return y
+
+
+def silu_mul(gu: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """silu(gu[:, :F]) * gu[:, F:] (model.py:93)."""
+    require_device(gu)
+    m, ld = _rows(gu)
+    f = gu.shape[1] // 2
+    if out is None:
+        out = torch.empty((m, f), dtype=gu.dtype, device=gu.device)
+    _, ldh = _rows(out)
+    check(_lib.load().fs_silu_mul(ptr(gu), ld, ptr(out), ldh, m, f, _dt(gu), stream_ptr()), "silu_mul")
+    return out
+
+
+def embedding(ids: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """weight[ids] for int64 ids of any shape -> (ids.numel(), d) (model.py:134-135)."""
+    require_device(ids, weight)
+    ids = ids.reshape(-1)
+    if ids.dtype != torch.int64:
+        ids = ids.long()
+    ids = ids.contiguous()
+    vocab, d = weight.shape
+    if out is None:
+        out = torch.empty((ids.numel(), d), dtype=weight.dtype, device=weight.device)
+    _, ldo = _rows(out)
+    check(_lib.load().fs_embedding(ptr(ids), ids.numel(), ptr(weight.contiguous()), d, vocab, ptr(out), ldo,
+                                   _dt(weight), stream_ptr()), "embedding")
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# KV cache + attention
+# ------------------------------------------------------------------------------------------------
+def qkv_rope_write(qkv: torch.Tensor, positions: torch.Tensor, T: int, n_heads: int, rope_cos: torch.Tensor,
+                   rope_sin: torch.Tensor, tables: torch.Tensor, layout: KVLayout,
+                   slots: Optional[torch.Tensor] = None, q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Rotate q and k (model.py:40-45, 67) and write k, v into the pool (paged.py:74-78).
+
+    qkv: (B*T, (n_heads + 2*n_kv_heads) * head_dim); positions/slots: int32 (B*T,);
+    tables: int32 (B, max_blocks). Returns the rotated queries (B*T, n_heads * head_dim)."""
+    require_device(qkv, positions, tables)
+    m, ld = _rows(qkv)
+    d = layout.head_dim
+    if q_out is None:
+        q_out = torch.empty((m, n_heads * d), dtype=qkv.dtype, device=qkv.device)
+    _, ldq = _rows(q_out)
+    if positions.dtype != I32 or tables.dtype != I32 or (slots is not None and slots.dtype != I32):
+        raise ValueError("qkv_rope_write: positions, slots and tables must be int32")
+    check(_lib.load().fs_qkv_rope_write(ptr(qkv), ld, m, T, n_heads, ptr(positions), ptr(slots), ptr(rope_cos),
+                                        ptr(rope_sin), rope_cos.shape[0], ptr(tables), tables.stride(0),
+                                        tables.shape[1], layout, ptr(q_out), ldq, stream_ptr()), "qkv_rope_write")
+    return q_out
+
+
+def paged_kv_write(k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor, tables: torch.Tensor,
+                   layout: KVLayout) -> None:
+    """Scatter k, v (B, n_kv_heads, T, head_dim) to the pool slots of positions (B, T) (paged.py:74-78)."""
+    require_device(k, v, positions, tables)
+    if k.shape != v.shape or k.stride() != v.stride() or k.stride(3) != 1:
+        raise ValueError("paged_kv_write: k and v must share shape and strides, head_dim contiguous")
+    b, h, t, d = k.shape
+    if positions.dtype != I32 or tables.dtype != I32:
+        raise ValueError("paged_kv_write: positions and tables must be int32")
+    check(_lib.load().fs_paged_kv_write(ptr(k), ptr(v), k.stride(0), k.stride(1), k.stride(2), b, t,
+                                        ptr(positions.contiguous()), ptr(tables), tables.stride(0), tables.shape[1],
+                                        layout, stream_ptr()), "paged_kv_write")
+
+
+def paged_gather(layout: KVLayout, tables: torch.Tensor, dtype, device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Every block of every table row, in table order: (B, n_kv_heads, max_blocks*block_size, head_dim)."""
+    b, nb = tables.shape
+    shape = (b, layout.n_kv_heads, nb * layout.block_size, layout.head_dim)
+    k_all = torch.empty(shape, dtype=dtype, device=device)
+    v_all = torch.empty(shape, dtype=dtype, device=device)
+    check(_lib.load().fs_paged_gather(layout, ptr(tables), tables.stride(0), b, nb, ptr(k_all), ptr(v_all),
+                                      stream_ptr()), "paged_gather")
+    return k_all, v_all
+
+
+def paged_attention(q: torch.Tensor, layout: KVLayout, tables: torch.Tensor, positions: torch.Tensor,
+                    scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal GQA attention of q (B, T, n_heads, head_dim) over the paged keys (model.py:70-76).
+
+    positions: int32 (B, T); query (b, t) sees the keys at positions 0..positions[b, t]."""
+    require_device(q, tables, positions)
+    b, t, h, d = q.shape
+    if q.stride(3) != 1:
+        raise ValueError("paged_attention: head_dim must be contiguous")
+    if positions.dtype != I32 or tables.dtype != I32 or positions.shape != (b, t):
+        raise ValueError("paged_attention: positions (B, T) and tables must be int32")
+    positions = positions.contiguous()
+    if out is None:
+        out = torch.empty((b, t, h, d), dtype=q.dtype, device=q.device)
+    nb = tables.shape[1]
+    lib = _lib.load()
+    need = lib.fs_paged_attention_workspace_size(b, t, h, d, nb, layout.block_size)
+    ws = _ws(need, q.device)
+    timing = ATTN_EVENTS is not None and t == ATTN_EVENT_T
+    if timing:
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        ev[0].record()
+    check(lib.fs_paged_attention(ptr(q), q.stride(0), q.stride(1), q.stride(2), layout, ptr(tables),
+                                 tables.stride(0), nb, ptr(positions), b, t, h, float(scale), ptr(out), out.stride(0),
+                                 out.stride(1), out.stride(2), ptr(ws), ws.numel(), stream_ptr()), "paged_attention")
+    if timing:
+        ev[1].record()
+        ATTN_EVENTS.append(ev)
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# sampling / acceptance
+# ------------------------------------------------------------------------------------------------
+def probs_from_logits(logits: torch.Tensor, temperature: float) -> torch.Tensor:
+    """softmax(f32(logits) / T), or the one-hot of the argmax in the logits dtype at T == 0 (sampling.py:9-13)."""
+    require_device(logits)
+    shape = logits.shape
+    x = logits.reshape(-1, shape[-1])
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    r, ld = x.shape[0], x.stride(0)
+    v = shape[-1]
+    out_dtype = torch.float32 if temperature > 0 else logits.dtype
+    out = torch.empty((r, v), dtype=out_dtype, device=logits.device)
+    lib = _lib.load()
+    ws = _ws(lib.fs_sampling_workspace_size(r, v), logits.device)
+    check(lib.fs_probs_from_logits(ptr(x), ld, r, v, float(temperature), _dt(x), ptr(out), v, DTYPE_CODE[out_dtype],
+                                   ptr(ws), ws.numel(), stream_ptr()), "probs_from_logits")
+    return out.reshape(shape)
+
+
+def sample_logits(logits: torch.Tensor, temperature, noise: Optional[torch.Tensor] = None,
+                  out32: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Token ids (int64, logits.shape[:-1]) for logits (..., V) (sampling.py:16-21).
+
+    temperature: a float for every row, or a float32 device tensor with one value per row.
+    noise: float32 Exp(1) noise with the logits' shape (the categorical draw is argmax(p / noise));
+    None makes every row greedy. out32: optional int32 view that also receives the tokens."""
+    require_device(logits)
+    shape = logits.shape
+    x = logits.reshape(-1, shape[-1])
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    r, ld = x.shape[0], x.stride(0)
+    v = shape[-1]
+    tok = torch.empty((r,), dtype=torch.int64, device=logits.device)
+    t_ptr, t_all = 0, 0.0
+    if isinstance(temperature, torch.Tensor):
+        require_device(temperature)
+        temperature = temperature.to(torch.float32).reshape(-1).contiguous()
+        if temperature.numel() != r:
+            raise ValueError("sample_logits: one temperature per row")
+        t_ptr = ptr(temperature)
+    else:
+        t_all = float(temperature)
+        if t_all < 0:
+            raise ValueError("temperature must be >= 0")
+    e_ptr, lde = 0, 0
+    if noise is not None:
+        require_device(noise)
+        noise = noise.reshape(-1, v)
+        if noise.dtype != torch.float32 or noise.shape[0] != r or noise.stride(1) != 1:
+            raise ValueError("sample_logits: noise must be float32 with the logits' shape")
+        e_ptr, lde = ptr(noise), noise.stride(0)
+    o32, ld32 = 0, 0
+    if out32 is not None:
+        o32, ld32 = ptr(out32), out32.stride(0) if out32.dim() else 1
+    lib = _lib.load()
+    ws = _ws(lib.fs_sampling_workspace_size(r, v), logits.device)
+    check(lib.fs_sample_logits(ptr(x), ld, r, v, t_ptr, t_all, e_ptr, lde, _dt(x), ptr(tok), o32, ld32, ptr(ws),
+                               ws.numel(), stream_ptr()), "sample_logits")
+    return tok.reshape(shape[:-1])
+
+
+def spec_accept(tgt: torch.Tensor, dft: torch.Tensor, draft_tokens: torch.Tensor, k_eff: Optional[torch.Tensor],
+                temperature: torch.Tensor, u: torch.Tensor, noise: torch.Tensor,
+                seq_len: Optional[torch.Tensor] = None, out_tokens: Optional[torch.Tensor] = None,
+                n_accepted: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Batched verify_draft from logits (speculative.py:20-33, sampling.py:9-13).
+
+    tgt (B, K+1, V), dft (B, K, V) logits; draft_tokens int32 (B, K); k_eff int32 (B,) or None (= K);
+    temperature float32 (B,); u float32 (B, K) uniforms; noise float32 (B, V) Exp(1);
+    seq_len int32 (B,) cached lengths, advanced in place by 1 + n_accepted.
+    Returns out_tokens int32 (B, K+1) (accepted, extra, then -1) and n_accepted int32 (B,)."""
+    require_device(tgt, dft, draft_tokens, temperature, u, noise)
+    b, k1, v = tgt.shape
+    k = k1 - 1
+    if dft.shape != (b, k, v) or dft.dtype != tgt.dtype:
+        raise ValueError(f"spec_accept: draft logits {tuple(dft.shape)} vs target {tuple(tgt.shape)}")
+    if tgt.stride(2) != 1 or dft.stride(2) != 1:
+        raise ValueError("spec_accept: vocab dim must be contiguous")
+    for name, t, dt, shp in (("draft_tokens", draft_tokens, I32, (b, k)), ("temperature", temperature,
+                             torch.float32, (b,)), ("u", u, torch.float32, (b, k)), ("noise", noise, torch.float32,
+                             (b, v))):
+        if t.dtype != dt or tuple(t.shape) != shp or not t.is_contiguous():
+            raise ValueError(f"spec_accept: {name} must be contiguous {dt} {shp}")
+    if k_eff is not None and (k_eff.dtype != I32 or k_eff.shape != (b,)):
+        raise ValueError("spec_accept: k_eff must be int32 (B,)")
+    if out_tokens is None:
+        out_tokens = torch.empty((b, k + 1), dtype=I32, device=tgt.device)
+    if n_accepted is None:
+        n_accepted = torch.empty((b,), dtype=I32, device=tgt.device)
+    lib = _lib.load()
+    ws = _ws(lib.fs_spec_accept_workspace_size(b, k, v), tgt.device)
+    check(lib.fs_spec_accept(ptr(tgt), tgt.stride(0), tgt.stride(1), ptr(dft), dft.stride(0), dft.stride(1) if k else 0,
+                             b, k, v, _dt(tgt), ptr(draft_tokens), ptr(k_eff), ptr(temperature), ptr(u), ptr(noise),
+                             noise.stride(0), ptr(out_tokens), ptr(n_accepted), ptr(seq_len), ptr(ws), ws.numel(),
+                             stream_ptr()), "spec_accept")
+    return out_tokens, n_accepted
+
+
+def verify_probs(p: torch.Tensor, q: torch.Tensor, draft_tokens: torch.Tensor, u: torch.Tensor,
+                 noise: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """verify_draft on probability rows p (K+1, V), q (K, V) (speculative.py:20-33)."""
+    require_device(p, q, draft_tokens, u, noise)
+    k1, v = p.shape
+    k = k1 - 1
+    if q.shape != (k, v) or q.dtype != p.dtype or p.stride(1) != 1 or (k and q.stride(1) != 1):
+        raise ValueError("verify_probs: p (K+1, V) and q (K, V) of one dtype, contiguous rows")
+    if draft_tokens.dtype != I32 or draft_tokens.numel() != k or u.numel() != k or noise.numel() != v:
+        raise ValueError("verify_probs: draft_tokens int32 (K,), u (K,), noise (V,)")
+    out = torch.empty((k + 1,), dtype=I32, device=p.device)
+    n = torch.empty((1,), dtype=I32, device=p.device)
+    lib = _lib.load()
+    ws = _ws(lib.fs_spec_accept_workspace_size(1, k, v), p.device)
+    check(lib.fs_verify_probs(ptr(p), p.stride(0), ptr(q), q.stride(0) if k else 0, k, v, _dt(p),
+                              ptr(draft_tokens.contiguous()), ptr(u.contiguous()), ptr(noise.contiguous()), ptr(out),
+                              ptr(n), ptr(ws), ws.numel(), stream_ptr()), "verify_probs")
+    return out, n

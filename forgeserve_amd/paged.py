@@ -1,0 +1,127 @@
+"""Paged KV cache (paged.py:20-82 in the reference) with the pool resident in HBM.
+
+The pool holds every layer in two allocations: keys (n_layers, num_blocks, n_kv_heads, block_size,
+head_dim) and values stored dim-major (n_layers, num_blocks, n_kv_heads, head_dim, block_size).
+`pool.k[layer]` and `pool.v[layer]` are (num_blocks, n_kv_heads, block_size, head_dim) views of them,
+the reference's shape, so code that indexes the pool directly keeps working. One (block, kv-head)
+tile of keys is block_size*head_dim contiguous elements (4 KB at 16 x 128 bf16), and the values of a
+block for one dim are block_size contiguous elements: the attention kernel streams both with 16-byte
+and 8-byte loads and never gathers.
+
+The block allocator and the block tables stay on the host, as in the reference; tables are copied
+to the GPU (int32) once per step and shared by every layer's view.
+"""
+
+from typing import List, Optional, Tuple
+
+import torch
+
+from . import ops
+from .config import ModelConfig
+from .parallel import SINGLE, TPContext
+
+
+class OutOfBlocks(RuntimeError):
+    pass
+
+
+class BlockAllocator:
+    """LIFO free list; block 0 is handed out first (paged.py:24-39)."""
+
+    def __init__(self, num_blocks: int):
+        self.num_blocks = num_blocks
+        self._free = list(range(num_blocks - 1, -1, -1))
+
+    @property
+    def num_free(self) -> int:
+        return len(self._free)
+
+    def allocate(self, n: int) -> List[int]:
+        if n > len(self._free):
+            raise OutOfBlocks(f"need {n} blocks, {len(self._free)} free")
+        out = self._free[len(self._free) - n:][::-1]
+        del self._free[len(self._free) - n:]
+        return out
+
+    def release(self, blocks: List[int]) -> None:
+        self._free.extend(blocks)
+
+
+class PagedKVPool:
+    """The block pool of every layer (paged.py:42-58)."""
+
+    def __init__(self, cfg: ModelConfig, num_blocks: int, block_size: int = 16, tp: TPContext = SINGLE,
+                 dtype=torch.float32, device=None):
+        if device is None:
+            device = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() else "cuda"
+        h = cfg.n_kv_heads // tp.size
+        d = cfg.head_dim
+        self.cfg = cfg
+        self.block_size = block_size
+        self.num_blocks = num_blocks
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.k_store = torch.zeros((cfg.n_layers, num_blocks, h, block_size, d), dtype=dtype, device=self.device)
+        self.v_store = torch.zeros((cfg.n_layers, num_blocks, h, d, block_size), dtype=dtype, device=self.device)
+        self.k = [self.k_store[i] for i in range(cfg.n_layers)]
+        self.v = [self.v_store[i].transpose(-1, -2) for i in range(cfg.n_layers)]
+        self.allocator = BlockAllocator(num_blocks)
+        self._layouts = None
+
+    def blocks_for(self, n_tokens: int) -> int:
+        return -(-n_tokens // self.block_size)
+
+    def layout(self, layer: int):
+        if self._layouts is None:
+            self._layouts = [ops.kv_layout(self.k[i], self.v[i]) for i in range(len(self.k))]
+        return self._layouts[layer]
+
+    def views(self, block_tables: torch.Tensor, positions: torch.Tensor) -> List["PagedLayerView"]:
+        """One view per layer for a step. block_tables: (B, max_blocks), positions: (B, T)."""
+        step = _Step(self, block_tables, positions)
+        return [PagedLayerView(self, layer, block_tables, positions, step) for layer in range(len(self.k))]
+
+
+class _Step:
+    """Device copies of a step's block tables and positions, shared by the views of every layer."""
+
+    def __init__(self, pool: PagedKVPool, tables: torch.Tensor, positions: torch.Tensor):
+        if tables.dim() != 2 or positions.dim() != 2 or tables.shape[0] != positions.shape[0]:
+            raise ValueError(f"block_tables (B, max_blocks) and positions (B, T): {tuple(tables.shape)}, "
+                             f"{tuple(positions.shape)}")
+        if tables.device.type == "cpu" and tables.numel() and (int(tables.min()) < 0 or
+                                                              int(tables.max()) >= pool.num_blocks):
+            raise IndexError(f"block table entries must be in [0, {pool.num_blocks})")
+        self.tables = tables.to(device=pool.device, dtype=torch.int32, non_blocking=True).contiguous()
+        self.positions = positions.to(device=pool.device, dtype=torch.int32, non_blocking=True).contiguous()
+
+
+class PagedLayerView:
+    """What one attention layer sees during one step (paged.py:61-82)."""
+
+    def __init__(self, pool: PagedKVPool, layer: int, block_tables: torch.Tensor, positions: torch.Tensor,
+                 step: Optional[_Step] = None):
+        self.pool, self.layer, self.tables, self.positions = pool, layer, block_tables, positions
+        self._step = step if step is not None else _Step(pool, block_tables, positions)
+
+    @property
+    def length(self) -> int:
+        raise NotImplementedError("paged views need explicit positions")
+
+    def update(self, k: torch.Tensor, v: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Write k, v (B, n_kv_heads, T, head_dim) at their positions, then return every table block of
+        every row in table order, (B, n_kv_heads, max_blocks*block_size, head_dim)."""
+        if k.stride() != v.stride() or k.stride(3) != 1:
+            k, v = k.contiguous(), v.contiguous()
+        lay = self.pool.layout(self.layer)
+        ops.paged_kv_write(k, v, self._step.positions, self._step.tables, lay)
+        return ops.paged_gather(lay, self._step.tables, self.pool.dtype, self.pool.device)
+
+    # ---- device path used by the model -------------------------------------------------------------
+    def prepare(self, b: int, t: int, h: int, d: int, dtype, device, positions: torch.Tensor):
+        if dtype != self.pool.dtype:
+            raise ValueError(f"pool dtype {self.pool.dtype} does not match the model's {dtype}")
+        return self.pool.layout(self.layer), self._step.tables, None, positions
+
+    def commit(self, t: int) -> None:
+        pass

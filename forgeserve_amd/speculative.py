@@ -1,0 +1,292 @@
+"""Speculative decoding on the GPU (speculative.py:1-86 in the reference).
+
+Two entry points:
+
+* `verify_draft` / `speculative_generate`: the reference's single-sequence API. The forwards, the
+  draft draws and the acceptance run as HIP kernels; the random numbers are drawn from the caller's
+  generator in exactly the order the reference draws them (draft Exp(1) vectors, then one uniform per
+  examined proposal, then one Exp(1) vector for the final draw), so a seeded run reproduces the
+  reference's tokens.
+
+* `SpeculativeBatch` / `speculative_generate_batch`: batched speculation over paged KV pools, the
+  throughput path. Per round it runs k draft decode steps (T = 2 for the first step, which re-feeds
+  the previous token so a fully accepted round needs no separate catch-up forward), one target
+  verify pass over the k+1 window, and one fused acceptance launch that also advances the cached
+  lengths on the device. Randomness comes from the device generator as tensors (u, E) handed to the
+  kernels; the only device-to-host copy per round is (n_accepted, out_tokens).
+"""
+
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from . import ops
+from .kv import new_contiguous_cache
+from .paged import OutOfBlocks, PagedKVPool
+from .sampling import exp_noise, probs_from_logits
+
+I32 = torch.int32
+
+
+def _clone_generator(gen: torch.Generator) -> torch.Generator:
+    g = torch.Generator(device=gen.device)
+    g.set_state(gen.get_state())
+    return g
+
+
+def verify_draft(p: torch.Tensor, q: torch.Tensor, draft_tokens: List[int], generator=None) -> Tuple[List[int], int]:
+    """p (k+1, V) target probabilities, q (k, V) draft probabilities, k draft tokens ->
+    (accepted draft tokens, one extra token from the target) (speculative.py:20-33)."""
+    k = len(draft_tokens)
+    v = p.shape[-1]
+    dev = p.device
+    gen = generator if generator is not None else torch.default_generator
+    # the reference draws u_i lazily, one per examined proposal; a clone yields the same values
+    peek = _clone_generator(gen)
+    u = torch.tensor([float(torch.rand((), generator=peek, device=gen.device)) for _ in range(k)],
+                     dtype=torch.float32)
+    u = u.to(dev)
+    xs = torch.tensor(list(draft_tokens), dtype=I32).to(dev)
+    qq = q if k else p[:0]
+    # decisions do not depend on the noise: find the first rejection, then draw the noise the
+    # reference would draw after exactly that many uniforms
+    _, n = ops.verify_probs(p, qq, xs, u, torch.ones(v, dtype=torch.float32, device=dev))
+    j = int(n[0])
+    for _ in range(min(j + 1, k)):
+        torch.rand((), generator=gen, device=gen.device)
+    noise = exp_noise((v,), gen, dev)
+    out, _ = ops.verify_probs(p, qq, xs, u, noise)
+    toks = out[: j + 1].tolist()
+    return toks[:j], toks[j]
+
+
+@torch.no_grad()
+def speculative_generate(target, draft, prompt: List[int], max_new_tokens: int, k: int = 4,
+                         temperature: float = 0.0, generator=None):
+    """Generate with `target`, drafting k tokens at a time with `draft` (speculative.py:36-86).
+
+    Returns (new tokens, {"rounds", "proposed", "accepted"}). One sequence."""
+    if target.cfg.vocab_size != draft.cfg.vocab_size:
+        raise ValueError("target and draft must share a vocabulary")
+    limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
+    tokens = list(prompt)
+    kv_t, kv_d = new_contiguous_cache(target.cfg.n_layers), new_contiguous_cache(draft.cfg.n_layers)
+    if len(tokens) > 1:
+        target(torch.tensor([tokens[:-1]]), kv=kv_t, last_only=True)
+        draft(torch.tensor([tokens[:-1]]), kv=kv_d, last_only=True)
+    stats = {"rounds": 0, "proposed": 0, "accepted": 0}
+    start = len(tokens)
+    dev = target.device
+    v = target.cfg.vocab_size
+
+    while len(tokens) - start < max_new_tokens and len(tokens) < limit:
+        remaining = min(max_new_tokens - (len(tokens) - start), limit - len(tokens))
+        k_eff = min(k, remaining - 1)
+        cached = kv_t[0].length
+
+        xs, qs, cur = [], [], tokens[-1]
+        for _ in range(k_eff):
+            logits = draft(torch.tensor([[cur]]), kv=kv_d)[0, -1]
+            q = probs_from_logits(logits, temperature)
+            if temperature == 0:
+                cur = int(ops.sample_logits(logits, 0.0))
+            else:
+                cur = int(ops.sample_logits(logits, float(temperature), exp_noise((1, v), generator, dev)))
+            xs.append(cur)
+            qs.append(q)
+
+        p = probs_from_logits(target(torch.tensor([[tokens[-1]] + xs]), kv=kv_t)[0], temperature)
+        accepted, extra = verify_draft(p, torch.stack(qs) if qs else p[:0], xs, generator)
+        tokens += accepted + [extra]
+        stats["rounds"] += 1
+        stats["proposed"] += k_eff
+        stats["accepted"] += len(accepted)
+
+        want = cached + 1 + len(accepted)
+        for view in kv_t:
+            view.truncate(want)
+        have = kv_d[0].length
+        if have > want:
+            for view in kv_d:
+                view.truncate(want)
+        elif have < want:
+            draft(torch.tensor([tokens[have:want]]), kv=kv_d, last_only=True)
+    return tokens[start:], stats
+
+
+# ------------------------------------------------------------------------------------------------
+# batched speculation over paged pools
+# ------------------------------------------------------------------------------------------------
+class _Seq:
+    __slots__ = ("tokens", "start", "max_new", "temperature", "blocks_t", "blocks_d", "done", "eos_id")
+
+    def __init__(self, tokens, max_new, temperature, eos_id=None):
+        self.tokens = list(tokens)
+        self.start = len(tokens)
+        self.max_new = max_new
+        self.temperature = float(temperature)
+        self.blocks_t: List[int] = []
+        self.blocks_d: List[int] = []
+        self.done = False
+        self.eos_id = eos_id
+
+
+class SpeculativeBatch:
+    """Batched draft-then-verify rounds over paged KV pools (one pool for the target, one for the draft).
+
+    Sequence state lives on the host (token lists, block lists); KV, logits, draft tokens, random
+    numbers and acceptance results live on the GPU. `round()` advances every active sequence by
+    1 + (accepted proposals) tokens."""
+
+    def __init__(self, target, draft, num_blocks: int, block_size: int = 16, k: int = 4,
+                 draft_num_blocks: Optional[int] = None, generator: Optional[torch.Generator] = None):
+        if target.cfg.vocab_size != draft.cfg.vocab_size:
+            raise ValueError("target and draft must share a vocabulary")
+        self.target, self.draft, self.k = target, draft, k
+        self.dev, self.dtype = target.device, target.dtype
+        self.pool_t = PagedKVPool(target.cfg, num_blocks, block_size, dtype=self.dtype, device=self.dev)
+        self.pool_d = PagedKVPool(draft.cfg, draft_num_blocks or num_blocks, block_size, dtype=self.dtype,
+                                  device=self.dev)
+        self.block_size = block_size
+        self.limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
+        self.gen = generator
+        self.seqs: List[_Seq] = []
+        self.stats = {"rounds": 0, "proposed": 0, "accepted": 0}
+
+    # ---- sequences ------------------------------------------------------------------------------
+    def _grow(self, seq: _Seq, n_tokens: int) -> None:
+        for pool, blocks in ((self.pool_t, seq.blocks_t), (self.pool_d, seq.blocks_d)):
+            need = pool.blocks_for(n_tokens) - len(blocks)
+            if need > 0:
+                blocks += pool.allocator.allocate(need)
+
+    def release(self, seq: _Seq) -> None:
+        self.pool_t.allocator.release(seq.blocks_t)
+        self.pool_d.allocator.release(seq.blocks_d)
+        seq.blocks_t, seq.blocks_d = [], []
+
+    def add(self, prompt: Sequence[int], max_new_tokens: int, temperature: float = 0.0, eos_id=None,
+            prefill: bool = True) -> _Seq:
+        """Add a sequence; with prefill, its prompt (all but the last token) is run through both models."""
+        if not 0 < len(prompt) < self.limit:
+            raise ValueError(f"prompt length must be in 1..{self.limit - 1}")
+        seq = _Seq(prompt, max_new_tokens, temperature, eos_id)
+        self._grow(seq, len(seq.tokens))
+        if prefill and len(seq.tokens) > 1:
+            n = len(seq.tokens) - 1
+            idx = torch.tensor([seq.tokens[:-1]])
+            pos = torch.arange(n)[None]
+            for model, pool, blocks in ((self.target, self.pool_t, seq.blocks_t),
+                                        (self.draft, self.pool_d, seq.blocks_d)):
+                model(idx, pos, pool.views(torch.tensor([blocks]), pos), last_only=True)
+        self.seqs.append(seq)
+        return seq
+
+    def active(self) -> List[_Seq]:
+        return [s for s in self.seqs if not s.done]
+
+    # ---- one round --------------------------------------------------------------------------------
+    def _remaining(self, s: _Seq) -> int:
+        return min(s.max_new - (len(s.tokens) - s.start), self.limit - len(s.tokens))
+
+    def _finish_check(self, s: _Seq) -> None:
+        if self._remaining(s) <= 0 or (s.eos_id is not None and s.eos_id in s.tokens[s.start:]):
+            if s.eos_id is not None and s.eos_id in s.tokens[s.start:]:
+                cut = s.tokens.index(s.eos_id, s.start) + 1
+                del s.tokens[cut:]
+            s.done = True
+            self.release(s)
+
+    def _tables(self, lists: List[List[int]]) -> torch.Tensor:
+        width = max(1, max(len(x) for x in lists))
+        t = torch.zeros((len(lists), width), dtype=I32)
+        for i, x in enumerate(lists):
+            if x:
+                t[i, : len(x)] = torch.tensor(x, dtype=I32)
+        return t.to(self.dev, non_blocking=True)
+
+    @torch.no_grad()
+    def round(self) -> int:
+        """One draft-then-verify round for every active sequence. Returns the tokens committed."""
+        seqs = self.active()
+        if not seqs:
+            return 0
+        b = len(seqs)
+        k_eff = [max(0, min(self.k, self._remaining(s) - 1)) for s in seqs]
+        k = max(k_eff)
+        n = [len(s.tokens) for s in seqs]
+        for s, ni in zip(seqs, n):
+            self._grow(s, ni + k)
+        tab_t = self._tables([s.blocks_t for s in seqs])
+        tab_d = self._tables([s.blocks_d for s in seqs])
+        v = self.target.cfg.vocab_size
+        temps = torch.tensor([s.temperature for s in seqs], dtype=torch.float32).to(self.dev, non_blocking=True)
+        sampling = any(s.temperature > 0 for s in seqs)
+
+        # 1. draft: step 0 re-feeds (tokens[-2], tokens[-1]) at (n-2, n-1); step i feeds x_{i-1} at n-1+i
+        dft_logits = torch.empty((b, k, v), dtype=self.dtype, device=self.dev)
+        draft_tok = torch.empty((b, k), dtype=I32, device=self.dev)
+        last = torch.tensor([s.tokens[-1] for s in seqs], dtype=torch.int64)
+        prev = torch.tensor([s.tokens[-2] if len(s.tokens) > 1 else 0 for s in seqs], dtype=torch.int64)
+        cur = None
+        for i in range(k):
+            if i == 0:
+                idx = torch.stack([prev, last], 1).to(self.dev, non_blocking=True)
+                pos = torch.tensor([[ni - 2 if ni > 1 else -1, ni - 1] if k_eff[r] > 0 else [-1, -1]
+                                    for r, ni in enumerate(n)])
+            else:
+                idx = cur.to(torch.int64)[:, None]
+                pos = torch.tensor([[ni - 1 + i if i < k_eff[r] else -1] for r, ni in enumerate(n)])
+            views = self.pool_d.views(tab_d, pos)
+            logits = self.draft(idx, pos, views, last_only=True)[:, 0]
+            dft_logits[:, i].copy_(logits)
+            noise = None
+            if sampling:
+                noise = torch.empty((b, v), dtype=torch.float32, device=self.dev).exponential_(generator=self.gen)
+            ops.sample_logits(logits, temps, noise, out32=draft_tok[:, i])
+            cur = draft_tok[:, i]
+
+        # 2. target verify over [tokens[-1], x_0 .. x_{k-1}] at n-1 .. n-1+k
+        idx = torch.cat([last.to(self.dev)[:, None], draft_tok.to(torch.int64)], 1) if k else last[:, None]
+        pos = torch.tensor([[ni - 1 + t if t <= k_eff[r] else -1 for t in range(k + 1)] for r, ni in enumerate(n)])
+        tgt_logits = self.target(idx, pos, self.pool_t.views(tab_t, pos))
+
+        # 3. acceptance (+ device-side rollback of the cached lengths)
+        u = torch.rand((b, max(k, 1)), dtype=torch.float32, device=self.dev, generator=self.gen)[:, :k].contiguous()
+        noise = torch.empty((b, v), dtype=torch.float32, device=self.dev).exponential_(generator=self.gen)
+        keff_dev = torch.tensor(k_eff, dtype=I32).to(self.dev, non_blocking=True)
+        out_tok, n_acc = ops.spec_accept(tgt_logits, dft_logits, draft_tok, keff_dev, temps, u, noise)
+        res = torch.cat([n_acc[:, None], out_tok], 1).cpu()
+
+        committed = 0
+        for r, s in enumerate(seqs):
+            a = int(res[r, 0])
+            new = res[r, 1: a + 2].tolist()
+            s.tokens += new
+            committed += len(new)
+            self.stats["proposed"] += k_eff[r]
+            self.stats["accepted"] += a
+            self._finish_check(s)
+        self.stats["rounds"] += 1
+        return committed
+
+    def run(self) -> None:
+        while self.active():
+            self.round()
+
+
+@torch.no_grad()
+def speculative_generate_batch(target, draft, prompts: List[List[int]], max_new_tokens, k: int = 4,
+                               temperature=0.0, generator: Optional[torch.Generator] = None,
+                               block_size: int = 16, num_blocks: Optional[int] = None):
+    """Batched speculative decoding; returns (list of new-token lists, stats)."""
+    n = len(prompts)
+    max_new = list(max_new_tokens) if isinstance(max_new_tokens, (list, tuple)) else [max_new_tokens] * n
+    temps = list(temperature) if isinstance(temperature, (list, tuple)) else [temperature] * n
+    if num_blocks is None:
+        limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
+        num_blocks = sum(-(-min(len(p) + m + k + 1, limit + k) // block_size) + 1 for p, m in zip(prompts, max_new))
+    sb = SpeculativeBatch(target, draft, num_blocks, block_size, k, generator=generator)
+    seqs = [sb.add(p, m, t) for p, m, t in zip(prompts, max_new, temps)]
+    sb.run()
+    return [s.tokens[s.start:] for s in seqs], sb.stats

@@ -1,0 +1,186 @@
+/*
+ * forgeserve_amd: C ABI of the MI355X (gfx950) speculative-decoding hot path.
+ *
+ * Every pointer is caller-owned device memory unless stated otherwise; the library allocates
+ * nothing. Every call is asynchronous on the HIP stream passed as `stream` (a hipStream_t, NULL for
+ * the null stream) and returns
+ *     0                 on success,
+ *     FS_ERR_ARG (<0)   for an argument error found on the host (nothing was launched),
+ *     > 0               a hipError_t reported by the launch.
+ * fs_last_error() returns a thread-local message for the last non-zero return.
+ *
+ * Strides are in elements. Element types are given by a dtype code (FS_F32, FS_BF16, FS_F16).
+ * Positions are int32; a negative position marks a padding token of a ragged batch: its KV slot is
+ * not written and its attention output row is zero (the reference has no padding tokens; ragged
+ * batches are this library's extension for batched speculation).
+ *
+ * The reference (forgeserve, pure PyTorch) has no C interface. Each entry point names the Python
+ * function it replaces; INTEGRATION.md shows the ctypes binding a maintainer would add there.
+ */
+#ifndef FORGESERVE_AMD_H
+#define FORGESERVE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FS_F32 0
+#define FS_BF16 1
+#define FS_F16 2
+
+#define FS_ERR_ARG (-1)
+
+/* Layout of one layer of a paged KV pool.
+ * Key element (block, head, slot, dim) lives at k[block*k_block + head*k_head + slot*k_slot + dim*k_dim],
+ * value element likewise with the v_* strides. The fast attention path wants
+ * k_slot == head_dim, k_dim == 1 (slot-major keys) and v_slot == 1, v_dim == block_size
+ * (dim-major values, so a block's 16 keys of one dim are 32 contiguous bytes). */
+typedef struct fs_kv_layout {
+  void* k;
+  void* v;
+  int64_t k_block, k_head, k_slot, k_dim;
+  int64_t v_block, v_head, v_slot, v_dim;
+  int32_t block_size;
+  int32_t n_kv_heads;
+  int32_t head_dim;
+  int32_t dtype;
+  int64_t num_blocks; /* block ids outside [0, num_blocks) are never dereferenced */
+} fs_kv_layout;
+
+const char* fs_last_error(void);
+int fs_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------- */
+/* KV cache                                                                                         */
+/* ---------------------------------------------------------------------------------------------- */
+
+/* Fused rotary embedding + paged KV write for one layer of one forward.
+ * Replaces model.py:64-67 (q/k/v split and apply_rope, model.py:40-45) and the scatter of
+ * paged.py:74-78. qkv holds n_tokens rows of [q (n_heads*head_dim) | k | v] (the fused projection
+ * output), row stride qkv_stride. Token m belongs to batch row m / T. Rotary: half-split rotation
+ * at positions[m] with cos/sin rounded to the dtype (model.py:42-45); tables are f32
+ * [rope_len, head_dim/2]. The key/value of token m go to cache position slots[m] (slots == NULL:
+ * the rotary position, as in a paged view; a contiguous cache appends at its length instead,
+ * kv.py:21-24). q_out receives the rotated queries, row stride q_stride, layout
+ * [n_tokens, n_heads, head_dim]. */
+int fs_qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_t T, int32_t n_heads,
+                      const int32_t* positions, const int32_t* slots, const float* rope_cos, const float* rope_sin,
+                      int32_t rope_len, const int32_t* block_tables, int64_t table_stride,
+                      int32_t max_blocks, const fs_kv_layout* kv, void* q_out, int64_t q_stride,
+                      void* stream);
+
+/* Scatter already-rotated keys/values into the pool: paged.py:74-78.
+ * k_new/v_new element (b, h, t, d) at base + b*s_b + h*s_h + t*s_t + d (dim contiguous). */
+int fs_paged_kv_write(const void* k_new, const void* v_new, int64_t s_b, int64_t s_h, int64_t s_t,
+                      int32_t B, int32_t T, const int32_t* positions, const int32_t* block_tables,
+                      int64_t table_stride, int32_t max_blocks, const fs_kv_layout* kv, void* stream);
+
+/* Gather every block of every row's table in table order: paged.py:80-81.
+ * k_out, v_out: contiguous [B, n_kv_heads, max_blocks*block_size, head_dim]. */
+int fs_paged_gather(const fs_kv_layout* kv, const int32_t* block_tables, int64_t table_stride, int32_t B,
+                    int32_t max_blocks, void* k_out, void* v_out, void* stream);
+
+/* ---------------------------------------------------------------------------------------------- */
+/* Attention                                                                                        */
+/* ---------------------------------------------------------------------------------------------- */
+
+/* Causal GQA attention of each row's T queries over its paged keys/values.
+ * Replaces the gather of paged.py:80-81 plus model.py:70-76 (repeat_interleave, key <= query-position
+ * mask, scaled_dot_product_attention). q/out element (b, t, h, d) at base + b*s_b + t*s_t + h*s_h + d.
+ * Query head h reads KV head h / (n_heads / n_kv_heads) (model.py:70-71). Query (b, t) sees the keys
+ * at positions 0..positions[b*T+t] (model.py:75). workspace must hold
+ * fs_paged_attention_workspace_size(...) bytes. */
+int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
+                       const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                       const int32_t* positions, int32_t B, int32_t T, int32_t n_heads, float scale,
+                       void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32_t n_heads, int32_t head_dim,
+                                          int32_t max_blocks, int32_t block_size);
+
+/* ---------------------------------------------------------------------------------------------- */
+/* Dense ops of the decoder (model.py)                                                              */
+/* ---------------------------------------------------------------------------------------------- */
+
+/* C[M,N] = A[M,K] . B[N,K]^T (+ R[M,N]) in the dtype, f32 accumulation, one rounding of the product
+ * and, with R, a second rounding of the sum (nn.Linear then `x + ...`: model.py:77, 93, 105-106,
+ * 119-120). Rows may be strided; columns are contiguous. */
+int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, const void* R,
+            int64_t ldr, int64_t M, int64_t N, int64_t K, int32_t dtype, void* stream);
+
+/* RMSNorm of model.py:29-31, optionally after a residual add (model.py:105-106):
+ * if delta != NULL: x_out = x + delta (rounded to the dtype) is written, then normed.
+ * y = ((x32 * rsqrt(mean(x32^2) + eps)) rounded to the dtype) * weight, rounded to the dtype. */
+int fs_add_rmsnorm(const void* x, int64_t ldx, const void* delta, int64_t ldd, void* x_out, int64_t ldxo,
+                   const void* weight, void* y, int64_t ldy, int64_t M, int64_t N, float eps,
+                   int32_t dtype, void* stream);
+
+/* SwiGLU gate: h = silu(gu[:, :F]) * gu[:, F:2F], each op rounded to the dtype (model.py:93). */
+int fs_silu_mul(const void* gu, int64_t ldgu, void* h, int64_t ldh, int64_t M, int64_t F, int32_t dtype,
+                void* stream);
+
+/* Embedding lookup (model.py:134-135): out[m] = weight[ids[m]]; ids int64. */
+int fs_embedding(const int64_t* ids, int64_t M, const void* weight, int64_t d_model, int64_t vocab,
+                 void* out, int64_t ldo, int32_t dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------------------- */
+/* Sampling and acceptance                                                                          */
+/* ---------------------------------------------------------------------------------------------- */
+
+/* probs_from_logits (sampling.py:9-13) for R rows of V: temperature > 0 gives
+ * softmax(f32(logits) / temperature) in f32 (out_dtype must be FS_F32); temperature == 0 gives the
+ * one-hot of the first argmax in the logits dtype (out_dtype == dtype). */
+int fs_probs_from_logits(const void* logits, int64_t ld, int64_t R, int64_t V, float temperature,
+                         int32_t dtype, void* out, int64_t ldo, int32_t out_dtype, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
+/* sample (sampling.py:16-21) and the draft draw of speculative.py:61-62, for R rows.
+ * Temperature of row r: temperature[r] (device f32 [R]) or, if temperature is NULL, temperature_all.
+ * T == 0 -> first argmax of the logits; else argmax_v( p_v / E[r, v] ) with p = softmax(logits / T)
+ * (torch.multinomial(p, 1) == argmax(p / Exp(1) noise), first index on ties).
+ * E == NULL makes every row take the argmax. tokens_out: int64 [R]; if tokens_out32 is not NULL the
+ * tokens are also written there as int32 with stride ld_tok32. */
+int fs_sample_logits(const void* logits, int64_t ld, int64_t R, int64_t V, const float* temperature,
+                     float temperature_all, const float* E, int64_t ldE, int32_t dtype, int64_t* tokens_out,
+                     int32_t* tokens_out32, int64_t ld_tok32, void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
+int64_t fs_sampling_workspace_size(int64_t R, int64_t V);
+
+/* Batched speculative acceptance: probs_from_logits + verify_draft (speculative.py:20-33) for B
+ * sequences in one stream-ordered call, no host round trip.
+ *   tgt: [B, K+1, V] target logits (row (b,i) at tgt + b*tgt_sb + i*tgt_si)
+ *   dft: [B, K, V] draft logits (same convention)
+ *   draft_tokens int32 [B, K]; k_eff int32 [B] (<= K, proposals of sequence b);
+ *   temperature f32 [B]; u f32 [B, K] uniforms; E f32 [B, V] Exp(1) noise for the one final draw.
+ * For i < k_eff[b]: ratio = p_i(x_i) / q_i(x_i) if q_i(x_i) > 0 else 1; accept while u[b,i] < min(1, ratio).
+ * At the first rejection j the extra token is argmax_v( w_v / E_v ) with w = r / sum(r),
+ * r = max(p_j - q_j, 0) (w = p_j if sum(r) == 0); if all are accepted, w = p_{k_eff}.
+ * Outputs: out_tokens int32 [B, K+1] (accepted proposals, then the extra token, then -1),
+ * n_accepted int32 [B]. If seq_len != NULL it is the device-side rollback: on entry seq_len[b] is
+ * the number of cached tokens before the verify window, on exit cached + 1 + n_accepted
+ * (speculative.py:77). */
+int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
+                   int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype, const int32_t* draft_tokens,
+                   const int32_t* k_eff, const float* temperature, const float* u, const float* E,
+                   int64_t ldE, int32_t* out_tokens, int32_t* n_accepted, int32_t* seq_len, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
+/* verify_draft (speculative.py:20-33) on probabilities instead of logits: p [K+1, V] rows at
+ * p + i*ldp, q [K, V]; one sequence, K proposals; p and q in `dtype` (f32 from a softmax, or the
+ * logits dtype for one-hot rows). Same outputs as fs_spec_accept with B = 1. */
+int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_t ldq, int32_t K, int64_t V,
+                    int32_t dtype, const int32_t* draft_tokens, const float* u, const float* E,
+                    int32_t* out_tokens, int32_t* n_accepted, void* workspace, int64_t workspace_bytes,
+                    void* stream);
+
+int64_t fs_spec_accept_workspace_size(int32_t B, int32_t K, int64_t V);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FORGESERVE_AMD_H */

@@ -1,0 +1,321 @@
+"""Kernel-level parity of the HIP path against the CPU oracle (bit-exact for integer/decision work,
+within the stated tolerance for floating point). Every case prints its name before it launches."""
+
+import math
+
+import pytest
+import torch
+
+from forgeserve_amd import ops
+from oracle import reference_cpu as orc
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def case(*a):
+    print("case:", *a, flush=True)
+
+
+def rel_err(got, ref):
+    return (got.double() - ref.double()).abs().max().item() / max(ref.double().abs().max().item(), 1e-30)
+
+
+# ---- GEMM -------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("m,n,k", [(1, 48, 64), (7, 256, 688), (64, 1000, 256), (65, 384, 512), (448, 640, 4096),
+                                   (130, 96, 192)])
+def test_gemm_matches_fp64(dtype, m, n, k):
+    case("gemm", dtype, m, n, k)
+    g = torch.Generator().manual_seed(m * 7 + n)
+    a = torch.randn(m, k, generator=g).to(dtype)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(dtype)
+    ref = a.double() @ w.double().T
+    out = ops.gemm(a.to(DEV), w.to(DEV)).cpu()
+    tol = 1e-5 if dtype == torch.float32 else 8e-3
+    assert rel_err(out, ref) < tol
+    if dtype == torch.bfloat16:
+        # one rounding of the f32 accumulation: at most one bf16 ulp from the exactly rounded product
+        exact = ref.to(torch.bfloat16).float()
+        assert ((out.float() - exact).abs() <= exact.abs() * 2 ** -7 + 1e-30).float().mean() > 0.999
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gemm_rows_do_not_depend_on_the_batch(dtype):
+    """A row's result is bit-identical whether it is computed alone, among 64 rows or among 448."""
+    case("gemm invariance", dtype)
+    g = torch.Generator().manual_seed(1)
+    a = torch.randn(448, 512, generator=g).to(dtype).to(DEV)
+    w = (torch.randn(384, 512, generator=g) * 0.05).to(dtype).to(DEV)
+    full = ops.gemm(a, w)
+    mid = ops.gemm(a[:64], w)
+    for i in (0, 5, 63):
+        assert torch.equal(ops.gemm(a[i: i + 1], w)[0], full[i])
+        assert torch.equal(mid[i], full[i])
+    assert torch.equal(ops.gemm(a[100:107], w), full[100:107])
+
+
+def test_gemm_residual_epilogue():
+    case("gemm residual")
+    g = torch.Generator().manual_seed(2)
+    a = torch.randn(70, 256, generator=g).bfloat16().to(DEV)
+    w = (torch.randn(128, 256, generator=g) * 0.05).bfloat16().to(DEV)
+    r = torch.randn(70, 128, generator=g).bfloat16().to(DEV)
+    fused = ops.gemm(a, w, residual=r)
+    two_step = (ops.gemm(a, w).float() + r.float()).bfloat16()   # x + linear(...) rounds twice
+    assert torch.equal(fused, two_step)
+
+
+# ---- row ops ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rmsnorm_and_residual(dtype):
+    case("rmsnorm", dtype)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(33, 4096, generator=g).to(dtype)
+    d = torch.randn(33, 4096, generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(4096, generator=g)).to(dtype)
+    x_out = torch.empty_like(x, device=DEV)
+    y = ops.add_rmsnorm(x.to(DEV), w.to(DEV), 1e-5, delta=d.to(DEV), x_out=x_out).cpu()
+    xs = x + d
+    assert torch.equal(x_out.cpu(), xs)
+    ref = orc.rms_norm(xs, w, 1e-5)
+    if dtype == torch.float32:
+        torch.testing.assert_close(y, ref, atol=1e-5, rtol=1e-5)
+    else:   # the sum of squares is ordered differently from torch's: at most one bf16 ulp apart
+        assert ((y.float() - ref.float()).abs() <= ref.float().abs() * 2 ** -7 * 1.01).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_silu_mul(dtype):
+    case("silu_mul", dtype)
+    g = torch.Generator().manual_seed(4)
+    gu = (torch.randn(17, 2 * 688, generator=g) * 3).to(dtype)
+    h = ops.silu_mul(gu.to(DEV)).cpu()
+    ref = torch.nn.functional.silu(gu[:, :688]) * gu[:, 688:]
+    if dtype == torch.float32:
+        torch.testing.assert_close(h, ref, atol=1e-6, rtol=1e-6)
+    else:
+        assert ((h.float() - ref.float()).abs() <= ref.float().abs() * 2 ** -7 * 1.01 + 1e-30).all()
+
+
+def test_embedding():
+    case("embedding")
+    w = torch.randn(100, 48).bfloat16()
+    ids = torch.tensor([[3, 99, 0], [7, 7, 50]])
+    assert torch.equal(ops.embedding(ids.to(DEV), w.to(DEV)).cpu(), w[ids.reshape(-1)])
+
+
+# ---- KV write + rotary ----------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,d,bs", [(torch.float32, 8, 4), (torch.float32, 32, 16), (torch.bfloat16, 128, 16),
+                                        (torch.bfloat16, 64, 16)])
+def test_qkv_rope_write(dtype, d, bs):
+    case("qkv_rope_write", dtype, d, bs)
+    from forgeserve_amd import PagedKVPool, ModelConfig
+    h, hkv, b, t = 8, 2, 3, 5
+    cfg = ModelConfig(vocab_size=10, d_model=h * d, n_layers=1, n_heads=h, n_kv_heads=hkv, max_seq_len=200)
+    s = orc.Shape.of(cfg)
+    cos, sin = orc.rope_tables(s)
+    pool = PagedKVPool(cfg, 40, bs, dtype=dtype, device=DEV)
+    perm = torch.randperm(40, generator=torch.Generator().manual_seed(5))
+    nbk = -(-44 // bs)                       # positions reach 43
+    tables = perm[: b * nbk].reshape(b, nbk)
+    pos = torch.tensor([[0, 1, 2, 3, 4], [17, 18, 19, 20, 21], [40, 41, 42, 43, -1]])
+    qkv = torch.randn(b * t, (h + 2 * hkv) * d, generator=torch.Generator().manual_seed(6)).to(dtype)
+    q = ops.qkv_rope_write(qkv.to(DEV), pos.reshape(-1).int().to(DEV), t, h, cos.to(DEV), sin.to(DEV),
+                           tables.int().to(DEV), pool.layout(0)).cpu()
+    x = qkv.view(b, t, h + 2 * hkv, d).transpose(1, 2)
+    valid = pos.clamp(min=0)
+    q_ref = orc.rotate(x[:, :h], cos, sin, valid).transpose(1, 2).reshape(b * t, h * d)
+    k_ref = orc.rotate(x[:, h:h + hkv], cos, sin, valid)
+    v_ref = x[:, h + hkv:]
+    ok = (pos >= 0).reshape(-1)
+    assert torch.equal(q[ok], q_ref[ok])
+    kp, vp = pool.k[0].cpu(), pool.v[0].cpu()
+    for bi in range(b):
+        for ti in range(t):
+            p = int(pos[bi, ti])
+            if p < 0:
+                continue
+            blk = int(tables[bi, p // bs])
+            assert torch.equal(kp[blk, :, p % bs], k_ref[bi, :, ti])
+            assert torch.equal(vp[blk, :, p % bs], v_ref[bi, :, ti])
+
+
+# ---- paged attention --------------------------------------------------------------------------------------
+def _paged_case(b, t, h, hkv, d, bs, ctx, nblocks, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    maxb = max(-(-c // bs) for c in ctx)
+    perm = torch.randperm(nblocks, generator=g)
+    tables = torch.zeros(b, maxb, dtype=torch.long)
+    used = 0
+    for i, c in enumerate(ctx):
+        nb = -(-c // bs)
+        tables[i, :nb] = perm[used: used + nb]
+        used += nb
+    k = torch.randn(nblocks, hkv, bs, d, generator=g).to(dtype)
+    v = torch.randn(nblocks, hkv, bs, d, generator=g).to(dtype)
+    q = torch.randn(b, t, h, d, generator=g).to(dtype)
+    pos = torch.tensor([[c - t + i for i in range(t)] for c in ctx])
+    return q, k, v, tables, pos
+
+
+def _oracle_attention(q, k, v, tables, pos, rep):
+    """Gather the table blocks (paged.py:80-81) and run the oracle attention in f32."""
+    b = q.shape[0]
+    nb = tables.shape[1]
+    k_all = k.float()[tables].permute(0, 2, 1, 3, 4).reshape(b, k.shape[1], nb * k.shape[2], k.shape[3])
+    v_all = v.float()[tables].permute(0, 2, 1, 3, 4).reshape(b, k.shape[1], nb * k.shape[2], k.shape[3])
+    out = orc.attention_math(q.float().transpose(1, 2), k_all, v_all, pos, rep)
+    return out.transpose(1, 2)
+
+
+def _run_attention(q, k, v, tables, pos, dtype, bs, pool_layout=True):
+    from forgeserve_amd import PagedKVPool, ModelConfig
+    nblocks, hkv, _, d = k.shape
+    h = q.shape[2]
+    cfg = ModelConfig(vocab_size=8, d_model=h * d, n_layers=1, n_heads=h, n_kv_heads=hkv, max_seq_len=8)
+    pool = PagedKVPool(cfg, nblocks, bs, dtype=dtype, device=DEV)
+    pool.k[0].copy_(k.to(DEV))
+    pool.v[0].copy_(v.to(DEV))
+    out = ops.paged_attention(q.to(DEV), pool.layout(0), tables.int().to(DEV), pos.int().to(DEV),
+                              1.0 / math.sqrt(d))
+    return out, pool
+
+
+@pytest.mark.parametrize("d,bs,t", [(8, 4, 3), (32, 16, 5), (16, 7, 2), (128, 16, 1)])
+def test_attention_generic_f32(d, bs, t):
+    case("attention f32", d, bs, t)
+    ctx = [9, 40, 300, 513]
+    q, k, v, tables, pos = _paged_case(4, t, 8, 2, d, bs, ctx, 300, torch.float32, d + bs)
+    out, _ = _run_attention(q, k, v, tables, pos, torch.float32, bs)
+    ref = _oracle_attention(q, k, v, tables, pos, 4)
+    torch.testing.assert_close(out.cpu(), ref, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("d,t,g", [(128, 5, 4), (128, 7, 4), (64, 5, 4), (128, 1, 4), (128, 9, 4), (64, 3, 8)])
+def test_attention_mfma_bf16(d, t, g):
+    case("attention bf16 mfma", d, t, g)
+    hkv = 2
+    ctx = [t + 1, 100, 257, 1000, 4097]
+    q, k, v, tables, pos = _paged_case(len(ctx), t, hkv * g, hkv, d, 16, ctx, 600, torch.bfloat16, d * t + g)
+    out, _ = _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
+    ref = _oracle_attention(q, k, v, tables, pos, g)
+    assert rel_err(out.cpu().float(), ref) < 2e-2
+
+
+def test_attention_verify_equals_decode_bitwise():
+    """A query's output does not depend on T: the k+1-token verify pass and 1-token decodes at the
+    same positions produce identical bits (the batch-invariance that keeps greedy tokens identical)."""
+    case("attention invariance")
+    t = 7
+    ctx = [300, 511, 512, 513, 2049]
+    q, k, v, tables, pos = _paged_case(len(ctx), t, 32, 8, 128, 16, ctx, 800, torch.bfloat16, 9)
+    full, pool = _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
+    lay = pool.layout(0)
+    tab = tables.int().to(DEV)
+    for i in range(t):
+        one = ops.paged_attention(q[:, i: i + 1].to(DEV), lay, tab, pos[:, i: i + 1].int().to(DEV),
+                                  1.0 / math.sqrt(128))
+        assert torch.equal(one[:, 0], full[:, i]), i
+    # a row alone gives the same bits as inside the batch
+    one_row = ops.paged_attention(q[3:4].to(DEV), lay, tab[3:4], pos[3:4].int().to(DEV), 1.0 / math.sqrt(128))
+    assert torch.equal(one_row[0], full[3])
+
+
+def test_attention_padding_rows_are_zero():
+    case("attention padding")
+    q, k, v, tables, pos = _paged_case(2, 3, 8, 2, 128, 16, [50, 70], 20, torch.bfloat16, 4)
+    pos[1, 2] = -1
+    out, _ = _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
+    assert torch.count_nonzero(out[1, 2]) == 0
+
+
+def test_attention_c3_shape():
+    """B=32, T=5, 32/8 heads, D=128, bf16, contexts U[512, 4096], a 12288-block pool in random order."""
+    case("attention c3")
+    g = torch.Generator().manual_seed(6)
+    ctx = torch.randint(512, 4097, (32,), generator=g).tolist()
+    q, k, v, tables, pos = _paged_case(32, 5, 32, 8, 128, 16, ctx, 12288, torch.bfloat16, 6)
+    out, _ = _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
+    ref = _oracle_attention(q, k, v, tables, pos, 4)
+    err = (out.cpu().float() - ref).abs()
+    assert err.max().item() / ref.abs().max().item() < 2e-2
+    assert err.mean().item() < 2e-3
+
+
+# ---- sampling / acceptance ----------------------------------------------------------------------------
+def _c2_inputs(b=64, k=5, v=32000, seed=3, dtype=torch.float32):
+    tgt = torch.randn(b, k + 1, v, generator=torch.Generator().manual_seed(seed)) * 2.0
+    dft = tgt[:, :k] + torch.randn(b, k, v, generator=torch.Generator().manual_seed(seed + 1)) * 0.5
+    return tgt.to(dtype), dft.to(dtype)
+
+
+@pytest.mark.parametrize("temperature", [1.0, 0.0, 0.7])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_spec_accept_c2_bit_exact(temperature, dtype):
+    """Batch 64, k=5, V=32000: accepted lengths, replacement and bonus tokens identical to the oracle's
+    verify_draft on the same injected uniforms and Exp(1) noise."""
+    case("spec_accept c2", temperature, dtype)
+    b, k, v = 64, 5, 32000
+    tgt, dft = _c2_inputs(dtype=dtype)
+    g = torch.Generator().manual_seed(5)
+    xs = torch.zeros(b, k, dtype=torch.int32)
+    for bi in range(b):
+        for i in range(k):
+            if temperature == 0:
+                xs[bi, i] = int(dft[bi, i].float().argmax())
+            else:
+                qrow = orc.probs_from_logits(dft[bi, i].float(), temperature)
+                xs[bi, i] = orc.draw(qrow, orc.exp_noise(v, g))
+    u = torch.rand(b, k, generator=g)
+    e = torch.empty(b, v).exponential_(generator=g)
+    k_eff = torch.tensor([k if i % 7 else i % 5 for i in range(b)], dtype=torch.int32)
+    seq = torch.randint(100, 1000, (b,), generator=g, dtype=torch.int32)
+    temps = torch.full((b,), float(temperature))
+    out, n = ops.spec_accept(tgt.to(DEV), dft.to(DEV), xs.to(DEV), k_eff.to(DEV), temps.to(DEV), u.to(DEV), e.to(DEV),
+                             seq_len=(seq_dev := seq.to(DEV)))
+    out, n, seq_after = out.cpu(), n.cpu(), seq_dev.cpu()
+    for bi in range(b):
+        ke = int(k_eff[bi])
+        tl = tgt[bi, : ke + 1]
+        dl = dft[bi, :ke]
+        p = orc.probs_from_logits(tl, temperature) if temperature else orc.probs_from_logits(tl.float(), 0)
+        q = orc.probs_from_logits(dl, temperature) if temperature else orc.probs_from_logits(dl.float(), 0)
+        acc, extra = orc.verify_with_noise(p, q, xs[bi, :ke].tolist(), u[bi], e[bi])
+        assert int(n[bi]) == len(acc), bi
+        assert out[bi, : len(acc) + 1].tolist() == acc + [extra], bi
+        assert (out[bi, len(acc) + 1:] == -1).all()
+        assert int(seq_after[bi]) == int(seq[bi]) + 1 + len(acc)
+
+
+@pytest.mark.parametrize("temperature", [0.0, 0.8])
+def test_sample_logits(temperature):
+    case("sample_logits", temperature)
+    g = torch.Generator().manual_seed(8)
+    x = (torch.randn(37, 5003, generator=g) * 3).bfloat16()
+    e = torch.empty(37, 5003).exponential_(generator=g)
+    got = ops.sample_logits(x.to(DEV), temperature, e.to(DEV) if temperature else None).cpu().tolist()
+    want = [orc.draw(orc.probs_from_logits(x[r].float(), temperature), e[r]) if temperature else int(x[r].argmax())
+            for r in range(37)]
+    assert got == want
+
+
+def test_probs_from_logits():
+    case("probs_from_logits")
+    x = torch.randn(5, 20000) * 4
+    p = ops.probs_from_logits(x.to(DEV), 0.7).cpu()
+    torch.testing.assert_close(p, orc.probs_from_logits(x, 0.7), atol=1e-7, rtol=2e-5)
+    hot = ops.probs_from_logits(x.bfloat16().to(DEV), 0).cpu()
+    assert torch.equal(hot, orc.probs_from_logits(x.bfloat16(), 0))
+
+
+def test_verify_draft_reference_streams():
+    """forgeserve_amd.verify_draft on the GPU reproduces the reference's outcomes for seeded generators."""
+    case("verify_draft golden")
+    from forgeserve_amd import verify_draft
+    from helpers import golden_json
+    for c in golden_json("verify_cases.json"):
+        p = torch.tensor(c["p"], dtype=torch.float32).to(DEV)
+        q = torch.tensor(c["q"], dtype=torch.float32).reshape(c["k"], c["V"]).to(DEV)
+        got = verify_draft(p, q, c["xs"], torch.Generator().manual_seed(c["seed"]))
+        assert got == (c["accepted"], c["extra"]), c["seed"]

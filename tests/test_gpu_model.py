@@ -1,0 +1,202 @@
+"""The decoder, the caches, generate, speculative decoding and the engine on the GPU against the
+reference's own outputs (tests/golden/) and the CPU oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+import forgeserve_amd as fa
+from helpers import C1, SMALL, golden_json, golden_npz, oracle_model, product_model
+from oracle import reference_cpu as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def case(*a):
+    print("case:", *a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def small():
+    return product_model(SMALL, 1, 0.25)
+
+
+@pytest.fixture(scope="module")
+def small_draft():
+    return product_model(SMALL, 7, 0.25)
+
+
+def test_small_logits_match_reference(small):
+    case("small logits")
+    gold = golden_npz("model_small.npz")
+    idx = torch.from_numpy(gold["idx"])
+    np.testing.assert_allclose(small(idx).cpu().numpy(), gold["logits"], atol=1e-4, rtol=1e-4)
+    shifted = small(idx[:1, :5], positions=torch.arange(5)[None] + 11)
+    np.testing.assert_allclose(shifted.cpu().numpy(), gold["logits_shifted"], atol=1e-4, rtol=1e-4)
+
+
+def test_cache_one_token_at_a_time_matches_full_forward(small):
+    """tests/test_model.py:31-42 of the reference."""
+    case("cache equivalence")
+    idx = torch.randint(0, 64, (2, 20))
+    kv = fa.new_contiguous_cache(3)
+    steps = torch.cat([small(idx[:, i: i + 1], kv=kv) for i in range(20)], dim=1)
+    torch.testing.assert_close(steps, small(idx), atol=1e-4, rtol=1e-4)
+    kv = fa.new_contiguous_cache(3)
+    small(idx[:, :10], kv=kv)
+    torch.testing.assert_close(small(idx[:, 10:], kv=kv), small(idx)[:, 10:], atol=1e-4, rtol=1e-4)
+
+
+def test_paged_forward_matches_reference(small):
+    case("paged forward")
+    gold = golden_npz("model_small.npz")
+    seq = torch.from_numpy(gold["paged_seq"])
+    table = torch.from_numpy(gold["paged_table"])
+    pool = fa.PagedKVPool(small.cfg, num_blocks=16, block_size=4)
+    got = [small(seq[:, :12], torch.arange(12)[None], pool.views(table, torch.arange(12)[None]))]
+    for i in range(12, 30):
+        pos = torch.tensor([[i]])
+        got.append(small(seq[:, i: i + 1], pos, pool.views(table, pos)))
+    np.testing.assert_allclose(torch.cat(got, 1).cpu().numpy(), gold["paged_logits"], atol=1e-4, rtol=1e-4)
+
+
+def test_paged_update_write_then_read_back():
+    """tests/test_paged.py:20-41 of the reference through PagedLayerView.update."""
+    case("paged update")
+    cfg = fa.ModelConfig(vocab_size=64, d_model=64, n_layers=3, n_heads=8, n_kv_heads=4, max_seq_len=64)
+    pool = fa.PagedKVPool(cfg, num_blocks=10, block_size=4)
+    table = torch.tensor([[7, 2, 9]])
+    k = torch.randn(1, 4, 10, 8, device="cuda")
+    v = torch.randn_like(k)
+    k_all, v_all = pool.views(table, torch.arange(10)[None])[0].update(k, v)
+    assert k_all.shape == (1, 4, 12, 8)
+    assert torch.equal(k_all[:, :, :10], k) and torch.equal(v_all[:, :, :10], v)
+    assert torch.equal(pool.k[0][2, :, 1], k[0, :, 5]) and torch.equal(pool.v[0][2, :, 1], v[0, :, 5])
+    pool = fa.PagedKVPool(cfg, num_blocks=8, block_size=4)
+    k = torch.randn(2, 4, 6, 8, device="cuda")
+    k_all, _ = pool.views(torch.tensor([[0, 1], [2, 3]]), torch.arange(6)[None].expand(2, 6))[0].update(k, k.clone())
+    assert torch.equal(k_all[:, :, :6], k)
+
+
+def test_generate_matches_reference(small):
+    case("generate")
+    gold = golden_json("model_small.json")
+    for i, p in enumerate(gold["prompts"]):
+        assert fa.generate(small, torch.tensor([p]), 20)[0].tolist() == gold["generate_greedy"][i]
+        got = fa.generate(small, torch.tensor([p]), 20, temperature=1.0, generator=torch.Generator().manual_seed(21 + i))
+        assert got[0].tolist() == gold["generate_t1"][i]
+
+
+def test_speculative_matches_reference_streams(small, small_draft):
+    case("speculative golden")
+    gold = golden_json("model_small.json")
+    for kk in (1, 3, 6):
+        for p, want in zip(gold["prompts"], gold["spec"][f"greedy_k{kk}"]):
+            assert list(fa.speculative_generate(small, small_draft, p, 20, k=kk)) == want, (kk, p)
+    for i, (p, want) in enumerate(zip(gold["prompts"], gold["spec"]["t1_k3"])):
+        got = fa.speculative_generate(small, small_draft, p, 20, k=3, temperature=1.0,
+                                      generator=torch.Generator().manual_seed(31 + i))
+        assert list(got) == want, p
+    for i, (p, want) in enumerate(zip(gold["prompts"], gold["spec"]["t07_k4_self"])):
+        got = fa.speculative_generate(small, small, p, 25, k=4, temperature=0.7,
+                                      generator=torch.Generator().manual_seed(41 + i))
+        assert list(got) == want, p
+
+
+def test_speculative_stopping_and_vocab_checks(small, small_draft):
+    """tests/test_speculative.py:46-57 of the reference."""
+    case("speculative stopping")
+    for n in (1, 2, 7):
+        got, _ = fa.speculative_generate(small, small_draft, [1, 2, 3], n, k=5)
+        assert len(got) == n
+    got, _ = fa.speculative_generate(small, small_draft, list(range(1, 60)), 100, k=4)
+    assert 59 + len(got) == small.cfg.max_seq_len
+    other = product_model(dict(SMALL, vocab_size=32), 7, 0.25)
+    with pytest.raises(ValueError):
+        fa.speculative_generate(small, other, [1, 2], 3)
+
+
+def test_c1_end_to_end_matches_reference():
+    """Tiny config: 4 layers, d 256, 8/4 heads, ffn 688, vocab 512, fp32, early-exit draft of 1 layer,
+    k=4, 64 new tokens: logits, greedy and seeded T=0.8 speculative tokens + stats equal the reference's."""
+    case("c1")
+    target = product_model(C1, 0, 0.02)
+    draft = fa.early_exit_draft(target, 1)
+    gold = golden_json("model_c1.json")
+    prompt = gold["prompt"]
+    np.testing.assert_allclose(target(torch.tensor([prompt]))[0].cpu().numpy(), golden_npz("model_c1.npz")["logits"],
+                               atol=1e-4, rtol=1e-4)
+    assert fa.generate(target, torch.tensor([prompt]), 64)[0].tolist()[16:] == gold["greedy"]
+    assert list(fa.speculative_generate(target, draft, prompt, 64, k=4)) == gold["spec_greedy"]
+    got = fa.speculative_generate(target, draft, prompt, 64, k=4, temperature=0.8,
+                                  generator=torch.Generator().manual_seed(2))
+    assert list(got) == gold["spec_t08"]
+
+
+def test_engine_matches_reference_runs(small):
+    case("engine golden")
+    gold = golden_json("engine_runs.json")
+    for name, run in gold["runs"].items():
+        e = fa.Engine(small, num_blocks=run["num_blocks"], block_size=4, max_batch=5, seed=run["seed"])
+        ids = [e.add_request(p, n, temperature=run["temperature"]) for p, n in gold["requests"]]
+        out = e.run()
+        assert [out[i] for i in ids] == run["outputs"], name
+        assert e.preemptions == run["preemptions"], name
+        assert e.pool.allocator.num_free == run["num_blocks"]
+
+
+def test_engine_errors(small):
+    """tests/test_engine.py:106-120 of the reference."""
+    case("engine errors")
+    e = fa.Engine(small, num_blocks=4, block_size=4)
+    with pytest.raises(ValueError):
+        e.add_request([], 5)
+    with pytest.raises(ValueError):
+        e.add_request(list(range(1, 40)), 5)
+    e = fa.Engine(small, num_blocks=2, block_size=4)
+    e.add_request([1, 2, 3, 4, 5], 30)
+    with pytest.raises(RuntimeError):
+        e.run()
+
+
+# ---- bf16 models on the MFMA path ------------------------------------------------------------------------
+BF = dict(vocab_size=1000, d_model=512, n_layers=3, n_heads=4, n_kv_heads=1, ffn_dim=1024, max_seq_len=512)
+
+
+@pytest.fixture(scope="module")
+def bf_target():
+    return product_model(BF, 3, 0.06, dtype=torch.bfloat16)
+
+
+def test_bf16_logits_within_tolerance(bf_target):
+    """bf16 logits within 2e-2 relative of the reference's f32 math on the same (bf16-rounded) weights."""
+    case("bf16 logits")
+    w, s = oracle_model(BF, 3, 0.06)
+    w = {k: v.bfloat16().float() for k, v in w.items()}
+    idx = torch.randint(0, 1000, (2, 40))
+    ref = orc.forward(w, s, idx)
+    got = bf_target(idx).float().cpu()
+    assert (got - ref).abs().max().item() / ref.abs().max().item() < 2e-2
+
+
+def test_bf16_speculative_batch_equals_greedy_generate(bf_target):
+    """Batched paged speculation (greedy) emits exactly the target's own greedy tokens, bit for bit,
+    for every row: verify, decode and prefill rows are computed identically (batch invariance)."""
+    case("bf16 batch == greedy")
+    draft = fa.early_exit_draft(bf_target, 1)
+    g = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, 1000, (int(n),), generator=g).tolist() for n in torch.randint(2, 60, (6,), generator=g)]
+    want = [fa.generate(bf_target, torch.tensor([p]), 40)[0].tolist()[len(p):] for p in prompts]
+    got, stats = fa.speculative_generate_batch(bf_target, draft, prompts, 40, k=4)
+    assert got == want
+    assert stats["accepted"] <= stats["proposed"]
+    single, _ = fa.speculative_generate(bf_target, draft, prompts[0], 40, k=4)
+    assert single == want[0]
+
+
+def test_bf16_batch_perfect_draft_accepts_everything(bf_target):
+    case("bf16 perfect draft")
+    prompts = [[1, 2, 3], [4, 5, 6, 7, 8]]
+    got, stats = fa.speculative_generate_batch(bf_target, bf_target, prompts, 25, k=4)
+    assert stats["accepted"] == stats["proposed"]
+    assert got == [fa.generate(bf_target, torch.tensor([p]), 25)[0].tolist()[len(p):] for p in prompts]
