@@ -4,8 +4,9 @@
 // Reference: paged.py:80-81 (gather every table block) + model.py:70-76 (repeat_interleave GQA,
 // key_pos <= query_pos mask, scaled_dot_product_attention with scale 1/sqrt(D)).
 //
-// Work split (both kernels): the keys of a row are cut into fixed chunks of SPLIT absolute positions;
-// chunk s covers keys [s*SPLIT, (s+1)*SPLIT). Each workgroup produces the softmax partial
+// Work split (both kernels): the keys of a row are cut into fixed chunks of `split` absolute positions
+// (256 unless FS_ATTN_SPLIT says otherwise; fixed for the life of the process); chunk s covers keys
+// [s*split, (s+1)*split). Each workgroup produces the softmax partial
 // (running max m, sum l, unnormalised output acc) of its chunk, and attn_combine merges the chunks of
 // a query in increasing chunk order. A query at position p only ever reads the chunks that hold
 // keys <= p, and inside a chunk keys above p contribute exact zeros, so the output of a query does
@@ -20,12 +21,12 @@
 // With the transposed products every lane owns whole query rows (row = lane % 16), so the softmax
 // statistics, the P operand and the O rescale stay in the lane's own registers.
 #include <math.h>
+#include <stdlib.h>
 
 #include "common.h"
 
 namespace {
 
-constexpr int SPLIT = 256;           // keys per chunk (multiple of 16)
 constexpr int QTILE = 32;            // query rows per MFMA workgroup
 constexpr float LOG2E = 1.4426950408889634f;
 
@@ -42,6 +43,7 @@ struct AttnParams {
   float* ws_acc;                     // [B*T*H][nsplit][D]
   float* ws_ml;                      // [B*T*H][nsplit][2]
   int32_t nsplit;
+  int32_t split;                     // keys per chunk: a multiple of 16, at most 512
 };
 
 FS_DEVICE int64_t row_index(const AttnParams& P, int b, int t, int h) { return ((int64_t)b * P.T + t) * P.H + h; }
@@ -49,16 +51,18 @@ FS_DEVICE int64_t row_index(const AttnParams& P, int b, int t, int h) { return (
 // ------------------------------------------------------------------------------------------------
 // MFMA kernel (bf16)
 // ------------------------------------------------------------------------------------------------
-template <int D>
-__global__ void __launch_bounds__(64) attn_mfma_bf16_kernel(AttnParams P) {
+// BSZ: the pool's block size when it is known at compile time (16), else 0 (any multiple of 16).
+template <int D, int BSZ>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) attn_mfma_bf16_kernel(AttnParams P) {
   constexpr int KS = D / 32;   // k-steps of the QK^T product
   constexpr int MT = D / 16;   // 16-dim tiles of the PV product
   const int lane = threadIdx.x;
   const int l16 = lane & 15, g = lane >> 4;
-  const int s = blockIdx.x;
-  const int bh = blockIdx.y;
+  // heads of one (row, chunk) are adjacent workgroups: their tiles are neighbours in the pool
   const int Hkv = P.kv.n_kv_heads;
-  const int b = bh / Hkv, hkv = bh - b * Hkv;
+  const int s = blockIdx.x / Hkv;
+  const int hkv = blockIdx.x - s * Hkv;
+  const int b = blockIdx.y;
   const int row0 = blockIdx.z * QTILE;
   const int nrows = min(QTILE, P.T * P.G - row0);
   const int* posb = P.pos + (int64_t)b * P.T;
@@ -75,9 +79,10 @@ __global__ void __launch_bounds__(64) attn_mfma_bf16_kernel(AttnParams P) {
     const int t0 = row0 / P.G, t1 = (row0 + nrows - 1) / P.G;
     for (int t = t0; t <= t1; ++t) qmax = max(qmax, posb[t]);
   }
-  const int kbeg = s * SPLIT;
+  qmax = __builtin_amdgcn_readfirstlane(qmax);  // the same in every lane: keep the loop scalar
+  const int kbeg = s * P.split;
   if (qmax < kbeg) return;  // no query of this tile sees this chunk: the combine never reads it
-  const int kend = min(kbeg + SPLIT, qmax + 1);
+  const int kend = min(kbeg + P.split, qmax + 1);
   const int ntiles = (kend - kbeg + 15) >> 4;
   const bool two = nrows > 16;
 
@@ -101,10 +106,11 @@ __global__ void __launch_bounds__(64) attn_mfma_bf16_kernel(AttnParams P) {
     }
   }
 
-  // physical block ids of this chunk (SPLIT / block_size <= 16 entries), one per lane
-  const int BS = P.kv.block_size;
+  // physical block ids of this chunk (at most P.split/16 + 1 entries), one per lane
+  const int BS = BSZ ? BSZ : P.kv.block_size;
+  const int64_t v_dim = BSZ ? BSZ : P.kv.v_dim;   // == block_size (dim-major values)
   const int first_blk = kbeg / BS;
-  const int nblk = (kend - 1) / BS - first_blk + 1;   // <= SPLIT/16 + 1 <= 64
+  const int nblk = (kend - 1) / BS - first_blk + 1;
   int my_phys = -1;
   if (lane < nblk && first_blk + lane < P.max_blocks) {
     const int v = P.table[(int64_t)b * P.table_stride + first_blk + lane];
@@ -125,24 +131,25 @@ __global__ void __launch_bounds__(64) attn_mfma_bf16_kernel(AttnParams P) {
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_run[2] = {0.f, 0.f};
 
-  bf16x8_t kf[KS];
-  short4_t vf[MT];
-  bool tile_valid = false;
+  // Three tile buffers in registers: while tile t is consumed, tiles t+1 and t+2 are in flight.
+  bf16x8_t kb0[KS], kb1[KS], kb2[KS];
+  short4_t vb0[MT], vb1[MT], vb2[MT];
+  bool ok0 = false, ok1 = false, ok2 = false;
 
   auto load_tile = [&](int kt, bf16x8_t (&kd)[KS], short4_t (&vd)[MT], bool& valid) {
     const int j0 = kbeg + 16 * kt;
-    const int bi = j0 / BS - first_blk;
-    const int64_t phys = __shfl(my_phys, bi, 64);
-    valid = phys >= 0;  // bi < nblk: the tile lies inside the chunk's block list
+    const int bi = j0 / BS - first_blk;   // < nblk: the tile lies inside the chunk's block list
+    const int64_t phys = __builtin_amdgcn_readfirstlane(__shfl(my_phys, bi, 64));  // wave-uniform block id
+    valid = phys >= 0;
     const int slot0 = j0 - (j0 / BS) * BS;
     if (valid) {
-      const u16* kt_ = kpool + phys * P.kv.k_block + k_head_off + (int64_t)(slot0 + l16) * P.kv.k_slot;
+      const u16* kt_ = kpool + phys * P.kv.k_block + k_head_off + (int64_t)(slot0 + l16) * D;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kd[ks] = *reinterpret_cast<const bf16x8_t*>(kt_ + 32 * ks + 8 * g);
       const u16* vt_ = vpool + phys * P.kv.v_block + v_head_off + slot0 + 4 * g;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        vd[mt] = *reinterpret_cast<const short4_t*>(vt_ + (int64_t)(16 * mt + l16) * P.kv.v_dim);
+        vd[mt] = *reinterpret_cast<const short4_t*>(vt_ + (int64_t)(16 * mt + l16) * v_dim);
     } else {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kd[ks] = bf16x8_t{};
@@ -151,13 +158,7 @@ __global__ void __launch_bounds__(64) attn_mfma_bf16_kernel(AttnParams P) {
     }
   };
 
-  load_tile(0, kf, vf, tile_valid);
-  for (int kt = 0; kt < ntiles; ++kt) {
-    bf16x8_t kn[KS];
-    short4_t vn[MT];
-    bool next_valid = false;
-    if (kt + 1 < ntiles) load_tile(kt + 1, kn, vn, next_valid);
-
+  auto consume = [&](int kt, const bf16x8_t (&kf)[KS], short4_t (&vf)[MT], bool tile_valid) {
     const int j0 = kbeg + 16 * kt;
     // keys past the furthest query (possibly never written) must not reach the PV product
     if (j0 + 15 > qmax) {
@@ -169,7 +170,6 @@ __global__ void __launch_bounds__(64) attn_mfma_bf16_kernel(AttnParams P) {
         }
       }
     }
-
     float4_t sc[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -180,8 +180,8 @@ __global__ void __launch_bounds__(64) attn_mfma_bf16_kernel(AttnParams P) {
           sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[nt][ks], sc[nt], 0, 0, 0);
       }
     }
-
     short4_t pf[2];
+    float alpha[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       float sv[4];
@@ -196,39 +196,45 @@ __global__ void __launch_bounds__(64) attn_mfma_bf16_kernel(AttnParams P) {
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
       const float m_new = fmaxf(m_run[nt], tmax);
-      const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run[nt] - m_new);
+      alpha[nt] = (m_new == -INFINITY) ? 1.f : exp2f(m_run[nt] - m_new);
       float psum = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float p = (sv[i] == -INFINITY) ? 0.f : exp2f(sv[i] - m_new);
-        const uint16_t pb = f32_to_bf16(p);
-        pf[nt][i] = (short)pb;
+        pf[nt][i] = (short)f32_to_bf16(p);
         psum += p;
       }
-      l_run[nt] = l_run[nt] * alpha + psum;
+      l_run[nt] = l_run[nt] * alpha[nt] + psum;
       m_run[nt] = m_new;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        acc[mt][nt][0] *= alpha;
-        acc[mt][nt][1] *= alpha;
-        acc[mt][nt][2] *= alpha;
-        acc[mt][nt][3] *= alpha;
-      }
     }
-
+    // unconditional rescale: a branch here splits the accumulators' live ranges and spills
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        acc[mt][nt][0] *= alpha[nt];
+        acc[mt][nt][1] *= alpha[nt];
+        acc[mt][nt][2] *= alpha[nt];
+        acc[mt][nt][3] *= alpha[nt];
+      }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[mt], pf[0], acc[mt][0], 0, 0, 0);
       if (two) acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[mt], pf[1], acc[mt][1], 0, 0, 0);
     }
+  };
 
-    if (kt + 1 < ntiles) {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = kn[ks];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) vf[mt] = vn[mt];
-      tile_valid = next_valid;
-    }
+  load_tile(0, kb0, vb0, ok0);
+  if (ntiles > 1) load_tile(1, kb1, vb1, ok1);
+  for (int kt = 0; kt < ntiles; kt += 3) {
+    if (kt + 2 < ntiles) load_tile(kt + 2, kb2, vb2, ok2);
+    consume(kt, kb0, vb0, ok0);
+    if (kt + 1 >= ntiles) break;
+    if (kt + 3 < ntiles) load_tile(kt + 3, kb0, vb0, ok0);
+    consume(kt + 1, kb1, vb1, ok1);
+    if (kt + 2 >= ntiles) break;
+    if (kt + 4 < ntiles) load_tile(kt + 4, kb1, vb1, ok1);
+    consume(kt + 2, kb2, vb2, ok2);
   }
 
   // write this chunk's partial for every real row of the tile that sees the chunk
@@ -270,9 +276,9 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnParams P) {
   const int bt = (int)(R / P.H);
   const int b = bt / P.T, t = bt - b * P.T;
   const int pos = P.pos[bt];
-  const int kbeg = s * SPLIT;
+  const int kbeg = s * P.split;
   if (pos < kbeg) return;
-  const int kend = min(kbeg + SPLIT, pos + 1);
+  const int kend = min(kbeg + P.split, pos + 1);
   const int D = P.kv.head_dim, BS = P.kv.block_size;
   const int hkv = h / P.G;
   const T_* qrow = reinterpret_cast<const T_*>(P.q) + (int64_t)b * P.q_sb + (int64_t)t * P.q_st + (int64_t)h * P.q_sh;
@@ -355,7 +361,7 @@ __global__ void __launch_bounds__(64) attn_combine_kernel(AttnParams P, void* ou
     for (int d = lane; d < D; d += 64) E::store(orow, d, 0.f);
     return;
   }
-  const int ns = min(pos / SPLIT + 1, P.nsplit);  // keys past the table were never visible
+  const int ns = min(pos / P.split + 1, P.nsplit);  // keys past the table were never visible
   const float* ml = P.ws_ml + R * P.nsplit * 2;
   float M = -INFINITY;
   for (int s = 0; s < ns; ++s) M = fmaxf(M, ml[2 * s]);
@@ -391,9 +397,19 @@ bool mfma_eligible(const fs_kv_layout& kv, const void* q, int64_t q_sb, int64_t 
   return true;
 }
 
+int attn_split() {
+  static const int split = [] {
+    const char* e = getenv("FS_ATTN_SPLIT");
+    int v = e ? atoi(e) : 256;
+    if (v < 16 || v > 512 || v % 16) v = 256;  // a chunk's block list must fit one wavefront
+    return v;
+  }();
+  return split;
+}
+
 int64_t nsplit_for(int32_t max_blocks, int32_t block_size) {
   const int64_t S = (int64_t)max_blocks * block_size;
-  return (S + SPLIT - 1) / SPLIT;
+  return (S + attn_split() - 1) / attn_split();
 }
 
 }  // namespace
@@ -443,6 +459,7 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
   P.G = n_heads / kv->n_kv_heads;
   P.scale_log2 = scale * LOG2E;
   P.nsplit = (int32_t)nsplit_for(max_blocks, kv->block_size);
+  P.split = attn_split();
   const int64_t rows = (int64_t)B * T * n_heads;
   P.ws_acc = reinterpret_cast<float*>(workspace);
   P.ws_ml = P.ws_acc + rows * P.nsplit * kv->head_dim;
@@ -450,11 +467,15 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
   hipStream_t st = fs::as_stream(stream);
   if (mfma_eligible(*kv, q, q_sb, q_st, q_sh)) {
     const int qtiles = (T * P.G + QTILE - 1) / QTILE;
-    dim3 grid((unsigned)P.nsplit, (unsigned)(B * kv->n_kv_heads), (unsigned)qtiles);
-    if (kv->head_dim == 128)
-      attn_mfma_bf16_kernel<128><<<grid, 64, 0, st>>>(P);
-    else
-      attn_mfma_bf16_kernel<64><<<grid, 64, 0, st>>>(P);
+    dim3 grid((unsigned)(P.nsplit * kv->n_kv_heads), (unsigned)B, (unsigned)qtiles);
+    const bool bs16 = kv->block_size == 16;
+    if (kv->head_dim == 128) {
+      if (bs16) attn_mfma_bf16_kernel<128, 16><<<grid, 64, 0, st>>>(P);
+      else attn_mfma_bf16_kernel<128, 0><<<grid, 64, 0, st>>>(P);
+    } else {
+      if (bs16) attn_mfma_bf16_kernel<64, 16><<<grid, 64, 0, st>>>(P);
+      else attn_mfma_bf16_kernel<64, 0><<<grid, 64, 0, st>>>(P);
+    }
   } else {
     dim3 grid((unsigned)rows, (unsigned)P.nsplit);
     switch (kv->dtype) {

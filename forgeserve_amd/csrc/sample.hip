@@ -271,73 +271,70 @@ struct AcceptArgs {
   const float* u;        // [B, K]
   const float* E;        // [B, V]
   int64_t ldE;
-  const Stat* stats;     // [B*(2K+1)][nch] (logits mode)
+  Stat* stats;           // [B*(2K+1)][nch] chunk partials (logits mode)
+  Stat* mstats;          // [B*(2K+1)] merged row statistics (logits mode)
   float* resid;          // [B][nch]
   float* pv;             // [B][nch]
   int* pi;               // [B][nch]
   int* jpos;             // [B]
 };
 
-// Value of p (row i < n0) or q (row >= n0) at column v, and the row's merged stats.
-template <int DT, bool PROBS>
-struct Dist {
-  const typename Elem<DT>::T* row;
-  Stat st;
-  float T;
-  FS_DEVICE float at_x(float x) const { return PROBS ? x : softmax_at(x, T, st); }
-};
+FS_DEVICE int keff_of(const AcceptArgs& A, int b) { return A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K; }
 
-// First rejected proposal (or k_eff when every proposal is accepted): speculative.py:25-29.
+// launch 2 (one 64-lane workgroup per sequence): merge every used row's chunk statistics (one lane
+// per row), then walk the proposals in order: the first rejection (speculative.py:25-29), or k_eff.
 template <int DT, bool PROBS>
-FS_DEVICE int decide(const AcceptArgs& A, int b, int ke, float T) {
+__global__ void __launch_bounds__(64) accept_decide_kernel(AcceptArgs A) {
+  const int b = blockIdx.x;
+  const int ke = keff_of(A, b);
+  const float T = PROBS ? 1.f : A.temps[b];
   const int per = A.rs.n0 + A.rs.n1;
+  if (!PROBS) {
+    for (int r = threadIdx.x; r < per; r += 64) {
+      const bool used = r < A.rs.n0 ? r <= ke : (r - A.rs.n0) < ke;
+      if (used) A.mstats[(int64_t)b * per + r] = merge_row(A.stats + ((int64_t)b * per + r) * A.nch, A.nch);
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x != 0) return;
+  int j = ke;
   for (int i = 0; i < ke; ++i) {
     const int x = A.draft[(int64_t)b * A.K + i];
-    if (x < 0 || x >= A.V) return i;  // an invalid proposal can never be accepted
-    float px, qx;
+    if (x < 0 || x >= A.V) { j = i; break; }  // an invalid proposal is never accepted
     const auto* pr = row_ptr<DT>(A.rs, b, i);
     const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + i);
+    float px, qx;
     if (PROBS) {
       px = Elem<DT>::load(pr, x);
       qx = Elem<DT>::load(qr, x);
     } else if (T > 0.f) {
-      const Stat sp = merge_row(A.stats + ((int64_t)b * per + i) * A.nch, A.nch);
-      const Stat sq = merge_row(A.stats + ((int64_t)b * per + A.rs.n0 + i) * A.nch, A.nch);
-      px = softmax_at(Elem<DT>::load(pr, x), T, sp);
-      qx = softmax_at(Elem<DT>::load(qr, x), T, sq);
+      px = softmax_at(Elem<DT>::load(pr, x), T, A.mstats[(int64_t)b * per + i]);
+      qx = softmax_at(Elem<DT>::load(qr, x), T, A.mstats[(int64_t)b * per + A.rs.n0 + i]);
     } else {  // one-hot rows of the first argmax (sampling.py:11-12)
-      px = merge_row(A.stats + ((int64_t)b * per + i) * A.nch, A.nch).ai == x ? 1.f : 0.f;
-      qx = merge_row(A.stats + ((int64_t)b * per + A.rs.n0 + i) * A.nch, A.nch).ai == x ? 1.f : 0.f;
+      px = A.mstats[(int64_t)b * per + i].ai == x ? 1.f : 0.f;
+      qx = A.mstats[(int64_t)b * per + A.rs.n0 + i].ai == x ? 1.f : 0.f;
     }
-    const float ratio = qx > 0.f ? Elem<DT>::round(px / qx) : 1.0f;
-    if (!(A.u[(int64_t)b * A.K + i] < fminf(1.0f, ratio))) return i;
+    const float ratio = qx > 0.f ? Elem<DT>::round(px / qx) : 1.0f;   // speculative.py:26
+    if (!(A.u[(int64_t)b * A.K + i] < fminf(1.0f, ratio))) { j = i; break; }
   }
-  return ke;
+  A.jpos[b] = j;
 }
 
-// launch 2: decision (recomputed by every chunk workgroup) + residual partial sums of the rejected row
+// launch 3: residual partial sums of the rejected row pair (speculative.py:30)
 template <int DT, bool PROBS>
 __global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) {
   __shared__ float shf[THREADS / 64];
-  __shared__ int shj;
-  __shared__ Stat shp, shq;
   const int c = blockIdx.x, b = blockIdx.y;
-  const int ke = A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K;
+  const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
-  const int per = A.rs.n0 + A.rs.n1;
-  if (threadIdx.x == 0) {
-    const int j = decide<DT, PROBS>(A, b, ke, T);
-    shj = j;
-    if (c == 0) A.jpos[b] = j;
-    if (!PROBS && j < ke && T > 0.f) {
-      shp = merge_row(A.stats + ((int64_t)b * per + j) * A.nch, A.nch);
-      shq = merge_row(A.stats + ((int64_t)b * per + A.rs.n0 + j) * A.nch, A.nch);
-    }
-  }
-  __syncthreads();
-  const int j = shj;
+  const int j = A.jpos[b];
   if (j >= ke || (!PROBS && T <= 0.f)) return;  // bonus token or greedy: no residual
-  const Stat sp = shp, sq = shq;
+  const int per = A.rs.n0 + A.rs.n1;
+  Stat sp{}, sq{};
+  if (!PROBS) {
+    sp = A.mstats[(int64_t)b * per + j];
+    sq = A.mstats[(int64_t)b * per + A.rs.n0 + j];
+  }
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + j);
   const bool vec_ok = (A.V % VEC) == 0 && (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr)) & 15) == 0);
@@ -353,39 +350,38 @@ __global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) 
       if (v0 + jj >= A.V) continue;
       const float p = PROBS ? xp[jj] : softmax_at(xp[jj], T, sp);
       const float q = PROBS ? xq[jj] : softmax_at(xq[jj], T, sq);
-      ls += fmaxf(Elem<DT>::round(p - q), 0.f);  // (p - q).clamp(min=0), speculative.py:30
+      ls += fmaxf(Elem<DT>::round(p - q), 0.f);  // (p - q).clamp(min=0)
     }
   }
   const float tot = block_sum(ls, shf);
   if (threadIdx.x == 0) A.resid[(int64_t)b * A.nch + c] = tot;
 }
 
-// launch 3: argmax over a chunk of w_v / E_v with w the normalised residual or the bonus row
+// launch 4: argmax over a chunk of w_v / E_v with w the normalised residual or the bonus row
 template <int DT, bool PROBS>
 __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
   __shared__ float shf[THREADS / 64];
   __shared__ int shi[THREADS / 64];
-  __shared__ Stat shp, shq;
   __shared__ float shs;
   const int c = blockIdx.x, b = blockIdx.y;
-  const int ke = A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K;
+  const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
   if (!PROBS && T <= 0.f) return;
   const int per = A.rs.n0 + A.rs.n1;
   const int j = A.jpos[b];
   const bool bonus = j >= ke;
   if (threadIdx.x == 0) {
-    if (!PROBS) {
-      shp = merge_row(A.stats + ((int64_t)b * per + j) * A.nch, A.nch);
-      if (!bonus) shq = merge_row(A.stats + ((int64_t)b * per + A.rs.n0 + j) * A.nch, A.nch);
-    }
     float s = 0.f;
     if (!bonus)
       for (int cc = 0; cc < A.nch; ++cc) s += A.resid[(int64_t)b * A.nch + cc];
     shs = Elem<DT>::round(s);
   }
   __syncthreads();
-  const Stat sp = shp, sq = shq;
+  Stat sp{}, sq{};
+  if (!PROBS) {
+    sp = A.mstats[(int64_t)b * per + j];
+    if (!bonus) sq = A.mstats[(int64_t)b * per + A.rs.n0 + j];
+  }
   const float s = shs;
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j);
@@ -424,19 +420,18 @@ __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
   }
 }
 
-// launch 4: outputs and the device-side rollback (one thread per sequence)
+// launch 5: outputs and the device-side rollback (one thread per sequence)
 template <int DT, bool PROBS>
 __global__ void accept_final_kernel(AcceptArgs A, int B, int32_t* __restrict__ out_tokens,
                                     int32_t* __restrict__ n_acc, int32_t* __restrict__ seq_len) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
-  const int ke = A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K;
   const float T = PROBS ? 1.f : A.temps[b];
   const int per = A.rs.n0 + A.rs.n1;
   const int j = A.jpos[b];
   int extra;
   if (!PROBS && T <= 0.f) {
-    extra = merge_row(A.stats + ((int64_t)b * per + j) * A.nch, A.nch).ai;  // argmax of target row j
+    extra = A.mstats[(int64_t)b * per + j].ai;  // argmax of target row j
   } else {
     float v = A.pv[(int64_t)b * A.nch];
     extra = A.pi[(int64_t)b * A.nch];
@@ -493,7 +488,8 @@ int64_t nchunks(int64_t V) { return (V + CH - 1) / CH; }
 int64_t accept_ws(int64_t B, int64_t K, int64_t V) {
   const int64_t nch = nchunks(V);
   auto r = [](int64_t n) { return ((n + 255) / 256) * 256; };
-  return r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) + 3 * r(B * nch * 4) + r(B * 4) + r(4);
+  return r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) + r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) +
+         3 * r(B * nch * 4) + r(B * 4) + r(4);
 }
 
 bool dtype_ok(int32_t dt) { return dt == FS_F32 || dt == FS_BF16 || dt == FS_F16; }
@@ -502,15 +498,18 @@ template <int DT>
 int launch_accept(const AcceptArgs& A, int B, bool probs, int32_t* out_tokens, int32_t* n_acc, int32_t* seq_len,
                   hipStream_t s) {
   const int per = A.rs.n0 + A.rs.n1;
+  const dim3 chunks((unsigned)A.nch, (unsigned)B);
   if (!probs) {
     stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(B * per)), THREADS, 0, s>>>(A.rs, A.V, A.nch, A.temps, 0.f,
-                                                                                  A.k_eff, const_cast<Stat*>(A.stats));
-    accept_residual_kernel<DT, false><<<dim3((unsigned)A.nch, (unsigned)B), THREADS, 0, s>>>(A);
-    accept_argmax_kernel<DT, false><<<dim3((unsigned)A.nch, (unsigned)B), THREADS, 0, s>>>(A);
+                                                                                  A.k_eff, A.stats);
+    accept_decide_kernel<DT, false><<<dim3((unsigned)B), 64, 0, s>>>(A);
+    accept_residual_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
+    accept_argmax_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
     accept_final_kernel<DT, false><<<dim3((unsigned)((B + 63) / 64)), 64, 0, s>>>(A, B, out_tokens, n_acc, seq_len);
   } else {
-    accept_residual_kernel<DT, true><<<dim3((unsigned)A.nch, (unsigned)B), THREADS, 0, s>>>(A);
-    accept_argmax_kernel<DT, true><<<dim3((unsigned)A.nch, (unsigned)B), THREADS, 0, s>>>(A);
+    accept_decide_kernel<DT, true><<<dim3((unsigned)B), 64, 0, s>>>(A);
+    accept_residual_kernel<DT, true><<<chunks, THREADS, 0, s>>>(A);
+    accept_argmax_kernel<DT, true><<<chunks, THREADS, 0, s>>>(A);
     accept_final_kernel<DT, true><<<dim3((unsigned)((B + 63) / 64)), 64, 0, s>>>(A, B, out_tokens, n_acc, seq_len);
   }
   return fs::launch_status("spec_accept");
@@ -627,6 +626,7 @@ extern "C" int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, c
   A.E = E;
   A.ldE = ldE;
   A.stats = cv.take<Stat>((int64_t)B * (2 * K + 1) * nch);
+  A.mstats = cv.take<Stat>((int64_t)B * (2 * K + 1));
   A.resid = cv.take<float>((int64_t)B * nch);
   A.pv = cv.take<float>((int64_t)B * nch);
   A.pi = cv.take<int>((int64_t)B * nch);
@@ -662,6 +662,7 @@ extern "C" int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_
   A.E = E;
   A.ldE = V;
   A.stats = cv.take<Stat>((int64_t)(2 * K + 1) * nch);
+  A.mstats = cv.take<Stat>((int64_t)(2 * K + 1));
   A.resid = cv.take<float>(nch);
   A.pv = cv.take<float>(nch);
   A.pi = cv.take<int>(nch);
