@@ -48,6 +48,7 @@ template <> struct Elem<FS_BF16> {
   static FS_DEVICE void store(T* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
   static FS_DEVICE float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
   static FS_DEVICE float to_f32(T v) { return bf16_to_f32(v); }
+  static FS_DEVICE T store_bits(float v) { return f32_to_bf16(v); }
 };
 template <> struct Elem<FS_F16> {
   typedef uint16_t T;

@@ -261,75 +261,87 @@ __global__ void sample_final_kernel(int R, int nch, const float* __restrict__ te
 // acceptance
 // ------------------------------------------------------------------------------------------------
 struct AcceptArgs {
-  RowSet rs;          // n0 = K+1 target rows, n1 = K draft rows
+  RowSet rs;             // n0 = K+1 target rows, n1 = K draft rows
   int32_t K;
   int64_t V;
   int nch;
+  int B;
   const int32_t* draft;  // [B, K]
   const int32_t* k_eff;  // [B] or null (= K)
   const float* temps;    // [B] (ignored for probabilities)
   const float* u;        // [B, K]
   const float* E;        // [B, V]
   int64_t ldE;
+  int32_t* counters;     // [2*B] chunk workgroups finished per sequence, per launch (zero between calls)
   Stat* stats;           // [B*(2K+1)][nch] chunk partials (logits mode)
   Stat* mstats;          // [B*(2K+1)] merged row statistics (logits mode)
-  float* resid;          // [B][nch]
+  float* rsum;           // [B] residual sum of the rejected row pair (rounded to the dtype)
   float* pv;             // [B][nch]
   int* pi;               // [B][nch]
   int* jpos;             // [B]
+  int32_t* out_tokens;   // [B, K+1]
+  int32_t* n_acc;        // [B]
+  int32_t* seq_len;      // [B] or null
 };
 
 FS_DEVICE int keff_of(const AcceptArgs& A, int b) { return A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K; }
 
-// launch 2 (one 64-lane workgroup per sequence): merge every used row's chunk statistics (one lane
-// per row), then walk the proposals in order: the first rejection (speculative.py:25-29), or k_eff.
+FS_DEVICE void write_outputs(const AcceptArgs& A, int b, int j, int extra) {
+  int32_t* o = A.out_tokens + (int64_t)b * (A.K + 1);
+  for (int i = 0; i < j; ++i) o[i] = A.draft[(int64_t)b * A.K + i];
+  o[j] = extra;
+  for (int i = j + 1; i <= A.K; ++i) o[i] = -1;
+  A.n_acc[b] = j;
+  if (A.seq_len) A.seq_len[b] = A.seq_len[b] + 1 + j;  // want = cached + 1 + len(accepted) (speculative.py:77)
+}
+
+// The per-sequence step between the two vocab-wide passes, run by one workgroup: merge the row
+// statistics (logits mode), walk the proposals (speculative.py:25-29), then either finish a greedy
+// sequence (the extra token is the argmax of target row j) or sum the residual of the rejected pair
+// (speculative.py:30-31) for the sampling pass.
 template <int DT, bool PROBS>
-__global__ void __launch_bounds__(64) accept_decide_kernel(AcceptArgs A) {
-  const int b = blockIdx.x;
+FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
+  __shared__ int sh_j;
+  __shared__ float shf[THREADS / 64];
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
   const int per = A.rs.n0 + A.rs.n1;
   if (!PROBS) {
-    for (int r = threadIdx.x; r < per; r += 64) {
+    for (int r = threadIdx.x; r < per; r += blockDim.x) {
       const bool used = r < A.rs.n0 ? r <= ke : (r - A.rs.n0) < ke;
       if (used) A.mstats[(int64_t)b * per + r] = merge_row(A.stats + ((int64_t)b * per + r) * A.nch, A.nch);
     }
+    __threadfence_block();
     __syncthreads();
   }
-  if (threadIdx.x != 0) return;
-  int j = ke;
-  for (int i = 0; i < ke; ++i) {
-    const int x = A.draft[(int64_t)b * A.K + i];
-    if (x < 0 || x >= A.V) { j = i; break; }  // an invalid proposal is never accepted
-    const auto* pr = row_ptr<DT>(A.rs, b, i);
-    const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + i);
-    float px, qx;
-    if (PROBS) {
-      px = Elem<DT>::load(pr, x);
-      qx = Elem<DT>::load(qr, x);
-    } else if (T > 0.f) {
-      px = softmax_at(Elem<DT>::load(pr, x), T, A.mstats[(int64_t)b * per + i]);
-      qx = softmax_at(Elem<DT>::load(qr, x), T, A.mstats[(int64_t)b * per + A.rs.n0 + i]);
-    } else {  // one-hot rows of the first argmax (sampling.py:11-12)
-      px = A.mstats[(int64_t)b * per + i].ai == x ? 1.f : 0.f;
-      qx = A.mstats[(int64_t)b * per + A.rs.n0 + i].ai == x ? 1.f : 0.f;
+  if (threadIdx.x == 0) {
+    int j = ke;
+    for (int i = 0; i < ke; ++i) {
+      const int x = A.draft[(int64_t)b * A.K + i];
+      if (x < 0 || x >= A.V) { j = i; break; }  // an invalid proposal is never accepted
+      const auto* pr = row_ptr<DT>(A.rs, b, i);
+      const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + i);
+      float px, qx;
+      if (PROBS) {
+        px = Elem<DT>::load(pr, x);
+        qx = Elem<DT>::load(qr, x);
+      } else if (T > 0.f) {
+        px = softmax_at(Elem<DT>::load(pr, x), T, A.mstats[(int64_t)b * per + i]);
+        qx = softmax_at(Elem<DT>::load(qr, x), T, A.mstats[(int64_t)b * per + A.rs.n0 + i]);
+      } else {  // one-hot rows of the first argmax (sampling.py:11-12)
+        px = A.mstats[(int64_t)b * per + i].ai == x ? 1.f : 0.f;
+        qx = A.mstats[(int64_t)b * per + A.rs.n0 + i].ai == x ? 1.f : 0.f;
+      }
+      const float ratio = qx > 0.f ? Elem<DT>::round(px / qx) : 1.0f;  // speculative.py:26
+      if (!(A.u[(int64_t)b * A.K + i] < fminf(1.0f, ratio))) { j = i; break; }
     }
-    const float ratio = qx > 0.f ? Elem<DT>::round(px / qx) : 1.0f;   // speculative.py:26
-    if (!(A.u[(int64_t)b * A.K + i] < fminf(1.0f, ratio))) { j = i; break; }
+    sh_j = j;
+    A.jpos[b] = j;
+    if (!PROBS && T <= 0.f) write_outputs(A, b, j, A.mstats[(int64_t)b * per + j].ai);
   }
-  A.jpos[b] = j;
-}
-
-// launch 3: residual partial sums of the rejected row pair (speculative.py:30)
-template <int DT, bool PROBS>
-__global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) {
-  __shared__ float shf[THREADS / 64];
-  const int c = blockIdx.x, b = blockIdx.y;
-  const int ke = keff_of(A, b);
-  const float T = PROBS ? 1.f : A.temps[b];
-  const int j = A.jpos[b];
-  if (j >= ke || (!PROBS && T <= 0.f)) return;  // bonus token or greedy: no residual
-  const int per = A.rs.n0 + A.rs.n1;
+  __syncthreads();
+  const int j = sh_j;
+  if ((!PROBS && T <= 0.f) || j >= ke) return;  // greedy (done) or bonus token (no residual)
   Stat sp{}, sq{};
   if (!PROBS) {
     sp = A.mstats[(int64_t)b * per + j];
@@ -339,9 +351,7 @@ __global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) 
   const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + j);
   const bool vec_ok = (A.V % VEC) == 0 && (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr)) & 15) == 0);
   float ls = 0.f;
-#pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+  for (int64_t v0 = (int64_t)threadIdx.x * VEC; v0 < A.V; v0 += (int64_t)blockDim.x * VEC) {
     float xp[8], xq[8];
     load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp);
     load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq);
@@ -354,35 +364,99 @@ __global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) 
     }
   }
   const float tot = block_sum(ls, shf);
-  if (threadIdx.x == 0) A.resid[(int64_t)b * A.nch + c] = tot;
+  if (threadIdx.x == 0) A.rsum[b] = Elem<DT>::round(tot);
 }
 
-// launch 4: argmax over a chunk of w_v / E_v with w the normalised residual or the bonus row
+// launch 1 (logits): per-(row, chunk) statistics; the last chunk workgroup of a sequence runs its step
+template <int DT>
+__global__ void __launch_bounds__(THREADS) accept_stats_kernel(AcceptArgs A) {
+  __shared__ float shf[THREADS / 64];
+  __shared__ int shi[THREADS / 64];
+  __shared__ int sh_last;
+  const int c = blockIdx.x;
+  const int rho = blockIdx.y;
+  const int per = A.rs.n0 + A.rs.n1;
+  const int b = rho / per, i = rho - b * per;
+  const int ke = keff_of(A, b);
+  if (i < A.rs.n0 ? i > ke : (i - A.rs.n0) >= ke) return;  // a row this sequence does not use
+  const float T = A.temps[b];
+  const auto* row = row_ptr<DT>(A.rs, b, i);
+  const bool vec_ok = (A.V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
+  float x[UNROLL][8];
+  float lmax = -INFINITY, amv = -INFINITY;
+  int ami = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+    load8<DT>(row, v0, A.V, vec_ok, -INFINITY, x[u]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (v0 + j < A.V) argmax_merge(amv, ami, x[u][j], (int)(v0 + j));
+  }
+  block_argmax(amv, ami, shf, shi);
+  Stat st;
+  st.av = amv;
+  st.ai = ami;
+  if (T > 0.f) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        x[u][j] = x[u][j] / T;
+        lmax = fmaxf(lmax, x[u][j]);
+      }
+    const float m = block_max(lmax, shf);
+    float ls = 0.f;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ls += (x[u][j] == -INFINITY) ? 0.f : expf(x[u][j] - m);
+    st.m = m;
+    st.s = block_sum(ls, shf);
+  } else {
+    st.m = amv;
+    st.s = 0.f;
+  }
+  if (threadIdx.x == 0) {
+    A.stats[(int64_t)rho * A.nch + c] = st;
+    __threadfence();  // release this chunk's statistics
+    const int needed = (2 * ke + 1) * A.nch;
+    const int prev = atomicAdd(&A.counters[b], 1);
+    sh_last = prev == needed - 1;
+  }
+  __syncthreads();
+  if (!sh_last) return;
+  __threadfence();  // acquire the other chunks' statistics
+  sequence_step<DT, false>(A, b);
+  if (threadIdx.x == 0) atomicExch(&A.counters[b], 0);
+}
+
+// launch 1 (probabilities): one workgroup per sequence runs its step
+template <int DT>
+__global__ void __launch_bounds__(THREADS) accept_probs_step_kernel(AcceptArgs A) {
+  sequence_step<DT, true>(A, blockIdx.x);
+}
+
+// launch 2: argmax over a chunk of w_v / E_v (w the normalised residual, or the bonus row); the last
+// chunk workgroup of a sequence merges the chunk winners and writes the outputs.
 template <int DT, bool PROBS>
 __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
   __shared__ float shf[THREADS / 64];
   __shared__ int shi[THREADS / 64];
-  __shared__ float shs;
+  __shared__ int sh_last;
   const int c = blockIdx.x, b = blockIdx.y;
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
-  if (!PROBS && T <= 0.f) return;
+  if (!PROBS && T <= 0.f) return;  // greedy sequences were finished by launch 1
   const int per = A.rs.n0 + A.rs.n1;
   const int j = A.jpos[b];
   const bool bonus = j >= ke;
-  if (threadIdx.x == 0) {
-    float s = 0.f;
-    if (!bonus)
-      for (int cc = 0; cc < A.nch; ++cc) s += A.resid[(int64_t)b * A.nch + cc];
-    shs = Elem<DT>::round(s);
-  }
-  __syncthreads();
   Stat sp{}, sq{};
   if (!PROBS) {
     sp = A.mstats[(int64_t)b * per + j];
     if (!bonus) sq = A.mstats[(int64_t)b * per + A.rs.n0 + j];
   }
-  const float s = shs;
+  const float s = bonus ? 0.f : A.rsum[b];
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j);
   const float* er = A.E + (int64_t)b * A.ldE;
@@ -417,32 +491,18 @@ __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
   if (threadIdx.x == 0) {
     A.pv[(int64_t)b * A.nch + c] = bv;
     A.pi[(int64_t)b * A.nch + c] = bi;
+    __threadfence();
+    const int prev = atomicAdd(&A.counters[A.B + b], 1);
+    sh_last = prev == A.nch - 1;
   }
-}
-
-// launch 5: outputs and the device-side rollback (one thread per sequence)
-template <int DT, bool PROBS>
-__global__ void accept_final_kernel(AcceptArgs A, int B, int32_t* __restrict__ out_tokens,
-                                    int32_t* __restrict__ n_acc, int32_t* __restrict__ seq_len) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= B) return;
-  const float T = PROBS ? 1.f : A.temps[b];
-  const int per = A.rs.n0 + A.rs.n1;
-  const int j = A.jpos[b];
-  int extra;
-  if (!PROBS && T <= 0.f) {
-    extra = A.mstats[(int64_t)b * per + j].ai;  // argmax of target row j
-  } else {
-    float v = A.pv[(int64_t)b * A.nch];
-    extra = A.pi[(int64_t)b * A.nch];
-    for (int c = 1; c < A.nch; ++c) argmax_merge(v, extra, A.pv[(int64_t)b * A.nch + c], A.pi[(int64_t)b * A.nch + c]);
-  }
-  int32_t* o = out_tokens + (int64_t)b * (A.K + 1);
-  for (int i = 0; i < j; ++i) o[i] = A.draft[(int64_t)b * A.K + i];
-  o[j] = extra;
-  for (int i = j + 1; i <= A.K; ++i) o[i] = -1;
-  n_acc[b] = j;
-  if (seq_len) seq_len[b] = seq_len[b] + 1 + j;  // want = cached + 1 + len(accepted)
+  __syncthreads();
+  if (!sh_last || threadIdx.x != 0) return;
+  __threadfence();
+  float v = A.pv[(int64_t)b * A.nch];
+  int extra = A.pi[(int64_t)b * A.nch];
+  for (int cc = 1; cc < A.nch; ++cc) argmax_merge(v, extra, A.pv[(int64_t)b * A.nch + cc], A.pi[(int64_t)b * A.nch + cc]);
+  write_outputs(A, b, j, extra);
+  atomicExch(&A.counters[A.B + b], 0);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -485,32 +545,40 @@ struct Carve {
 
 int64_t nchunks(int64_t V) { return (V + CH - 1) / CH; }
 
+constexpr int64_t ACCEPT_COUNTER_BYTES = 2 * 65535 * 4 + 8;   // two counters per sequence, B <= 65535
+
 int64_t accept_ws(int64_t B, int64_t K, int64_t V) {
   const int64_t nch = nchunks(V);
   auto r = [](int64_t n) { return ((n + 255) / 256) * 256; };
-  return r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) + r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) +
-         3 * r(B * nch * 4) + r(B * 4) + r(4);
+  return ACCEPT_COUNTER_BYTES + r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) +
+         r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) + 2 * r(B * nch * 4) + 2 * r(B * 4);
+}
+
+// Carve the acceptance workspace: a fixed counter region first (the part that must be zero between
+// calls; fixed so that a later call never reads another call's data as counters).
+void carve_accept(AcceptArgs& A, void* workspace, int64_t B, int64_t K, int nch) {
+  Carve cv{reinterpret_cast<char*>(workspace)};
+  A.counters = cv.take<int32_t>(ACCEPT_COUNTER_BYTES / 4);
+  A.stats = cv.take<Stat>(B * (2 * K + 1) * nch);
+  A.mstats = cv.take<Stat>(B * (2 * K + 1));
+  A.pv = cv.take<float>(B * nch);
+  A.pi = cv.take<int>(B * nch);
+  A.rsum = cv.take<float>(B);
+  A.jpos = cv.take<int>(B);
 }
 
 bool dtype_ok(int32_t dt) { return dt == FS_F32 || dt == FS_BF16 || dt == FS_F16; }
 
 template <int DT>
-int launch_accept(const AcceptArgs& A, int B, bool probs, int32_t* out_tokens, int32_t* n_acc, int32_t* seq_len,
-                  hipStream_t s) {
+int launch_accept(const AcceptArgs& A, bool probs, hipStream_t s) {
   const int per = A.rs.n0 + A.rs.n1;
-  const dim3 chunks((unsigned)A.nch, (unsigned)B);
+  const dim3 chunks((unsigned)A.nch, (unsigned)A.B);
   if (!probs) {
-    stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(B * per)), THREADS, 0, s>>>(A.rs, A.V, A.nch, A.temps, 0.f,
-                                                                                  A.k_eff, A.stats);
-    accept_decide_kernel<DT, false><<<dim3((unsigned)B), 64, 0, s>>>(A);
-    accept_residual_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
+    accept_stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(A.B * per)), THREADS, 0, s>>>(A);
     accept_argmax_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
-    accept_final_kernel<DT, false><<<dim3((unsigned)((B + 63) / 64)), 64, 0, s>>>(A, B, out_tokens, n_acc, seq_len);
   } else {
-    accept_decide_kernel<DT, true><<<dim3((unsigned)B), 64, 0, s>>>(A);
-    accept_residual_kernel<DT, true><<<chunks, THREADS, 0, s>>>(A);
+    accept_probs_step_kernel<DT><<<dim3((unsigned)A.B), THREADS, 0, s>>>(A);
     accept_argmax_kernel<DT, true><<<chunks, THREADS, 0, s>>>(A);
-    accept_final_kernel<DT, true><<<dim3((unsigned)((B + 63) / 64)), 64, 0, s>>>(A, B, out_tokens, n_acc, seq_len);
   }
   return fs::launch_status("spec_accept");
 }
@@ -613,29 +681,27 @@ extern "C" int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, c
   FS_CHECK_ARG(workspace_bytes >= accept_ws(B, K, V), "spec_accept: workspace %lld < %lld", (long long)workspace_bytes,
                (long long)accept_ws(B, K, V));
   const int nch = (int)nchunks(V);
-  Carve cv{reinterpret_cast<char*>(workspace)};
   AcceptArgs A;
   A.rs = RowSet{tgt, tgt_sb, tgt_si, K + 1, dft ? dft : tgt, dft_sb, dft_si, K};
   A.K = K;
   A.V = V;
   A.nch = nch;
+  A.B = B;
   A.draft = draft_tokens;
   A.k_eff = k_eff;
   A.temps = temperature;
   A.u = u;
   A.E = E;
   A.ldE = ldE;
-  A.stats = cv.take<Stat>((int64_t)B * (2 * K + 1) * nch);
-  A.mstats = cv.take<Stat>((int64_t)B * (2 * K + 1));
-  A.resid = cv.take<float>((int64_t)B * nch);
-  A.pv = cv.take<float>((int64_t)B * nch);
-  A.pi = cv.take<int>((int64_t)B * nch);
-  A.jpos = cv.take<int>(B);
+  A.out_tokens = out_tokens;
+  A.n_acc = n_accepted;
+  A.seq_len = seq_len;
+  carve_accept(A, workspace, B, K, nch);
   hipStream_t s = fs::as_stream(stream);
   switch (dtype) {
-    case FS_F32: return launch_accept<FS_F32>(A, B, false, out_tokens, n_accepted, seq_len, s);
-    case FS_BF16: return launch_accept<FS_BF16>(A, B, false, out_tokens, n_accepted, seq_len, s);
-    default: return launch_accept<FS_F16>(A, B, false, out_tokens, n_accepted, seq_len, s);
+    case FS_F32: return launch_accept<FS_F32>(A, false, s);
+    case FS_BF16: return launch_accept<FS_BF16>(A, false, s);
+    default: return launch_accept<FS_F16>(A, false, s);
   }
 }
 
@@ -649,28 +715,26 @@ extern "C" int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_
   FS_CHECK_ARG(K >= 0 && V > 0 && V < 0x7fffffff, "verify_probs: K %d V %lld", K, (long long)V);
   FS_CHECK_ARG(workspace_bytes >= accept_ws(1, K, V), "verify_probs: workspace too small");
   const int nch = (int)nchunks(V);
-  Carve cv{reinterpret_cast<char*>(workspace)};
   AcceptArgs A;
   A.rs = RowSet{p, 0, ldp, K + 1, q ? q : p, 0, ldq, K};
   A.K = K;
   A.V = V;
   A.nch = nch;
+  A.B = 1;
   A.draft = draft_tokens;
   A.k_eff = nullptr;
   A.temps = nullptr;
   A.u = u;
   A.E = E;
   A.ldE = V;
-  A.stats = cv.take<Stat>((int64_t)(2 * K + 1) * nch);
-  A.mstats = cv.take<Stat>((int64_t)(2 * K + 1));
-  A.resid = cv.take<float>(nch);
-  A.pv = cv.take<float>(nch);
-  A.pi = cv.take<int>(nch);
-  A.jpos = cv.take<int>(1);
+  A.out_tokens = out_tokens;
+  A.n_acc = n_accepted;
+  A.seq_len = nullptr;
+  carve_accept(A, workspace, 1, K, nch);
   hipStream_t s = fs::as_stream(stream);
   switch (dtype) {
-    case FS_F32: return launch_accept<FS_F32>(A, 1, true, out_tokens, n_accepted, nullptr, s);
-    case FS_BF16: return launch_accept<FS_BF16>(A, 1, true, out_tokens, n_accepted, nullptr, s);
-    default: return launch_accept<FS_F16>(A, 1, true, out_tokens, n_accepted, nullptr, s);
+    case FS_F32: return launch_accept<FS_F32>(A, true, s);
+    case FS_BF16: return launch_accept<FS_BF16>(A, true, s);
+    default: return launch_accept<FS_F16>(A, true, s);
   }
 }

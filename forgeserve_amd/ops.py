@@ -31,6 +31,21 @@ def _ws(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
+_PERSISTENT = {}
+
+
+def _persistent_ws(name: str, nbytes: int, device) -> torch.Tensor:
+    """A per-device workspace for kernels that chain their launches with counters: zero-filled when
+    allocated; every call leaves the counters at zero again, so it is reused without clearing.
+    Calls are stream-ordered on torch's current stream, so consecutive calls never overlap."""
+    key = (name, torch.device(device))
+    ws = _PERSISTENT.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(int(nbytes * 1.25), 1 << 20), dtype=torch.uint8, device=key[1])
+        _PERSISTENT[key] = ws
+    return ws
+
+
 def _rows(t: torch.Tensor) -> Tuple[int, int]:
     """(rows, row stride) of a 2-D tensor whose last dim is contiguous."""
     if t.dim() != 2 or (t.stride(1) != 1 and t.shape[1] > 1):
@@ -190,7 +205,7 @@ def paged_attention(q: torch.Tensor, layout: KVLayout, tables: torch.Tensor, pos
     nb = tables.shape[1]
     lib = _lib.load()
     need = lib.fs_paged_attention_workspace_size(b, t, h, d, nb, layout.block_size)
-    ws = _ws(need, q.device)
+    ws = _persistent_ws("attention", need, q.device)
     timing = ATTN_EVENTS is not None and t == ATTN_EVENT_T
     if timing:
         ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -297,7 +312,7 @@ def spec_accept(tgt: torch.Tensor, dft: torch.Tensor, draft_tokens: torch.Tensor
     if n_accepted is None:
         n_accepted = torch.empty((b,), dtype=I32, device=tgt.device)
     lib = _lib.load()
-    ws = _ws(lib.fs_spec_accept_workspace_size(b, k, v), tgt.device)
+    ws = _persistent_ws("accept", lib.fs_spec_accept_workspace_size(b, k, v), tgt.device)
     check(lib.fs_spec_accept(ptr(tgt), tgt.stride(0), tgt.stride(1), ptr(dft), dft.stride(0), dft.stride(1) if k else 0,
                              b, k, v, _dt(tgt), ptr(draft_tokens), ptr(k_eff), ptr(temperature), ptr(u), ptr(noise),
                              noise.stride(0), ptr(out_tokens), ptr(n_accepted), ptr(seq_len), ptr(ws), ws.numel(),
@@ -318,7 +333,7 @@ def verify_probs(p: torch.Tensor, q: torch.Tensor, draft_tokens: torch.Tensor, u
     out = torch.empty((k + 1,), dtype=I32, device=p.device)
     n = torch.empty((1,), dtype=I32, device=p.device)
     lib = _lib.load()
-    ws = _ws(lib.fs_spec_accept_workspace_size(1, k, v), p.device)
+    ws = _persistent_ws("accept", lib.fs_spec_accept_workspace_size(1, k, v), p.device)
     check(lib.fs_verify_probs(ptr(p), p.stride(0), ptr(q), q.stride(0) if k else 0, k, v, _dt(p),
                               ptr(draft_tokens.contiguous()), ptr(u.contiguous()), ptr(noise.contiguous()), ptr(out),
                               ptr(n), ptr(ws), ws.numel(), stream_ptr()), "verify_probs")
