@@ -5,7 +5,7 @@
 // key_pos <= query_pos mask, scaled_dot_product_attention with scale 1/sqrt(D)).
 //
 // Work split (both kernels): the keys of a row are cut into fixed chunks of `split` absolute positions
-// (256 unless FS_ATTN_SPLIT says otherwise; fixed for the life of the process); chunk s covers keys
+// (512 unless FS_ATTN_SPLIT says otherwise; fixed for the life of the process); chunk s covers keys
 // [s*split, (s+1)*split). Each workgroup produces the softmax partial
 // (running max m, sum l, unnormalised output acc) of its chunk, and attn_combine merges the chunks of
 // a query in increasing chunk order. A query at position p only ever reads the chunks that hold
@@ -42,10 +42,6 @@ struct AttnParams {
   float scale_log2;                  // scale * log2(e): scores are kept in the log2 domain
   float* ws_acc;                     // [B*T*H][nsplit][D]
   float* ws_ml;                      // [B*T*H][nsplit][2]
-  int32_t* counters;                 // [B*Hkv*qtiles] chunks finished per group (zero between calls)
-  void* out;                         // output [B, T, H, D] (strides o_sb, o_st, o_sh)
-  int64_t o_sb, o_st, o_sh;
-  int32_t qtiles;
   int32_t nsplit;
   int32_t split;                     // keys per chunk: a multiple of 16, at most 512
 };
@@ -265,43 +261,6 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) at
     }
   }
 
-  // The last chunk of this (row, kv head, query tile) group to finish merges the group's partials.
-  __threadfence();  // release this chunk's partials
-  const int grp = (b * Hkv + hkv) * P.qtiles + blockIdx.z;
-  int prev = 0;
-  if (lane == 0) prev = atomicAdd(&P.counters[grp], 1);
-  prev = __shfl(prev, 0, 64);
-  const int needed = min(qmax / P.split + 1, P.nsplit);  // chunks holding keys <= qmax: all of them run
-  if (prev != needed - 1) return;
-  __threadfence();  // acquire the other chunks' partials
-  typedef Elem<FS_BF16> E;
-  for (int r = 0; r < nrows; ++r) {
-    const int rr = row0 + r;
-    const int t = rr / P.G, h = hkv * P.G + (rr - t * P.G);
-    const int pos = posb[t];
-    u16* orow = reinterpret_cast<u16*>(P.out) + (int64_t)b * P.o_sb + (int64_t)t * P.o_st + (int64_t)h * P.o_sh;
-    if (pos < 0) {
-      for (int d = lane; d < D; d += 64) orow[d] = 0;
-      continue;
-    }
-    const int ns = min(pos / P.split + 1, P.nsplit);
-    const int64_t R = row_index(P, b, t, h);
-    const float* ml = P.ws_ml + R * P.nsplit * 2;
-    const float* pa = P.ws_acc + R * P.nsplit * D;
-    float M = -INFINITY;
-    for (int c = 0; c < ns; ++c) M = fmaxf(M, ml[2 * c]);
-    float L = 0.f, a0 = 0.f, a1 = 0.f;
-    for (int c = 0; c < ns; ++c) {
-      const float mc = ml[2 * c];
-      const float w = (mc == -INFINITY) ? 0.f : exp2f(mc - M);
-      L += w * ml[2 * c + 1];
-      a0 += w * pa[(int64_t)c * D + lane];
-      if (D > 64) a1 += w * pa[(int64_t)c * D + 64 + lane];
-    }
-    orow[lane] = E::store_bits(L > 0.f ? a0 / L : 0.f);
-    if (D > 64) orow[64 + lane] = E::store_bits(L > 0.f ? a1 / L : 0.f);
-  }
-  if (lane == 0) atomicExch(&P.counters[grp], 0);  // leave the counter at zero for the next call
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -444,18 +403,12 @@ bool mfma_eligible(const fs_kv_layout& kv, const void* q, int64_t q_sb, int64_t 
 int attn_split() {
   static const int split = [] {
     const char* e = getenv("FS_ATTN_SPLIT");
-    int v = e ? atoi(e) : 256;
-    if (v < 16 || v > 512 || v % 16) v = 256;  // a chunk's block list must fit one wavefront
+    int v = e ? atoi(e) : 512;
+    if (v < 16 || v > 512 || v % 16) v = 512;  // a chunk's block list must fit one wavefront
     return v;
   }();
   return split;
 }
-
-// Group counters live in a fixed region at the start of every workspace, whatever the call's shape,
-// so counters are never laid over another call's partial sums: one int per (row, kv head, 32-row
-// query tile), at most MAX_GROUPS groups per call.
-constexpr int64_t MAX_GROUPS = 262144;
-int64_t counters_bytes(int32_t, int32_t, int32_t) { return MAX_GROUPS * 4; }
 
 int64_t nsplit_for(int32_t max_blocks, int32_t block_size) {
   const int64_t S = (int64_t)max_blocks * block_size;
@@ -469,7 +422,7 @@ extern "C" int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32
   if (B <= 0 || T <= 0 || n_heads <= 0 || head_dim <= 0 || max_blocks <= 0 || block_size <= 0) return 0;
   const int64_t rows = (int64_t)B * T * n_heads;
   const int64_t ns = nsplit_for(max_blocks, block_size);
-  return counters_bytes(B, T, n_heads) + rows * ns * (head_dim + 2) * (int64_t)sizeof(float) + 256;
+  return rows * ns * (head_dim + 2) * (int64_t)sizeof(float) + 256;
 }
 
 extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
@@ -511,21 +464,12 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
   P.nsplit = (int32_t)nsplit_for(max_blocks, kv->block_size);
   P.split = attn_split();
   const int64_t rows = (int64_t)B * T * n_heads;
-  P.counters = reinterpret_cast<int32_t*>(workspace);
-  P.ws_acc = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + counters_bytes(B, T, n_heads));
+  P.ws_acc = reinterpret_cast<float*>(workspace);
   P.ws_ml = P.ws_acc + rows * P.nsplit * kv->head_dim;
-  P.out = out;
-  P.o_sb = o_sb;
-  P.o_st = o_st;
-  P.o_sh = o_sh;
-  P.qtiles = (T * P.G + QTILE - 1) / QTILE;
 
   hipStream_t st = fs::as_stream(stream);
   if (mfma_eligible(*kv, q, q_sb, q_st, q_sh)) {
     const int qtiles = (T * P.G + QTILE - 1) / QTILE;
-    FS_CHECK_ARG((int64_t)B * kv->n_kv_heads * qtiles <= MAX_GROUPS,
-                 "paged_attention: %lld (row, kv head, query tile) groups exceed %lld per call",
-                 (long long)B * kv->n_kv_heads * qtiles, (long long)MAX_GROUPS);
     dim3 grid((unsigned)(P.nsplit * kv->n_kv_heads), (unsigned)B, (unsigned)qtiles);
     const bool bs16 = kv->block_size == 16;
     if (kv->head_dim == 128) {
@@ -535,7 +479,6 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
       if (bs16) attn_mfma_bf16_kernel<64, 16><<<grid, 64, 0, st>>>(P);
       else attn_mfma_bf16_kernel<64, 0><<<grid, 64, 0, st>>>(P);
     }
-    return fs::launch_status("paged_attention");  // the combine runs inside the kernel
   } else {
     dim3 grid((unsigned)rows, (unsigned)P.nsplit);
     switch (kv->dtype) {

@@ -19,8 +19,8 @@ namespace {
 
 constexpr int THREADS = 256;
 constexpr int VEC = 8;                       // consecutive columns per thread group
-constexpr int UNROLL = 2;                    // groups per thread per chunk
-constexpr int CH = THREADS * VEC * UNROLL;   // 4096 columns per chunk
+constexpr int UNROLL = 8;                    // groups per thread per chunk: 8 16-byte loads in flight
+constexpr int CH = THREADS * VEC * UNROLL;   // 16384 columns per chunk
 
 struct Stat {
   float m;    // max of x/T (T > 0) or of x (T == 0)
@@ -137,6 +137,51 @@ FS_DEVICE Stat merge_row(const Stat* st, int nch) {
 // p_v of a row from logits and merged stats (T > 0): softmax(f32(x) / T) (sampling.py:13).
 FS_DEVICE float softmax_at(float x, float T, const Stat& st) { return expf(x / T - st.m) / st.s; }
 
+// One chunk of one row: first argmax of x and, for T > 0, (m, s) = (max of x/T, sum of exp(x/T - m)),
+// accumulated online per thread (each element enters once, in increasing column order per thread)
+// and merged across the workgroup in a fixed order. All loads of the chunk are issued up front.
+template <int DT>
+FS_DEVICE Stat chunk_stat(const typename Elem<DT>::T* row, int c, int64_t V, float T, float* shf, int* shi) {
+  const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
+  float x[UNROLL][8];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u)
+    load8<DT>(row, (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC, V, vec_ok, -INFINITY, x[u]);
+  float amv = -INFINITY, m = -INFINITY, sum = 0.f;
+  int ami = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (v0 + j >= V) continue;
+      argmax_merge(amv, ami, x[u][j], (int)(v0 + j));
+      if (T > 0.f) {
+        const float y = x[u][j] / T;
+        if (y > m) {
+          sum = (m == -INFINITY ? 0.f : sum * expf(m - y)) + 1.f;
+          m = y;
+        } else if (y != -INFINITY) {
+          sum += expf(y - m);
+        }
+      }
+    }
+  }
+  block_argmax(amv, ami, shf, shi);
+  Stat st;
+  st.av = amv;
+  st.ai = ami;
+  if (T > 0.f) {
+    const float M = block_max(m, shf);
+    st.m = M;
+    st.s = block_sum(m == -INFINITY ? 0.f : sum * expf(m - M), shf);
+  } else {
+    st.m = amv;
+    st.s = 0.f;
+  }
+  return st;
+}
+
 // ------------------------------------------------------------------------------------------------
 // launch 1: per-(row, chunk) statistics
 // ------------------------------------------------------------------------------------------------
@@ -156,43 +201,7 @@ __global__ void __launch_bounds__(THREADS) stats_kernel(RowSet rs, int64_t V, in
   }
   const float T = temps ? temps[b] : t_all;
   const auto* row = row_ptr<DT>(rs, b, i);
-  const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
-  float x[UNROLL][8];
-  float lmax = -INFINITY, amv = -INFINITY;
-  int ami = 0x7fffffff;
-#pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
-    load8<DT>(row, v0, V, vec_ok, -INFINITY, x[u]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (v0 + j < V) argmax_merge(amv, ami, x[u][j], (int)(v0 + j));
-    }
-  }
-  block_argmax(amv, ami, shf, shi);
-  Stat st;
-  st.av = amv;
-  st.ai = ami;
-  if (T > 0.f) {
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        x[u][j] = x[u][j] / T;  // -inf padding stays -inf
-        lmax = fmaxf(lmax, x[u][j]);
-      }
-    const float m = block_max(lmax, shf);
-    float ls = 0.f;
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ls += (x[u][j] == -INFINITY) ? 0.f : expf(x[u][j] - m);
-    st.m = m;
-    st.s = block_sum(ls, shf);
-  } else {
-    st.m = amv;
-    st.s = 0.f;
-  }
+  const Stat st = chunk_stat<DT>(row, c, V, T, shf, shi);
   if (threadIdx.x == 0) out[(int64_t)rho * nch + c] = st;
 }
 
@@ -272,10 +281,9 @@ struct AcceptArgs {
   const float* u;        // [B, K]
   const float* E;        // [B, V]
   int64_t ldE;
-  int32_t* counters;     // [2*B] chunk workgroups finished per sequence, per launch (zero between calls)
   Stat* stats;           // [B*(2K+1)][nch] chunk partials (logits mode)
   Stat* mstats;          // [B*(2K+1)] merged row statistics (logits mode)
-  float* rsum;           // [B] residual sum of the rejected row pair (rounded to the dtype)
+  float* resid;          // [B][nch] residual partial sums of the rejected row pair
   float* pv;             // [B][nch]
   int* pi;               // [B][nch]
   int* jpos;             // [B]
@@ -295,14 +303,11 @@ FS_DEVICE void write_outputs(const AcceptArgs& A, int b, int j, int extra) {
   if (A.seq_len) A.seq_len[b] = A.seq_len[b] + 1 + j;  // want = cached + 1 + len(accepted) (speculative.py:77)
 }
 
-// The per-sequence step between the two vocab-wide passes, run by one workgroup: merge the row
-// statistics (logits mode), walk the proposals (speculative.py:25-29), then either finish a greedy
-// sequence (the extra token is the argmax of target row j) or sum the residual of the rejected pair
-// (speculative.py:30-31) for the sampling pass.
+// launch 2, one workgroup per sequence: merge the row statistics (logits mode, one lane per row),
+// walk the proposals (speculative.py:25-29) and finish a greedy sequence (the extra token is the
+// argmax of target row j).
 template <int DT, bool PROBS>
 FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
-  __shared__ int sh_j;
-  __shared__ float shf[THREADS / 64];
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
   const int per = A.rs.n0 + A.rs.n1;
@@ -335,13 +340,21 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
       const float ratio = qx > 0.f ? Elem<DT>::round(px / qx) : 1.0f;  // speculative.py:26
       if (!(A.u[(int64_t)b * A.K + i] < fminf(1.0f, ratio))) { j = i; break; }
     }
-    sh_j = j;
     A.jpos[b] = j;
     if (!PROBS && T <= 0.f) write_outputs(A, b, j, A.mstats[(int64_t)b * per + j].ai);
   }
-  __syncthreads();
-  const int j = sh_j;
+}
+
+// launch 3: residual partial sums of the rejected row pair (speculative.py:30), one chunk each
+template <int DT, bool PROBS>
+__global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) {
+  __shared__ float shf[THREADS / 64];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int ke = keff_of(A, b);
+  const float T = PROBS ? 1.f : A.temps[b];
+  const int j = A.jpos[b];
   if ((!PROBS && T <= 0.f) || j >= ke) return;  // greedy (done) or bonus token (no residual)
+  const int per = A.rs.n0 + A.rs.n1;
   Stat sp{}, sq{};
   if (!PROBS) {
     sp = A.mstats[(int64_t)b * per + j];
@@ -350,29 +363,34 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + j);
   const bool vec_ok = (A.V % VEC) == 0 && (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr)) & 15) == 0);
+  float xp[UNROLL][8], xq[UNROLL][8];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+    load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp[u]);
+    load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq[u]);
+  }
   float ls = 0.f;
-  for (int64_t v0 = (int64_t)threadIdx.x * VEC; v0 < A.V; v0 += (int64_t)blockDim.x * VEC) {
-    float xp[8], xq[8];
-    load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp);
-    load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq);
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
       if (v0 + jj >= A.V) continue;
-      const float p = PROBS ? xp[jj] : softmax_at(xp[jj], T, sp);
-      const float q = PROBS ? xq[jj] : softmax_at(xq[jj], T, sq);
+      const float p = PROBS ? xp[u][jj] : softmax_at(xp[u][jj], T, sp);
+      const float q = PROBS ? xq[u][jj] : softmax_at(xq[u][jj], T, sq);
       ls += fmaxf(Elem<DT>::round(p - q), 0.f);  // (p - q).clamp(min=0)
     }
   }
   const float tot = block_sum(ls, shf);
-  if (threadIdx.x == 0) A.rsum[b] = Elem<DT>::round(tot);
+  if (threadIdx.x == 0) A.resid[(int64_t)b * A.nch + c] = tot;
 }
 
-// launch 1 (logits): per-(row, chunk) statistics; the last chunk workgroup of a sequence runs its step
+// launch 1 (logits): per-(row, chunk) statistics of every row a sequence uses
 template <int DT>
 __global__ void __launch_bounds__(THREADS) accept_stats_kernel(AcceptArgs A) {
   __shared__ float shf[THREADS / 64];
   __shared__ int shi[THREADS / 64];
-  __shared__ int sh_last;
   const int c = blockIdx.x;
   const int rho = blockIdx.y;
   const int per = A.rs.n0 + A.rs.n1;
@@ -381,73 +399,25 @@ __global__ void __launch_bounds__(THREADS) accept_stats_kernel(AcceptArgs A) {
   if (i < A.rs.n0 ? i > ke : (i - A.rs.n0) >= ke) return;  // a row this sequence does not use
   const float T = A.temps[b];
   const auto* row = row_ptr<DT>(A.rs, b, i);
-  const bool vec_ok = (A.V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
-  float x[UNROLL][8];
-  float lmax = -INFINITY, amv = -INFINITY;
-  int ami = 0x7fffffff;
-#pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
-    load8<DT>(row, v0, A.V, vec_ok, -INFINITY, x[u]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (v0 + j < A.V) argmax_merge(amv, ami, x[u][j], (int)(v0 + j));
-  }
-  block_argmax(amv, ami, shf, shi);
-  Stat st;
-  st.av = amv;
-  st.ai = ami;
-  if (T > 0.f) {
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        x[u][j] = x[u][j] / T;
-        lmax = fmaxf(lmax, x[u][j]);
-      }
-    const float m = block_max(lmax, shf);
-    float ls = 0.f;
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ls += (x[u][j] == -INFINITY) ? 0.f : expf(x[u][j] - m);
-    st.m = m;
-    st.s = block_sum(ls, shf);
-  } else {
-    st.m = amv;
-    st.s = 0.f;
-  }
-  if (threadIdx.x == 0) {
-    A.stats[(int64_t)rho * A.nch + c] = st;
-    __threadfence();  // release this chunk's statistics
-    const int needed = (2 * ke + 1) * A.nch;
-    const int prev = atomicAdd(&A.counters[b], 1);
-    sh_last = prev == needed - 1;
-  }
-  __syncthreads();
-  if (!sh_last) return;
-  __threadfence();  // acquire the other chunks' statistics
-  sequence_step<DT, false>(A, b);
-  if (threadIdx.x == 0) atomicExch(&A.counters[b], 0);
+  const Stat st = chunk_stat<DT>(row, c, A.V, T, shf, shi);
+  if (threadIdx.x == 0) A.stats[(int64_t)rho * A.nch + c] = st;
 }
 
-// launch 1 (probabilities): one workgroup per sequence runs its step
-template <int DT>
-__global__ void __launch_bounds__(THREADS) accept_probs_step_kernel(AcceptArgs A) {
-  sequence_step<DT, true>(A, blockIdx.x);
+// launch 2: one workgroup per sequence runs its step (logits or probabilities)
+template <int DT, bool PROBS>
+__global__ void __launch_bounds__(64) accept_step_kernel(AcceptArgs A) {
+  sequence_step<DT, PROBS>(A, blockIdx.x);
 }
 
-// launch 2: argmax over a chunk of w_v / E_v (w the normalised residual, or the bonus row); the last
-// chunk workgroup of a sequence merges the chunk winners and writes the outputs.
+// launch 4: argmax over a chunk of w_v / E_v (w the normalised residual, or the bonus row)
 template <int DT, bool PROBS>
 __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
   __shared__ float shf[THREADS / 64];
   __shared__ int shi[THREADS / 64];
-  __shared__ int sh_last;
   const int c = blockIdx.x, b = blockIdx.y;
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
-  if (!PROBS && T <= 0.f) return;  // greedy sequences were finished by launch 1
+  if (!PROBS && T <= 0.f) return;  // greedy sequences were finished by the step
   const int per = A.rs.n0 + A.rs.n1;
   const int j = A.jpos[b];
   const bool bonus = j >= ke;
@@ -456,7 +426,10 @@ __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
     sp = A.mstats[(int64_t)b * per + j];
     if (!bonus) sq = A.mstats[(int64_t)b * per + A.rs.n0 + j];
   }
-  const float s = bonus ? 0.f : A.rsum[b];
+  float s = 0.f;  // the residual sum, merged in chunk order (every workgroup merges the same way)
+  if (!bonus)
+    for (int cc = 0; cc < A.nch; ++cc) s += A.resid[(int64_t)b * A.nch + cc];
+  s = Elem<DT>::round(s);
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j);
   const float* er = A.E + (int64_t)b * A.ldE;
@@ -491,18 +464,19 @@ __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
   if (threadIdx.x == 0) {
     A.pv[(int64_t)b * A.nch + c] = bv;
     A.pi[(int64_t)b * A.nch + c] = bi;
-    __threadfence();
-    const int prev = atomicAdd(&A.counters[A.B + b], 1);
-    sh_last = prev == A.nch - 1;
   }
-  __syncthreads();
-  if (!sh_last || threadIdx.x != 0) return;
-  __threadfence();
+}
+
+// launch 5: merge the chunk winners of sampled sequences, write outputs and the rollback
+template <bool PROBS>
+__global__ void accept_final_kernel(AcceptArgs A) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= A.B) return;
+  if (!PROBS && A.temps[b] <= 0.f) return;  // greedy sequences were finished by the step
   float v = A.pv[(int64_t)b * A.nch];
   int extra = A.pi[(int64_t)b * A.nch];
-  for (int cc = 1; cc < A.nch; ++cc) argmax_merge(v, extra, A.pv[(int64_t)b * A.nch + cc], A.pi[(int64_t)b * A.nch + cc]);
-  write_outputs(A, b, j, extra);
-  atomicExch(&A.counters[A.B + b], 0);
+  for (int c = 1; c < A.nch; ++c) argmax_merge(v, extra, A.pv[(int64_t)b * A.nch + c], A.pi[(int64_t)b * A.nch + c]);
+  write_outputs(A, b, A.jpos[b], extra);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -545,25 +519,20 @@ struct Carve {
 
 int64_t nchunks(int64_t V) { return (V + CH - 1) / CH; }
 
-constexpr int64_t ACCEPT_COUNTER_BYTES = 2 * 65535 * 4 + 8;   // two counters per sequence, B <= 65535
-
 int64_t accept_ws(int64_t B, int64_t K, int64_t V) {
   const int64_t nch = nchunks(V);
   auto r = [](int64_t n) { return ((n + 255) / 256) * 256; };
-  return ACCEPT_COUNTER_BYTES + r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) +
-         r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) + 2 * r(B * nch * 4) + 2 * r(B * 4);
+  return r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) +
+         r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) + 3 * r(B * nch * 4) + r(B * 4);
 }
 
-// Carve the acceptance workspace: a fixed counter region first (the part that must be zero between
-// calls; fixed so that a later call never reads another call's data as counters).
 void carve_accept(AcceptArgs& A, void* workspace, int64_t B, int64_t K, int nch) {
   Carve cv{reinterpret_cast<char*>(workspace)};
-  A.counters = cv.take<int32_t>(ACCEPT_COUNTER_BYTES / 4);
   A.stats = cv.take<Stat>(B * (2 * K + 1) * nch);
   A.mstats = cv.take<Stat>(B * (2 * K + 1));
   A.pv = cv.take<float>(B * nch);
   A.pi = cv.take<int>(B * nch);
-  A.rsum = cv.take<float>(B);
+  A.resid = cv.take<float>(B * nch);
   A.jpos = cv.take<int>(B);
 }
 
@@ -573,12 +542,18 @@ template <int DT>
 int launch_accept(const AcceptArgs& A, bool probs, hipStream_t s) {
   const int per = A.rs.n0 + A.rs.n1;
   const dim3 chunks((unsigned)A.nch, (unsigned)A.B);
+  const dim3 finals((unsigned)((A.B + 63) / 64));
   if (!probs) {
     accept_stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(A.B * per)), THREADS, 0, s>>>(A);
+    accept_step_kernel<DT, false><<<dim3((unsigned)A.B), 64, 0, s>>>(A);
+    accept_residual_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
     accept_argmax_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
+    accept_final_kernel<false><<<finals, 64, 0, s>>>(A);
   } else {
-    accept_probs_step_kernel<DT><<<dim3((unsigned)A.B), THREADS, 0, s>>>(A);
+    accept_step_kernel<DT, true><<<dim3((unsigned)A.B), 64, 0, s>>>(A);
+    accept_residual_kernel<DT, true><<<chunks, THREADS, 0, s>>>(A);
     accept_argmax_kernel<DT, true><<<chunks, THREADS, 0, s>>>(A);
+    accept_final_kernel<true><<<finals, 64, 0, s>>>(A);
   }
   return fs::launch_status("spec_accept");
 }

@@ -35,13 +35,12 @@ _PERSISTENT = {}
 
 
 def _persistent_ws(name: str, nbytes: int, device) -> torch.Tensor:
-    """A per-device workspace for kernels that chain their launches with counters: zero-filled when
-    allocated; every call leaves the counters at zero again, so it is reused without clearing.
-    Calls are stream-ordered on torch's current stream, so consecutive calls never overlap."""
+    """A per-device scratch buffer reused across calls (calls are ordered on torch's current stream,
+    so consecutive users never overlap); grown when a call needs more."""
     key = (name, torch.device(device))
     ws = _PERSISTENT.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(int(nbytes * 1.25), 1 << 20), dtype=torch.uint8, device=key[1])
+        ws = torch.empty(max(int(nbytes * 1.25), 1 << 20), dtype=torch.uint8, device=key[1])
         _PERSISTENT[key] = ws
     return ws
 

@@ -90,11 +90,8 @@ int fs_paged_gather(const fs_kv_layout* kv, const int32_t* block_tables, int64_t
  * Replaces the gather of paged.py:80-81 plus model.py:70-76 (repeat_interleave, key <= query-position
  * mask, scaled_dot_product_attention). q/out element (b, t, h, d) at base + b*s_b + t*s_t + h*s_h + d.
  * Query head h reads KV head h / (n_heads / n_kv_heads) (model.py:70-71). Query (b, t) sees the keys
- * at positions 0..positions[b*T+t] (model.py:75).
- * workspace: at least fs_paged_attention_workspace_size(...) bytes, 256-byte aligned, ZERO-FILLED
- * before its first use; every call leaves its first bytes (chunk counters) at zero again, so one
- * workspace can be reused by later calls without clearing. Calls that share a workspace must not
- * overlap (one stream). */
+ * at positions 0..positions[b*T+t] (model.py:75). workspace: at least
+ * fs_paged_attention_workspace_size(...) bytes, 256-byte aligned, any contents. */
 int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
                        const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
                        const int32_t* positions, int32_t B, int32_t T, int32_t n_heads, float scale,
@@ -180,9 +177,7 @@ int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_t ldq, int3
                     int32_t* out_tokens, int32_t* n_accepted, void* workspace, int64_t workspace_bytes,
                     void* stream);
 
-/* Workspace of fs_spec_accept / fs_verify_probs: 256-byte aligned, ZERO-FILLED before its first use;
- * every call leaves its first bytes (per-sequence counters) at zero again, so it can be reused without
- * clearing. Calls that share a workspace must not overlap (one stream). */
+/* Workspace of fs_spec_accept / fs_verify_probs (256-byte aligned, any contents). */
 int64_t fs_spec_accept_workspace_size(int32_t B, int32_t K, int64_t V);
 
 #ifdef __cplusplus

@@ -320,19 +320,3 @@ def test_verify_draft_reference_streams():
         got = verify_draft(p, q, c["xs"], torch.Generator().manual_seed(c["seed"]))
         assert got == (c["accepted"], c["extra"]), c["seed"]
 
-
-def test_chained_kernels_leave_their_counters_at_zero():
-    """Attention and acceptance chain their launches with counters at the start of a persistent
-    workspace; after any call the counters must be back at zero (the next call relies on it)."""
-    case("workspace counters")
-    from forgeserve_amd.ops import _PERSISTENT
-    q, k, v, tables, pos = _paged_case(3, 7, 32, 8, 128, 16, [700, 1500, 90], 300, torch.bfloat16, 12)
-    _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
-    tgt, dft = _c2_inputs(b=5, k=3, v=9000)
-    ops.spec_accept(tgt.to(DEV), dft.to(DEV), torch.zeros(5, 3, dtype=torch.int32, device=DEV), None,
-                    torch.tensor([1.0, 0.0, 0.5, 1.0, 2.0], device=DEV), torch.rand(5, 3, device=DEV),
-                    torch.empty(5, 9000, device=DEV).exponential_())
-    torch.cuda.synchronize()
-    regions = {"attention": 262144 * 4, "accept": 2 * 65535 * 4}
-    for (name, _), ws in _PERSISTENT.items():
-        assert torch.count_nonzero(ws[: regions[name]]) == 0, name
