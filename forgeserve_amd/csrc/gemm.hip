@@ -135,6 +135,153 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(const uint16_t* __restri
 }
 
 // ------------------------------------------------------------------------------------------------
+// bf16 MFMA kernel with an LDS ring fed by direct global->LDS loads (M > 64, K % 64 == 0)
+//
+// 4 waves in 2x2 compute a BM x BN tile of C. K advances in 64-deep stages; NS stages live in LDS and
+// NS-1 are in flight while one is consumed. Every 16-byte chunk of a stage is copied by
+// global_load_lds_dwordx4 (lane l of an instruction lands at LDS base + 16*l), so in-flight data
+// costs no VGPRs. Rows are stored with their eight 16-byte chunks XOR-swizzled by (row & 7): the
+// MFMA operand reads (ds_read_b128, 8 lanes per bank cycle) are conflict-free. The loads are issued
+// from inline asm, so the waits are explicit (`s_waitcnt vmcnt`) and one barrier per stage orders
+// the LDS ring. Operand roles, k order and the one-accumulator chain match gemm_bf16_kernel.
+// ------------------------------------------------------------------------------------------------
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+FS_DEVICE void dma16(const void* g, uint32_t lds) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(lds);  // the LDS base is the same for the whole wave
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(l) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int N>
+FS_DEVICE void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN, int NS>
+__global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __restrict__ X, int64_t ldx,
+                                                            const uint16_t* __restrict__ W, int64_t ldw,
+                                                            uint16_t* __restrict__ C, int64_t ldc,
+                                                            const uint16_t* __restrict__ R, int64_t ldr, int64_t M,
+                                                            int64_t N, int64_t K, int tiles_m, int ntiles) {
+  constexpr int KB = 64;                       // k per stage
+  constexpr int ROWB = KB * 2;                 // bytes per stage row (128)
+  constexpr int XB = BM * ROWB, WB = BN * ROWB, STAGE = XB + WB;
+  constexpr int XI = XB / 4096, WI = WB / 4096;  // dma instructions per wave per stage (4 waves x 1 KB)
+  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
+  static_assert(XB % 4096 == 0 && WB % 4096 == 0, "tile rows must fill whole 1 KB wave copies");
+  __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE];
+
+  // XCD-aware order: workgroup ids go round-robin over the 8 XCDs; give each XCD a contiguous range
+  // of tiles, M fastest, so the M tiles that share a weight tile share that XCD's L2.
+  const int per_xcd = (ntiles + 7) / 8;
+  const int tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (tile >= ntiles) return;
+  const int64_t m0 = (int64_t)(tile % tiles_m) * BM;
+  const int64_t n0 = (int64_t)(tile / tiles_m) * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+
+  // this lane's source rows/chunks for its share of a stage (fixed across stages but for k0)
+  const uint16_t* xsrc[XI];
+  const uint16_t* wsrc[WI];
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int P = (i * 4 + wave) * 64 + lane;  // 16-byte chunk index inside the X stage
+    const int r = P >> 3, c = (P & 7) ^ (r & 7);
+    int64_t gr = m0 + r;
+    gr = gr < M ? gr : M - 1;
+    xsrc[i] = X + gr * ldx + 8 * c;
+  }
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    const int P = (i * 4 + wave) * 64 + lane;
+    const int r = P >> 3, c = (P & 7) ^ (r & 7);
+    int64_t gr = n0 + r;
+    gr = gr < N ? gr : N - 1;
+    wsrc[i] = W + gr * ldw + 8 * c;
+  }
+  auto issue = [&](int kt) {
+    const uint32_t base = lds0 + (uint32_t)((kt % NS) * STAGE);
+    const int64_t k0 = (int64_t)kt * KB;
+#pragma unroll
+    for (int i = 0; i < XI; ++i) dma16(xsrc[i] + k0, base + (uint32_t)((i * 4 + wave) * 1024));
+#pragma unroll
+    for (int i = 0; i < WI; ++i) dma16(wsrc[i] + k0, base + XB + (uint32_t)((i * 4 + wave) * 1024));
+  };
+
+  float4_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (int)(K / KB);
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) issue(s);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    // stages issued after kt and still allowed in flight: min(NS - 2, nk - 1 - kt)
+    const int later = min(NS - 2, nk - 1 - kt);
+    if (later >= 2) wait_vm<2 * (XI + WI)>();
+    else if (later == 1) wait_vm<XI + WI>();
+    else wait_vm<0>();
+    __syncthreads();  // stage kt has landed for every wave; stage kt-1 is no longer being read
+    if (kt + NS - 1 < nk) issue(kt + NS - 1);
+    const char* st = smem + (kt % NS) * STAGE;
+#pragma unroll
+    for (int ks = 0; ks < KB / 32; ++ks) {
+      bf16x8_t xf[TM], wf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WM + 16 * i + l16, c = (4 * ks + g) ^ (r & 7);
+        xf[i] = *reinterpret_cast<const bf16x8_t*>(st + r * ROWB + 16 * c);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn * WN + 16 * j + l16, c = (4 * ks + g) ^ (r & 7);
+        wf[j] = *reinterpret_cast<const bf16x8_t*>(st + XB + r * ROWB + 16 * c);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], xf[i], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // acc[i][j]: lane (l16, g) holds C[m = 16i + l16][n = 16j + 4g + r], r = 0..3 (wave-local)
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t row = m0 + wm * WM + 16 * i + l16;
+    if (row >= M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col0 = n0 + wn * WN + 16 * j + 4 * g;
+      uint16_t o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = Elem<FS_BF16>::round(acc[i][j][r]);
+        if (R && col0 + r < N) v = v + bf16_to_f32(R[row * ldr + col0 + r]);
+        o[r] = f32_to_bf16(v);
+      }
+      if (col0 + 3 < N && ((ldc | col0) & 3) == 0) {
+        typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+        *reinterpret_cast<u32x2*>(C + row * ldc + col0) =
+            u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (col0 + r < N) C[row * ldc + col0 + r] = o[r];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
 // VALU kernel (f32 / f16 / unaligned bf16): 64x64 tile, 16-deep k stages, 4x4 outputs per thread
 // ------------------------------------------------------------------------------------------------
 template <int DT>
@@ -204,6 +351,22 @@ extern "C" int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, v
   if (M == 0) return 0;
   hipStream_t s = fs::as_stream(stream);
   const bool mfma = dtype == FS_BF16 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B);
+  if (mfma && M > 64 && K % 64 == 0) {
+    const uint16_t* a = (const uint16_t*)A;
+    const uint16_t* b = (const uint16_t*)B;
+    const int tm = (int)((M + 127) / 128);
+    const int tn256 = (int)((N + 255) / 256), tn128 = (int)((N + 127) / 128);
+    if ((int64_t)tm * tn256 >= 256) {  // enough tiles to fill the chip with the larger tile
+      const int nt = tm * tn256;
+      gemm_bf16_lds_kernel<128, 256, 3><<<dim3((unsigned)(8 * ((nt + 7) / 8))), 256, 0, s>>>(
+          a, lda, b, ldb, (uint16_t*)C, ldc, (const uint16_t*)R, ldr, M, N, K, tm, nt);
+    } else {
+      const int nt = tm * tn128;
+      gemm_bf16_lds_kernel<128, 128, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8))), 256, 0, s>>>(
+          a, lda, b, ldb, (uint16_t*)C, ldc, (const uint16_t*)R, ldr, M, N, K, tm, nt);
+    }
+    return fs::launch_status("gemm_bf16_lds");
+  }
   if (mfma) {
     const uint16_t* a = (const uint16_t*)A;
     const uint16_t* b = (const uint16_t*)B;

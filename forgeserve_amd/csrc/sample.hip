@@ -21,6 +21,7 @@ constexpr int THREADS = 256;
 constexpr int VEC = 8;                       // consecutive columns per thread group
 constexpr int UNROLL = 8;                    // groups per thread per chunk: 8 16-byte loads in flight
 constexpr int CH = THREADS * VEC * UNROLL;   // 16384 columns per chunk
+constexpr float LOG2E_F = 1.4426950408889634f;
 
 struct Stat {
   float m;    // max of x/T (T > 0) or of x (T == 0)
@@ -126,7 +127,7 @@ FS_DEVICE Stat merge_row(const Stat* st, int nch) {
   float S = 0.f;
   for (int c = 0; c < nch; ++c) {
     const float mc = st[c].m;
-    S += (mc == -INFINITY) ? 0.f : st[c].s * expf(mc - M);
+    S += (mc == -INFINITY) ? 0.f : st[c].s * __builtin_amdgcn_exp2f((mc - M) * LOG2E_F);
   }
   for (int c = 1; c < nch; ++c) argmax_merge(r.av, r.ai, st[c].av, st[c].ai);
   r.m = M;
@@ -137,9 +138,9 @@ FS_DEVICE Stat merge_row(const Stat* st, int nch) {
 // p_v of a row from logits and merged stats (T > 0): softmax(f32(x) / T) (sampling.py:13).
 FS_DEVICE float softmax_at(float x, float T, const Stat& st) { return expf(x / T - st.m) / st.s; }
 
-// One chunk of one row: first argmax of x and, for T > 0, (m, s) = (max of x/T, sum of exp(x/T - m)),
-// accumulated online per thread (each element enters once, in increasing column order per thread)
-// and merged across the workgroup in a fixed order. All loads of the chunk are issued up front.
+// One chunk of one row. T == 0: the first argmax of x. T > 0: (m, s) = (max of y, sum of exp(y - m))
+// with y = x / T (a true division, skipped when T == 1 where it is exact). The chunk's loads are all
+// issued up front; the values stay in registers for the max pass and the exp pass.
 template <int DT>
 FS_DEVICE Stat chunk_stat(const typename Elem<DT>::T* row, int c, int64_t V, float T, float* shf, int* shi) {
   const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
@@ -147,40 +148,59 @@ FS_DEVICE Stat chunk_stat(const typename Elem<DT>::T* row, int c, int64_t V, flo
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u)
     load8<DT>(row, (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC, V, vec_ok, -INFINITY, x[u]);
-  float amv = -INFINITY, m = -INFINITY, sum = 0.f;
-  int ami = 0x7fffffff;
-#pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (v0 + j >= V) continue;
-      argmax_merge(amv, ami, x[u][j], (int)(v0 + j));
-      if (T > 0.f) {
-        const float y = x[u][j] / T;
-        if (y > m) {
-          sum = (m == -INFINITY ? 0.f : sum * expf(m - y)) + 1.f;
-          m = y;
-        } else if (y != -INFINITY) {
-          sum += expf(y - m);
-        }
-      }
-    }
-  }
-  block_argmax(amv, ami, shf, shi);
   Stat st;
-  st.av = amv;
-  st.ai = ami;
-  if (T > 0.f) {
-    const float M = block_max(m, shf);
-    st.m = M;
-    st.s = block_sum(m == -INFINITY ? 0.f : sum * expf(m - M), shf);
-  } else {
-    st.m = amv;
+  if (T <= 0.f) {
+    float amv = -INFINITY;
+    int ami = 0x7fffffff;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (v0 + j < V) argmax_merge(amv, ami, x[u][j], (int)(v0 + j));
+    }
+    block_argmax(amv, ami, shf, shi);
+    st.m = st.av = amv;
+    st.ai = ami;
     st.s = 0.f;
+    return st;
   }
+  if (T != 1.f) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[u][j] = x[u][j] / T;  // padding stays -inf
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, x[u][j]);
+  const float M = block_max(m, shf);
+  const float ML = M * LOG2E_F;
+  float sum = 0.f;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += __builtin_amdgcn_exp2f(fmaf(x[u][j], LOG2E_F, -ML));  // exp(-inf) = 0
+  st.m = M;
+  st.s = block_sum(sum, shf);
+  st.av = M;
+  st.ai = 0;
   return st;
 }
+
+// Softmax value of one column for the vocab-wide passes: exp(y - M) / S evaluated as
+// exp2(y*log2e - M*log2e) * (1/S). The accept/reject test itself uses softmax_at (expf, true divides).
+struct FastSoftmax {
+  float T, ML, invS;
+  FS_DEVICE FastSoftmax() : T(1.f), ML(0.f), invS(1.f) {}
+  FS_DEVICE FastSoftmax(float t, const Stat& st) : T(t), ML(st.m * LOG2E_F), invS(1.f / st.s) {}
+  FS_DEVICE float operator()(float x) const {
+    const float y = T == 1.f ? x : x / T;
+    return __builtin_amdgcn_exp2f(fmaf(y, LOG2E_F, -ML)) * invS;
+  }
+};
 
 // ------------------------------------------------------------------------------------------------
 // launch 1: per-(row, chunk) statistics
@@ -222,7 +242,7 @@ __global__ void __launch_bounds__(THREADS) sample_argmax_kernel(RowSet rs, int64
   if (T <= 0.f) return;
   if (threadIdx.x == 0) shs = merge_row(stats + (int64_t)r * nch, nch);
   __syncthreads();
-  const Stat st = shs;
+  const FastSoftmax fs(T, shs);
   const auto* row = row_ptr<DT>(rs, r, 0);
   const float* er = E + (int64_t)r * ldE;
   const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0) &&
@@ -237,7 +257,7 @@ __global__ void __launch_bounds__(THREADS) sample_argmax_kernel(RowSet rs, int64
     load8_f32(er, v0, V, vec_ok, e);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      if (v0 + j < V) argmax_merge(bv, bi, softmax_at(x[j], T, st) / e[j], (int)(v0 + j));
+      if (v0 + j < V) argmax_merge(bv, bi, fs(x[j]) / e[j], (int)(v0 + j));
     }
   }
   block_argmax(bv, bi, shf, shi);
@@ -355,10 +375,10 @@ __global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) 
   const int j = A.jpos[b];
   if ((!PROBS && T <= 0.f) || j >= ke) return;  // greedy (done) or bonus token (no residual)
   const int per = A.rs.n0 + A.rs.n1;
-  Stat sp{}, sq{};
+  FastSoftmax sp, sq;
   if (!PROBS) {
-    sp = A.mstats[(int64_t)b * per + j];
-    sq = A.mstats[(int64_t)b * per + A.rs.n0 + j];
+    sp = FastSoftmax(T, A.mstats[(int64_t)b * per + j]);
+    sq = FastSoftmax(T, A.mstats[(int64_t)b * per + A.rs.n0 + j]);
   }
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + j);
@@ -377,8 +397,8 @@ __global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) 
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
       if (v0 + jj >= A.V) continue;
-      const float p = PROBS ? xp[u][jj] : softmax_at(xp[u][jj], T, sp);
-      const float q = PROBS ? xq[u][jj] : softmax_at(xq[u][jj], T, sq);
+      const float p = PROBS ? xp[u][jj] : sp(xp[u][jj]);
+      const float q = PROBS ? xq[u][jj] : sq(xq[u][jj]);
       ls += fmaxf(Elem<DT>::round(p - q), 0.f);  // (p - q).clamp(min=0)
     }
   }
@@ -421,10 +441,10 @@ __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
   const int per = A.rs.n0 + A.rs.n1;
   const int j = A.jpos[b];
   const bool bonus = j >= ke;
-  Stat sp{}, sq{};
+  FastSoftmax sp, sq;
   if (!PROBS) {
-    sp = A.mstats[(int64_t)b * per + j];
-    if (!bonus) sq = A.mstats[(int64_t)b * per + A.rs.n0 + j];
+    sp = FastSoftmax(T, A.mstats[(int64_t)b * per + j]);
+    if (!bonus) sq = FastSoftmax(T, A.mstats[(int64_t)b * per + A.rs.n0 + j]);
   }
   float s = 0.f;  // the residual sum, merged in chunk order (every workgroup merges the same way)
   if (!bonus)
@@ -448,12 +468,12 @@ __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
       if (v0 + jj >= A.V) continue;
-      const float p = PROBS ? xp[jj] : softmax_at(xp[jj], T, sp);
+      const float p = PROBS ? xp[jj] : sp(xp[jj]);
       float w;
       if (bonus) {
         w = p;  // speculative.py:33
       } else {
-        const float q = PROBS ? xq[jj] : softmax_at(xq[jj], T, sq);
+        const float q = PROBS ? xq[jj] : sq(xq[jj]);
         const float r = fmaxf(Elem<DT>::round(p - q), 0.f);
         w = s > 0.f ? Elem<DT>::round(r / s) : p;  // speculative.py:31
       }
