@@ -23,11 +23,16 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace {
 
-constexpr int QTILE = 32;            // query rows per MFMA workgroup
+constexpr int QTILE = 32;            // query rows per MFMA wave
+constexpr int MAX_HEADS_PER_WG = 8;  // waves (KV heads) per MFMA workgroup, at most
+constexpr int PLAN_THREADS = 256;
+constexpr int64_t WS_HEADER = 256;    // workspace: item count, then the item list, then the partials
 constexpr float LOG2E = 1.4426950408889634f;
 
 struct AttnParams {
@@ -44,50 +49,207 @@ struct AttnParams {
   float* ws_ml;                      // [B*T*H][nsplit][2]
   int32_t nsplit;
   int32_t split;                     // keys per chunk: a multiple of 16, at most 512
+  struct AttnItem* items;            // MFMA path: the work list written by attn_plan_kernel
+  int32_t* n_items;                  // its length
 };
+
+// Reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48) with the gfx950
+// row swaps: permlane16_swap of (x, x) yields {rows 0,0,2,2 ; rows 1,1,3,3} of x, permlane32_swap
+// yields {lanes 0-31 twice ; lanes 32-63 twice}. Both steps are symmetric, so every lane ends with
+// the same value, and the sum adds (g0 + g1) + (g2 + g3) in every lane.
+FS_DEVICE float max_across_groups(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+FS_DEVICE float sum_across_groups(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Four floats to bf16 (round to nearest even) with gfx950's packed conversion, as MFMA operand bits.
+FS_DEVICE short4_t bf16_rne4(const float (&v)[4]) {
+  typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+  const bf16x2 a = __builtin_convertvector((f32x2){v[0], v[1]}, bf16x2);
+  const bf16x2 b = __builtin_convertvector((f32x2){v[2], v[3]}, bf16x2);
+  const uint32_t ua = __builtin_bit_cast(uint32_t, a), ub = __builtin_bit_cast(uint32_t, b);
+  return short4_t{(short)(ua & 0xffff), (short)(ua >> 16), (short)(ub & 0xffff), (short)(ub >> 16)};
+}
 
 FS_DEVICE int64_t row_index(const AttnParams& P, int b, int t, int h) { return ((int64_t)b * P.T + t) * P.H + h; }
 
 // ------------------------------------------------------------------------------------------------
+// work plan: the (query tile, chunk) items that hold visible keys
+// ------------------------------------------------------------------------------------------------
+struct AttnItem {
+  int32_t b, z, s, qmax;   // batch row, query tile, chunk, furthest query position of the tile
+};
+
+FS_DEVICE int tile_qmax(const AttnParams& P, int b, int z) {
+  const int row0 = z * QTILE;
+  const int nrows = min(QTILE, P.T * P.G - row0);
+  const int t0 = row0 / P.G, t1 = (row0 + nrows - 1) / P.G;
+  const int* posb = P.pos + (int64_t)b * P.T;
+  int q = -1;
+  for (int t = t0; t <= t1; ++t) q = max(q, posb[t]);
+  return q;
+}
+
+FS_DEVICE int tile_chunks(const AttnParams& P, int qmax) { return qmax < 0 ? 0 : min(qmax / P.split + 1, P.nsplit); }
+
+// One workgroup lists every item: first the chunks that lie wholly below their tile's furthest
+// query (the full chunks), tile by tile, then the last chunk of each tile. The shorter last chunks
+// thus make up the attention kernel's final round, where they even out the finish.
+__global__ void __launch_bounds__(PLAN_THREADS) attn_plan_kernel(AttnParams P) {
+  __shared__ int sa[PLAN_THREADS], sb[PLAN_THREADS];
+  const int tid = threadIdx.x;
+  const int qtiles = (P.T * P.G + QTILE - 1) / QTILE;
+  const int U = P.B * qtiles;
+  int nf = 0;
+  for (int u = tid; u < U; u += PLAN_THREADS) nf += max(tile_chunks(P, tile_qmax(P, u / qtiles, u % qtiles)) - 1, 0);
+  sa[tid] = nf;
+  __syncthreads();
+  for (int off = PLAN_THREADS / 2; off > 0; off >>= 1) {
+    if (tid < off) sa[tid] += sa[tid + off];
+    __syncthreads();
+  }
+  const int n_full = sa[0];
+  __syncthreads();
+  int base_full = 0, base_last = 0;
+  for (int u0 = 0; u0 < U; u0 += PLAN_THREADS) {
+    const int u = u0 + tid;
+    int b = 0, z = 0, qm = -1, nch = 0;
+    if (u < U) {
+      b = u / qtiles;
+      z = u - b * qtiles;
+      qm = tile_qmax(P, b, z);
+      nch = tile_chunks(P, qm);
+    }
+    const int f = max(nch - 1, 0), l = nch > 0 ? 1 : 0;
+    sa[tid] = f;
+    sb[tid] = l;
+    __syncthreads();
+    for (int off = 1; off < PLAN_THREADS; off <<= 1) {   // inclusive scans
+      const int xa = tid >= off ? sa[tid - off] : 0;
+      const int xb = tid >= off ? sb[tid - off] : 0;
+      __syncthreads();
+      sa[tid] += xa;
+      sb[tid] += xb;
+      __syncthreads();
+    }
+    const int ef = base_full + sa[tid] - f, el = n_full + base_last + sb[tid] - l;
+    for (int c = 0; c < f; ++c) P.items[ef + c] = AttnItem{b, z, c, qm};
+    if (l) P.items[el] = AttnItem{b, z, nch - 1, qm};
+    base_full += sa[PLAN_THREADS - 1];
+    base_last += sb[PLAN_THREADS - 1];
+    __syncthreads();
+  }
+  if (tid == 0) P.n_items[0] = n_full + base_last;
+}
+
+// ------------------------------------------------------------------------------------------------
 // MFMA kernel (bf16)
 // ------------------------------------------------------------------------------------------------
-// BSZ: the pool's block size when it is known at compile time (16), else 0 (any multiple of 16).
-template <int D, int BSZ>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) attn_mfma_bf16_kernel(AttnParams P) {
-  constexpr int KS = D / 32;   // k-steps of the QK^T product
-  constexpr int MT = D / 16;   // 16-dim tiles of the PV product
-  const int lane = threadIdx.x;
-  const int l16 = lane & 15, g = lane >> 4;
-  // heads of one (row, chunk) are adjacent workgroups: their tiles are neighbours in the pool
-  const int Hkv = P.kv.n_kv_heads;
-  const int s = blockIdx.x / Hkv;
-  const int hkv = blockIdx.x - s * Hkv;
-  const int b = blockIdx.y;
-  const int row0 = blockIdx.z * QTILE;
-  const int nrows = min(QTILE, P.T * P.G - row0);
-  const int* posb = P.pos + (int64_t)b * P.T;
+// What one wave needs of an item before its first tile load.
+struct ItemRegs {
+  int b, z, s, qmax;     // wave-uniform
+  int rpos[2];           // positions of the lane's two query rows (row = 16*nt + lane%16), -1: none
+  int phys;              // lane i: table entry of the chunk's i-th block (-1 past the table)
+};
 
-  // positions of this lane's two rows (row = 16*nt + l16), and the tile's furthest position
-  int rpos[2];
-  int qmax = -1;
+template <int BSZ>
+FS_DEVICE void fetch_item(const AttnParams& P, int64_t e_idx, ItemRegs& it) {
+  // the list is read-only here: a constant-address-space load keeps it on the scalar unit
+  typedef __attribute__((address_space(4))) const AttnItem ConstItem;
+  ConstItem* ep = (ConstItem*)(uintptr_t)(P.items + e_idx);
+  const AttnItem e{ep->b, ep->z, ep->s, ep->qmax};
+  it.b = e.b;
+  it.z = e.z;
+  it.s = e.s;
+  it.qmax = e.qmax;
+  const int lane = threadIdx.x & 63, l16 = lane & 15;
+  const int row0 = e.z * QTILE;
+  const int nrows = min(QTILE, P.T * P.G - row0);
+  const int* posb = P.pos + (int64_t)e.b * P.T;
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int r = 16 * nt + l16;
-    rpos[nt] = (r < nrows) ? posb[(row0 + r) / P.G] : -1;
+    it.rpos[nt] = (r < nrows) ? posb[(row0 + r) / P.G] : -1;
   }
-  {
-    const int t0 = row0 / P.G, t1 = (row0 + nrows - 1) / P.G;
-    for (int t = t0; t <= t1; ++t) qmax = max(qmax, posb[t]);
-  }
-  qmax = __builtin_amdgcn_readfirstlane(qmax);  // the same in every lane: keep the loop scalar
+  const int BS = BSZ ? BSZ : P.kv.block_size;
+  const int kbeg = e.s * P.split;
+  const int kend = min(kbeg + P.split, e.qmax + 1);
+  const int first_blk = kbeg / BS;
+  const int nblk = (kend - 1) / BS - first_blk + 1;   // <= split/16 + 1 <= 33 lanes
+  it.phys = -1;   // raw table entry, checked where it is used so that nothing waits for it here
+  if (lane < nblk && first_blk + lane < P.max_blocks) it.phys = P.table[(int64_t)e.b * P.table_stride + first_blk + lane];
+}
+
+// One item for one wave: chunk it.s of batch row it.b, KV head hkv, query tile it.z. `next` runs
+// once, three tiles before the end (it takes and fetches the wave's next item).
+template <int D, int BSZ, class F>
+__device__ __attribute__((always_inline)) inline void attn_mfma_item(const AttnParams& P, const ItemRegs& it,
+                                                                     int hkv, F&& next) {
+  constexpr int KS = D / 32;   // k-steps of the QK^T product
+  constexpr int MT = D / 16;   // 16-dim tiles of the PV product
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int b = it.b, s = it.s, qmax = it.qmax;
+  const int row0 = it.z * QTILE;
+  const int nrows = min(QTILE, P.T * P.G - row0);
+  const int rpos[2] = {it.rpos[0], it.rpos[1]};
+  const int my_phys = it.phys;
   const int kbeg = s * P.split;
-  if (qmax < kbeg) return;  // no query of this tile sees this chunk: the combine never reads it
+  if (qmax < kbeg) return;  // not listed by the plan; kept as a guard
   const int kend = min(kbeg + P.split, qmax + 1);
   const int ntiles = (kend - kbeg + 15) >> 4;
   const bool two = nrows > 16;
+  const int BS = BSZ ? BSZ : P.kv.block_size;
+  const int64_t v_dim = BSZ ? BSZ : P.kv.v_dim;   // == block_size (dim-major values)
+  const int first_blk = kbeg / BS;
+
+  typedef uint16_t u16;
+  const u16* kpool = reinterpret_cast<const u16*>(P.kv.k);
+  const u16* vpool = reinterpret_cast<const u16*>(P.kv.v);
+  const int64_t k_head_off = (int64_t)hkv * P.kv.k_head;
+  const int64_t v_head_off = (int64_t)hkv * P.kv.v_head;
+
+  // Three tile buffers in registers: while tile t is consumed, tiles t+1 and t+2 are in flight.
+  // Every load is unconditional (a prefetch past the end re-reads the last tile, an unmapped block
+  // reads block 0 and is masked in consume) so that each wait before a consume counts exactly the
+  // loads issued after that tile, on every path through the loop.
+  bf16x8_t kb0[KS], kb1[KS], kb2[KS];
+  short4_t vb0[MT], vb1[MT], vb2[MT];
+
+  auto block_of = [&](int j0) {   // physical block holding key j0, -1 when unmapped
+    const int v = __builtin_amdgcn_readlane(my_phys, j0 / BS - first_blk);
+    return (v >= 0 && v < P.kv.num_blocks) ? v : -1;
+  };
+
+  auto load_tile = [&](int kt, bf16x8_t (&kd)[KS], short4_t (&vd)[MT]) {
+    const int j0 = kbeg + 16 * min(kt, ntiles - 1);
+    const int phys = block_of(j0);
+    const int64_t pb = phys >= 0 ? phys : 0;
+    const int slot0 = j0 - (j0 / BS) * BS;
+    const u16* kt_ = kpool + pb * P.kv.k_block + k_head_off + (int64_t)(slot0 + l16) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)   // read once per launch: nontemporal
+      kd[ks] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(kt_ + 32 * ks + 8 * g));
+    const u16* vt_ = vpool + pb * P.kv.v_block + v_head_off + slot0 + 4 * g;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      vd[mt] = __builtin_nontemporal_load(reinterpret_cast<const short4_t*>(vt_ + (int64_t)(16 * mt + l16) * v_dim));
+  };
+
+  load_tile(0, kb0, vb0);
+  load_tile(1, kb1, vb1);
 
   // Q fragments (B operand of S^T): Q[row][32*ks + 8*g .. +8]
-  typedef uint16_t u16;
   const u16* qbase = reinterpret_cast<const u16*>(P.q);
   bf16x8_t qf[2][KS];
 #pragma unroll
@@ -106,22 +268,6 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) at
     }
   }
 
-  // physical block ids of this chunk (at most P.split/16 + 1 entries), one per lane
-  const int BS = BSZ ? BSZ : P.kv.block_size;
-  const int64_t v_dim = BSZ ? BSZ : P.kv.v_dim;   // == block_size (dim-major values)
-  const int first_blk = kbeg / BS;
-  const int nblk = (kend - 1) / BS - first_blk + 1;
-  int my_phys = -1;
-  if (lane < nblk && first_blk + lane < P.max_blocks) {
-    const int v = P.table[(int64_t)b * P.table_stride + first_blk + lane];
-    my_phys = (v >= 0 && v < P.kv.num_blocks) ? v : -1;
-  }
-
-  const u16* kpool = reinterpret_cast<const u16*>(P.kv.k);
-  const u16* vpool = reinterpret_cast<const u16*>(P.kv.v);
-  const int64_t k_head_off = (int64_t)hkv * P.kv.k_head;
-  const int64_t v_head_off = (int64_t)hkv * P.kv.v_head;
-
   float4_t acc[MT][2];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -131,42 +277,15 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) at
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_run[2] = {0.f, 0.f};
 
-  // Three tile buffers in registers: while tile t is consumed, tiles t+1 and t+2 are in flight.
-  bf16x8_t kb0[KS], kb1[KS], kb2[KS];
-  short4_t vb0[MT], vb1[MT], vb2[MT];
-  bool ok0 = false, ok1 = false, ok2 = false;
-
-  auto load_tile = [&](int kt, bf16x8_t (&kd)[KS], short4_t (&vd)[MT], bool& valid) {
+  auto consume = [&](int kt, const bf16x8_t (&kf)[KS], short4_t (&vf)[MT]) {
     const int j0 = kbeg + 16 * kt;
-    const int bi = j0 / BS - first_blk;   // < nblk: the tile lies inside the chunk's block list
-    const int64_t phys = __builtin_amdgcn_readfirstlane(__shfl(my_phys, bi, 64));  // wave-uniform block id
-    valid = phys >= 0;
-    const int slot0 = j0 - (j0 / BS) * BS;
-    if (valid) {
-      const u16* kt_ = kpool + phys * P.kv.k_block + k_head_off + (int64_t)(slot0 + l16) * D;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)   // read once per launch: nontemporal
-        kd[ks] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(kt_ + 32 * ks + 8 * g));
-      const u16* vt_ = vpool + phys * P.kv.v_block + v_head_off + slot0 + 4 * g;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        vd[mt] = __builtin_nontemporal_load(
-            reinterpret_cast<const short4_t*>(vt_ + (int64_t)(16 * mt + l16) * v_dim));
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kd[ks] = bf16x8_t{};
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) vd[mt] = short4_t{0, 0, 0, 0};
-    }
-  };
-
-  auto consume = [&](int kt, const bf16x8_t (&kf)[KS], short4_t (&vf)[MT], bool tile_valid) {
-    const int j0 = kbeg + 16 * kt;
-    // keys past the furthest query (possibly never written) must not reach the PV product
-    if (j0 + 15 > qmax) {
+    const bool tile_valid = block_of(j0) >= 0;
+    // keys of an unmapped block, and keys past the furthest query (possibly never written), must not
+    // reach the PV product: their values may be anything
+    if (!tile_valid || j0 + 15 > qmax) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (j0 + 4 * g + i > qmax) {
+        if (!tile_valid || j0 + 4 * g + i > qmax) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) vf[mt][i] = 0;
         }
@@ -195,17 +314,17 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) at
         sv[i] = vis ? sc[nt][i] * P.scale_log2 : -INFINITY;
         tmax = fmaxf(tmax, sv[i]);
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      tmax = max_across_groups(tmax);
       const float m_new = fmaxf(m_run[nt], tmax);
       alpha[nt] = (m_new == -INFINITY) ? 1.f : exp2f(m_run[nt] - m_new);
       float psum = 0.f;
+      float pv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = (sv[i] == -INFINITY) ? 0.f : exp2f(sv[i] - m_new);
-        pf[nt][i] = (short)f32_to_bf16(p);
-        psum += p;
+        pv[i] = (sv[i] == -INFINITY) ? 0.f : exp2f(sv[i] - m_new);
+        psum += pv[i];
       }
+      pf[nt] = bf16_rne4(pv);
       l_run[nt] = l_run[nt] * alpha[nt] + psum;
       m_run[nt] = m_new;
     }
@@ -226,25 +345,26 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) at
     }
   };
 
-  load_tile(0, kb0, vb0, ok0);
-  if (ntiles > 1) load_tile(1, kb1, vb1, ok1);
+  const int kp = max(ntiles - 3, 0);   // the tile before which `next` runs, exactly once
   for (int kt = 0; kt < ntiles; kt += 3) {
-    if (kt + 2 < ntiles) load_tile(kt + 2, kb2, vb2, ok2);
-    consume(kt, kb0, vb0, ok0);
+    load_tile(kt + 2, kb2, vb2);
+    if (kt == kp) next();
+    consume(kt, kb0, vb0);
     if (kt + 1 >= ntiles) break;
-    if (kt + 3 < ntiles) load_tile(kt + 3, kb0, vb0, ok0);
-    consume(kt + 1, kb1, vb1, ok1);
+    load_tile(kt + 3, kb0, vb0);
+    if (kt + 1 == kp) next();
+    consume(kt + 1, kb1, vb1);
     if (kt + 2 >= ntiles) break;
-    if (kt + 4 < ntiles) load_tile(kt + 4, kb1, vb1, ok1);
-    consume(kt + 2, kb2, vb2, ok2);
+    load_tile(kt + 4, kb1, vb1);
+    if (kt + 2 == kp) next();
+    consume(kt + 2, kb2, vb2);
   }
 
   // write this chunk's partial for every real row of the tile that sees the chunk
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     float lsum = l_run[nt];
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
+    lsum = sum_across_groups(lsum);
     const int r = 16 * nt + l16;
     if (r >= nrows || rpos[nt] < kbeg) continue;
     const int rr = row0 + r;
@@ -260,7 +380,53 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) at
       pm[1] = lsum;
     }
   }
+}
 
+// Persistent kernel: as many workgroups as the GPU holds at once, each of hpw waves over the hpw KV
+// heads of a head group, so the heads' tiles of a block (neighbours in the pool) stream from one CU
+// at about the same time. Plan unit r = (plan item r / ngrp, head group r % ngrp); the units are
+// dealt round-robin over the first geff workgroups, geff chosen so that every round but the last is
+// full and the last has as few idle workgroups as the count allows. Inside a workgroup the waves
+// take (unit, head) pairs from an LDS counter, so waves that the memory system serves faster take
+// more; each wave takes and fetches its next pair while the current one still streams.
+template <int D, int BSZ>
+__global__ void __launch_bounds__(64 * MAX_HEADS_PER_WG) __attribute__((amdgpu_waves_per_eu(2)))
+attn_mfma_bf16_kernel(AttnParams P) {
+  __shared__ int unit_ctr;
+  const int hpw = blockDim.x >> 6;
+  const int ngrp = P.kv.n_kv_heads / hpw;
+  const int64_t total = (int64_t)P.n_items[0] * ngrp;
+  if (total == 0) return;
+  const int64_t rounds = (total + gridDim.x - 1) / gridDim.x;
+  const int64_t geff = (total + rounds - 1) / rounds;
+  if ((int64_t)blockIdx.x >= geff) return;   // both returns are uniform over the workgroup
+  // This workgroup's share: plan units r_j = blockIdx.x + j * geff, j < nj, each hpw heads. Its waves
+  // take (j, head) pairs in order from an LDS counter, so a wave that streams faster takes more.
+  const int64_t nj = (total - blockIdx.x + geff - 1) / geff;
+  const int units = (int)(nj * hpw);
+  if (threadIdx.x == 0) unit_ctr = 0;
+  __syncthreads();
+  auto take = [&]() {
+    int t = 0;
+    if ((threadIdx.x & 63) == 0) t = atomicAdd(&unit_ctr, 1);
+    return __builtin_amdgcn_readlane(t, 0);
+  };
+  auto unit_r = [&](int u) { return (int64_t)blockIdx.x + (int64_t)(u / hpw) * geff; };
+  int u = take();
+  if (u >= units) return;
+  ItemRegs cur, nxt;
+  fetch_item<BSZ>(P, unit_r(u) / ngrp, cur);
+  for (;;) {
+    int un = units;
+    // the next unit is taken a few tiles before this one ends, and its metadata fetched then
+    attn_mfma_item<D, BSZ>(P, cur, (int)(unit_r(u) % ngrp) * hpw + u % hpw, [&]() {
+      un = take();
+      fetch_item<BSZ>(P, unit_r(un < units ? un : u) / ngrp, nxt);
+    });
+    if (un >= units) break;
+    cur = nxt;
+    u = un;
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -347,13 +513,16 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnParams P) {
 // ------------------------------------------------------------------------------------------------
 // combine: out[b,t,h,:] = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s, chunks in increasing order
 // ------------------------------------------------------------------------------------------------
+constexpr int COMBINE_ROWS = 4;   // rows (waves) per combine workgroup
+
 template <int DT>
-__global__ void __launch_bounds__(64) attn_combine_kernel(AttnParams P, void* out, int64_t o_sb, int64_t o_st,
-                                                          int64_t o_sh) {
+__global__ void __launch_bounds__(64 * COMBINE_ROWS) attn_combine_kernel(AttnParams P, void* out, int64_t o_sb,
+                                                                         int64_t o_st, int64_t o_sh) {
   typedef Elem<DT> E;
   typedef typename E::T T_;
-  const int lane = threadIdx.x;
-  const int64_t R = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int64_t R = (int64_t)blockIdx.x * COMBINE_ROWS + (threadIdx.x >> 6);
+  if (R >= (int64_t)P.B * P.T * P.H) return;
   const int h = (int)(R % P.H);
   const int bt = (int)(R / P.H);
   const int b = bt / P.T, t = bt - b * P.T;
@@ -366,19 +535,40 @@ __global__ void __launch_bounds__(64) attn_combine_kernel(AttnParams P, void* ou
   }
   const int ns = min(pos / P.split + 1, P.nsplit);  // keys past the table were never visible
   const float* ml = P.ws_ml + R * P.nsplit * 2;
+  const float* pa = P.ws_acc + R * P.nsplit * D;
   float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, ml[2 * s]);
+  for (int s = lane; s < ns; s += 64) M = fmaxf(M, ml[2 * s]);
+  M = wave_max(M);
+  // Chunk s's weight and weighted sum live in lane s % 64; the partial rows are loaded eight chunks
+  // at a time and summed in increasing chunk order.
   float L = 0.f;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  const float* pa = P.ws_acc + R * P.nsplit * D;
-  for (int s = 0; s < ns; ++s) {
-    const float ms = ml[2 * s];
-    const float w = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
-    L += w * ml[2 * s + 1];
+  for (int s0 = 0; s0 < ns; s0 += 64) {
+    float w = 0.f, lw = 0.f;
+    if (s0 + lane < ns) {
+      const float ms = ml[2 * (s0 + lane)];
+      w = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+      lw = w * ml[2 * (s0 + lane) + 1];
+    }
+    const int n = min(64, ns - s0);
+    for (int j = 0; j < n; j += 8) {
+      float v[8][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d = lane + 64 * c;
-      if (d < D) acc[c] += w * pa[(int64_t)s * D + d];
+      for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int d = lane + 64 * c;
+          v[jj][c] = (j + jj < n && d < D) ? pa[(int64_t)(s0 + j + jj) * D + d] : 0.f;
+        }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        if (j + jj < n) {
+          const float wj = __builtin_amdgcn_readlane(__float_as_int(w), j + jj);
+          L += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lw), j + jj));
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[c] += __int_as_float(wj) * v[jj][c];
+        }
+      }
     }
   }
 #pragma unroll
@@ -410,9 +600,41 @@ int attn_split() {
   return split;
 }
 
+// Workgroups of `threads` threads of `fn` that the current device holds at once (cached per device,
+// kernel and size).
+int64_t resident_wgs(const void* fn, int threads) {
+  struct Entry { int dev; const void* fn; int threads; int64_t wgs; };
+  static Entry cache[64];
+  static int n_cache = 0;
+  static std::mutex mu;
+  std::lock_guard<std::mutex> lock(mu);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  for (int i = 0; i < n_cache; ++i)
+    if (cache[i].dev == dev && cache[i].fn == fn && cache[i].threads == threads) return cache[i].wgs;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0) != hipSuccess || per_cu <= 0) return -1;
+  const int64_t w = (int64_t)cus * per_cu;
+  if (n_cache < 64) cache[n_cache++] = Entry{dev, fn, threads, w};
+  return w;
+}
+
 int64_t nsplit_for(int32_t max_blocks, int32_t block_size) {
   const int64_t S = (int64_t)max_blocks * block_size;
   return (S + attn_split() - 1) / attn_split();
+}
+
+// Upper bound of the plan's length: every (row, query tile, chunk).
+int64_t max_items(int32_t B, int32_t T, int32_t n_heads, int32_t max_blocks, int32_t block_size) {
+  const int64_t qtiles = ((int64_t)T * n_heads + QTILE - 1) / QTILE;   // n_heads bounds the group size
+  return (int64_t)B * qtiles * nsplit_for(max_blocks, block_size);
+}
+
+int heads_per_wg(int n_kv_heads) {
+  int h = n_kv_heads < MAX_HEADS_PER_WG ? n_kv_heads : MAX_HEADS_PER_WG;
+  while (n_kv_heads % h) --h;
+  return h;
 }
 
 }  // namespace
@@ -422,7 +644,8 @@ extern "C" int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32
   if (B <= 0 || T <= 0 || n_heads <= 0 || head_dim <= 0 || max_blocks <= 0 || block_size <= 0) return 0;
   const int64_t rows = (int64_t)B * T * n_heads;
   const int64_t ns = nsplit_for(max_blocks, block_size);
-  return rows * ns * (head_dim + 2) * (int64_t)sizeof(float) + 256;
+  const int64_t list = (max_items(B, T, n_heads, max_blocks, block_size) * (int64_t)sizeof(AttnItem) + 255) / 256 * 256;
+  return WS_HEADER + list + rows * ns * (head_dim + 2) * (int64_t)sizeof(float) + 256;
 }
 
 extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
@@ -464,20 +687,33 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
   P.nsplit = (int32_t)nsplit_for(max_blocks, kv->block_size);
   P.split = attn_split();
   const int64_t rows = (int64_t)B * T * n_heads;
-  P.ws_acc = reinterpret_cast<float*>(workspace);
+  char* ws = reinterpret_cast<char*>(workspace);
+  const int64_t list = (max_items(B, T, n_heads, max_blocks, kv->block_size) * (int64_t)sizeof(AttnItem) + 255) / 256 * 256;
+  P.n_items = reinterpret_cast<int32_t*>(ws);
+  P.items = reinterpret_cast<AttnItem*>(ws + WS_HEADER);
+  P.ws_acc = reinterpret_cast<float*>(ws + WS_HEADER + list);
   P.ws_ml = P.ws_acc + rows * P.nsplit * kv->head_dim;
 
   hipStream_t st = fs::as_stream(stream);
   if (mfma_eligible(*kv, q, q_sb, q_st, q_sh)) {
-    const int qtiles = (T * P.G + QTILE - 1) / QTILE;
-    dim3 grid((unsigned)(P.nsplit * kv->n_kv_heads), (unsigned)B, (unsigned)qtiles);
     const bool bs16 = kv->block_size == 16;
+    const void* fn = kv->head_dim == 128
+                         ? (bs16 ? (const void*)attn_mfma_bf16_kernel<128, 16> : (const void*)attn_mfma_bf16_kernel<128, 0>)
+                         : (bs16 ? (const void*)attn_mfma_bf16_kernel<64, 16> : (const void*)attn_mfma_bf16_kernel<64, 0>);
+    const int threads = 64 * heads_per_wg(kv->n_kv_heads);
+    const int64_t wgs = resident_wgs(fn, threads);
+    if (wgs <= 0) {
+      fs::set_error("paged_attention: device occupancy query failed");
+      return (int)hipErrorUnknown;
+    }
+    attn_plan_kernel<<<1, PLAN_THREADS, 0, st>>>(P);
+    const unsigned grid = (unsigned)wgs;
     if (kv->head_dim == 128) {
-      if (bs16) attn_mfma_bf16_kernel<128, 16><<<grid, 64, 0, st>>>(P);
-      else attn_mfma_bf16_kernel<128, 0><<<grid, 64, 0, st>>>(P);
+      if (bs16) attn_mfma_bf16_kernel<128, 16><<<grid, threads, 0, st>>>(P);
+      else attn_mfma_bf16_kernel<128, 0><<<grid, threads, 0, st>>>(P);
     } else {
-      if (bs16) attn_mfma_bf16_kernel<64, 16><<<grid, 64, 0, st>>>(P);
-      else attn_mfma_bf16_kernel<64, 0><<<grid, 64, 0, st>>>(P);
+      if (bs16) attn_mfma_bf16_kernel<64, 16><<<grid, threads, 0, st>>>(P);
+      else attn_mfma_bf16_kernel<64, 0><<<grid, threads, 0, st>>>(P);
     }
   } else {
     dim3 grid((unsigned)rows, (unsigned)P.nsplit);
@@ -488,11 +724,11 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
     }
   }
   if (int e = fs::launch_status("paged_attention")) return e;
-  dim3 cgrid((unsigned)rows);
+  dim3 cgrid((unsigned)((rows + COMBINE_ROWS - 1) / COMBINE_ROWS));
   switch (kv->dtype) {
-    case FS_F32: attn_combine_kernel<FS_F32><<<cgrid, 64, 0, st>>>(P, out, o_sb, o_st, o_sh); break;
-    case FS_BF16: attn_combine_kernel<FS_BF16><<<cgrid, 64, 0, st>>>(P, out, o_sb, o_st, o_sh); break;
-    default: attn_combine_kernel<FS_F16><<<cgrid, 64, 0, st>>>(P, out, o_sb, o_st, o_sh); break;
+    case FS_F32: attn_combine_kernel<FS_F32><<<cgrid, 64 * COMBINE_ROWS, 0, st>>>(P, out, o_sb, o_st, o_sh); break;
+    case FS_BF16: attn_combine_kernel<FS_BF16><<<cgrid, 64 * COMBINE_ROWS, 0, st>>>(P, out, o_sb, o_st, o_sh); break;
+    default: attn_combine_kernel<FS_F16><<<cgrid, 64 * COMBINE_ROWS, 0, st>>>(P, out, o_sb, o_st, o_sh); break;
   }
   return fs::launch_status("paged_attention_combine");
 }
