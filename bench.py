@@ -15,7 +15,13 @@ launching stream around every verify-attention launch of the timed rounds, again
 verify pass, one draft layer's decode step, the LM head and the acceptance at the same shapes,
 scaled to a round.
 
-    python bench.py [--gpus 1] [--steps 128] [--warmup 4]
+    python bench.py [--gpus 1] [--steps 128] [--warmup 4] [--temperature 0.0]
+
+Kernel-only modes (one JSON line each, used for the rocprofv3 counter runs):
+    python bench.py --kernel attention   the verify attention alone: B=64, T=7, 32/8 heads, head_dim 128,
+                                         bf16, contexts U[2048,8192], block 16, tables a random permutation
+    python bench.py --kernel accept      the fused acceptance alone: B=64, k=6, V=128256, bf16 logits
+    python bench.py --kernel copy        1 GiB device-to-device copies, f32 and bf16 (counter calibration)
 """
 
 import argparse
@@ -150,6 +156,125 @@ def cpu_baseline(torch, committed_per_round):
     }
 
 
+def profiled_traffic(name):
+    """HBM bytes per call measured with rocprofv3 counters, from the summary committed under profiles/
+    (its line `traffic_bytes_per_call: N`), or None."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        m = re.search(r"traffic_bytes_per_call:\s*(\d+)", open(path).read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
+def time_accept(torch, ops, reps, warmup):
+    """The acceptance kernel alone at the benchmark shape (bf16 logits, V = 128256): mean seconds per call.
+    The call is captured once into a graph and replayed, so the host's launch overhead is not timed."""
+    v = CFG["vocab_size"]
+    g = torch.Generator(device="cuda").manual_seed(3)
+    tl = torch.randn(BATCH, K + 1, v, device="cuda", generator=g).mul_(2).bfloat16()
+    dl = (tl[:, :K].float() + torch.randn(BATCH, K, v, device="cuda", generator=g) * 0.5).bfloat16()
+    xs = dl.float().argmax(-1).int()
+    temps = torch.ones(BATCH, device="cuda")
+    u = torch.rand(BATCH, K, device="cuda", generator=g)
+    e = torch.empty(BATCH, v, device="cuda").exponential_(generator=g)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(max(warmup, 1)):
+            ops.spec_accept(tl, dl, xs, None, temps, u, e)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.spec_accept(tl, dl, xs, None, temps, u, e)
+    graph.replay()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in ev:
+        a.record()
+        graph.replay()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e-3
+
+
+def attention_inputs(torch, fa, seed=0):
+    """Verify-attention inputs at the benchmark shape: contexts U[2048,8192] (the round benchmark's
+    seed), the k+1 = 7 query positions at the end of each context, block tables a random permutation
+    of the pool, N(0,1) bf16 queries, keys and values."""
+    g = torch.Generator().manual_seed(seed)
+    ctxs = torch.randint(CTX_LO, CTX_HI + 1, (BATCH,), generator=g).tolist()
+    nb = [-(-c // BLOCK) for c in ctxs]
+    n_pool = sum(nb) + 16
+    perm = torch.randperm(n_pool, generator=g)
+    tables = torch.zeros(BATCH, max(nb), dtype=torch.int32)
+    at = 0
+    for i, n in enumerate(nb):
+        tables[i, :n] = perm[at:at + n].int()
+        at += n
+    cfg = fa.ModelConfig(vocab_size=8, d_model=CFG["n_heads"] * 128, n_layers=1, n_heads=CFG["n_heads"],
+                         n_kv_heads=CFG["n_kv_heads"], max_seq_len=16)
+    pool = fa.PagedKVPool(cfg, n_pool, BLOCK, dtype=torch.bfloat16, device="cuda")
+    pool.k_store.normal_()
+    pool.v_store.normal_()
+    q = torch.randn(BATCH, K + 1, CFG["n_heads"], 128, device="cuda").bfloat16()
+    pos = torch.tensor([[c - (K + 1) + i for i in range(K + 1)] for c in ctxs], dtype=torch.int32).cuda()
+    return ctxs, pool, q, pos, tables.cuda()
+
+
+def kernel_mode(args):
+    import torch
+
+    import forgeserve_amd as fa
+    from forgeserve_amd import ops
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    steps, warmup = args.steps, args.warmup
+    if args.kernel == "attention":
+        ctxs, pool, q, pos, tab = attention_inputs(torch, fa, args.seed)
+        lay = pool.layout(0)
+        for _ in range(warmup):
+            ops.paged_attention(q, lay, tab, pos, 128 ** -0.5)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for a, b in ev:
+            a.record()
+            ops.paged_attention(q, lay, tab, pos, 128 ** -0.5)
+            b.record()
+        torch.cuda.synchronize()
+        sec = sum(a.elapsed_time(b) for a, b in ev) / steps * 1e-3
+        byts = attn_bytes(ctxs, K + 1, CFG["n_heads"], CFG["n_kv_heads"], 128, BLOCK)
+        out = {"kernel": "paged_attention verify", "calls": steps, "avg_us": round(sec * 1e6, 2),
+               "algorithmic_bytes": byts, "achieved_GBs": round(byts / sec / 1e9, 1)}
+    elif args.kernel == "accept":
+        sec = time_accept(torch, ops, steps, warmup)
+        byts = accept_bytes(BATCH, K, CFG["vocab_size"])
+        out = {"kernel": "spec_accept", "calls": steps, "avg_us": round(sec * 1e6, 2), "algorithmic_bytes": byts,
+               "achieved_GBs": round(byts / sec / 1e9, 1)}
+    else:
+        # 1 GiB device copies: f32 (16 bytes per lane per load) and bf16 (8 bytes per lane per load)
+        out = {"kernel": "copy 1 GiB", "calls": steps}
+        for name, dt, n in (("f32", torch.float32, 1 << 28), ("bf16", torch.bfloat16, 1 << 29)):
+            src = torch.randn(n, device="cuda").to(dt)
+            dst = torch.empty_like(src)
+            for _ in range(warmup):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(steps):
+                dst.copy_(src)
+            b.record()
+            torch.cuda.synchronize()
+            sec = a.elapsed_time(b) / steps * 1e-3
+            out[name] = {"avg_us": round(sec * 1e6, 2), "read_bytes": 1 << 30, "write_bytes": 1 << 30,
+                         "achieved_GBs": round(2 * (1 << 30) / sec / 1e9, 1)}
+            del src, dst
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,11 +283,15 @@ def main():
     ap.add_argument("--temperature", type=float, default=0.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--kernel", choices=("round", "attention", "accept", "copy"), default="round")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         sys.exit(2)
+    if args.kernel != "round":
+        kernel_mode(args)
+        return
 
     import torch
 
@@ -228,33 +357,8 @@ def main():
     accepted = sb.stats["accepted"] - acc0["accepted"]
     value = committed / elapsed
 
-    # the acceptance kernel alone at the benchmark shape (bf16 logits, V = 128256)
     v = CFG["vocab_size"]
-    tl = torch.randn(BATCH, K + 1, v, device="cuda").mul_(2).bfloat16()
-    dl = (tl[:, :K].float() + torch.randn(BATCH, K, v, device="cuda") * 0.5).bfloat16()
-    xs = dl.float().argmax(-1).int()
-    temps = torch.ones(BATCH, device="cuda")
-    u = torch.rand(BATCH, K, device="cuda")
-    e = torch.empty(BATCH, v, device="cuda").exponential_()
-    # captured once into a graph and replayed, so the host's launch overhead is not timed
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for _ in range(3):
-            ops.spec_accept(tl, dl, xs, None, temps, u, e)
-    torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        ops.spec_accept(tl, dl, xs, None, temps, u, e)
-    graph.replay()
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
-    for a, b in ev:
-        a.record()
-        graph.replay()
-        b.record()
-    torch.cuda.synchronize()
-    acc_avg = sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e-3
+    acc_avg = time_accept(torch, ops, 20, 3)
     acc_gbs = accept_bytes(BATCH, K, v) / acc_avg / 1e9
 
     result = {
@@ -277,12 +381,15 @@ def main():
                        "rate": round(accepted / max(proposed, 1), 4),
                        "committed_per_round": round(committed / args.steps, 2)},
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "paged_attention verify (attn_mfma_bf16_kernel<128> + attn_combine_kernel)",
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic("paged_attention_verify_8b.md"),
+                     "kernel": "paged_attention verify: attn_plan_kernel + attn_mfma_bf16_kernel<128,16> + "
+                               "attn_combine_kernel, one call per layer",
                      "avg_launch_us": round(attn_avg * 1e6, 2),
                      "algorithmic_bytes_per_launch": int(attn_traffic)},
         "accept_kernel": {"avg_us": round(acc_avg * 1e6, 2), "achieved_GBs": round(acc_gbs, 1),
-                          "algorithmic_bytes": accept_bytes(BATCH, K, v)},
+                          "algorithmic_bytes": accept_bytes(BATCH, K, v),
+                          "traffic": profiled_traffic("spec_accept_8b.md")},
     }
     if not args.no_cpu_baseline:
         log("timing the CPU baseline ...")
