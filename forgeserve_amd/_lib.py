@@ -42,7 +42,9 @@ SIGNATURES = {
     "fs_paged_attention": (c_i32, [c_p, c_i64, c_i64, c_i64, ctypes.POINTER(KVLayout), c_p, c_i64, c_i32, c_p,
                                    c_i32, c_i32, c_i32, c_f32, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p]),
     "fs_paged_attention_workspace_size": (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
-    "fs_gemm": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i32, c_p]),
+    "fs_gemm": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i32, c_p, c_i64,
+                        c_p]),
+    "fs_gemm_workspace_size": (c_i64, [c_i64, c_i64, c_i64, c_i32]),
     "fs_add_rmsnorm": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_f32, c_i32, c_p]),
     "fs_silu_mul": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i32, c_p]),
     "fs_embedding": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_i32, c_p]),

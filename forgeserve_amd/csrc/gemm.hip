@@ -163,7 +163,8 @@ __global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ W, int64_t ldw,
                                                             uint16_t* __restrict__ C, int64_t ldc,
                                                             const uint16_t* __restrict__ R, int64_t ldr, int64_t M,
-                                                            int64_t N, int64_t K, int tiles_m, int ntiles) {
+                                                            int64_t N, int64_t K, int tiles_m, int ntiles,
+                                                            float* __restrict__ part) {
   constexpr int KB = 64;                       // k per stage
   constexpr int ROWB = KB * 2;                 // bytes per stage row (128)
   constexpr int XB = BM * ROWB, WB = BN * ROWB, STAGE = XB + WB;
@@ -204,9 +205,13 @@ __global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __re
     gr = gr < N ? gr : N - 1;
     wsrc[i] = W + gr * ldw + 8 * c;
   }
+  // split-K: workgroup row blockIdx.y takes the k-range [split*K/S, (split+1)*K/S)
+  const int split = blockIdx.y;
+  const int nk = (int)(K / KB) / (int)gridDim.y;
+  const int64_t kbase = (int64_t)split * nk * KB;
   auto issue = [&](int kt) {
     const uint32_t base = lds0 + (uint32_t)((kt % NS) * STAGE);
-    const int64_t k0 = (int64_t)kt * KB;
+    const int64_t k0 = kbase + (int64_t)kt * KB;
 #pragma unroll
     for (int i = 0; i < XI; ++i) dma16(xsrc[i] + k0, base + (uint32_t)((i * 4 + wave) * 1024));
 #pragma unroll
@@ -219,7 +224,6 @@ __global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __re
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = (int)(K / KB);
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nk) issue(s);
@@ -254,6 +258,19 @@ __global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __re
   }
 
   // acc[i][j]: lane (l16, g) holds C[m = 16i + l16][n = 16j + 4g + r], r = 0..3 (wave-local)
+  if (part) {   // split-K: f32 partial of this k-range, summed in split order by gemm_splitk_reduce_kernel
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t row = m0 + wm * WM + 16 * i + l16;
+      if (row >= M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t col0 = n0 + wn * WN + 16 * j + 4 * g;   // N % 4 == 0 on this path
+        if (col0 < N) *reinterpret_cast<float4_t*>(part + ((int64_t)split * M + row) * N + col0) = acc[i][j];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int64_t row = m0 + wm * WM + 16 * i + l16;
@@ -278,6 +295,40 @@ __global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __re
           if (col0 + r < N) C[row * ldc + col0 + r] = o[r];
       }
     }
+  }
+}
+
+// C = round(sum_s part[s]) (+ R, rounded again): the split-K partials added in increasing split order,
+// then the same epilogue as the unsplit kernel. Four consecutive elements per thread (N % 4 == 0).
+__global__ void __launch_bounds__(256) gemm_splitk_reduce_kernel(const float* __restrict__ part, int splits,
+                                                                 int64_t M, int64_t N, uint16_t* __restrict__ C,
+                                                                 int64_t ldc, const uint16_t* __restrict__ R,
+                                                                 int64_t ldr) {
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (e >= M * N) return;
+  const int64_t row = e / N, col = e - row * N;
+  float4_t a = *reinterpret_cast<const float4_t*>(part + e);
+  for (int sp = 1; sp < splits; ++sp) {
+    const float4_t b = *reinterpret_cast<const float4_t*>(part + (int64_t)sp * M * N + e);
+    a[0] += b[0];
+    a[1] += b[1];
+    a[2] += b[2];
+    a[3] += b[3];
+  }
+  uint16_t o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = Elem<FS_BF16>::round(a[r]);
+    if (R) v = v + bf16_to_f32(R[row * ldr + col + r]);
+    o[r] = f32_to_bf16(v);
+  }
+  if (((ldc | col) & 3) == 0) {
+    typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+    *reinterpret_cast<u32x2*>(C + row * ldc + col) =
+        u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) C[row * ldc + col + r] = o[r];
   }
 }
 
@@ -340,10 +391,28 @@ __global__ void __launch_bounds__(256) gemm_valu_kernel(const typename Elem<DT>:
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Split-K factor of a bf16 GEMM with K % 64 == 0. It depends on (N, K) only, never on M, so a row's
+// arithmetic (the k-ranges and the order their partials are added) is the same whatever the batch:
+// a decode step and a verify pass produce bit-identical rows. Narrow outputs (N < 16384) are split
+// so that a 64-row decode step still spreads its weight stream over the whole GPU.
+int split_for(int64_t N, int64_t K) {
+  if (K % 64) return 1;
+  int s = 1;
+  while (s < 8 && N * (2 * s) <= 16384 && (K / 64) % (2 * s) == 0 && K / (2 * s) >= 512) s *= 2;
+  return s;
+}
+
 }  // namespace
 
+extern "C" int64_t fs_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int32_t dtype) {
+  if (M <= 0 || N <= 0 || K <= 0 || dtype != FS_BF16) return 0;
+  const int s = split_for(N, K);
+  return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
+}
+
 extern "C" int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, const void* R,
-                       int64_t ldr, int64_t M, int64_t N, int64_t K, int32_t dtype, void* stream) {
+                       int64_t ldr, int64_t M, int64_t N, int64_t K, int32_t dtype, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
   FS_CHECK_ARG(A && B && C, "gemm: null pointer");
   FS_CHECK_ARG(dtype == FS_F32 || dtype == FS_BF16 || dtype == FS_F16, "gemm: dtype %d", dtype);
   FS_CHECK_ARG(M >= 0 && N > 0 && K > 0, "gemm: M %lld N %lld K %lld", (long long)M, (long long)N, (long long)K);
@@ -351,23 +420,46 @@ extern "C" int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, v
   if (M == 0) return 0;
   hipStream_t s = fs::as_stream(stream);
   const bool mfma = dtype == FS_BF16 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B);
-  if (mfma && M > 64 && K % 64 == 0) {
+  if (mfma && K % 64 == 0) {
     const uint16_t* a = (const uint16_t*)A;
     const uint16_t* b = (const uint16_t*)B;
-    const int tm = (int)((M + 127) / 128);
-    const int tn256 = (int)((N + 255) / 256), tn128 = (int)((N + 127) / 128);
-    if ((int64_t)tm * tn256 >= 256) {  // enough tiles to fill the chip with the larger tile
-      const int nt = tm * tn256;
-      gemm_bf16_lds_kernel<128, 256, 3><<<dim3((unsigned)(8 * ((nt + 7) / 8))), 256, 0, s>>>(
-          a, lda, b, ldb, (uint16_t*)C, ldc, (const uint16_t*)R, ldr, M, N, K, tm, nt);
-    } else {
-      const int nt = tm * tn128;
-      gemm_bf16_lds_kernel<128, 128, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8))), 256, 0, s>>>(
-          a, lda, b, ldb, (uint16_t*)C, ldc, (const uint16_t*)R, ldr, M, N, K, tm, nt);
+    const int splits = N % 4 == 0 ? split_for(N, K) : 1;
+    float* part = nullptr;
+    if (splits > 1) {
+      const int64_t need = (int64_t)splits * M * N * (int64_t)sizeof(float);
+      FS_CHECK_ARG(workspace && workspace_bytes >= need && (reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+                   "gemm: workspace %lld < %lld bytes (or unaligned)", (long long)workspace_bytes, (long long)need);
+      part = reinterpret_cast<float*>(workspace);
     }
-    return fs::launch_status("gemm_bf16_lds");
+    uint16_t* c = splits > 1 ? nullptr : (uint16_t*)C;
+    const uint16_t* r = (const uint16_t*)R;
+    if (M <= 64) {
+      const int nt = (int)((N + 63) / 64);
+      gemm_bf16_lds_kernel<64, 64, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 256, 0, s>>>(
+          a, lda, b, ldb, c, ldc, r, ldr, M, N, K, 1, nt, part);
+    } else {
+      const int tm = (int)((M + 127) / 128);
+      const int tn256 = (int)((N + 255) / 256), tn128 = (int)((N + 127) / 128);
+      if ((int64_t)tm * tn256 * splits >= 256) {  // enough tiles to fill the chip with the larger tile
+        const int nt = tm * tn256;
+        gemm_bf16_lds_kernel<128, 256, 3><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 256, 0, s>>>(
+            a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part);
+      } else {
+        const int nt = tm * tn128;
+        gemm_bf16_lds_kernel<128, 128, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 256, 0, s>>>(
+            a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part);
+      }
+    }
+    if (int e = fs::launch_status("gemm_bf16_lds")) return e;
+    if (splits > 1) {
+      const int64_t n4 = M * N / 4;
+      gemm_splitk_reduce_kernel<<<dim3((unsigned)((n4 + 255) / 256)), 256, 0, s>>>(part, splits, M, N, (uint16_t*)C,
+                                                                                   ldc, r, ldr);
+      return fs::launch_status("gemm_splitk_reduce");
+    }
+    return 0;
   }
-  if (mfma) {
+  if (mfma) {   // K % 64 != 0: register-staged MFMA tiles, no split
     const uint16_t* a = (const uint16_t*)A;
     const uint16_t* b = (const uint16_t*)B;
     if (M > 64) {

@@ -83,8 +83,11 @@ def gemm(a: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
         _, ldr = _rows(residual)
         if residual.shape != out.shape or residual.dtype != a.dtype:
             raise ValueError("gemm: residual shape/dtype")
-    check(_lib.load().fs_gemm(ptr(a), lda, ptr(w), ldb, ptr(out), ldc, ptr(residual), ldr, m, n, k, _dt(a),
-                              stream_ptr()), "gemm")
+    lib = _lib.load()
+    need = lib.fs_gemm_workspace_size(m, n, k, _dt(a))
+    ws = _persistent_ws("gemm", need, a.device) if need > 0 else None
+    check(lib.fs_gemm(ptr(a), lda, ptr(w), ldb, ptr(out), ldc, ptr(residual), ldr, m, n, k, _dt(a), ptr(ws),
+                      ws.numel() if ws is not None else 0, stream_ptr()), "gemm")
     return out
 
 

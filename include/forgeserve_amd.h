@@ -107,9 +107,15 @@ int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32_t n_heads,
 
 /* C[M,N] = A[M,K] . B[N,K]^T (+ R[M,N]) in the dtype, f32 accumulation, one rounding of the product
  * and, with R, a second rounding of the sum (nn.Linear then `x + ...`: model.py:77, 93, 105-106,
- * 119-120). Rows may be strided; columns are contiguous. */
+ * 119-120). Rows may be strided; columns are contiguous. A row of C does not depend on M (the
+ * k-order, including any split of K, is a function of N and K only). workspace: at least
+ * fs_gemm_workspace_size(M, N, K, dtype) bytes, 16-byte aligned, any contents (may be NULL when
+ * that size is 0); calls that share a workspace must be ordered on one stream. */
 int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, const void* R,
-            int64_t ldr, int64_t M, int64_t N, int64_t K, int32_t dtype, void* stream);
+            int64_t ldr, int64_t M, int64_t N, int64_t K, int32_t dtype, void* workspace,
+            int64_t workspace_bytes, void* stream);
+
+int64_t fs_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int32_t dtype);
 
 /* RMSNorm of model.py:29-31, optionally after a residual add (model.py:105-106):
  * if delta != NULL: x_out = x + delta (rounded to the dtype) is written, then normed.

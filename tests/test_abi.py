@@ -45,7 +45,7 @@ def test_abi_version(lib):
 
 
 def test_argument_errors_are_reported_not_launched(lib):
-    rc = lib.fs_gemm(None, 0, None, 0, None, 0, None, 0, 4, 4, 4, 1, None)
+    rc = lib.fs_gemm(None, 0, None, 0, None, 0, None, 0, 4, 4, 4, 1, None, 0, None)
     assert rc == -1 and b"null" in lib.fs_last_error()
     rc = lib.fs_spec_accept(None, 0, 0, None, 0, 0, 1, 1, 10, 1, None, None, None, None, None, 0, None, None, None,
                             None, 0, None)
@@ -61,3 +61,7 @@ def test_workspace_sizes_are_positive(lib):
     assert lib.fs_spec_accept_workspace_size(64, 6, 128256) > 0
     assert lib.fs_sampling_workspace_size(64, 128256) > 0
     assert lib.fs_paged_attention_workspace_size(0, 1, 1, 1, 1, 1) == 0
+    # split-K partials: a function of (N, K) only, sized for M rows
+    assert lib.fs_gemm_workspace_size(448, 4096, 4096, 1) == 4 * 448 * 4096 * 4
+    assert lib.fs_gemm_workspace_size(64, 28672, 4096, 1) == 0
+    assert lib.fs_gemm_workspace_size(64, 4096, 4096, 0) == 0

@@ -24,7 +24,7 @@ def rel_err(got, ref):
 # ---- GEMM -------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("m,n,k", [(1, 48, 64), (7, 256, 688), (64, 1000, 256), (65, 384, 512), (448, 640, 4096),
-                                   (130, 96, 192)])
+                                   (130, 96, 192), (20, 4096, 1024), (100, 2048, 2048)])  # the last two split K
 def test_gemm_matches_fp64(dtype, m, n, k):
     case("gemm", dtype, m, n, k)
     g = torch.Generator().manual_seed(m * 7 + n)
@@ -41,12 +41,13 @@ def test_gemm_matches_fp64(dtype, m, n, k):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_gemm_rows_do_not_depend_on_the_batch(dtype):
+@pytest.mark.parametrize("n,k", [(384, 512), (2048, 2048)])   # (2048, 2048) splits K four ways
+def test_gemm_rows_do_not_depend_on_the_batch(dtype, n, k):
     """A row's result is bit-identical whether it is computed alone, among 64 rows or among 448."""
-    case("gemm invariance", dtype)
+    case("gemm invariance", dtype, n, k)
     g = torch.Generator().manual_seed(1)
-    a = torch.randn(448, 512, generator=g).to(dtype).to(DEV)
-    w = (torch.randn(384, 512, generator=g) * 0.05).to(dtype).to(DEV)
+    a = torch.randn(448, k, generator=g).to(dtype).to(DEV)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(dtype).to(DEV)
     full = ops.gemm(a, w)
     mid = ops.gemm(a[:64], w)
     for i in (0, 5, 63):
@@ -55,12 +56,13 @@ def test_gemm_rows_do_not_depend_on_the_batch(dtype):
     assert torch.equal(ops.gemm(a[100:107], w), full[100:107])
 
 
-def test_gemm_residual_epilogue():
-    case("gemm residual")
+@pytest.mark.parametrize("n,k", [(128, 256), (4096, 1024)])   # (4096, 1024) splits K
+def test_gemm_residual_epilogue(n, k):
+    case("gemm residual", n, k)
     g = torch.Generator().manual_seed(2)
-    a = torch.randn(70, 256, generator=g).bfloat16().to(DEV)
-    w = (torch.randn(128, 256, generator=g) * 0.05).bfloat16().to(DEV)
-    r = torch.randn(70, 128, generator=g).bfloat16().to(DEV)
+    a = torch.randn(70, k, generator=g).bfloat16().to(DEV)
+    w = (torch.randn(n, k, generator=g) * 0.05).bfloat16().to(DEV)
+    r = torch.randn(70, n, generator=g).bfloat16().to(DEV)
     fused = ops.gemm(a, w, residual=r)
     two_step = (ops.gemm(a, w).float() + r.float()).bfloat16()   # x + linear(...) rounds twice
     assert torch.equal(fused, two_step)
