@@ -158,8 +158,8 @@ FS_DEVICE void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int BM, int BN, int NS>
-__global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __restrict__ X, int64_t ldx,
+template <int BM, int BN, int NS, int WGM = 2, int WGN = 2>
+__global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uint16_t* __restrict__ X, int64_t ldx,
                                                             const uint16_t* __restrict__ W, int64_t ldw,
                                                             uint16_t* __restrict__ C, int64_t ldc,
                                                             const uint16_t* __restrict__ R, int64_t ldr, int64_t M,
@@ -167,10 +167,12 @@ __global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __re
                                                             float* __restrict__ part) {
   constexpr int KB = 64;                       // k per stage
   constexpr int ROWB = KB * 2;                 // bytes per stage row (128)
+  constexpr int NW = WGM * WGN;                // waves: WGM along M, WGN along N
   constexpr int XB = BM * ROWB, WB = BN * ROWB, STAGE = XB + WB;
-  constexpr int XI = XB / 4096, WI = WB / 4096;  // dma instructions per wave per stage (4 waves x 1 KB)
-  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
-  static_assert(XB % 4096 == 0 && WB % 4096 == 0, "tile rows must fill whole 1 KB wave copies");
+  constexpr int XI = XB / (NW * 1024), WI = WB / (NW * 1024);  // dma instructions per wave per stage
+  constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
+  static_assert(XB % (NW * 1024) == 0 && WB % (NW * 1024) == 0, "tile rows must fill whole 1 KB wave copies");
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tiles are whole 16x16 MFMA tiles");
   __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE];
 
   // XCD-aware order: workgroup ids go round-robin over the 8 XCDs; give each XCD a contiguous range
@@ -183,7 +185,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __re
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g = lane >> 4;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
   // this lane's source rows/chunks for its share of a stage (fixed across stages but for k0)
@@ -191,7 +193,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __re
   const uint16_t* wsrc[WI];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
-    const int P = (i * 4 + wave) * 64 + lane;  // 16-byte chunk index inside the X stage
+    const int P = (i * NW + wave) * 64 + lane;  // 16-byte chunk index inside the X stage
     const int r = P >> 3, c = (P & 7) ^ (r & 7);
     int64_t gr = m0 + r;
     gr = gr < M ? gr : M - 1;
@@ -199,7 +201,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __re
   }
 #pragma unroll
   for (int i = 0; i < WI; ++i) {
-    const int P = (i * 4 + wave) * 64 + lane;
+    const int P = (i * NW + wave) * 64 + lane;
     const int r = P >> 3, c = (P & 7) ^ (r & 7);
     int64_t gr = n0 + r;
     gr = gr < N ? gr : N - 1;
@@ -213,9 +215,9 @@ __global__ void __launch_bounds__(256) gemm_bf16_lds_kernel(const uint16_t* __re
     const uint32_t base = lds0 + (uint32_t)((kt % NS) * STAGE);
     const int64_t k0 = kbase + (int64_t)kt * KB;
 #pragma unroll
-    for (int i = 0; i < XI; ++i) dma16(xsrc[i] + k0, base + (uint32_t)((i * 4 + wave) * 1024));
+    for (int i = 0; i < XI; ++i) dma16(xsrc[i] + k0, base + (uint32_t)((i * NW + wave) * 1024));
 #pragma unroll
-    for (int i = 0; i < WI; ++i) dma16(wsrc[i] + k0, base + XB + (uint32_t)((i * 4 + wave) * 1024));
+    for (int i = 0; i < WI; ++i) dma16(wsrc[i] + k0, base + XB + (uint32_t)((i * NW + wave) * 1024));
   };
 
   float4_t acc[TM][TN];
@@ -438,15 +440,21 @@ extern "C" int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, v
       gemm_bf16_lds_kernel<64, 64, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 256, 0, s>>>(
           a, lda, b, ldb, c, ldc, r, ldr, M, N, K, 1, nt, part);
     } else {
-      const int tm = (int)((M + 127) / 128);
-      const int tn256 = (int)((N + 255) / 256), tn128 = (int)((N + 127) / 128);
-      if ((int64_t)tm * tn256 * splits >= 256) {  // enough tiles to fill the chip with the larger tile
-        const int nt = tm * tn256;
-        gemm_bf16_lds_kernel<128, 256, 3><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 256, 0, s>>>(
+      // tile by how many tiles (x splits) the shape yields: the largest tile that still fills the
+      // GPU (measured at M = 448 and 128 on the decoder's projections)
+      const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256) * splits;
+      const int64_t t128 = ((M + 127) / 128) * ((N + 255) / 256) * splits;
+      if (t256 >= 192) {
+        const int tm = (int)((M + 255) / 256), nt = tm * (int)((N + 255) / 256);
+        gemm_bf16_lds_kernel<256, 256, 2, 4, 2><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 512, 0, s>>>(
+            a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part);
+      } else if (t128 >= 128) {
+        const int tm = (int)((M + 127) / 128), nt = tm * (int)((N + 255) / 256);
+        gemm_bf16_lds_kernel<128, 256, 3, 2, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 512, 0, s>>>(
             a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part);
       } else {
-        const int nt = tm * tn128;
-        gemm_bf16_lds_kernel<128, 128, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 256, 0, s>>>(
+        const int tm = (int)((M + 127) / 128), nt = tm * (int)((N + 127) / 128);
+        gemm_bf16_lds_kernel<128, 128, 4, 2, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 512, 0, s>>>(
             a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part);
       }
     }
