@@ -21,6 +21,15 @@ constexpr int THREADS = 256;
 constexpr int VEC = 8;                       // consecutive columns per thread group
 constexpr int UNROLL = 8;                    // groups per thread per chunk: 8 16-byte loads in flight
 constexpr int CH = THREADS * VEC * UNROLL;   // 16384 columns per chunk
+constexpr int UNROLL_R = 2;                  // the acceptance's residual and argmax passes:
+constexpr int CHR = THREADS * VEC * UNROLL_R;  // 4096 columns per chunk (many workgroups for two rows)
+
+// Arithmetic type of the probabilities: the logits path works on the float32 softmax
+// (sampling.py:13), the probabilities path in the dtype it is given.
+template <int DT, bool PROBS>
+struct ProbType {
+  static constexpr int value = PROBS ? DT : FS_F32;
+};
 constexpr float LOG2E_F = 1.4426950408889634f;
 
 struct Stat {
@@ -293,7 +302,8 @@ struct AcceptArgs {
   RowSet rs;             // n0 = K+1 target rows, n1 = K draft rows
   int32_t K;
   int64_t V;
-  int nch;
+  int nch;               // 16K-column chunks of the statistics pass
+  int nchr;              // 4K-column chunks of the residual and argmax passes
   int B;
   const int32_t* draft;  // [B, K]
   const int32_t* k_eff;  // [B] or null (= K)
@@ -303,9 +313,9 @@ struct AcceptArgs {
   int64_t ldE;
   Stat* stats;           // [B*(2K+1)][nch] chunk partials (logits mode)
   Stat* mstats;          // [B*(2K+1)] merged row statistics (logits mode)
-  float* resid;          // [B][nch] residual partial sums of the rejected row pair
-  float* pv;             // [B][nch]
-  int* pi;               // [B][nch]
+  float* resid;          // [B][nchr] residual partial sums of the rejected row pair
+  float* pv;             // [B][nchr]
+  int* pi;               // [B][nchr]
   int* jpos;             // [B]
   int32_t* out_tokens;   // [B, K+1]
   int32_t* n_acc;        // [B]
@@ -339,27 +349,35 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
     __threadfence_block();
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    int j = ke;
-    for (int i = 0; i < ke; ++i) {
+  // every proposal's test at once, one lane each; the first rejection ends the walk (speculative.py:25-29)
+  int j = ke;
+  for (int i0 = 0; i0 < ke && j == ke; i0 += 64) {
+    const int i = i0 + (int)threadIdx.x;
+    bool accept = false;
+    if (threadIdx.x < 64 && i < ke) {
       const int x = A.draft[(int64_t)b * A.K + i];
-      if (x < 0 || x >= A.V) { j = i; break; }  // an invalid proposal is never accepted
-      const auto* pr = row_ptr<DT>(A.rs, b, i);
-      const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + i);
-      float px, qx;
-      if (PROBS) {
-        px = Elem<DT>::load(pr, x);
-        qx = Elem<DT>::load(qr, x);
-      } else if (T > 0.f) {
-        px = softmax_at(Elem<DT>::load(pr, x), T, A.mstats[(int64_t)b * per + i]);
-        qx = softmax_at(Elem<DT>::load(qr, x), T, A.mstats[(int64_t)b * per + A.rs.n0 + i]);
-      } else {  // one-hot rows of the first argmax (sampling.py:11-12)
-        px = A.mstats[(int64_t)b * per + i].ai == x ? 1.f : 0.f;
-        qx = A.mstats[(int64_t)b * per + A.rs.n0 + i].ai == x ? 1.f : 0.f;
+      if (x >= 0 && x < A.V) {   // an invalid proposal is never accepted
+        const auto* pr = row_ptr<DT>(A.rs, b, i);
+        const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + i);
+        float px, qx;
+        if (PROBS) {
+          px = Elem<DT>::load(pr, x);
+          qx = Elem<DT>::load(qr, x);
+        } else if (T > 0.f) {
+          px = softmax_at(Elem<DT>::load(pr, x), T, A.mstats[(int64_t)b * per + i]);
+          qx = softmax_at(Elem<DT>::load(qr, x), T, A.mstats[(int64_t)b * per + A.rs.n0 + i]);
+        } else {  // one-hot rows of the first argmax (sampling.py:11-12)
+          px = A.mstats[(int64_t)b * per + i].ai == x ? 1.f : 0.f;
+          qx = A.mstats[(int64_t)b * per + A.rs.n0 + i].ai == x ? 1.f : 0.f;
+        }
+        const float ratio = qx > 0.f ? Elem<ProbType<DT, PROBS>::value>::round(px / qx) : 1.0f;  // speculative.py:26
+        accept = A.u[(int64_t)b * A.K + i] < fminf(1.0f, ratio);
       }
-      const float ratio = qx > 0.f ? Elem<DT>::round(px / qx) : 1.0f;  // speculative.py:26
-      if (!(A.u[(int64_t)b * A.K + i] < fminf(1.0f, ratio))) { j = i; break; }
     }
+    const uint64_t rejected = __ballot(threadIdx.x < 64 && i < ke && !accept);
+    if (rejected) j = i0 + __ffsll((unsigned long long)rejected) - 1;
+  }
+  if (threadIdx.x == 0) {
     A.jpos[b] = j;
     if (!PROBS && T <= 0.f) write_outputs(A, b, j, A.mstats[(int64_t)b * per + j].ai);
   }
@@ -368,6 +386,7 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
 // launch 3: residual partial sums of the rejected row pair (speculative.py:30), one chunk each
 template <int DT, bool PROBS>
 __global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) {
+  constexpr int PD = ProbType<DT, PROBS>::value;
   __shared__ float shf[THREADS / 64];
   const int c = blockIdx.x, b = blockIdx.y;
   const int ke = keff_of(A, b);
@@ -383,27 +402,27 @@ __global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) 
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + j);
   const bool vec_ok = (A.V % VEC) == 0 && (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr)) & 15) == 0);
-  float xp[UNROLL][8], xq[UNROLL][8];
+  float xp[UNROLL_R][8], xq[UNROLL_R][8];
 #pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+  for (int u = 0; u < UNROLL_R; ++u) {
+    const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
     load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp[u]);
     load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq[u]);
   }
   float ls = 0.f;
 #pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+  for (int u = 0; u < UNROLL_R; ++u) {
+    const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
       if (v0 + jj >= A.V) continue;
       const float p = PROBS ? xp[u][jj] : sp(xp[u][jj]);
       const float q = PROBS ? xq[u][jj] : sq(xq[u][jj]);
-      ls += fmaxf(Elem<DT>::round(p - q), 0.f);  // (p - q).clamp(min=0)
+      ls += fmaxf(Elem<PD>::round(p - q), 0.f);  // (p - q).clamp(min=0)
     }
   }
   const float tot = block_sum(ls, shf);
-  if (threadIdx.x == 0) A.resid[(int64_t)b * A.nch + c] = tot;
+  if (threadIdx.x == 0) A.resid[(int64_t)b * A.nchr + c] = tot;
 }
 
 // launch 1 (logits): per-(row, chunk) statistics of every row a sequence uses
@@ -432,6 +451,7 @@ __global__ void __launch_bounds__(64) accept_step_kernel(AcceptArgs A) {
 // launch 4: argmax over a chunk of w_v / E_v (w the normalised residual, or the bonus row)
 template <int DT, bool PROBS>
 __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
+  constexpr int PD = ProbType<DT, PROBS>::value;
   __shared__ float shf[THREADS / 64];
   __shared__ int shi[THREADS / 64];
   const int c = blockIdx.x, b = blockIdx.y;
@@ -448,55 +468,61 @@ __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
   }
   float s = 0.f;  // the residual sum, merged in chunk order (every workgroup merges the same way)
   if (!bonus)
-    for (int cc = 0; cc < A.nch; ++cc) s += A.resid[(int64_t)b * A.nch + cc];
-  s = Elem<DT>::round(s);
+    for (int cc = 0; cc < A.nchr; ++cc) s += A.resid[(int64_t)b * A.nchr + cc];
+  s = Elem<PD>::round(s);
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j);
   const float* er = A.E + (int64_t)b * A.ldE;
   const bool vec_ok = (A.V % VEC) == 0 &&
                       (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr) |
                          reinterpret_cast<uintptr_t>(er)) & 15) == 0);
+  float xp[UNROLL_R][8], xq[UNROLL_R][8], e[UNROLL_R][8];
+#pragma unroll
+  for (int u = 0; u < UNROLL_R; ++u) {   // every load of the chunk in flight before any arithmetic
+    const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+    load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp[u]);
+    if (!bonus) load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq[u]);
+    load8_f32(er, v0, A.V, vec_ok, e[u]);
+  }
   float bv = -INFINITY;
   int bi = 0x7fffffff;
 #pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
-    float xp[8], xq[8], e[8];
-    load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp);
-    if (!bonus) load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq);
-    load8_f32(er, v0, A.V, vec_ok, e);
+  for (int u = 0; u < UNROLL_R; ++u) {
+    const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
       if (v0 + jj >= A.V) continue;
-      const float p = PROBS ? xp[jj] : sp(xp[jj]);
+      const float p = PROBS ? xp[u][jj] : sp(xp[u][jj]);
       float w;
       if (bonus) {
         w = p;  // speculative.py:33
       } else {
-        const float q = PROBS ? xq[jj] : sq(xq[jj]);
-        const float r = fmaxf(Elem<DT>::round(p - q), 0.f);
-        w = s > 0.f ? Elem<DT>::round(r / s) : p;  // speculative.py:31
+        const float q = PROBS ? xq[u][jj] : sq(xq[u][jj]);
+        const float r = fmaxf(Elem<PD>::round(p - q), 0.f);
+        w = s > 0.f ? Elem<PD>::round(r / s) : p;  // speculative.py:31
       }
-      argmax_merge(bv, bi, w / e[jj], (int)(v0 + jj));
+      argmax_merge(bv, bi, w / e[u][jj], (int)(v0 + jj));
     }
   }
   block_argmax(bv, bi, shf, shi);
   if (threadIdx.x == 0) {
-    A.pv[(int64_t)b * A.nch + c] = bv;
-    A.pi[(int64_t)b * A.nch + c] = bi;
+    A.pv[(int64_t)b * A.nchr + c] = bv;
+    A.pi[(int64_t)b * A.nchr + c] = bi;
   }
 }
 
-// launch 5: merge the chunk winners of sampled sequences, write outputs and the rollback
+// launch 5: merge the chunk winners of sampled sequences, write outputs and the rollback; one wave
+// per sequence, lane c holding chunk c's winner (winners merged by value, then lowest index)
 template <bool PROBS>
-__global__ void accept_final_kernel(AcceptArgs A) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= A.B) return;
+__global__ void __launch_bounds__(64) accept_final_kernel(AcceptArgs A) {
+  const int b = blockIdx.x;
   if (!PROBS && A.temps[b] <= 0.f) return;  // greedy sequences were finished by the step
-  float v = A.pv[(int64_t)b * A.nch];
-  int extra = A.pi[(int64_t)b * A.nch];
-  for (int c = 1; c < A.nch; ++c) argmax_merge(v, extra, A.pv[(int64_t)b * A.nch + c], A.pi[(int64_t)b * A.nch + c]);
-  write_outputs(A, b, A.jpos[b], extra);
+  float v = -INFINITY;
+  int extra = 0x7fffffff;
+  for (int c = threadIdx.x; c < A.nchr; c += 64)
+    argmax_merge(v, extra, A.pv[(int64_t)b * A.nchr + c], A.pi[(int64_t)b * A.nchr + c]);
+  wave_argmax(v, extra);
+  if (threadIdx.x == 0) write_outputs(A, b, A.jpos[b], extra);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -539,20 +565,22 @@ struct Carve {
 
 int64_t nchunks(int64_t V) { return (V + CH - 1) / CH; }
 
+int64_t nchunks_r(int64_t V) { return (V + CHR - 1) / CHR; }
+
 int64_t accept_ws(int64_t B, int64_t K, int64_t V) {
-  const int64_t nch = nchunks(V);
+  const int64_t nch = nchunks(V), nchr = nchunks_r(V);
   auto r = [](int64_t n) { return ((n + 255) / 256) * 256; };
   return r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) +
-         r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) + 3 * r(B * nch * 4) + r(B * 4);
+         r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) + 3 * r(B * nchr * 4) + r(B * 4);
 }
 
-void carve_accept(AcceptArgs& A, void* workspace, int64_t B, int64_t K, int nch) {
+void carve_accept(AcceptArgs& A, void* workspace, int64_t B, int64_t K, int nch, int nchr) {
   Carve cv{reinterpret_cast<char*>(workspace)};
   A.stats = cv.take<Stat>(B * (2 * K + 1) * nch);
   A.mstats = cv.take<Stat>(B * (2 * K + 1));
-  A.pv = cv.take<float>(B * nch);
-  A.pi = cv.take<int>(B * nch);
-  A.resid = cv.take<float>(B * nch);
+  A.pv = cv.take<float>(B * nchr);
+  A.pi = cv.take<int>(B * nchr);
+  A.resid = cv.take<float>(B * nchr);
   A.jpos = cv.take<int>(B);
 }
 
@@ -561,8 +589,8 @@ bool dtype_ok(int32_t dt) { return dt == FS_F32 || dt == FS_BF16 || dt == FS_F16
 template <int DT>
 int launch_accept(const AcceptArgs& A, bool probs, hipStream_t s) {
   const int per = A.rs.n0 + A.rs.n1;
-  const dim3 chunks((unsigned)A.nch, (unsigned)A.B);
-  const dim3 finals((unsigned)((A.B + 63) / 64));
+  const dim3 chunks((unsigned)A.nchr, (unsigned)A.B);
+  const dim3 finals((unsigned)A.B);
   if (!probs) {
     accept_stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(A.B * per)), THREADS, 0, s>>>(A);
     accept_step_kernel<DT, false><<<dim3((unsigned)A.B), 64, 0, s>>>(A);
@@ -681,6 +709,7 @@ extern "C" int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, c
   A.K = K;
   A.V = V;
   A.nch = nch;
+  A.nchr = (int)nchunks_r(V);
   A.B = B;
   A.draft = draft_tokens;
   A.k_eff = k_eff;
@@ -691,7 +720,7 @@ extern "C" int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, c
   A.out_tokens = out_tokens;
   A.n_acc = n_accepted;
   A.seq_len = seq_len;
-  carve_accept(A, workspace, B, K, nch);
+  carve_accept(A, workspace, B, K, nch, A.nchr);
   hipStream_t s = fs::as_stream(stream);
   switch (dtype) {
     case FS_F32: return launch_accept<FS_F32>(A, false, s);
@@ -715,6 +744,7 @@ extern "C" int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_
   A.K = K;
   A.V = V;
   A.nch = nch;
+  A.nchr = (int)nchunks_r(V);
   A.B = 1;
   A.draft = draft_tokens;
   A.k_eff = nullptr;
@@ -725,7 +755,7 @@ extern "C" int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_
   A.out_tokens = out_tokens;
   A.n_acc = n_accepted;
   A.seq_len = nullptr;
-  carve_accept(A, workspace, 1, K, nch);
+  carve_accept(A, workspace, 1, K, nch, A.nchr);
   hipStream_t s = fs::as_stream(stream);
   switch (dtype) {
     case FS_F32: return launch_accept<FS_F32>(A, true, s);
