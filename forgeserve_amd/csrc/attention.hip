@@ -23,14 +23,11 @@
 #include <math.h>
 #include <stdlib.h>
 
-#include <mutex>
-
 #include "common.h"
 
 namespace {
 
 constexpr int QTILE = 32;            // query rows per MFMA wave
-constexpr int MAX_HEADS_PER_WG = 8;  // waves (KV heads) per MFMA workgroup, at most
 constexpr int PLAN_THREADS = 256;
 constexpr int64_t WS_HEADER = 256;    // workspace: item count, then the item list, then the partials
 constexpr float LOG2E = 1.4426950408889634f;
@@ -48,9 +45,14 @@ struct AttnParams {
   float* ws_acc;                     // [B*T*H][nsplit][D]
   float* ws_ml;                      // [B*T*H][nsplit][2]
   int32_t nsplit;
-  int32_t split;                     // keys per chunk: a multiple of 16, at most 512
+  int32_t split;                     // keys per chunk: a multiple of 16
   struct AttnItem* items;            // MFMA path: the work list written by attn_plan_kernel
   int32_t* n_items;                  // its length
+  // MFMA path: a query that sees one chunk only (position < split, or nsplit == 1) has its output
+  // written by that chunk's workgroup, and attn_combine leaves it alone
+  int32_t direct;
+  void* out;
+  int64_t o_sb, o_st, o_sh;
 };
 
 // Reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48) with the gfx950
@@ -100,118 +102,147 @@ FS_DEVICE int tile_qmax(const AttnParams& P, int b, int z) {
   return q;
 }
 
-FS_DEVICE int tile_chunks(const AttnParams& P, int qmax) { return qmax < 0 ? 0 : min(qmax / P.split + 1, P.nsplit); }
+// Chunks a query tile reads. With direct outputs a tile of padding queries still gets chunk 0, whose
+// workgroup writes their zero outputs.
+FS_DEVICE int tile_chunks(const AttnParams& P, int qmax) {
+  return qmax < 0 ? (P.direct ? 1 : 0) : min(qmax / P.split + 1, P.nsplit);
+}
+
+constexpr int UNIT_WAVES = 8;                  // waves per unit workgroup
+constexpr int MAX_SPLIT = 64 * 16 * UNIT_WAVES;   // keys per chunk, at most: a wave's tiles fit one wavefront
 
 // One workgroup lists every item: first the chunks that lie wholly below their tile's furthest
-// query (the full chunks), tile by tile, then the last chunk of each tile. The shorter last chunks
-// thus make up the attention kernel's final round, where they even out the finish.
+// query (the full chunks), tile by tile, then the last chunk of each tile, longest first. Workgroups
+// start in list order, so the short last chunks even out the finish (longest-first list scheduling).
+// Inclusive scan of one int per thread over the workgroup: lane scans inside each wave, then the
+// wave totals (two barriers). `tot` receives the workgroup's total.
+FS_DEVICE int block_scan(int x, int* sh, int& tot) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) sh[wv] = x;
+  __syncthreads();
+  int before = 0;
+  tot = 0;
+#pragma unroll
+  for (int k = 0; k < PLAN_THREADS / 64; ++k) {
+    const int t = sh[k];
+    if (k < wv) before += t;
+    tot += t;
+  }
+  __syncthreads();
+  return x + before;
+}
+
 __global__ void __launch_bounds__(PLAN_THREADS) attn_plan_kernel(AttnParams P) {
-  __shared__ int sa[PLAN_THREADS], sb[PLAN_THREADS];
+  __shared__ int sh[PLAN_THREADS / 64];
+  __shared__ int cursor[MAX_SPLIT / 16 + 1];   // last chunks by length in 16-key tiles
   const int tid = threadIdx.x;
   const int qtiles = (P.T * P.G + QTILE - 1) / QTILE;
   const int U = P.B * qtiles;
-  int nf = 0;
-  for (int u = tid; u < U; u += PLAN_THREADS) nf += max(tile_chunks(P, tile_qmax(P, u / qtiles, u % qtiles)) - 1, 0);
-  sa[tid] = nf;
-  __syncthreads();
-  for (int off = PLAN_THREADS / 2; off > 0; off >>= 1) {
-    if (tid < off) sa[tid] += sa[tid + off];
-    __syncthreads();
+  const int nlen = P.split / 16;   // a last chunk holds 1..nlen tiles (an empty one counts as 1)
+  for (int i = tid; i <= nlen; i += PLAN_THREADS) cursor[i] = 0;
+  // the thread's first tile (u = tid) stays in registers; tiles past the first PLAN_THREADS are
+  // recomputed when needed
+  int qm0 = -1, nch0 = 0;
+  if (tid < U) {
+    qm0 = tile_qmax(P, tid / qtiles, tid % qtiles);
+    nch0 = tile_chunks(P, qm0);
   }
-  const int n_full = sa[0];
-  __syncthreads();
-  int base_full = 0, base_last = 0;
-  for (int u0 = 0; u0 < U; u0 += PLAN_THREADS) {
-    const int u = u0 + tid;
-    int b = 0, z = 0, qm = -1, nch = 0;
-    if (u < U) {
-      b = u / qtiles;
-      z = u - b * qtiles;
-      qm = tile_qmax(P, b, z);
+  auto tile = [&](int u, int& qm, int& nch) {
+    if (u == tid) {
+      qm = qm0;
+      nch = nch0;
+    } else {
+      qm = tile_qmax(P, u / qtiles, u % qtiles);
       nch = tile_chunks(P, qm);
     }
-    const int f = max(nch - 1, 0), l = nch > 0 ? 1 : 0;
-    sa[tid] = f;
-    sb[tid] = l;
-    __syncthreads();
-    for (int off = 1; off < PLAN_THREADS; off <<= 1) {   // inclusive scans
-      const int xa = tid >= off ? sa[tid - off] : 0;
-      const int xb = tid >= off ? sb[tid - off] : 0;
-      __syncthreads();
-      sa[tid] += xa;
-      sb[tid] += xb;
-      __syncthreads();
+  };
+  auto last_tiles = [&](int qm, int nch) { return max(min((qm + 1 - (nch - 1) * P.split + 15) >> 4, nlen), 1); };
+  __syncthreads();
+  int nf = 0;
+  for (int u = tid; u < U; u += PLAN_THREADS) {   // full chunks, and a histogram of the last chunks' lengths
+    int qm, nch;
+    tile(u, qm, nch);
+    nf += max(nch - 1, 0);
+    if (nch > 0) atomicAdd(&cursor[last_tiles(qm, nch)], 1);
+  }
+  int n_full;
+  block_scan(nf, sh, n_full);
+  {   // exclusive scan from the longest length down: cursor[len] = first slot of that length
+    constexpr int PER = (MAX_SPLIT / 16 + PLAN_THREADS - 1) / PLAN_THREADS;
+    int c[PER], loc = 0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {   // thread tid owns lengths nlen - PER*tid - k
+      const int len = nlen - PER * tid - k;
+      c[k] = len >= 1 ? cursor[len] : 0;
+      loc += c[k];
     }
-    const int ef = base_full + sa[tid] - f, el = n_full + base_last + sb[tid] - l;
-    for (int c = 0; c < f; ++c) P.items[ef + c] = AttnItem{b, z, c, qm};
-    if (l) P.items[el] = AttnItem{b, z, nch - 1, qm};
-    base_full += sa[PLAN_THREADS - 1];
-    base_last += sb[PLAN_THREADS - 1];
+    int n_last;
+    int run = n_full + block_scan(loc, sh, n_last) - loc;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int len = nlen - PER * tid - k;
+      if (len >= 1) cursor[len] = run;
+      run += c[k];
+    }
+    if (tid == 0) P.n_items[0] = n_full + n_last;
     __syncthreads();
   }
-  if (tid == 0) P.n_items[0] = n_full + base_last;
+  int base_full = 0;
+  for (int u0 = 0; u0 < U; u0 += PLAN_THREADS) {
+    const int u = u0 + tid;
+    int qm = -1, nch = 0;
+    if (u < U) tile(u, qm, nch);
+    const int b = u / qtiles, z = u - b * qtiles;
+    const int f = max(nch - 1, 0);
+    int n_round;
+    const int ef = base_full + block_scan(f, sh, n_round) - f;
+    for (int c = 0; c < f; ++c) P.items[ef + c] = AttnItem{b, z, c, qm};
+    // the slot order inside one length is whatever the atomics give: it only changes which
+    // workgroup runs an item, never what the item computes
+    if (nch > 0) P.items[atomicAdd(&cursor[last_tiles(qm, nch)], 1)] = AttnItem{b, z, nch - 1, qm};
+    base_full += n_round;
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
 // MFMA kernel (bf16)
 // ------------------------------------------------------------------------------------------------
-// What one wave needs of an item before its first tile load.
-struct ItemRegs {
-  int b, z, s, qmax;     // wave-uniform
-  int rpos[2];           // positions of the lane's two query rows (row = 16*nt + lane%16), -1: none
-  int phys;              // lane i: table entry of the chunk's i-th block (-1 past the table)
-};
+// ------------------------------------------------------------------------------------------------
+// unit kernel: one workgroup of UNIT_WAVES waves per (plan item, KV head)
+// ------------------------------------------------------------------------------------------------
+// The item's keys [kbeg, kend) are cut into 16-key tiles; wave w takes tiles w, w + UNIT_WAVES, ...
+// in increasing order and keeps its own softmax partial, and the waves' partials are merged through
+// LDS in wave order. Which tiles a wave sees, and in what order, depends only on absolute key
+// positions, and a tile wholly above a query's position leaves that query's partial exactly as it
+// was; a query's result therefore does not depend on the other queries of its tile.
 
-template <int BSZ>
-FS_DEVICE void fetch_item(const AttnParams& P, int64_t e_idx, ItemRegs& it) {
-  // the list is read-only here: a constant-address-space load keeps it on the scalar unit
-  typedef __attribute__((address_space(4))) const AttnItem ConstItem;
-  ConstItem* ep = (ConstItem*)(uintptr_t)(P.items + e_idx);
-  const AttnItem e{ep->b, ep->z, ep->s, ep->qmax};
-  it.b = e.b;
-  it.z = e.z;
-  it.s = e.s;
-  it.qmax = e.qmax;
-  const int lane = threadIdx.x & 63, l16 = lane & 15;
-  const int row0 = e.z * QTILE;
-  const int nrows = min(QTILE, P.T * P.G - row0);
-  const int* posb = P.pos + (int64_t)e.b * P.T;
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int r = 16 * nt + l16;
-    it.rpos[nt] = (r < nrows) ? posb[(row0 + r) / P.G] : -1;
-  }
-  const int BS = BSZ ? BSZ : P.kv.block_size;
-  const int kbeg = e.s * P.split;
-  const int kend = min(kbeg + P.split, e.qmax + 1);
-  const int first_blk = kbeg / BS;
-  const int nblk = (kend - 1) / BS - first_blk + 1;   // <= split/16 + 1 <= 33 lanes
-  it.phys = -1;   // raw table entry, checked where it is used so that nothing waits for it here
-  if (lane < nblk && first_blk + lane < P.max_blocks) it.phys = P.table[(int64_t)e.b * P.table_stride + first_blk + lane];
-}
-
-// One item for one wave: chunk it.s of batch row it.b, KV head hkv, query tile it.z. `next` runs
-// once, three tiles before the end (it takes and fetches the wave's next item).
-template <int D, int BSZ, class F>
-__device__ __attribute__((always_inline)) inline void attn_mfma_item(const AttnParams& P, const ItemRegs& it,
-                                                                     int hkv, F&& next) {
+template <int D, int BSZ>
+__device__ __attribute__((always_inline)) inline void attn_wave_tiles(const AttnParams& P, int b, int kbeg, int kend,
+                                                                      int qmax, int row0, int nrows,
+                                                                      const int (&rpos)[2], int hkv, int w,
+                                                                      float4_t (*red_acc)[64], float* red_m,
+                                                                      float* red_l) {
   constexpr int KS = D / 32;   // k-steps of the QK^T product
   constexpr int MT = D / 16;   // 16-dim tiles of the PV product
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, g = lane >> 4;
-  const int b = it.b, s = it.s, qmax = it.qmax;
-  const int row0 = it.z * QTILE;
-  const int nrows = min(QTILE, P.T * P.G - row0);
-  const int rpos[2] = {it.rpos[0], it.rpos[1]};
-  const int my_phys = it.phys;
-  const int kbeg = s * P.split;
-  if (qmax < kbeg) return;  // not listed by the plan; kept as a guard
-  const int kend = min(kbeg + P.split, qmax + 1);
   const int ntiles = (kend - kbeg + 15) >> 4;
+  const int nt_w = ntiles > w ? (ntiles - w + UNIT_WAVES - 1) / UNIT_WAVES : 0;   // <= 64 tiles
   const bool two = nrows > 16;
   const int BS = BSZ ? BSZ : P.kv.block_size;
   const int64_t v_dim = BSZ ? BSZ : P.kv.v_dim;   // == block_size (dim-major values)
-  const int first_blk = kbeg / BS;
+
+  // lane i: raw table entry of the block holding this wave's i-th tile (-1 past the table)
+  int my_phys = -1;
+  if (lane < nt_w) {
+    const int blk = (kbeg + 16 * (w + UNIT_WAVES * lane)) / BS;
+    if (blk < P.max_blocks) my_phys = P.table[(int64_t)b * P.table_stride + blk];
+  }
 
   typedef uint16_t u16;
   const u16* kpool = reinterpret_cast<const u16*>(P.kv.k);
@@ -219,21 +250,23 @@ __device__ __attribute__((always_inline)) inline void attn_mfma_item(const AttnP
   const int64_t k_head_off = (int64_t)hkv * P.kv.k_head;
   const int64_t v_head_off = (int64_t)hkv * P.kv.v_head;
 
-  // Three tile buffers in registers: while tile t is consumed, tiles t+1 and t+2 are in flight.
+  // Three tile buffers in registers: while tile i is consumed, tiles i+1 and i+2 are in flight.
   // Every load is unconditional (a prefetch past the end re-reads the last tile, an unmapped block
   // reads block 0 and is masked in consume) so that each wait before a consume counts exactly the
   // loads issued after that tile, on every path through the loop.
   bf16x8_t kb0[KS], kb1[KS], kb2[KS];
   short4_t vb0[MT], vb1[MT], vb2[MT];
 
-  auto block_of = [&](int j0) {   // physical block holding key j0, -1 when unmapped
-    const int v = __builtin_amdgcn_readlane(my_phys, j0 / BS - first_blk);
+  auto key0 = [&](int i) { return kbeg + 16 * (w + UNIT_WAVES * i); };
+  auto block_of = [&](int i) {   // physical block of the wave's i-th tile, -1 when unmapped
+    const int v = __builtin_amdgcn_readlane(my_phys, i);
     return (v >= 0 && v < P.kv.num_blocks) ? v : -1;
   };
 
-  auto load_tile = [&](int kt, bf16x8_t (&kd)[KS], short4_t (&vd)[MT]) {
-    const int j0 = kbeg + 16 * min(kt, ntiles - 1);
-    const int phys = block_of(j0);
+  auto load_tile = [&](int i, bf16x8_t (&kd)[KS], short4_t (&vd)[MT]) {
+    const int ic = max(min(i, nt_w - 1), 0);   // a wave without tiles reads block 0 and consumes nothing
+    const int j0 = key0(ic);
+    const int phys = block_of(ic);
     const int64_t pb = phys >= 0 ? phys : 0;
     const int slot0 = j0 - (j0 / BS) * BS;
     const u16* kt_ = kpool + pb * P.kv.k_block + k_head_off + (int64_t)(slot0 + l16) * D;
@@ -277,17 +310,17 @@ __device__ __attribute__((always_inline)) inline void attn_mfma_item(const AttnP
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_run[2] = {0.f, 0.f};
 
-  auto consume = [&](int kt, const bf16x8_t (&kf)[KS], short4_t (&vf)[MT]) {
-    const int j0 = kbeg + 16 * kt;
-    const bool tile_valid = block_of(j0) >= 0;
+  auto consume = [&](int i, const bf16x8_t (&kf)[KS], short4_t (&vf)[MT]) {
+    const int j0 = key0(i);
+    const bool tile_valid = block_of(i) >= 0;
     // keys of an unmapped block, and keys past the furthest query (possibly never written), must not
     // reach the PV product: their values may be anything
     if (!tile_valid || j0 + 15 > qmax) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (!tile_valid || j0 + 4 * g + i > qmax) {
+      for (int e = 0; e < 4; ++e) {
+        if (!tile_valid || j0 + 4 * g + e > qmax) {
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) vf[mt][i] = 0;
+          for (int mt = 0; mt < MT; ++mt) vf[mt][e] = 0;
         }
       }
     }
@@ -308,11 +341,11 @@ __device__ __attribute__((always_inline)) inline void attn_mfma_item(const AttnP
       float sv[4];
       float tmax = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = j0 + 4 * g + i;
+      for (int e = 0; e < 4; ++e) {
+        const int key = j0 + 4 * g + e;
         const bool vis = tile_valid && key <= rpos[nt];
-        sv[i] = vis ? sc[nt][i] * P.scale_log2 : -INFINITY;
-        tmax = fmaxf(tmax, sv[i]);
+        sv[e] = vis ? sc[nt][e] * P.scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, sv[e]);
       }
       tmax = max_across_groups(tmax);
       const float m_new = fmaxf(m_run[nt], tmax);
@@ -320,9 +353,9 @@ __device__ __attribute__((always_inline)) inline void attn_mfma_item(const AttnP
       float psum = 0.f;
       float pv[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pv[i] = (sv[i] == -INFINITY) ? 0.f : exp2f(sv[i] - m_new);
-        psum += pv[i];
+      for (int e = 0; e < 4; ++e) {
+        pv[e] = (sv[e] == -INFINITY) ? 0.f : exp2f(sv[e] - m_new);
+        psum += pv[e];
       }
       pf[nt] = bf16_rne4(pv);
       l_run[nt] = l_run[nt] * alpha[nt] + psum;
@@ -345,87 +378,102 @@ __device__ __attribute__((always_inline)) inline void attn_mfma_item(const AttnP
     }
   };
 
-  const int kp = max(ntiles - 3, 0);   // the tile before which `next` runs, exactly once
-  for (int kt = 0; kt < ntiles; kt += 3) {
-    load_tile(kt + 2, kb2, vb2);
-    if (kt == kp) next();
-    consume(kt, kb0, vb0);
-    if (kt + 1 >= ntiles) break;
-    load_tile(kt + 3, kb0, vb0);
-    if (kt + 1 == kp) next();
-    consume(kt + 1, kb1, vb1);
-    if (kt + 2 >= ntiles) break;
-    load_tile(kt + 4, kb1, vb1);
-    if (kt + 2 == kp) next();
-    consume(kt + 2, kb2, vb2);
+  for (int i = 0; i < nt_w; i += 3) {
+    load_tile(i + 2, kb2, vb2);
+    consume(i, kb0, vb0);
+    if (i + 1 >= nt_w) break;
+    load_tile(i + 3, kb0, vb0);
+    consume(i + 1, kb1, vb1);
+    if (i + 2 >= nt_w) break;
+    load_tile(i + 4, kb1, vb1);
+    consume(i + 2, kb2, vb2);
   }
-
-  // write this chunk's partial for every real row of the tile that sees the chunk
+  // this wave's partial to LDS: acc by (query half, dim tile, lane), m and l by query row
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    float lsum = l_run[nt];
-    lsum = sum_across_groups(lsum);
-    const int r = 16 * nt + l16;
-    if (r >= nrows || rpos[nt] < kbeg) continue;
-    const int rr = row0 + r;
-    const int t = rr / P.G, h = hkv * P.G + (rr - t * P.G);
-    const int64_t R = row_index(P, b, t, h);
-    float* pa = P.ws_acc + (R * P.nsplit + s) * D;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      *reinterpret_cast<float4_t*>(pa + 16 * mt + 4 * g) = acc[mt][nt];
+    for (int mt = 0; mt < MT; ++mt) red_acc[nt * MT + mt][lane] = acc[mt][nt];
+    const float lsum = sum_across_groups(l_run[nt]);
     if (g == 0) {
-      float* pm = P.ws_ml + (R * P.nsplit + s) * 2;
-      pm[0] = m_run[nt];
-      pm[1] = lsum;
+      red_m[16 * nt + l16] = m_run[nt];
+      red_l[16 * nt + l16] = lsum;
     }
   }
 }
 
-// Persistent kernel: as many workgroups as the GPU holds at once, each of hpw waves over the hpw KV
-// heads of a head group, so the heads' tiles of a block (neighbours in the pool) stream from one CU
-// at about the same time. Plan unit r = (plan item r / ngrp, head group r % ngrp); the units are
-// dealt round-robin over the first geff workgroups, geff chosen so that every round but the last is
-// full and the last has as few idle workgroups as the count allows. Inside a workgroup the waves
-// take (unit, head) pairs from an LDS counter, so waves that the memory system serves faster take
-// more; each wave takes and fetches its next pair while the current one still streams.
 template <int D, int BSZ>
-__global__ void __launch_bounds__(64 * MAX_HEADS_PER_WG) __attribute__((amdgpu_waves_per_eu(2)))
-attn_mfma_bf16_kernel(AttnParams P) {
-  __shared__ int unit_ctr;
-  const int hpw = blockDim.x >> 6;
-  const int ngrp = P.kv.n_kv_heads / hpw;
-  const int64_t total = (int64_t)P.n_items[0] * ngrp;
-  if (total == 0) return;
-  const int64_t rounds = (total + gridDim.x - 1) / gridDim.x;
-  const int64_t geff = (total + rounds - 1) / rounds;
-  if ((int64_t)blockIdx.x >= geff) return;   // both returns are uniform over the workgroup
-  // This workgroup's share: plan units r_j = blockIdx.x + j * geff, j < nj, each hpw heads. Its waves
-  // take (j, head) pairs in order from an LDS counter, so a wave that streams faster takes more.
-  const int64_t nj = (total - blockIdx.x + geff - 1) / geff;
-  const int units = (int)(nj * hpw);
-  if (threadIdx.x == 0) unit_ctr = 0;
+__global__ void __launch_bounds__(64 * UNIT_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+attn_unit_kernel(AttnParams P) {
+  constexpr int MT = D / 16;
+  __shared__ float4_t red_acc[UNIT_WAVES][2 * MT][64];
+  __shared__ float red_m[UNIT_WAVES][QTILE], red_l[UNIT_WAVES][QTILE];
+  const int nkv = P.kv.n_kv_heads;
+  const int64_t e_idx = blockIdx.x / nkv;
+  const int hkv = (int)(blockIdx.x - e_idx * nkv);
+  if (e_idx >= P.n_items[0]) return;   // uniform over the workgroup
+  typedef __attribute__((address_space(4))) const AttnItem ConstItem;   // read-only: scalar loads
+  ConstItem* ep = (ConstItem*)(uintptr_t)(P.items + e_idx);
+  const int b = ep->b, z = ep->z, s = ep->s, qmax = ep->qmax;
+  const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform, in a scalar register
+  const int row0 = z * QTILE;
+  const int nrows = min(QTILE, P.T * P.G - row0);
+  const int* posb = P.pos + (int64_t)b * P.T;
+  int rpos[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int r = 16 * nt + l16;
+    rpos[nt] = (r < nrows) ? posb[(row0 + r) / P.G] : -1;
+  }
+  const int kbeg = s * P.split;
+  const int kend = min(kbeg + P.split, qmax + 1);
+
+  attn_wave_tiles<D, BSZ>(P, b, kbeg, kend, qmax, row0, nrows, rpos, hkv, w, red_acc[w], red_m[w], red_l[w]);
   __syncthreads();
-  auto take = [&]() {
-    int t = 0;
-    if ((threadIdx.x & 63) == 0) t = atomicAdd(&unit_ctr, 1);
-    return __builtin_amdgcn_readlane(t, 0);
-  };
-  auto unit_r = [&](int u) { return (int64_t)blockIdx.x + (int64_t)(u / hpw) * geff; };
-  int u = take();
-  if (u >= units) return;
-  ItemRegs cur, nxt;
-  fetch_item<BSZ>(P, unit_r(u) / ngrp, cur);
-  for (;;) {
-    int un = units;
-    // the next unit is taken a few tiles before this one ends, and its metadata fetched then
-    attn_mfma_item<D, BSZ>(P, cur, (int)(unit_r(u) % ngrp) * hpw + u % hpw, [&]() {
-      un = take();
-      fetch_item<BSZ>(P, unit_r(un < units ? un : u) / ngrp, nxt);
-    });
-    if (un >= units) break;
-    cur = nxt;
-    u = un;
+
+  // merge the waves' partials in wave order; wave w takes the (query half, 16-dim tile) pairs w,
+  // w + UNIT_WAVES, ...
+  for (int gi = w; gi < 2 * MT; gi += UNIT_WAVES) {
+    const int nt = gi / MT, mt = gi - nt * MT;
+    const int r = 16 * nt + l16;
+    if (r >= nrows) continue;
+    // a query that sees one chunk only is finished here (a padding query, position < 0, gets zeros
+    // from chunk 0); any other query gets this chunk's partial if the chunk holds keys it sees
+    const bool direct = P.direct && (rpos[nt] < P.split || P.nsplit == 1);
+    if (direct ? s != 0 : rpos[nt] < kbeg) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < UNIT_WAVES; ++v) M = fmaxf(M, red_m[v][r]);
+    float L = 0.f;
+    float4_t o = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < UNIT_WAVES; ++v) {
+      const float mv = red_m[v][r];
+      const float c = (mv == -INFINITY) ? 0.f : exp2f(mv - M);
+      L += c * red_l[v][r];
+      const float4_t a = red_acc[v][gi][lane];
+      o[0] += c * a[0];
+      o[1] += c * a[1];
+      o[2] += c * a[2];
+      o[3] += c * a[3];
+    }
+    const int rr = row0 + r;
+    const int t = rr / P.G, h = hkv * P.G + (rr - t * P.G);
+    if (direct) {   // the same normalisation as attn_combine's
+      const float f[4] = {L > 0.f ? o[0] / L : 0.f, L > 0.f ? o[1] / L : 0.f, L > 0.f ? o[2] / L : 0.f,
+                          L > 0.f ? o[3] / L : 0.f};
+      uint16_t* orow = reinterpret_cast<uint16_t*>(P.out) + (int64_t)b * P.o_sb + (int64_t)t * P.o_st +
+                       (int64_t)h * P.o_sh;
+      *reinterpret_cast<short4_t*>(orow + 16 * mt + 4 * g) = bf16_rne4(f);
+      continue;
+    }
+    const int64_t R = row_index(P, b, t, h);
+    *reinterpret_cast<float4_t*>(P.ws_acc + (R * P.nsplit + s) * D + 16 * mt + 4 * g) = o;
+    if (mt == 0 && g == 0) {
+      float* pm = P.ws_ml + (R * P.nsplit + s) * 2;
+      pm[0] = M;
+      pm[1] = L;
+    }
   }
 }
 
@@ -527,6 +575,7 @@ __global__ void __launch_bounds__(64 * COMBINE_ROWS) attn_combine_kernel(AttnPar
   const int bt = (int)(R / P.H);
   const int b = bt / P.T, t = bt - b * P.T;
   const int pos = P.pos[bt];
+  if (P.direct && (pos < P.split || P.nsplit == 1)) return;   // written by its chunk's workgroup
   const int D = P.kv.head_dim;
   T_* orow = reinterpret_cast<T_*>(out) + (int64_t)b * o_sb + (int64_t)t * o_st + (int64_t)h * o_sh;
   if (pos < 0) {
@@ -590,52 +639,33 @@ bool mfma_eligible(const fs_kv_layout& kv, const void* q, int64_t q_sb, int64_t 
   return true;
 }
 
+// Keys per chunk. The generic kernel uses 512. The MFMA path uses FS_ATTN_SPLIT (default 8192; a
+// multiple of 64 in [256, MAX_SPLIT]), read once: it must stay fixed for the life of the process, since
+// the chunk boundaries decide the rounding of every output.
+constexpr int GENERIC_SPLIT = 512;
+
 int attn_split() {
   static const int split = [] {
     const char* e = getenv("FS_ATTN_SPLIT");
-    int v = e ? atoi(e) : 512;
-    if (v < 16 || v > 512 || v % 16) v = 512;  // a chunk's block list must fit one wavefront
+    int v = e ? atoi(e) : 8192;
+    if (v < 256 || v > MAX_SPLIT || v % 64) v = 8192;
     return v;
   }();
   return split;
 }
 
-// Workgroups of `threads` threads of `fn` that the current device holds at once (cached per device,
-// kernel and size).
-int64_t resident_wgs(const void* fn, int threads) {
-  struct Entry { int dev; const void* fn; int threads; int64_t wgs; };
-  static Entry cache[64];
-  static int n_cache = 0;
-  static std::mutex mu;
-  std::lock_guard<std::mutex> lock(mu);
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return -1;
-  for (int i = 0; i < n_cache; ++i)
-    if (cache[i].dev == dev && cache[i].fn == fn && cache[i].threads == threads) return cache[i].wgs;
-  int cus = 0, per_cu = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0) != hipSuccess || per_cu <= 0) return -1;
-  const int64_t w = (int64_t)cus * per_cu;
-  if (n_cache < 64) cache[n_cache++] = Entry{dev, fn, threads, w};
-  return w;
-}
-
-int64_t nsplit_for(int32_t max_blocks, int32_t block_size) {
+int64_t nsplit_for(int32_t max_blocks, int32_t block_size, int split) {
   const int64_t S = (int64_t)max_blocks * block_size;
-  return (S + attn_split() - 1) / attn_split();
+  return (S + split - 1) / split;
 }
 
-// Upper bound of the plan's length: every (row, query tile, chunk).
-int64_t max_items(int32_t B, int32_t T, int32_t n_heads, int32_t max_blocks, int32_t block_size) {
+// Upper bound of the plan's length: every (row, query tile, chunk), at the smallest chunk size.
+int64_t max_items(int32_t B, int32_t T, int32_t n_heads, int32_t max_blocks, int32_t block_size, int split) {
   const int64_t qtiles = ((int64_t)T * n_heads + QTILE - 1) / QTILE;   // n_heads bounds the group size
-  return (int64_t)B * qtiles * nsplit_for(max_blocks, block_size);
+  return (int64_t)B * qtiles * nsplit_for(max_blocks, block_size, split);
 }
 
-int heads_per_wg(int n_kv_heads) {
-  int h = n_kv_heads < MAX_HEADS_PER_WG ? n_kv_heads : MAX_HEADS_PER_WG;
-  while (n_kv_heads % h) --h;
-  return h;
-}
+int min_split() { return attn_split() < GENERIC_SPLIT ? attn_split() : GENERIC_SPLIT; }
 
 }  // namespace
 
@@ -643,8 +673,9 @@ extern "C" int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32
                                                      int32_t max_blocks, int32_t block_size) {
   if (B <= 0 || T <= 0 || n_heads <= 0 || head_dim <= 0 || max_blocks <= 0 || block_size <= 0) return 0;
   const int64_t rows = (int64_t)B * T * n_heads;
-  const int64_t ns = nsplit_for(max_blocks, block_size);
-  const int64_t list = (max_items(B, T, n_heads, max_blocks, block_size) * (int64_t)sizeof(AttnItem) + 255) / 256 * 256;
+  const int64_t ns = nsplit_for(max_blocks, block_size, min_split());
+  const int64_t list =
+      (max_items(B, T, n_heads, max_blocks, block_size, min_split()) * (int64_t)sizeof(AttnItem) + 255) / 256 * 256;
   return WS_HEADER + list + rows * ns * (head_dim + 2) * (int64_t)sizeof(float) + 256;
 }
 
@@ -684,36 +715,39 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
   P.H = n_heads;
   P.G = n_heads / kv->n_kv_heads;
   P.scale_log2 = scale * LOG2E;
-  P.nsplit = (int32_t)nsplit_for(max_blocks, kv->block_size);
-  P.split = attn_split();
+  const bool mfma = mfma_eligible(*kv, q, q_sb, q_st, q_sh);
+  P.split = mfma ? attn_split() : GENERIC_SPLIT;
+  P.nsplit = (int32_t)nsplit_for(max_blocks, kv->block_size, P.split);
   const int64_t rows = (int64_t)B * T * n_heads;
   char* ws = reinterpret_cast<char*>(workspace);
-  const int64_t list = (max_items(B, T, n_heads, max_blocks, kv->block_size) * (int64_t)sizeof(AttnItem) + 255) / 256 * 256;
+  const int64_t list =
+      (max_items(B, T, n_heads, max_blocks, kv->block_size, min_split()) * (int64_t)sizeof(AttnItem) + 255) / 256 * 256;
   P.n_items = reinterpret_cast<int32_t*>(ws);
   P.items = reinterpret_cast<AttnItem*>(ws + WS_HEADER);
   P.ws_acc = reinterpret_cast<float*>(ws + WS_HEADER + list);
   P.ws_ml = P.ws_acc + rows * P.nsplit * kv->head_dim;
+  // direct outputs are stored 4 bf16 at a time
+  P.direct = mfma && (reinterpret_cast<uintptr_t>(out) & 7) == 0 && o_sb % 4 == 0 && o_st % 4 == 0 && o_sh % 4 == 0;
+  P.out = out;
+  P.o_sb = o_sb;
+  P.o_st = o_st;
+  P.o_sh = o_sh;
 
   hipStream_t st = fs::as_stream(stream);
-  if (mfma_eligible(*kv, q, q_sb, q_st, q_sh)) {
+  if (mfma) {
     const bool bs16 = kv->block_size == 16;
-    const void* fn = kv->head_dim == 128
-                         ? (bs16 ? (const void*)attn_mfma_bf16_kernel<128, 16> : (const void*)attn_mfma_bf16_kernel<128, 0>)
-                         : (bs16 ? (const void*)attn_mfma_bf16_kernel<64, 16> : (const void*)attn_mfma_bf16_kernel<64, 0>);
-    const int threads = 64 * heads_per_wg(kv->n_kv_heads);
-    const int64_t wgs = resident_wgs(fn, threads);
-    if (wgs <= 0) {
-      fs::set_error("paged_attention: device occupancy query failed");
-      return (int)hipErrorUnknown;
-    }
+    // one workgroup per (plan item, KV head); items past the plan's length exit at once
+    const int64_t qtiles = ((int64_t)T * P.G + QTILE - 1) / QTILE;
+    const int64_t units = (int64_t)B * qtiles * P.nsplit * kv->n_kv_heads;
+    FS_CHECK_ARG(units < 0x7fffffff, "paged_attention: %lld work units", (long long)units);
     attn_plan_kernel<<<1, PLAN_THREADS, 0, st>>>(P);
-    const unsigned grid = (unsigned)wgs;
+    const unsigned grid = (unsigned)units, threads = 64 * UNIT_WAVES;
     if (kv->head_dim == 128) {
-      if (bs16) attn_mfma_bf16_kernel<128, 16><<<grid, threads, 0, st>>>(P);
-      else attn_mfma_bf16_kernel<128, 0><<<grid, threads, 0, st>>>(P);
+      if (bs16) attn_unit_kernel<128, 16><<<grid, threads, 0, st>>>(P);
+      else attn_unit_kernel<128, 0><<<grid, threads, 0, st>>>(P);
     } else {
-      if (bs16) attn_mfma_bf16_kernel<64, 16><<<grid, threads, 0, st>>>(P);
-      else attn_mfma_bf16_kernel<64, 0><<<grid, threads, 0, st>>>(P);
+      if (bs16) attn_unit_kernel<64, 16><<<grid, threads, 0, st>>>(P);
+      else attn_unit_kernel<64, 0><<<grid, threads, 0, st>>>(P);
     }
   } else {
     dim3 grid((unsigned)rows, (unsigned)P.nsplit);
@@ -724,6 +758,7 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
     }
   }
   if (int e = fs::launch_status("paged_attention")) return e;
+  if (P.direct && P.nsplit == 1) return 0;   // every query sees one chunk: all outputs are written
   dim3 cgrid((unsigned)((rows + COMBINE_ROWS - 1) / COMBINE_ROWS));
   switch (kv->dtype) {
     case FS_F32: attn_combine_kernel<FS_F32><<<cgrid, 64 * COMBINE_ROWS, 0, st>>>(P, out, o_sb, o_st, o_sh); break;

@@ -226,10 +226,39 @@ def test_attention_verify_equals_decode_bitwise():
 
 def test_attention_padding_rows_are_zero():
     case("attention padding")
-    q, k, v, tables, pos = _paged_case(2, 3, 8, 2, 128, 16, [50, 70], 20, torch.bfloat16, 4)
+    q, k, v, tables, pos = _paged_case(3, 3, 8, 2, 128, 16, [50, 70, 30], 20, torch.bfloat16, 4)
     pos[1, 2] = -1
+    pos[2, :] = -1   # a row of padding only
     out, _ = _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
     assert torch.count_nonzero(out[1, 2]) == 0
+    assert torch.count_nonzero(out[2]) == 0
+    assert torch.count_nonzero(out[1, :2]) > 0
+
+
+LONG_CTX = [8, 8191, 8192, 8193, 8199, 20000]   # one, two and three 8192-key chunks
+
+
+def test_attention_long_contexts():
+    """Contexts that span several key chunks: queries past the first chunk are merged from per-chunk
+    partials, the others are finished by their chunk's workgroup."""
+    case("attention long", LONG_CTX)
+    q, k, v, tables, pos = _paged_case(len(LONG_CTX), 7, 8, 2, 128, 16, LONG_CTX, 3400, torch.bfloat16, 12)
+    out, _ = _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
+    ref = _oracle_attention(q, k, v, tables, pos, 4)
+    assert rel_err(out.cpu().float(), ref) < 2e-2
+
+
+def test_attention_long_verify_equals_decode_bitwise():
+    case("attention long invariance", LONG_CTX)
+    t = 7
+    q, k, v, tables, pos = _paged_case(len(LONG_CTX), t, 8, 2, 128, 16, LONG_CTX, 3400, torch.bfloat16, 13)
+    full, pool = _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
+    lay = pool.layout(0)
+    tab = tables.int().to(DEV)
+    for i in range(t):
+        one = ops.paged_attention(q[:, i: i + 1].to(DEV), lay, tab, pos[:, i: i + 1].int().to(DEV),
+                                  1.0 / math.sqrt(128))
+        assert torch.equal(one[:, 0], full[:, i]), i
 
 
 def test_attention_c3_shape():
