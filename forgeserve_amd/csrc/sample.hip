@@ -19,8 +19,8 @@ namespace {
 
 constexpr int THREADS = 256;
 constexpr int VEC = 8;                       // consecutive columns per thread group
-constexpr int UNROLL = 8;                    // groups per thread per chunk: 8 16-byte loads in flight
-constexpr int CH = THREADS * VEC * UNROLL;   // 16384 columns per chunk
+constexpr int UNROLL = 4;                    // groups per thread per chunk: 4 16-byte loads in flight
+constexpr int CH = THREADS * VEC * UNROLL;   // 8192 columns per chunk
 constexpr int UNROLL_R = 2;                  // the acceptance's residual and argmax passes:
 constexpr int CHR = THREADS * VEC * UNROLL_R;  // 4096 columns per chunk (many workgroups for two rows)
 
@@ -148,8 +148,9 @@ FS_DEVICE Stat merge_row(const Stat* st, int nch) {
 FS_DEVICE float softmax_at(float x, float T, const Stat& st) { return expf(x / T - st.m) / st.s; }
 
 // One chunk of one row. T == 0: the first argmax of x. T > 0: (m, s) = (max of y, sum of exp(y - m))
-// with y = x / T (a true division, skipped when T == 1 where it is exact). The chunk's loads are all
-// issued up front; the values stay in registers for the max pass and the exp pass.
+// with y = x * (1/T) (exact at T == 1; elsewhere within an ulp of sampling.py:13's x / T, a shift the
+// softmax absorbs). The chunk's loads are all issued up front; the values stay in registers for the
+// max pass and the exp pass.
 template <int DT>
 FS_DEVICE Stat chunk_stat(const typename Elem<DT>::T* row, int c, int64_t V, float T, float* shf, int* shi) {
   const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
@@ -175,10 +176,11 @@ FS_DEVICE Stat chunk_stat(const typename Elem<DT>::T* row, int c, int64_t V, flo
     return st;
   }
   if (T != 1.f) {
+    const float invT = 1.f / T;
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[u][j] = x[u][j] / T;  // padding stays -inf
+      for (int j = 0; j < 8; ++j) x[u][j] = x[u][j] * invT;  // padding stays -inf
   }
   float m = -INFINITY;
 #pragma unroll
@@ -200,15 +202,13 @@ FS_DEVICE Stat chunk_stat(const typename Elem<DT>::T* row, int c, int64_t V, flo
 }
 
 // Softmax value of one column for the vocab-wide passes: exp(y - M) / S evaluated as
-// exp2(y*log2e - M*log2e) * (1/S). The accept/reject test itself uses softmax_at (expf, true divides).
+// exp2(y*log2e - M*log2e) * (1/S) with y = x * (1/T) (exact at T = 1). The accept/reject test itself
+// uses softmax_at (expf, true divides).
 struct FastSoftmax {
-  float T, ML, invS;
-  FS_DEVICE FastSoftmax() : T(1.f), ML(0.f), invS(1.f) {}
-  FS_DEVICE FastSoftmax(float t, const Stat& st) : T(t), ML(st.m * LOG2E_F), invS(1.f / st.s) {}
-  FS_DEVICE float operator()(float x) const {
-    const float y = T == 1.f ? x : x / T;
-    return __builtin_amdgcn_exp2f(fmaf(y, LOG2E_F, -ML)) * invS;
-  }
+  float invT, ML, invS;
+  FS_DEVICE FastSoftmax() : invT(1.f), ML(0.f), invS(1.f) {}
+  FS_DEVICE FastSoftmax(float t, const Stat& st) : invT(1.f / t), ML(st.m * LOG2E_F), invS(1.f / st.s) {}
+  FS_DEVICE float operator()(float x) const { return __builtin_amdgcn_exp2f(fmaf(x * invT, LOG2E_F, -ML)) * invS; }
 };
 
 // ------------------------------------------------------------------------------------------------
@@ -302,7 +302,7 @@ struct AcceptArgs {
   RowSet rs;             // n0 = K+1 target rows, n1 = K draft rows
   int32_t K;
   int64_t V;
-  int nch;               // 16K-column chunks of the statistics pass
+  int nch;               // 8K-column chunks of the statistics pass
   int nchr;              // 4K-column chunks of the residual and argmax passes
   int B;
   const int32_t* draft;  // [B, K]
@@ -314,8 +314,9 @@ struct AcceptArgs {
   Stat* stats;           // [B*(2K+1)][nch] chunk partials (logits mode)
   Stat* mstats;          // [B*(2K+1)] merged row statistics (logits mode)
   float* resid;          // [B][nchr] residual partial sums of the rejected row pair
-  float* pv;             // [B][nchr]
-  int* pi;               // [B][nchr]
+  float* cmax;           // [B][nchr][2] max of the cheap keys p/E and r/E per chunk (0: none positive)
+  int* ncand;            // [B][nchr][2] candidates of each draw (> NCAND: the list overflowed)
+  int* cand;             // [B][nchr][2][NCAND] their column indices, in no particular order
   int* jpos;             // [B]
   int32_t* out_tokens;   // [B, K+1]
   int32_t* n_acc;        // [B]
@@ -333,96 +334,108 @@ FS_DEVICE void write_outputs(const AcceptArgs& A, int b, int j, int extra) {
   if (A.seq_len) A.seq_len[b] = A.seq_len[b] + 1 + j;  // want = cached + 1 + len(accepted) (speculative.py:77)
 }
 
-// launch 2, one workgroup per sequence: merge the row statistics (logits mode, one lane per row),
-// walk the proposals (speculative.py:25-29) and finish a greedy sequence (the extra token is the
+constexpr int STEP_WAVES = 4;
+constexpr int STEP_ROWS = 4;    // rows merged per wave and pass
+
+// The chunk statistics of rows r (one wave, lane c holding chunk c) merged as merge_row does: the
+// max over the chunks, Σ s_c 2^(m_c - M) added in chunk order, the first argmax.
+FS_DEVICE Stat merge_row_wave(const Stat& st, bool in, int nch) {
+  float M = wave_max(in ? st.m : -INFINITY);
+  const float term = (!in || st.m == -INFINITY) ? 0.f : st.s * __builtin_amdgcn_exp2f((st.m - M) * LOG2E_F);
+  float S = 0.f;
+  for (int c = 0; c < nch; ++c) S += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(term), c));
+  float av = in ? st.av : -INFINITY;
+  int ai = in ? st.ai : 0x7fffffff;
+  wave_argmax(av, ai);
+  return Stat{M, S, av, ai};
+}
+
+// The step of sequence b, run by one workgroup of STEP_WAVES waves: merge the row statistics
+// (logits mode: each wave takes STEP_ROWS rows at a time, one lane per chunk) into ms, then test
+// every proposal at once, one lane each; the first rejection ends the walk (speculative.py:25-29).
+// The proposals and their logits are loaded before the merge, so the two latencies overlap. Writes
+// jpos (the first rejected proposal, or k_eff) and finishes a greedy sequence (the extra token is the
 // argmax of target row j).
 template <int DT, bool PROBS>
-FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
+FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* ms) {
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
   const int per = A.rs.n0 + A.rs.n1;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave 0, lane i: proposal i of the first 64
+  int x0 = -1;
+  float u0 = 0.f, xp0 = 0.f, xq0 = 0.f;
+  if (w == 0 && lane < ke) {
+    x0 = A.draft[(int64_t)b * A.K + lane];
+    u0 = A.u[(int64_t)b * A.K + lane];
+    if (x0 >= 0 && x0 < A.V) {
+      xp0 = Elem<DT>::load(row_ptr<DT>(A.rs, b, lane), x0);
+      xq0 = Elem<DT>::load(row_ptr<DT>(A.rs, b, A.rs.n0 + lane), x0);
+    }
+  }
+  auto used = [&](int r) { return r < per && (r < A.rs.n0 ? r <= ke : (r - A.rs.n0) < ke); };
   if (!PROBS) {
-    for (int r = threadIdx.x; r < per; r += blockDim.x) {
-      const bool used = r < A.rs.n0 ? r <= ke : (r - A.rs.n0) < ke;
-      if (used) A.mstats[(int64_t)b * per + r] = merge_row(A.stats + ((int64_t)b * per + r) * A.nch, A.nch);
+    if (A.nch <= 64) {
+      for (int r0 = 0; r0 < per; r0 += STEP_WAVES * STEP_ROWS) {
+        Stat st[STEP_ROWS];
+#pragma unroll
+        for (int i = 0; i < STEP_ROWS; ++i) {
+          const int r = r0 + w + STEP_WAVES * i;
+          if (used(r) && lane < A.nch) st[i] = A.stats[((int64_t)b * per + r) * A.nch + lane];
+        }
+#pragma unroll
+        for (int i = 0; i < STEP_ROWS; ++i) {
+          const int r = r0 + w + STEP_WAVES * i;
+          if (!used(r)) continue;   // uniform over the wave
+          const Stat m = merge_row_wave(st[i], lane < A.nch, A.nch);
+          if (lane == 0) ms[r] = m;
+        }
+      }
+    } else {
+      for (int r = threadIdx.x; r < per; r += blockDim.x)
+        if (used(r)) ms[r] = merge_row(A.stats + ((int64_t)b * per + r) * A.nch, A.nch);
     }
     __threadfence_block();
     __syncthreads();
   }
-  // every proposal's test at once, one lane each; the first rejection ends the walk (speculative.py:25-29)
   int j = ke;
   for (int i0 = 0; i0 < ke && j == ke; i0 += 64) {
-    const int i = i0 + (int)threadIdx.x;
+    const int i = i0 + lane;
     bool accept = false;
-    if (threadIdx.x < 64 && i < ke) {
-      const int x = A.draft[(int64_t)b * A.K + i];
+    if (w == 0 && i < ke) {
+      int x = x0;
+      float u = u0, xp = xp0, xq = xq0;
+      if (i0 > 0) {   // proposals past the first 64
+        x = A.draft[(int64_t)b * A.K + i];
+        u = A.u[(int64_t)b * A.K + i];
+        if (x >= 0 && x < A.V) {
+          xp = Elem<DT>::load(row_ptr<DT>(A.rs, b, i), x);
+          xq = Elem<DT>::load(row_ptr<DT>(A.rs, b, A.rs.n0 + i), x);
+        }
+      }
       if (x >= 0 && x < A.V) {   // an invalid proposal is never accepted
-        const auto* pr = row_ptr<DT>(A.rs, b, i);
-        const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + i);
         float px, qx;
         if (PROBS) {
-          px = Elem<DT>::load(pr, x);
-          qx = Elem<DT>::load(qr, x);
+          px = xp;
+          qx = xq;
         } else if (T > 0.f) {
-          px = softmax_at(Elem<DT>::load(pr, x), T, A.mstats[(int64_t)b * per + i]);
-          qx = softmax_at(Elem<DT>::load(qr, x), T, A.mstats[(int64_t)b * per + A.rs.n0 + i]);
+          px = softmax_at(xp, T, ms[i]);
+          qx = softmax_at(xq, T, ms[A.rs.n0 + i]);
         } else {  // one-hot rows of the first argmax (sampling.py:11-12)
-          px = A.mstats[(int64_t)b * per + i].ai == x ? 1.f : 0.f;
-          qx = A.mstats[(int64_t)b * per + A.rs.n0 + i].ai == x ? 1.f : 0.f;
+          px = ms[i].ai == x ? 1.f : 0.f;
+          qx = ms[A.rs.n0 + i].ai == x ? 1.f : 0.f;
         }
         const float ratio = qx > 0.f ? Elem<ProbType<DT, PROBS>::value>::round(px / qx) : 1.0f;  // speculative.py:26
-        accept = A.u[(int64_t)b * A.K + i] < fminf(1.0f, ratio);
+        accept = u < fminf(1.0f, ratio);
       }
     }
-    const uint64_t rejected = __ballot(threadIdx.x < 64 && i < ke && !accept);
+    const uint64_t rejected = __ballot(w == 0 && i < ke && !accept);
     if (rejected) j = i0 + __ffsll((unsigned long long)rejected) - 1;
   }
   if (threadIdx.x == 0) {
     A.jpos[b] = j;
-    if (!PROBS && T <= 0.f) write_outputs(A, b, j, A.mstats[(int64_t)b * per + j].ai);
+    if (!PROBS && T <= 0.f) write_outputs(A, b, j, ms[j].ai);
   }
-}
-
-// launch 3: residual partial sums of the rejected row pair (speculative.py:30), one chunk each
-template <int DT, bool PROBS>
-__global__ void __launch_bounds__(THREADS) accept_residual_kernel(AcceptArgs A) {
-  constexpr int PD = ProbType<DT, PROBS>::value;
-  __shared__ float shf[THREADS / 64];
-  const int c = blockIdx.x, b = blockIdx.y;
-  const int ke = keff_of(A, b);
-  const float T = PROBS ? 1.f : A.temps[b];
-  const int j = A.jpos[b];
-  if ((!PROBS && T <= 0.f) || j >= ke) return;  // greedy (done) or bonus token (no residual)
-  const int per = A.rs.n0 + A.rs.n1;
-  FastSoftmax sp, sq;
-  if (!PROBS) {
-    sp = FastSoftmax(T, A.mstats[(int64_t)b * per + j]);
-    sq = FastSoftmax(T, A.mstats[(int64_t)b * per + A.rs.n0 + j]);
-  }
-  const auto* pr = row_ptr<DT>(A.rs, b, j);
-  const auto* qr = row_ptr<DT>(A.rs, b, A.rs.n0 + j);
-  const bool vec_ok = (A.V % VEC) == 0 && (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr)) & 15) == 0);
-  float xp[UNROLL_R][8], xq[UNROLL_R][8];
-#pragma unroll
-  for (int u = 0; u < UNROLL_R; ++u) {
-    const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
-    load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp[u]);
-    load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq[u]);
-  }
-  float ls = 0.f;
-#pragma unroll
-  for (int u = 0; u < UNROLL_R; ++u) {
-    const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      if (v0 + jj >= A.V) continue;
-      const float p = PROBS ? xp[u][jj] : sp(xp[u][jj]);
-      const float q = PROBS ? xq[u][jj] : sq(xq[u][jj]);
-      ls += fmaxf(Elem<PD>::round(p - q), 0.f);  // (p - q).clamp(min=0)
-    }
-  }
-  const float tot = block_sum(ls, shf);
-  if (threadIdx.x == 0) A.resid[(int64_t)b * A.nchr + c] = tot;
 }
 
 // launch 1 (logits): per-(row, chunk) statistics of every row a sequence uses
@@ -444,34 +457,82 @@ __global__ void __launch_bounds__(THREADS) accept_stats_kernel(AcceptArgs A) {
 
 // launch 2: one workgroup per sequence runs its step (logits or probabilities)
 template <int DT, bool PROBS>
-__global__ void __launch_bounds__(64) accept_step_kernel(AcceptArgs A) {
-  sequence_step<DT, PROBS>(A, blockIdx.x);
+__global__ void __launch_bounds__(64 * STEP_WAVES) accept_step_kernel(AcceptArgs A) {
+  const int b = blockIdx.x;
+  sequence_step<DT, PROBS>(A, b, A.mstats + (int64_t)b * (A.rs.n0 + A.rs.n1));
 }
 
-// launch 4: argmax over a chunk of w_v / E_v (w the normalised residual, or the bonus row)
+// The extra token is argmax_v fl(w_v / E_v) (multinomial as the argmax over Exp(1) noise), with
+// w = p for the bonus token or when Σr = 0, and w = fl(r / S) otherwise (speculative.py:30-33); S = Σ r
+// is known only once every chunk has summed its part. One pass therefore ranks the columns by cheap
+// keys, p_v · rcp(E_v) and r_v · rcp(E_v), which differ from the final keys (times S) by a few float32
+// roundings plus, for the residual, the rounding of r / S to the probability dtype. A column whose
+// cheap key is below max · (1 - margin) cannot win, with the margin 8 or more times that error (2^-18
+// for float32 arithmetic, 2^-6 for bf16 probabilities, 2^-8 for f16). Each chunk keeps the columns
+// within the margin of its own max (its candidates, nearly always one per set), and the final pass
+// scores them exactly. Chunks whose list overflowed, and sequences whose max is too small for a
+// relative bound, are rescanned exactly.
+constexpr int NCAND = 8;
+constexpr float CAND_MIN = 7.888609052210118e-31f;  // 2^-100: below it the bound is not relied on
+constexpr float MARGIN_F32 = 1.0f / 262144.0f;     // 2^-18
+
+template <int PD>
+struct CandMargin {
+  static constexpr float value = PD == FS_F32 ? MARGIN_F32 : (PD == FS_BF16 ? 1.0f / 64.0f : 1.0f / 256.0f);
+};
+
+FS_DEVICE float cand_threshold(float mx, float margin) { return isinf(mx) ? mx : mx - mx * margin; }
+
+// p, q, the residual and the exact keys of a column of the rejected pair (the final draw's arithmetic)
 template <int DT, bool PROBS>
-__global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
+struct PairRow {
+  const typename Elem<DT>::T* pr;
+  const typename Elem<DT>::T* qr;
+  FastSoftmax sp, sq;
+  FS_DEVICE float p_at(float x) const { return PROBS ? x : sp(x); }
+  FS_DEVICE float q_at(float x) const { return PROBS ? x : sq(x); }
+  FS_DEVICE float resid(float xp, float xq) const {   // (p - q).clamp(min=0)
+    return fmaxf(Elem<ProbType<DT, PROBS>::value>::round(p_at(xp) - q_at(xq)), 0.f);
+  }
+  FS_DEVICE float key_p(int64_t v, float e) const { return p_at(Elem<DT>::load(pr, v)) / e; }
+  FS_DEVICE float key_r(int64_t v, float s, float e) const {   // s > 0
+    const float r = resid(Elem<DT>::load(pr, v), Elem<DT>::load(qr, v));
+    return Elem<ProbType<DT, PROBS>::value>::round(r / s) / e;
+  }
+};
+
+// Candidates of one set: the columns whose cheap key reaches the threshold (LDS list, first NCAND kept)
+FS_DEVICE void collect(float key, int col, float th, int* n, int* list) {
+  if (key >= th) {
+    const int k = atomicAdd(n, 1);
+    if (k < NCAND) list[k] = col;
+  }
+}
+
+// launch 3: one pass over the rejected position's two rows and E, per chunk of CHR columns: the
+// residual partial sum, and the max and candidates of both draws (p / E and r / E)
+template <int DT, bool PROBS>
+__global__ void __launch_bounds__(THREADS) accept_pair_kernel(AcceptArgs A) {
   constexpr int PD = ProbType<DT, PROBS>::value;
   __shared__ float shf[THREADS / 64];
-  __shared__ int shi[THREADS / 64];
+  __shared__ int sh_n[2];
+  __shared__ int sh_c[2][NCAND];
   const int c = blockIdx.x, b = blockIdx.y;
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
   if (!PROBS && T <= 0.f) return;  // greedy sequences were finished by the step
   const int per = A.rs.n0 + A.rs.n1;
+  const Stat* ms = A.mstats + (int64_t)b * per;
   const int j = A.jpos[b];
   const bool bonus = j >= ke;
   FastSoftmax sp, sq;
   if (!PROBS) {
-    sp = FastSoftmax(T, A.mstats[(int64_t)b * per + j]);
-    if (!bonus) sq = FastSoftmax(T, A.mstats[(int64_t)b * per + A.rs.n0 + j]);
+    sp = FastSoftmax(T, ms[j]);
+    if (!bonus) sq = FastSoftmax(T, ms[A.rs.n0 + j]);
   }
-  float s = 0.f;  // the residual sum, merged in chunk order (every workgroup merges the same way)
-  if (!bonus)
-    for (int cc = 0; cc < A.nchr; ++cc) s += A.resid[(int64_t)b * A.nchr + cc];
-  s = Elem<PD>::round(s);
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j);
+  const PairRow<DT, PROBS> pair{pr, qr, sp, sq};
   const float* er = A.E + (int64_t)b * A.ldE;
   const bool vec_ok = (A.V % VEC) == 0 &&
                       (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr) |
@@ -484,45 +545,122 @@ __global__ void __launch_bounds__(THREADS) accept_argmax_kernel(AcceptArgs A) {
     if (!bonus) load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq[u]);
     load8_f32(er, v0, A.V, vec_ok, e[u]);
   }
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
+  float ls = 0.f, mp = 0.f, mr = 0.f;
+  float ap[UNROLL_R][8], ar[UNROLL_R][8];   // cheap keys (0 past the row)
 #pragma unroll
   for (int u = 0; u < UNROLL_R; ++u) {
     const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
-      if (v0 + jj >= A.V) continue;
-      const float p = PROBS ? xp[u][jj] : sp(xp[u][jj]);
-      float w;
-      if (bonus) {
-        w = p;  // speculative.py:33
-      } else {
-        const float q = PROBS ? xq[u][jj] : sq(xq[u][jj]);
-        const float r = fmaxf(Elem<PD>::round(p - q), 0.f);
-        w = s > 0.f ? Elem<PD>::round(r / s) : p;  // speculative.py:31
+      const bool in = v0 + jj < A.V;
+      const float re = __builtin_amdgcn_rcpf(e[u][jj]);
+      ap[u][jj] = in ? pair.p_at(xp[u][jj]) * re : 0.f;
+      mp = fmaxf(mp, ap[u][jj]);
+      ar[u][jj] = 0.f;
+      if (!bonus) {
+        const float r = in ? pair.resid(xp[u][jj], xq[u][jj]) : 0.f;
+        ls += r;
+        ar[u][jj] = r * re;
+        mr = fmaxf(mr, ar[u][jj]);
       }
-      argmax_merge(bv, bi, w / e[u][jj], (int)(v0 + jj));
     }
   }
-  block_argmax(bv, bi, shf, shi);
+  const float tot = bonus ? 0.f : block_sum(ls, shf);
+  const float cmp = block_max(mp, shf);
+  const float cmr = bonus ? 0.f : block_max(mr, shf);
+  if (threadIdx.x < 2) sh_n[threadIdx.x] = 0;
+  __syncthreads();
+  const float thp = cmp > 0.f ? cand_threshold(cmp, MARGIN_F32) : INFINITY;
+  const float thr = cmr > 0.f ? cand_threshold(cmr, CandMargin<PD>::value) : INFINITY;
+#pragma unroll
+  for (int u = 0; u < UNROLL_R; ++u) {
+    const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      collect(ap[u][jj], (int)(v0 + jj), thp, &sh_n[0], sh_c[0]);
+      collect(ar[u][jj], (int)(v0 + jj), thr, &sh_n[1], sh_c[1]);
+    }
+  }
+  __syncthreads();
+  const int64_t o = (int64_t)b * A.nchr + c;
   if (threadIdx.x == 0) {
-    A.pv[(int64_t)b * A.nchr + c] = bv;
-    A.pi[(int64_t)b * A.nchr + c] = bi;
+    A.resid[o] = tot;
+    A.cmax[2 * o] = cmp;
+    A.cmax[2 * o + 1] = cmr;
+    A.ncand[2 * o] = cmp > 0.f ? sh_n[0] : 0;
+    A.ncand[2 * o + 1] = cmr > 0.f ? sh_n[1] : 0;
+  }
+  if (threadIdx.x < 2 * NCAND) {
+    const int set = threadIdx.x / NCAND, k = threadIdx.x % NCAND;
+    if (k < sh_n[set]) A.cand[(2 * o + set) * NCAND + k] = sh_c[set][k];
   }
 }
 
-// launch 5: merge the chunk winners of sampled sequences, write outputs and the rollback; one wave
-// per sequence, lane c holding chunk c's winner (winners merged by value, then lowest index)
-template <bool PROBS>
+// launch 4: one wave per sampled sequence draws the extra token and writes the outputs and rollback:
+// the exact keys of the candidates of every chunk whose max reaches the margin (first index on ties),
+// with S summed over the chunks in increasing order.
+template <int DT, bool PROBS>
 __global__ void __launch_bounds__(64) accept_final_kernel(AcceptArgs A) {
-  const int b = blockIdx.x;
-  if (!PROBS && A.temps[b] <= 0.f) return;  // greedy sequences were finished by the step
+  constexpr int PD = ProbType<DT, PROBS>::value;
+  const int b = blockIdx.x, lane = threadIdx.x;
+  const float T = PROBS ? 1.f : A.temps[b];
+  if (!PROBS && T <= 0.f) return;  // greedy sequences were finished by the step
+  const int ke = keff_of(A, b);
+  const int j = A.jpos[b];
+  const bool bonus = j >= ke;
+  const int64_t o0 = (int64_t)b * A.nchr;
+  float s = 0.f;
+  if (!bonus) {
+    for (int c0 = 0; c0 < A.nchr; c0 += 64) {
+      const float rc = c0 + lane < A.nchr ? A.resid[o0 + c0 + lane] : 0.f;
+      const int n = min(64, A.nchr - c0);
+      for (int k = 0; k < n; ++k) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rc), k));
+    }
+    s = Elem<PD>::round(s);
+  }
+  const int set = (bonus || !(s > 0.f)) ? 0 : 1;   // 0: w = p (speculative.py:31, 33), 1: w = r / S
+  float gmax = 0.f;
+  for (int c = lane; c < A.nchr; c += 64) gmax = fmaxf(gmax, A.cmax[2 * (o0 + c) + set]);
+  gmax = wave_max(gmax);
+  const bool trust = gmax >= CAND_MIN;
+  const float th = cand_threshold(gmax, set ? CandMargin<PD>::value : MARGIN_F32);
+  const int per = A.rs.n0 + A.rs.n1;
+  FastSoftmax sp, sq;
+  if (!PROBS) {
+    sp = FastSoftmax(T, A.mstats[(int64_t)b * per + j]);
+    if (!bonus) sq = FastSoftmax(T, A.mstats[(int64_t)b * per + A.rs.n0 + j]);
+  }
+  const auto* pr = row_ptr<DT>(A.rs, b, j);
+  const PairRow<DT, PROBS> pair{pr, bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j), sp, sq};
+  const float* er = A.E + (int64_t)b * A.ldE;
+  auto key = [&](int64_t col) { return set ? pair.key_r(col, s, er[col]) : pair.key_p(col, er[col]); };
   float v = -INFINITY;
   int extra = 0x7fffffff;
-  for (int c = threadIdx.x; c < A.nchr; c += 64)
-    argmax_merge(v, extra, A.pv[(int64_t)b * A.nchr + c], A.pi[(int64_t)b * A.nchr + c]);
+  for (int c0 = 0; c0 < A.nchr; c0 += 64) {
+    // lane l: chunk c0 + l, kept if its max reaches the margin; the kept chunks are then taken in turn
+    const int cl = c0 + lane;
+    const bool in = cl < A.nchr;
+    const bool keep = in && (!trust || A.cmax[2 * (o0 + cl) + set] >= th);
+    const int ncl = in ? A.ncand[2 * (o0 + cl) + set] : 0;
+    uint64_t kept = __ballot(keep);
+    while (kept) {
+      const int k = __ffsll((unsigned long long)kept) - 1;
+      kept &= kept - 1;
+      const int c = c0 + k;
+      const int n = __builtin_amdgcn_readlane(ncl, k);
+      if (trust && n <= NCAND) {
+        if (lane < n) {
+          const int col = A.cand[(2 * (o0 + c) + set) * NCAND + lane];
+          argmax_merge(v, extra, key(col), col);
+        }
+      } else {   // exact rescan of the chunk
+        const int64_t hi = min((int64_t)(c + 1) * CHR, A.V);
+        for (int64_t col = (int64_t)c * CHR + lane; col < hi; col += 64) argmax_merge(v, extra, key(col), (int)col);
+      }
+    }
+  }
   wave_argmax(v, extra);
-  if (threadIdx.x == 0) write_outputs(A, b, A.jpos[b], extra);
+  if (lane == 0) write_outputs(A, b, j, extra);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -570,17 +708,18 @@ int64_t nchunks_r(int64_t V) { return (V + CHR - 1) / CHR; }
 int64_t accept_ws(int64_t B, int64_t K, int64_t V) {
   const int64_t nch = nchunks(V), nchr = nchunks_r(V);
   auto r = [](int64_t n) { return ((n + 255) / 256) * 256; };
-  return r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) +
-         r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) + 3 * r(B * nchr * 4) + r(B * 4);
+  return r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) + r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) +
+         r(B * nchr * 4) + 2 * r(B * nchr * 2 * 4) + r(B * nchr * 2 * NCAND * 4) + r(B * 4);
 }
 
 void carve_accept(AcceptArgs& A, void* workspace, int64_t B, int64_t K, int nch, int nchr) {
   Carve cv{reinterpret_cast<char*>(workspace)};
   A.stats = cv.take<Stat>(B * (2 * K + 1) * nch);
   A.mstats = cv.take<Stat>(B * (2 * K + 1));
-  A.pv = cv.take<float>(B * nchr);
-  A.pi = cv.take<int>(B * nchr);
   A.resid = cv.take<float>(B * nchr);
+  A.cmax = cv.take<float>(B * nchr * 2);
+  A.ncand = cv.take<int>(B * nchr * 2);
+  A.cand = cv.take<int>(B * nchr * 2 * NCAND);
   A.jpos = cv.take<int>(B);
 }
 
@@ -593,15 +732,13 @@ int launch_accept(const AcceptArgs& A, bool probs, hipStream_t s) {
   const dim3 finals((unsigned)A.B);
   if (!probs) {
     accept_stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(A.B * per)), THREADS, 0, s>>>(A);
-    accept_step_kernel<DT, false><<<dim3((unsigned)A.B), 64, 0, s>>>(A);
-    accept_residual_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
-    accept_argmax_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
-    accept_final_kernel<false><<<finals, 64, 0, s>>>(A);
+    accept_step_kernel<DT, false><<<dim3((unsigned)A.B), 64 * STEP_WAVES, 0, s>>>(A);
+    accept_pair_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
+    accept_final_kernel<DT, false><<<finals, 64, 0, s>>>(A);
   } else {
-    accept_step_kernel<DT, true><<<dim3((unsigned)A.B), 64, 0, s>>>(A);
-    accept_residual_kernel<DT, true><<<chunks, THREADS, 0, s>>>(A);
-    accept_argmax_kernel<DT, true><<<chunks, THREADS, 0, s>>>(A);
-    accept_final_kernel<true><<<finals, 64, 0, s>>>(A);
+    accept_step_kernel<DT, true><<<dim3((unsigned)A.B), 64 * STEP_WAVES, 0, s>>>(A);
+    accept_pair_kernel<DT, true><<<chunks, THREADS, 0, s>>>(A);
+    accept_final_kernel<DT, true><<<finals, 64, 0, s>>>(A);
   }
   return fs::launch_status("spec_accept");
 }

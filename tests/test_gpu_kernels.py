@@ -351,3 +351,63 @@ def test_verify_draft_reference_streams():
         got = verify_draft(p, q, c["xs"], torch.Generator().manual_seed(c["seed"]))
         assert got == (c["accepted"], c["extra"]), c["seed"]
 
+
+
+def _verify_probs_case(p, q, xs, u, e):
+    out, n = ops.verify_probs(p.to(DEV), q.to(DEV), torch.tensor(xs, dtype=torch.int32).to(DEV), u.to(DEV),
+                              e.to(DEV))
+    n = int(n.cpu())
+    return out.cpu()[: n + 1].tolist(), n
+
+
+def test_residual_draw_ties_and_edge_sums():
+    """The residual draw's corner cases, each against the oracle's verify_draft arithmetic:
+    many equal keys across a chunk boundary (the first index wins), a residual that sums to zero
+    (the draw falls back to p), and a residual too small for the candidates' relative bound."""
+    case("residual draw corners")
+    v = 10000
+    base = torch.full((v,), 1.0 / v)
+    u = torch.tensor([0.99])
+    ones = torch.ones(v)
+    # 1) equal residuals on columns 4090..4109 (two 4096-column chunks) with equal noise
+    p = base.clone().reshape(1, v).repeat(2, 1)
+    q = base.clone().reshape(1, v)
+    q[0, 7] = 4.0 / v   # proposal 7 has ratio 1/4: rejected by u = 0.99
+    p[0, 4090:4110] += 1.0 / v
+    got = _verify_probs_case(p, q, [7], u, ones)
+    want = orc.verify_with_noise(p, q, [7], u, ones)
+    assert got == (want[0] + [want[1]], len(want[0])) and want[1] == 4090
+    # 2) Σ max(p - q, 0) = 0: w = p
+    p = base.clone().reshape(1, v).repeat(2, 1)
+    p[0, 7] = 0.5 / v
+    e = torch.empty(v).exponential_(generator=torch.Generator().manual_seed(21))
+    got = _verify_probs_case(p, q[:, :].clone().fill_(1.0 / v), [7], u, e)
+    qq = torch.full((1, v), 1.0 / v)
+    want = orc.verify_with_noise(p, qq, [7], u, e)
+    assert got == (want[0] + [want[1]], len(want[0]))
+    # 3) a residual of 1e-36 at a single column: below the bound, the draw rescans exactly
+    p = base.clone().reshape(1, v).repeat(2, 1)
+    q = base.clone().reshape(1, v)
+    p[0, 7] = 0.5 / v
+    q[0, 1234] = 0.0
+    p[0, 1234] = 1e-36
+    got = _verify_probs_case(p, q, [7], u, e)
+    want = orc.verify_with_noise(p, q, [7], u, e)
+    assert got == (want[0] + [want[1]], len(want[0])) and want[1] == 1234
+
+
+def test_residual_draw_random_rows_bit_exact():
+    """Random probability rows (f32 and bf16) with forced rejections at every position."""
+    case("residual draw random")
+    g = torch.Generator().manual_seed(22)
+    for dtype in (torch.float32, torch.bfloat16):
+        for trial in range(6):
+            k, v = 4, 32000 + 17 * trial
+            p = torch.softmax(torch.randn(k + 1, v, generator=g) * 2, -1).to(dtype)
+            q = torch.softmax(torch.randn(k, v, generator=g) * 2, -1).to(dtype)
+            xs = torch.randint(0, v, (k,), generator=g).tolist()
+            u = torch.rand(k, generator=g) * (0.2 if trial % 2 else 1.0)
+            e = torch.empty(v).exponential_(generator=g)
+            got = _verify_probs_case(p, q, xs, u, e)
+            want = orc.verify_with_noise(p, q, xs, u, e)
+            assert got == (want[0] + [want[1]], len(want[0])), (dtype, trial)
