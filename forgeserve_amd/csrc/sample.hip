@@ -358,14 +358,13 @@ FS_DEVICE Stat merge_row_wave(const Stat& st, bool in, int nch) {
 // argmax of target row j).
 template <int DT, bool PROBS>
 FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* ms) {
-  const int ke = keff_of(A, b);
-  const float T = PROBS ? 1.f : A.temps[b];
   const int per = A.rs.n0 + A.rs.n1;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // wave 0, lane i: proposal i of the first 64
+  // No load waits for another: the proposals (wave 0, lane i: proposal i of the first 64) and the
+  // chunk statistics are fetched for all K positions and rows, and k_eff only decides what is used.
   int x0 = -1;
   float u0 = 0.f, xp0 = 0.f, xq0 = 0.f;
-  if (w == 0 && lane < ke) {
+  if (w == 0 && lane < A.K) {
     x0 = A.draft[(int64_t)b * A.K + lane];
     u0 = A.u[(int64_t)b * A.K + lane];
     if (x0 >= 0 && x0 < A.V) {
@@ -373,6 +372,8 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* ms) {
       xq0 = Elem<DT>::load(row_ptr<DT>(A.rs, b, A.rs.n0 + lane), x0);
     }
   }
+  const int ke = keff_of(A, b);
+  const float T = PROBS ? 1.f : A.temps[b];
   auto used = [&](int r) { return r < per && (r < A.rs.n0 ? r <= ke : (r - A.rs.n0) < ke); };
   if (!PROBS) {
     if (A.nch <= 64) {
@@ -381,7 +382,7 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* ms) {
 #pragma unroll
         for (int i = 0; i < STEP_ROWS; ++i) {
           const int r = r0 + w + STEP_WAVES * i;
-          if (used(r) && lane < A.nch) st[i] = A.stats[((int64_t)b * per + r) * A.nch + lane];
+          if (r < per && lane < A.nch) st[i] = A.stats[((int64_t)b * per + r) * A.nch + lane];
         }
 #pragma unroll
         for (int i = 0; i < STEP_ROWS; ++i) {
@@ -605,22 +606,31 @@ __global__ void __launch_bounds__(64) accept_final_kernel(AcceptArgs A) {
   const int b = blockIdx.x, lane = threadIdx.x;
   const float T = PROBS ? 1.f : A.temps[b];
   if (!PROBS && T <= 0.f) return;  // greedy sequences were finished by the step
+  const int64_t o0 = (int64_t)b * A.nchr;
+  // the first 64 chunks' records are fetched together with the step's outcome; chunks past 64
+  // (vocabularies over 64 chunks) are fetched as they are needed
+  const bool in0 = lane < A.nchr;
+  const float rc0 = in0 ? A.resid[o0 + lane] : 0.f;
+  const float cm0[2] = {in0 ? A.cmax[2 * (o0 + lane)] : 0.f, in0 ? A.cmax[2 * (o0 + lane) + 1] : 0.f};
+  const int nc0[2] = {in0 ? A.ncand[2 * (o0 + lane)] : 0, in0 ? A.ncand[2 * (o0 + lane) + 1] : 0};
   const int ke = keff_of(A, b);
   const int j = A.jpos[b];
   const bool bonus = j >= ke;
-  const int64_t o0 = (int64_t)b * A.nchr;
   float s = 0.f;
   if (!bonus) {
     for (int c0 = 0; c0 < A.nchr; c0 += 64) {
-      const float rc = c0 + lane < A.nchr ? A.resid[o0 + c0 + lane] : 0.f;
+      const float rc = c0 == 0 ? rc0 : (c0 + lane < A.nchr ? A.resid[o0 + c0 + lane] : 0.f);
       const int n = min(64, A.nchr - c0);
       for (int k = 0; k < n; ++k) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rc), k));
     }
     s = Elem<PD>::round(s);
   }
   const int set = (bonus || !(s > 0.f)) ? 0 : 1;   // 0: w = p (speculative.py:31, 33), 1: w = r / S
+  auto cmax_at = [&](int c0) {
+    return c0 == 0 ? cm0[set] : (c0 + lane < A.nchr ? A.cmax[2 * (o0 + c0 + lane) + set] : 0.f);
+  };
   float gmax = 0.f;
-  for (int c = lane; c < A.nchr; c += 64) gmax = fmaxf(gmax, A.cmax[2 * (o0 + c) + set]);
+  for (int c0 = 0; c0 < A.nchr; c0 += 64) gmax = fmaxf(gmax, cmax_at(c0));
   gmax = wave_max(gmax);
   const bool trust = gmax >= CAND_MIN;
   const float th = cand_threshold(gmax, set ? CandMargin<PD>::value : MARGIN_F32);
@@ -640,8 +650,8 @@ __global__ void __launch_bounds__(64) accept_final_kernel(AcceptArgs A) {
     // lane l: chunk c0 + l, kept if its max reaches the margin; the kept chunks are then taken in turn
     const int cl = c0 + lane;
     const bool in = cl < A.nchr;
-    const bool keep = in && (!trust || A.cmax[2 * (o0 + cl) + set] >= th);
-    const int ncl = in ? A.ncand[2 * (o0 + cl) + set] : 0;
+    const bool keep = in && (!trust || cmax_at(c0) >= th);
+    const int ncl = c0 == 0 ? nc0[set] : (in ? A.ncand[2 * (o0 + cl) + set] : 0);
     uint64_t kept = __ballot(keep);
     while (kept) {
       const int k = __ffsll((unsigned long long)kept) - 1;
