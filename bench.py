@@ -35,6 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0   # dense bf16
 CFG = dict(vocab_size=128256, d_model=4096, n_layers=32, n_heads=32, n_kv_heads=8, ffn_dim=14336,
            max_seq_len=10240)
 DRAFT_LAYERS = 4
@@ -169,9 +170,11 @@ def profiled_traffic(name):
     return int(m.group(1)) if m else None
 
 
-def time_accept(torch, ops, reps, warmup):
+def time_accept(torch, ops, reps, warmup, with_stats=False):
     """The acceptance kernel alone at the benchmark shape (bf16 logits, V = 128256): mean seconds per call.
-    The call is captured once into a graph and replayed, so the host's launch overhead is not timed."""
+    The call is captured once into a graph and replayed, so the host's launch overhead is not timed.
+    with_stats: the rows' softmax statistics are given, as the LM head's epilogue emits them in the
+    round (they are computed here once, outside the timed calls)."""
     v = CFG["vocab_size"]
     g = torch.Generator(device="cuda").manual_seed(3)
     tl = torch.randn(BATCH, K + 1, v, device="cuda", generator=g).mul_(2).bfloat16()
@@ -180,15 +183,22 @@ def time_accept(torch, ops, reps, warmup):
     temps = torch.ones(BATCH, device="cuda")
     u = torch.rand(BATCH, K, device="cuda", generator=g)
     e = torch.empty(BATCH, v, device="cuda").exponential_(generator=g)
+    st = None
+    if with_stats:
+        rows = torch.cat([tl, dl], 1).float()
+        mx = rows.max(-1).values
+        f = torch.stack([mx, torch.exp(rows - mx[..., None]).sum(-1), mx], -1).contiguous().view(torch.int32)
+        st = torch.cat([f, rows.argmax(-1).to(torch.int32)[..., None]], -1).contiguous()
+        del rows
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for _ in range(max(warmup, 1)):
-            ops.spec_accept(tl, dl, xs, None, temps, u, e)
+            ops.spec_accept(tl, dl, xs, None, temps, u, e, row_stats=st)
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        ops.spec_accept(tl, dl, xs, None, temps, u, e)
+        ops.spec_accept(tl, dl, xs, None, temps, u, e, row_stats=st)
     graph.replay()
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
@@ -198,6 +208,38 @@ def time_accept(torch, ops, reps, warmup):
         b.record()
     torch.cuda.synchronize()
     return sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e-3
+
+
+def time_gemms(torch, ops, model, m, reps=10):
+    """One layer's four GEMMs and the LM head at M rows (the verify pass: M = B*(k+1); a draft step:
+    M = B), with the model's own weights: {name: (seconds per call, flops)}."""
+    blk = model.layers[0]
+    d = model.cfg.d_model
+    shapes = {"qkv": (d, blk.attn.qkv_weight()), "o": (d, blk.attn.wo.weight),
+              "gate_up": (d, blk.mlp.gate_up_weight()), "down": (blk.mlp.w_down.weight.shape[1], blk.mlp.w_down.weight),
+              "head": (d, model.lm_head.weight)}
+    out = {}
+    for name, (kdim, w) in shapes.items():
+        x = torch.randn(m, kdim, device="cuda").to(w.dtype)
+        for _ in range(2):
+            ops.gemm(x, w)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in ev:
+            a.record()
+            ops.gemm(x, w)
+            b.record()
+        torch.cuda.synchronize()
+        out[name] = (sum(a.elapsed_time(b) for a, b in ev) / reps * 1e-3, 2.0 * m * kdim * w.shape[0])
+    return out
+
+
+def gemm_summary(times, layers, peak_tflops):
+    """Σ flops / Σ time over a pass's GEMMs (the layer GEMMs `layers` times, the head once)."""
+    t = sum(v[0] for k, v in times.items() if k != "head") * layers + times["head"][0]
+    f = sum(v[1] for k, v in times.items() if k != "head") * layers + times["head"][1]
+    return {"tflops": round(f / t / 1e12, 1), "frac": round(f / t / 1e12 / peak_tflops, 4),
+            "ms_per_pass": round(t * 1e3, 3),
+            "per_gemm_us": {k: round(v[0] * 1e6, 1) for k, v in times.items()}}
 
 
 def attention_inputs(torch, fa, seed=0):
@@ -248,11 +290,12 @@ def kernel_mode(args):
         byts = attn_bytes(ctxs, K + 1, CFG["n_heads"], CFG["n_kv_heads"], 128, BLOCK)
         out = {"kernel": "paged_attention verify", "calls": steps, "avg_us": round(sec * 1e6, 2),
                "algorithmic_bytes": byts, "achieved_GBs": round(byts / sec / 1e9, 1)}
-    elif args.kernel == "accept":
-        sec = time_accept(torch, ops, steps, warmup)
+    elif args.kernel in ("accept", "accept_stats"):
+        stats = args.kernel == "accept_stats"
+        sec = time_accept(torch, ops, steps, warmup, with_stats=stats)
         byts = accept_bytes(BATCH, K, CFG["vocab_size"])
-        out = {"kernel": "spec_accept", "calls": steps, "avg_us": round(sec * 1e6, 2), "algorithmic_bytes": byts,
-               "achieved_GBs": round(byts / sec / 1e9, 1)}
+        out = {"kernel": "spec_accept" + (" (row statistics given)" if stats else ""), "calls": steps,
+               "avg_us": round(sec * 1e6, 2), "algorithmic_bytes": byts, "achieved_GBs": round(byts / sec / 1e9, 1)}
     else:
         # 1 GiB device copies: f32 (16 bytes per lane per load) and bf16 (8 bytes per lane per load)
         out = {"kernel": "copy 1 GiB", "calls": steps}
@@ -283,7 +326,7 @@ def main():
     ap.add_argument("--temperature", type=float, default=0.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--kernel", choices=("round", "attention", "accept", "copy"), default="round")
+    ap.add_argument("--kernel", choices=("round", "attention", "accept", "accept_stats", "copy"), default="round")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -360,6 +403,9 @@ def main():
     v = CFG["vocab_size"]
     acc_avg = time_accept(torch, ops, 20, 3)
     acc_gbs = accept_bytes(BATCH, K, v) / acc_avg / 1e9
+    accs_avg = time_accept(torch, ops, 20, 3, with_stats=True)
+    gemm_verify = gemm_summary(time_gemms(torch, ops, target, BATCH * (K + 1)), CFG["n_layers"], MFMA_PEAK_TFLOPS)
+    gemm_draft = gemm_summary(time_gemms(torch, ops, draft, BATCH), draft.cfg.n_layers, MFMA_PEAK_TFLOPS)
 
     result = {
         "metric": "accepted tok/s (8B-shape, k=6, bs=64); verify-attn HBM GB/s vs peak",
@@ -390,7 +436,13 @@ def main():
                      "algorithmic_bytes_per_launch": int(attn_traffic)},
         "accept_kernel": {"avg_us": round(acc_avg * 1e6, 2), "achieved_GBs": round(acc_gbs, 1),
                           "algorithmic_bytes": accept_bytes(BATCH, K, v),
-                          "traffic": profiled_traffic("spec_accept_8b.md")},
+                          "traffic": profiled_traffic("spec_accept_8b.md"),
+                          # as the round runs it: the rows' statistics come from the LM heads' epilogue
+                          "with_head_stats": {"avg_us": round(accs_avg * 1e6, 2),
+                                              "effective_GBs": round(accept_bytes(BATCH, K, v) / accs_avg / 1e9, 1)}},
+        # MFMA utilisation of the dense GEMMs (bf16 dense peak 2.5 PFLOP/s), event-timed after the rounds
+        "gemm_verify_m448": gemm_verify,
+        "gemm_draft_m64": gemm_draft,
     }
     if not args.no_cpu_baseline:
         log("timing the CPU baseline ...")

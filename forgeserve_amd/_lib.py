@@ -45,6 +45,10 @@ SIGNATURES = {
     "fs_gemm": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i32, c_p, c_i64,
                         c_p]),
     "fs_gemm_workspace_size": (c_i64, [c_i64, c_i64, c_i64, c_i32]),
+    "fs_gemm_row_stats": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_p, c_p, c_i64, c_i64,
+                                  c_p]),
+    "fs_gemm_row_stats_parts": (c_i64, [c_i64, c_i64, c_i64]),
+    "fs_row_stats_merge": (c_i32, [c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_i64, c_i64, c_p]),
     "fs_add_rmsnorm": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_f32, c_i32, c_p]),
     "fs_silu_mul": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i32, c_p]),
     "fs_embedding": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_i32, c_p]),
@@ -54,6 +58,8 @@ SIGNATURES = {
     "fs_sampling_workspace_size": (c_i64, [c_i64, c_i64]),
     "fs_spec_accept": (c_i32, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i32, c_i32, c_i64, c_i32, c_p, c_p, c_p,
                                c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_i64, c_p]),
+    "fs_spec_accept_stats": (c_i32, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i32, c_i32, c_i64, c_i32, c_p, c_p, c_p,
+                                     c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_i64, c_p]),
     "fs_verify_probs": (c_i32, [c_p, c_i64, c_p, c_i64, c_i32, c_i64, c_i32, c_p, c_p, c_p, c_p, c_p, c_p, c_i64,
                                 c_p]),
     "fs_spec_accept_workspace_size": (c_i64, [c_i32, c_i32, c_i64]),

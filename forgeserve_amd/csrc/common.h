@@ -86,6 +86,13 @@ FS_DEVICE void wave_argmax(float& v, int& i) {
   }
 }
 
+// Softmax statistics of a run of logits x at temperature T: m = max of y = x/T, s = Σ exp(y - m),
+// and the first argmax (av, ai) of x. Runs are merged in a fixed order wherever they are combined.
+struct SoftmaxStat {
+  float m, s, av;
+  int ai;
+};
+
 // ------------------------------------------------------------------------------------------------
 // host side: error reporting shared by every entry point
 // ------------------------------------------------------------------------------------------------

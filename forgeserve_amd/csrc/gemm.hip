@@ -158,13 +158,22 @@ FS_DEVICE void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int BM, int BN, int NS, int WGM = 2, int WGN = 2>
+// Row statistics epilogue (the LM head feeding sampling and acceptance, sampling.py:13): for every
+// output row and every WN-column block of a wave, the softmax statistics of the stored (bf16-rounded)
+// values at that row's 1/T, written to stats[row * ld + column / WN].
+struct RowStatsOut {
+  const float* inv_t;   // [M], or null for T = 1
+  SoftmaxStat* stats;   // row m's nparts records at stats + m * ld
+  int64_t nparts, ld;
+};
+
+template <int BM, int BN, int NS, int WGM = 2, int WGN = 2, bool STATS = false>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uint16_t* __restrict__ X, int64_t ldx,
                                                             const uint16_t* __restrict__ W, int64_t ldw,
                                                             uint16_t* __restrict__ C, int64_t ldc,
                                                             const uint16_t* __restrict__ R, int64_t ldr, int64_t M,
                                                             int64_t N, int64_t K, int tiles_m, int ntiles,
-                                                            float* __restrict__ part) {
+                                                            float* __restrict__ part, RowStatsOut rs) {
   constexpr int KB = 64;                       // k per stage
   constexpr int ROWB = KB * 2;                 // bytes per stage row (128)
   constexpr int NW = WGM * WGN;                // waves: WGM along M, WGN along N
@@ -298,6 +307,49 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
       }
     }
   }
+  if (STATS) {   // (no residual on this path: the statistics are of the rounded products)
+    constexpr float L2E = 1.4426950408889634f;
+    const int64_t p = (n0 + wn * WN) / WN;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      // the four lanes l16 + 16g share a row: their shuffles never mix rows, so rows past M are
+      // harmless and are simply not written
+      const int64_t row = m0 + wm * WM + 16 * i + l16;
+      const float inv_t = (rs.inv_t && row < M) ? rs.inv_t[row] : 1.f;
+      float ym = -INFINITY, av = -INFINITY;
+      int ai = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t col0 = n0 + wn * WN + 16 * j + 4 * g;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (col0 + r >= N) continue;
+          const float v = Elem<FS_BF16>::round(acc[i][j][r]);
+          ym = fmaxf(ym, v * inv_t);
+          argmax_merge(av, ai, v, (int)(col0 + r));
+        }
+      }
+#pragma unroll
+      for (int o = 16; o <= 32; o <<= 1) {
+        ym = fmaxf(ym, __shfl_xor(ym, o, 64));
+        const float ov = __shfl_xor(av, o, 64);
+        const int oi = __shfl_xor(ai, o, 64);
+        argmax_merge(av, ai, ov, oi);
+      }
+      const float ml = ym * L2E;
+      float se = 0.f;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t col0 = n0 + wn * WN + 16 * j + 4 * g;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (col0 + r < N) se += __builtin_amdgcn_exp2f(fmaf(Elem<FS_BF16>::round(acc[i][j][r]) * inv_t, L2E, -ml));
+      }
+      se += __shfl_xor(se, 16, 64);   // (g0 + g1) + (g2 + g3) in every lane
+      se += __shfl_xor(se, 32, 64);
+      if (g == 0 && row < M && p < rs.nparts) rs.stats[row * rs.ld + p] = SoftmaxStat{ym, ym == -INFINITY ? 0.f : se, av, ai};
+    }
+  }
 }
 
 // C = round(sum_s part[s]) (+ R, rounded again): the split-K partials added in increasing split order,
@@ -404,7 +456,75 @@ int split_for(int64_t N, int64_t K) {
   return s;
 }
 
+// The LDS-kernel configuration a shape runs with: the largest tile that still fills the GPU (measured
+// at M = 448 and 128 on the decoder's projections); M <= 64 takes 64x64 tiles.
+struct LdsCfg {
+  int bm, bn, wgm, wgn;
+};
+
+LdsCfg lds_cfg(int64_t M, int64_t N, int splits) {
+  if (M <= 64) return LdsCfg{64, 64, 2, 2};
+  const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256) * splits;
+  const int64_t t128 = ((M + 127) / 128) * ((N + 255) / 256) * splits;
+  if (t256 >= 192) return LdsCfg{256, 256, 4, 2};
+  if (t128 >= 128) return LdsCfg{128, 256, 2, 4};
+  return LdsCfg{128, 128, 2, 4};
+}
+
+template <bool STATS>
+void launch_lds(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c, int64_t ldc,
+                const uint16_t* r, int64_t ldr, int64_t M, int64_t N, int64_t K, int splits, float* part,
+                RowStatsOut rs, hipStream_t s) {
+  const LdsCfg cf = lds_cfg(M, N, splits);
+  const int tm = (int)((M + cf.bm - 1) / cf.bm), nt = tm * (int)((N + cf.bn - 1) / cf.bn);
+  const dim3 grid((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits);
+  if (cf.bm == 64) {
+    gemm_bf16_lds_kernel<64, 64, 4, 2, 2, STATS><<<grid, 256, 0, s>>>(a, lda, b, ldb, c, ldc, r, ldr, M, N, K, 1, nt,
+                                                                     part, rs);
+  } else if (cf.bm == 256) {
+    gemm_bf16_lds_kernel<256, 256, 2, 4, 2, STATS><<<grid, 512, 0, s>>>(a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm,
+                                                                       nt, part, rs);
+  } else if (cf.bn == 256) {
+    gemm_bf16_lds_kernel<128, 256, 3, 2, 4, STATS><<<grid, 512, 0, s>>>(a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm,
+                                                                       nt, part, rs);
+  } else {
+    gemm_bf16_lds_kernel<128, 128, 4, 2, 4, STATS><<<grid, 512, 0, s>>>(a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm,
+                                                                       nt, part, rs);
+  }
+}
+
+bool lds_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t K) {
+  return K % 64 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B);
+}
+
 }  // namespace
+
+extern "C" int64_t fs_gemm_row_stats_parts(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64 || split_for(N, K) != 1) return 0;
+  const LdsCfg cf = lds_cfg(M, N, 1);
+  const int64_t wn = cf.bn / cf.wgn;
+  return (N + wn - 1) / wn;
+}
+
+extern "C" int fs_gemm_row_stats(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                                 int64_t M, int64_t N, int64_t K, const float* inv_temperature, void* stats,
+                                 int64_t stats_ld, int64_t nparts, void* stream) {
+  FS_CHECK_ARG(A && B && C && stats, "gemm_row_stats: null pointer");
+  FS_CHECK_ARG(M >= 0 && N > 0 && N < 0x7fffffff && K > 0, "gemm_row_stats: M %lld N %lld K %lld", (long long)M,
+               (long long)N, (long long)K);
+  FS_CHECK_ARG(lda >= K && ldb >= K && ldc >= N, "gemm_row_stats: leading dimensions");
+  FS_CHECK_ARG(lds_ok(A, lda, B, ldb, K), "gemm_row_stats: needs K %% 64 == 0 and 16-byte aligned rows");
+  const int64_t want = fs_gemm_row_stats_parts(M, N, K);
+  FS_CHECK_ARG(want > 0 && nparts == want, "gemm_row_stats: nparts %lld, the shape needs %lld", (long long)nparts,
+               (long long)want);
+  FS_CHECK_ARG(stats_ld >= nparts && (reinterpret_cast<uintptr_t>(stats) & 15) == 0,
+               "gemm_row_stats: stats_ld %lld < nparts (or stats not 16-byte aligned)", (long long)stats_ld);
+  if (M == 0) return 0;
+  launch_lds<true>((const uint16_t*)A, lda, (const uint16_t*)B, ldb, (uint16_t*)C, ldc, nullptr, 0, M, N, K, 1, nullptr,
+                   RowStatsOut{inv_temperature, reinterpret_cast<SoftmaxStat*>(stats), nparts, stats_ld},
+                   fs::as_stream(stream));
+  return fs::launch_status("gemm_row_stats");
+}
 
 extern "C" int64_t fs_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int32_t dtype) {
   if (M <= 0 || N <= 0 || K <= 0 || dtype != FS_BF16) return 0;
@@ -422,7 +542,7 @@ extern "C" int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, v
   if (M == 0) return 0;
   hipStream_t s = fs::as_stream(stream);
   const bool mfma = dtype == FS_BF16 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B);
-  if (mfma && K % 64 == 0) {
+  if (mfma && lds_ok(A, lda, B, ldb, K)) {
     const uint16_t* a = (const uint16_t*)A;
     const uint16_t* b = (const uint16_t*)B;
     const int splits = N % 4 == 0 ? split_for(N, K) : 1;
@@ -434,35 +554,12 @@ extern "C" int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, v
       part = reinterpret_cast<float*>(workspace);
     }
     uint16_t* c = splits > 1 ? nullptr : (uint16_t*)C;
-    const uint16_t* r = (const uint16_t*)R;
-    if (M <= 64) {
-      const int nt = (int)((N + 63) / 64);
-      gemm_bf16_lds_kernel<64, 64, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 256, 0, s>>>(
-          a, lda, b, ldb, c, ldc, r, ldr, M, N, K, 1, nt, part);
-    } else {
-      // tile by how many tiles (x splits) the shape yields: the largest tile that still fills the
-      // GPU (measured at M = 448 and 128 on the decoder's projections)
-      const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256) * splits;
-      const int64_t t128 = ((M + 127) / 128) * ((N + 255) / 256) * splits;
-      if (t256 >= 192) {
-        const int tm = (int)((M + 255) / 256), nt = tm * (int)((N + 255) / 256);
-        gemm_bf16_lds_kernel<256, 256, 2, 4, 2><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 512, 0, s>>>(
-            a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part);
-      } else if (t128 >= 128) {
-        const int tm = (int)((M + 127) / 128), nt = tm * (int)((N + 255) / 256);
-        gemm_bf16_lds_kernel<128, 256, 3, 2, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 512, 0, s>>>(
-            a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part);
-      } else {
-        const int tm = (int)((M + 127) / 128), nt = tm * (int)((N + 127) / 128);
-        gemm_bf16_lds_kernel<128, 128, 4, 2, 4><<<dim3((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits), 512, 0, s>>>(
-            a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part);
-      }
-    }
+    launch_lds<false>(a, lda, b, ldb, c, ldc, (const uint16_t*)R, ldr, M, N, K, splits, part, RowStatsOut{}, s);
     if (int e = fs::launch_status("gemm_bf16_lds")) return e;
     if (splits > 1) {
       const int64_t n4 = M * N / 4;
       gemm_splitk_reduce_kernel<<<dim3((unsigned)((n4 + 255) / 256)), 256, 0, s>>>(part, splits, M, N, (uint16_t*)C,
-                                                                                   ldc, r, ldr);
+                                                                                   ldc, (const uint16_t*)R, ldr);
       return fs::launch_status("gemm_splitk_reduce");
     }
     return 0;

@@ -32,12 +32,9 @@ struct ProbType {
 };
 constexpr float LOG2E_F = 1.4426950408889634f;
 
-struct Stat {
-  float m;    // max of x/T (T > 0) or of x (T == 0)
-  float s;    // sum of exp(x/T - m) (T > 0)
-  float av;   // argmax value (of x)
-  int ai;     // argmax index (first occurrence)
-};
+// m: max of x/T (T > 0) or of x (T == 0); s: sum of exp(x/T - m) (T > 0); (av, ai): the first
+// argmax of x (T == 0; a vocab-wide pass leaves it unset for T > 0)
+typedef SoftmaxStat Stat;
 
 // Rows of a batch of sequences: for sequence b, rows 0..n0-1 come from base0 (row i at
 // base0 + b*sb0 + i*si0) and rows n0..n0+n1-1 from base1.
@@ -313,6 +310,7 @@ struct AcceptArgs {
   int64_t ldE;
   Stat* stats;           // [B*(2K+1)][nch] chunk partials (logits mode)
   Stat* mstats;          // [B*(2K+1)] merged row statistics (logits mode)
+  bool premerged;        // mstats are the caller's (from the LM head's epilogue): no statistics pass
   float* resid;          // [B][nchr] residual partial sums of the rejected row pair
   float* cmax;           // [B][nchr][2] max of the cheap keys p/E and r/E per chunk (0: none positive)
   int* ncand;            // [B][nchr][2] candidates of each draw (> NCAND: the list overflowed)
@@ -375,7 +373,7 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* ms) {
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
   auto used = [&](int r) { return r < per && (r < A.rs.n0 ? r <= ke : (r - A.rs.n0) < ke); };
-  if (!PROBS) {
+  if (!PROBS && !A.premerged) {
     if (A.nch <= 64) {
       for (int r0 = 0; r0 < per; r0 += STEP_WAVES * STEP_ROWS) {
         Stat st[STEP_ROWS];
@@ -698,6 +696,39 @@ __global__ void __launch_bounds__(THREADS) probs_kernel(RowSet rs, int64_t V, in
 }
 
 // ------------------------------------------------------------------------------------------------
+// row statistics from per-block partials (the LM head GEMM's epilogue)
+// ------------------------------------------------------------------------------------------------
+// One workgroup per row, one pass: each thread folds blocks p = tid, tid + THREADS, ... in order into
+// a running (max, sum) (the sum rescaled when the max grows) and a first argmax; the threads are then
+// combined in the block-reduction order. Row m's records are at parts + m * ld; the merged record
+// goes to out[(m / group) * gstride + m % group + offset].
+__global__ void __launch_bounds__(THREADS) row_stats_merge_kernel(const Stat* __restrict__ parts, int64_t ld,
+                                                                  int64_t nparts, Stat* __restrict__ out, int group,
+                                                                  int64_t gstride, int64_t offset) {
+  __shared__ float shf[THREADS / 64];
+  __shared__ int shi[THREADS / 64];
+  const int64_t m = blockIdx.x;
+  const Stat* pr = parts + m * ld;
+  float mt = -INFINITY, st = 0.f, av = -INFINITY;
+  int ai = 0x7fffffff;
+  for (int64_t p = threadIdx.x; p < nparts; p += THREADS) {
+    const Stat x = pr[p];
+    argmax_merge(av, ai, x.av, x.ai);
+    if (x.m == -INFINITY) continue;
+    if (x.m > mt) {
+      st = st * __builtin_amdgcn_exp2f((mt - x.m) * LOG2E_F) + x.s;   // exp2(-inf) = 0 while empty
+      mt = x.m;
+    } else {
+      st += x.s * __builtin_amdgcn_exp2f((x.m - mt) * LOG2E_F);
+    }
+  }
+  const float M = block_max(mt, shf);
+  block_argmax(av, ai, shf, shi);
+  const float S = block_sum(mt == -INFINITY ? 0.f : st * __builtin_amdgcn_exp2f((mt - M) * LOG2E_F), shf);
+  if (threadIdx.x == 0) out[(m / group) * gstride + m % group + offset] = Stat{M, S, av, ai};
+}
+
+// ------------------------------------------------------------------------------------------------
 // workspace carving
 // ------------------------------------------------------------------------------------------------
 struct Carve {
@@ -731,6 +762,7 @@ void carve_accept(AcceptArgs& A, void* workspace, int64_t B, int64_t K, int nch,
   A.ncand = cv.take<int>(B * nchr * 2);
   A.cand = cv.take<int>(B * nchr * 2 * NCAND);
   A.jpos = cv.take<int>(B);
+  A.premerged = false;
 }
 
 bool dtype_ok(int32_t dt) { return dt == FS_F32 || dt == FS_BF16 || dt == FS_F16; }
@@ -741,7 +773,7 @@ int launch_accept(const AcceptArgs& A, bool probs, hipStream_t s) {
   const dim3 chunks((unsigned)A.nchr, (unsigned)A.B);
   const dim3 finals((unsigned)A.B);
   if (!probs) {
-    accept_stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(A.B * per)), THREADS, 0, s>>>(A);
+    if (!A.premerged) accept_stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(A.B * per)), THREADS, 0, s>>>(A);
     accept_step_kernel<DT, false><<<dim3((unsigned)A.B), 64 * STEP_WAVES, 0, s>>>(A);
     accept_pair_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
     accept_final_kernel<DT, false><<<finals, 64, 0, s>>>(A);
@@ -837,11 +869,12 @@ extern "C" int fs_probs_from_logits(const void* logits, int64_t ld, int64_t R, i
   return fs::launch_status("probs_from_logits");
 }
 
-extern "C" int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
-                              int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype,
-                              const int32_t* draft_tokens, const int32_t* k_eff, const float* temperature,
-                              const float* u, const float* E, int64_t ldE, int32_t* out_tokens, int32_t* n_accepted,
-                              int32_t* seq_len, void* workspace, int64_t workspace_bytes, void* stream) {
+namespace {
+int spec_accept_impl(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb, int64_t dft_si,
+                     int32_t B, int32_t K, int64_t V, int32_t dtype, const int32_t* draft_tokens, const int32_t* k_eff,
+                     const float* temperature, const float* u, const float* E, int64_t ldE, int32_t* out_tokens,
+                     int32_t* n_accepted, int32_t* seq_len, const void* row_stats, void* workspace,
+                     int64_t workspace_bytes, void* stream) {
   FS_CHECK_ARG(tgt && temperature && out_tokens && n_accepted && workspace, "spec_accept: null pointer");
   FS_CHECK_ARG(K == 0 || (dft && draft_tokens && u), "spec_accept: null draft inputs");
   FS_CHECK_ARG(E != nullptr, "spec_accept: E (Exp(1) noise) is required");
@@ -868,12 +901,51 @@ extern "C" int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, c
   A.n_acc = n_accepted;
   A.seq_len = seq_len;
   carve_accept(A, workspace, B, K, nch, A.nchr);
+  if (row_stats) {
+    FS_CHECK_ARG((reinterpret_cast<uintptr_t>(row_stats) & 15) == 0, "spec_accept: row statistics not 16-byte aligned");
+    A.mstats = const_cast<Stat*>(reinterpret_cast<const Stat*>(row_stats));   // read only
+  }
+  A.premerged = row_stats != nullptr;
   hipStream_t s = fs::as_stream(stream);
   switch (dtype) {
     case FS_F32: return launch_accept<FS_F32>(A, false, s);
     case FS_BF16: return launch_accept<FS_BF16>(A, false, s);
     default: return launch_accept<FS_F16>(A, false, s);
   }
+}
+}  // namespace
+
+extern "C" int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
+                              int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype,
+                              const int32_t* draft_tokens, const int32_t* k_eff, const float* temperature,
+                              const float* u, const float* E, int64_t ldE, int32_t* out_tokens, int32_t* n_accepted,
+                              int32_t* seq_len, void* workspace, int64_t workspace_bytes, void* stream) {
+  return spec_accept_impl(tgt, tgt_sb, tgt_si, dft, dft_sb, dft_si, B, K, V, dtype, draft_tokens, k_eff, temperature, u,
+                          E, ldE, out_tokens, n_accepted, seq_len, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int fs_spec_accept_stats(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
+                                    int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype,
+                                    const int32_t* draft_tokens, const int32_t* k_eff, const float* temperature,
+                                    const float* u, const float* E, int64_t ldE, const void* row_stats,
+                                    int32_t* out_tokens, int32_t* n_accepted, int32_t* seq_len, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+  FS_CHECK_ARG(row_stats != nullptr, "spec_accept_stats: null row statistics");
+  return spec_accept_impl(tgt, tgt_sb, tgt_si, dft, dft_sb, dft_si, B, K, V, dtype, draft_tokens, k_eff, temperature, u,
+                          E, ldE, out_tokens, n_accepted, seq_len, row_stats, workspace, workspace_bytes, stream);
+}
+
+extern "C" int fs_row_stats_merge(const void* parts, int64_t parts_ld, int64_t nparts, int64_t M, void* out,
+                                  int32_t group, int64_t gstride, int64_t offset, void* stream) {
+  FS_CHECK_ARG(parts && out, "row_stats_merge: null pointer");
+  FS_CHECK_ARG(nparts > 0 && parts_ld >= nparts && M >= 0 && M <= 0x7fffffff && group >= 1 && gstride >= 0 &&
+                   offset >= 0,
+               "row_stats_merge: nparts %lld ld %lld M %lld group %d", (long long)nparts, (long long)parts_ld,
+               (long long)M, group);
+  if (M == 0) return 0;
+  row_stats_merge_kernel<<<dim3((unsigned)M), THREADS, 0, fs::as_stream(stream)>>>(
+      reinterpret_cast<const Stat*>(parts), parts_ld, nparts, reinterpret_cast<Stat*>(out), group, gstride, offset);
+  return fs::launch_status("row_stats_merge");
 }
 
 extern "C" int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_t ldq, int32_t K, int64_t V,

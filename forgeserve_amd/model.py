@@ -175,19 +175,25 @@ class ForgeModel(nn.Module):
     def embed(self, idx):
         return ops.embedding(idx.to(self.device), self.tok_emb.weight).reshape(*idx.shape, self.cfg.d_model)
 
-    def head(self, x):
+    def head(self, x, stats=None):
+        """Final norm + tied head (model.py:137-138). stats = (inv_temperature (rows,), parts): also emit
+        the logits' per-row softmax statistics (ops.gemm_row_stats)."""
         shape = x.shape
         y = ops.add_rmsnorm(x.reshape(-1, shape[-1]), self.norm.weight, self.norm.eps)
+        if stats is not None:
+            return ops.gemm_row_stats(y, self.lm_head.weight, stats[0], stats[1]).reshape(*shape[:-1],
+                                                                                        self.cfg.vocab_size)
         return ops.gemm(y, self.lm_head.weight).reshape(*shape[:-1], self.cfg.vocab_size)
 
     @torch.no_grad()
     def forward(self, idx, positions: Optional[torch.Tensor] = None, kv: Optional[List] = None,
-                last_only: bool = False):
+                last_only: bool = False, head_stats=None):
         """idx (B, T) token ids -> logits (B, T, vocab) (model.py:141-159).
 
         positions (B, T): absolute positions; default continues after what `kv` holds.
         kv: one cache view per layer (ContiguousKV or PagedLayerView); None uses a fresh cache.
-        last_only: return only the logits of the last position, (B, 1, vocab)."""
+        last_only: return only the logits of the last position, (B, 1, vocab).
+        head_stats: (inv_temperature, parts) for the head's rows: see head()."""
         dev = self.device
         if dev.type != "cuda":
             raise RuntimeError("ForgeModel runs on the GPU: move it with .to('cuda') first")
@@ -208,8 +214,8 @@ class ForgeModel(nn.Module):
             x = layer.step(x, b, t, pos32, view, rope)
         if last_only:
             x = x.view(b, t, -1)[:, -1].contiguous()
-            return self.head(x).view(b, 1, -1)
-        return self.head(x).view(b, t, -1)
+            return self.head(x, head_stats).view(b, 1, -1)
+        return self.head(x, head_stats).view(b, t, -1)
 
 
 def early_exit_draft(target: ForgeModel, n_layers: int) -> ForgeModel:

@@ -91,6 +91,54 @@ def gemm(a: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
     return out
 
 
+def row_stats_parts(m: int, n: int, k: int) -> int:
+    """Column blocks per row of gemm_row_stats at this shape (0: the shape has no statistics epilogue)."""
+    return int(_lib.load().fs_gemm_row_stats_parts(m, n, k))
+
+
+def gemm_row_stats(a: torch.Tensor, w: torch.Tensor, inv_temperature: Optional[torch.Tensor],
+                   stats: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = a @ w.T (the LM head, model.py:137-138) and, per row and column block, the softmax
+    statistics of the stored logits at 1/T = inv_temperature[row] (sampling.py:13). stats: int32
+    (M, nparts, 4) records (max, sum, argmax value as float bits, argmax index); rows may be strided."""
+    require_device(a, w, stats)
+    m, lda = _rows(a)
+    n, ldb = _rows(w)
+    k = a.shape[1]
+    if w.shape[1] != k or a.dtype != w.dtype or a.dtype != torch.bfloat16:
+        raise ValueError(f"gemm_row_stats: bf16 {tuple(a.shape)} x {tuple(w.shape)}")
+    nparts = row_stats_parts(m, n, k)
+    if (stats.dtype != I32 or tuple(stats.shape) != (m, nparts, 4) or stats.stride(2) != 1 or stats.stride(1) != 4
+            or stats.stride(0) % 4):
+        raise ValueError(f"gemm_row_stats: stats must be int32 ({m}, {nparts}, 4) with whole records per row")
+    if inv_temperature is not None and (inv_temperature.dtype != torch.float32 or inv_temperature.shape != (m,)):
+        raise ValueError("gemm_row_stats: inv_temperature must be float32 (M,)")
+    if out is None:
+        out = torch.empty((m, n), dtype=a.dtype, device=a.device)
+    _, ldc = _rows(out)
+    check(_lib.load().fs_gemm_row_stats(ptr(a), lda, ptr(w), ldb, ptr(out), ldc, m, n, k, ptr(inv_temperature),
+                                        ptr(stats), stats.stride(0) // 4, nparts, stream_ptr()), "gemm_row_stats")
+    return out
+
+
+def row_stats_merge(parts: torch.Tensor, out: torch.Tensor, group: int = 1, gstride: int = 1,
+                    offset: int = 0) -> torch.Tensor:
+    """Merge gemm_row_stats' (M, nparts, 4) records into one per row: row m goes to record
+    (m // group) * gstride + m % group + offset of out (int32 (..., 4), contiguous)."""
+    require_device(parts, out)
+    m, nparts, _ = parts.shape
+    if parts.dtype != I32 or out.dtype != I32 or out.shape[-1] != 4 or not out.is_contiguous():
+        raise ValueError("row_stats_merge: int32 records of 4")
+    if parts.stride(2) != 1 or parts.stride(1) != 4 or parts.stride(0) % 4:
+        raise ValueError("row_stats_merge: parts must hold whole records per row")
+    last = ((m - 1) // group) * gstride + (m - 1) % group + offset if m else 0
+    if last >= out.numel() // 4:
+        raise ValueError("row_stats_merge: out is too small for the row mapping")
+    check(_lib.load().fs_row_stats_merge(ptr(parts), parts.stride(0) // 4, nparts, m, ptr(out), group, gstride, offset,
+                                         stream_ptr()), "row_stats_merge")
+    return out
+
+
 def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, delta: Optional[torch.Tensor] = None,
                 x_out: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y = RMSNorm(x [+ delta]) (model.py:29-31); with delta, x + delta is also written to x_out."""
@@ -288,12 +336,15 @@ def sample_logits(logits: torch.Tensor, temperature, noise: Optional[torch.Tenso
 def spec_accept(tgt: torch.Tensor, dft: torch.Tensor, draft_tokens: torch.Tensor, k_eff: Optional[torch.Tensor],
                 temperature: torch.Tensor, u: torch.Tensor, noise: torch.Tensor,
                 seq_len: Optional[torch.Tensor] = None, out_tokens: Optional[torch.Tensor] = None,
-                n_accepted: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                n_accepted: Optional[torch.Tensor] = None,
+                row_stats: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Batched verify_draft from logits (speculative.py:20-33, sampling.py:9-13).
 
     tgt (B, K+1, V), dft (B, K, V) logits; draft_tokens int32 (B, K); k_eff int32 (B,) or None (= K);
     temperature float32 (B,); u float32 (B, K) uniforms; noise float32 (B, V) Exp(1);
-    seq_len int32 (B,) cached lengths, advanced in place by 1 + n_accepted.
+    seq_len int32 (B,) cached lengths, advanced in place by 1 + n_accepted;
+    row_stats: int32 (B, 2K+1, 4) softmax statistics of the rows (row_stats_merge of the LM heads'
+    gemm_row_stats at 1/temperature), which skips the statistics pass.
     Returns out_tokens int32 (B, K+1) (accepted, extra, then -1) and n_accepted int32 (B,)."""
     require_device(tgt, dft, draft_tokens, temperature, u, noise)
     b, k1, v = tgt.shape
@@ -315,6 +366,16 @@ def spec_accept(tgt: torch.Tensor, dft: torch.Tensor, draft_tokens: torch.Tensor
         n_accepted = torch.empty((b,), dtype=I32, device=tgt.device)
     lib = _lib.load()
     ws = _persistent_ws("accept", lib.fs_spec_accept_workspace_size(b, k, v), tgt.device)
+    if row_stats is not None:
+        if row_stats.dtype != I32 or tuple(row_stats.shape) != (b, 2 * k + 1, 4) or not row_stats.is_contiguous():
+            raise ValueError(f"spec_accept: row_stats must be contiguous int32 ({b}, {2 * k + 1}, 4)")
+        require_device(row_stats)
+        check(lib.fs_spec_accept_stats(ptr(tgt), tgt.stride(0), tgt.stride(1), ptr(dft), dft.stride(0),
+                                       dft.stride(1) if k else 0, b, k, v, _dt(tgt), ptr(draft_tokens), ptr(k_eff),
+                                       ptr(temperature), ptr(u), ptr(noise), noise.stride(0), ptr(row_stats),
+                                       ptr(out_tokens), ptr(n_accepted), ptr(seq_len), ptr(ws), ws.numel(),
+                                       stream_ptr()), "spec_accept")
+        return out_tokens, n_accepted
     check(lib.fs_spec_accept(ptr(tgt), tgt.stride(0), tgt.stride(1), ptr(dft), dft.stride(0), dft.stride(1) if k else 0,
                              b, k, v, _dt(tgt), ptr(draft_tokens), ptr(k_eff), ptr(temperature), ptr(u), ptr(noise),
                              noise.stride(0), ptr(out_tokens), ptr(n_accepted), ptr(seq_len), ptr(ws), ws.numel(),

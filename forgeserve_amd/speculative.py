@@ -222,6 +222,21 @@ class SpeculativeBatch:
         v = self.target.cfg.vocab_size
         temps = torch.tensor([s.temperature for s in seqs], dtype=torch.float32).to(self.dev, non_blocking=True)
         sampling = any(s.temperature > 0 for s in seqs)
+        # The LM heads emit the logits' softmax statistics (sampling.py:13) as they write them, so the
+        # acceptance does not read the 2k+1 logit rows back to normalise them.
+        d = self.target.cfg.d_model
+        fused = (self.dtype == torch.bfloat16 and k > 0 and ops.row_stats_parts(b, v, d) > 0
+                 and ops.row_stats_parts(b * (k + 1), v, d) > 0)
+        if fused:
+            inv_t = torch.tensor([1.0 / s.temperature if s.temperature > 0 else 0.0 for s in seqs],
+                                 dtype=torch.float32)
+            inv_t_d = inv_t.to(self.dev, non_blocking=True)
+            inv_t_t = inv_t.repeat_interleave(k + 1).to(self.dev, non_blocking=True)
+            # draft step i writes its rows' records into parts_d[:, i]; one merge after the last step
+            parts_d = torch.empty((b, k, ops.row_stats_parts(b, v, d), 4), dtype=I32, device=self.dev)
+            parts_t = torch.empty((b * (k + 1), ops.row_stats_parts(b * (k + 1), v, d), 4), dtype=I32,
+                                  device=self.dev)
+            row_stats = torch.empty((b, 2 * k + 1, 4), dtype=I32, device=self.dev)
 
         # 1. draft: step 0 re-feeds (tokens[-2], tokens[-1]) at (n-2, n-1); step i feeds x_{i-1} at n-1+i
         dft_logits = torch.empty((b, k, v), dtype=self.dtype, device=self.dev)
@@ -238,7 +253,8 @@ class SpeculativeBatch:
                 idx = cur.to(torch.int64)[:, None]
                 pos = torch.tensor([[ni - 1 + i if i < k_eff[r] else -1] for r, ni in enumerate(n)])
             views = self.pool_d.views(tab_d, pos)
-            logits = self.draft(idx, pos, views, last_only=True)[:, 0]
+            logits = self.draft(idx, pos, views, last_only=True,
+                                head_stats=(inv_t_d, parts_d[:, i]) if fused else None)[:, 0]
             dft_logits[:, i].copy_(logits)
             noise = None
             if sampling:
@@ -246,16 +262,23 @@ class SpeculativeBatch:
             ops.sample_logits(logits, temps, noise, out32=draft_tok[:, i])
             cur = draft_tok[:, i]
 
+        if fused:   # draft row (b, i) is record b*k + i: sequence b's draft rows k+1 .. 2k
+            ops.row_stats_merge(parts_d.view(b * k, -1, 4), row_stats, k, 2 * k + 1, k + 1)
+
         # 2. target verify over [tokens[-1], x_0 .. x_{k-1}] at n-1 .. n-1+k
         idx = torch.cat([last.to(self.dev)[:, None], draft_tok.to(torch.int64)], 1) if k else last[:, None]
         pos = torch.tensor([[ni - 1 + t if t <= k_eff[r] else -1 for t in range(k + 1)] for r, ni in enumerate(n)])
-        tgt_logits = self.target(idx, pos, self.pool_t.views(tab_t, pos))
+        tgt_logits = self.target(idx, pos, self.pool_t.views(tab_t, pos),
+                                 head_stats=(inv_t_t, parts_t) if fused else None)
+        if fused:
+            ops.row_stats_merge(parts_t, row_stats, k + 1, 2 * k + 1, 0)
 
         # 3. acceptance (+ device-side rollback of the cached lengths)
         u = torch.rand((b, max(k, 1)), dtype=torch.float32, device=self.dev, generator=self.gen)[:, :k].contiguous()
         noise = torch.empty((b, v), dtype=torch.float32, device=self.dev).exponential_(generator=self.gen)
         keff_dev = torch.tensor(k_eff, dtype=I32).to(self.dev, non_blocking=True)
-        out_tok, n_acc = ops.spec_accept(tgt_logits, dft_logits, draft_tok, keff_dev, temps, u, noise)
+        out_tok, n_acc = ops.spec_accept(tgt_logits, dft_logits, draft_tok, keff_dev, temps, u, noise,
+                                         row_stats=row_stats if fused else None)
         res = torch.cat([n_acc[:, None], out_tok], 1).cpu()
 
         committed = 0

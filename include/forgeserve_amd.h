@@ -117,6 +117,29 @@ int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int
 
 int64_t fs_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int32_t dtype);
 
+/* The LM head (model.py:137-138) with the softmax statistics of its logits (sampling.py:13) as a
+ * by-product, so that sampling and acceptance need not read the logits back to normalise them.
+ * C = A . B^T as fs_gemm (bf16, K % 64 == 0, 16-byte aligned rows, no residual), and for every row m
+ * and every column block p of the kernel's tiling, stats[m * stats_ld + p] = {max of y, sum of
+ * exp(y - max), max of x, first index of that max} over the block's stored (bf16) values x, with
+ * y = x * inv_temperature[m] (inv_temperature NULL: 1). nparts must equal
+ * fs_gemm_row_stats_parts(M, N, K) (0: the shape has no such kernel). No counterpart in the
+ * reference: it computes softmax(logits.float() / T) from the stored logits. */
+int fs_gemm_row_stats(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M,
+                      int64_t N, int64_t K, const float* inv_temperature, void* stats, int64_t stats_ld,
+                      int64_t nparts, void* stream);
+
+int64_t fs_gemm_row_stats_parts(int64_t M, int64_t N, int64_t K);
+
+/* Merge fs_gemm_row_stats' per-block statistics (row m's nparts records at parts + m * parts_ld)
+ * into one record per row, in a fixed order: row m goes to out[(m / group) * gstride + m % group +
+ * offset] (records of 16 bytes: max, sum, argmax value, argmax index). With group = K+1,
+ * gstride = 2K+1 the target's verify rows land where fs_spec_accept_stats expects them; with the K
+ * draft steps' records interleaved per sequence (row b*K + i) and group = K, gstride = 2K+1,
+ * offset = K+1 the draft rows do. */
+int fs_row_stats_merge(const void* parts, int64_t parts_ld, int64_t nparts, int64_t M, void* out, int32_t group,
+                       int64_t gstride, int64_t offset, void* stream);
+
 /* RMSNorm of model.py:29-31, optionally after a residual add (model.py:105-106):
  * if delta != NULL: x_out = x + delta (rounded to the dtype) is written, then normed.
  * y = ((x32 * rsqrt(mean(x32^2) + eps)) rounded to the dtype) * weight, rounded to the dtype. */
@@ -174,6 +197,16 @@ int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* 
                    const int32_t* k_eff, const float* temperature, const float* u, const float* E,
                    int64_t ldE, int32_t* out_tokens, int32_t* n_accepted, int32_t* seq_len, void* workspace,
                    int64_t workspace_bytes, void* stream);
+
+/* fs_spec_accept with the rows' softmax statistics given (row_stats: [B][2K+1] records of
+ * fs_row_stats_merge at 1/temperature, target rows 0..K then draft rows; 16-byte aligned): the
+ * vocab-wide statistics pass is skipped. Replaces the same seam as fs_spec_accept (speculative.py:20-33
+ * with probs_from_logits), for callers whose LM head produced the statistics (fs_gemm_row_stats). */
+int fs_spec_accept_stats(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
+                         int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype, const int32_t* draft_tokens,
+                         const int32_t* k_eff, const float* temperature, const float* u, const float* E,
+                         int64_t ldE, const void* row_stats, int32_t* out_tokens, int32_t* n_accepted,
+                         int32_t* seq_len, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* verify_draft (speculative.py:20-33) on probabilities instead of logits: p [K+1, V] rows at
  * p + i*ldp, q [K, V]; one sequence, K proposals; p and q in `dtype` (f32 from a softmax, or the

@@ -411,3 +411,70 @@ def test_residual_draw_random_rows_bit_exact():
             got = _verify_probs_case(p, q, xs, u, e)
             want = orc.verify_with_noise(p, q, xs, u, e)
             assert got == (want[0] + [want[1]], len(want[0])), (dtype, trial)
+
+
+def _records(m, s, av, ai):
+    """(..., 4) int32 records of softmax statistics (max, sum, argmax value, argmax index)."""
+    f = torch.stack([m.float(), s.float(), av.float()], -1).contiguous().view(torch.int32)
+    return torch.cat([f, ai.to(torch.int32)[..., None]], -1).contiguous()
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 5003, 256), (100, 4096, 128), (448, 6000, 256)])
+def test_gemm_row_stats(m, n, k):
+    """The head GEMM's statistics epilogue, merged per row, against torch on the stored logits:
+    max and argmax exact, the sum of exponentials within float rounding."""
+    case("gemm row stats", m, n, k)
+    g = torch.Generator().manual_seed(m + n)
+    a = (torch.randn(m, k, generator=g) * 0.5).bfloat16().to(DEV)
+    w = (torch.randn(n, k, generator=g) * 0.5).bfloat16().to(DEV)
+    inv_t = torch.tensor([0.0 if r % 5 == 0 else 1.0 / (0.5 + (r % 3) * 0.25) for r in range(m)], dtype=torch.float32)
+    nparts = ops.row_stats_parts(m, n, k)
+    assert nparts > 0
+    parts = torch.empty((m, nparts, 4), dtype=torch.int32, device=DEV)
+    out = ops.gemm_row_stats(a, w, inv_t.to(DEV), parts)
+    assert torch.equal(out, ops.gemm(a, w))            # the logits are the plain GEMM's
+    rs = ops.row_stats_merge(parts, torch.empty((m, 4), dtype=torch.int32, device=DEV)).cpu()
+    x = out.cpu().float()
+    y = x * inv_t[:, None]
+    mx = y.max(-1).values
+    fl = rs[:, :3].contiguous().view(torch.float32)
+    assert torch.equal(fl[:, 0], mx)
+    assert torch.equal(fl[:, 2], x.max(-1).values)
+    assert torch.equal(rs[:, 3], x.argmax(-1).to(torch.int32))
+    want = torch.exp((y - mx[:, None]).double()).sum(-1)
+    assert ((fl[:, 1].double() - want).abs() / want).max() < 2e-6
+
+
+@pytest.mark.parametrize("temperature", [1.0, 0.7, 0.0])
+def test_spec_accept_with_row_stats_bit_exact(temperature):
+    """fs_spec_accept_stats (statistics given, as the LM head emits them) against the oracle."""
+    case("spec_accept row stats", temperature)
+    b, k, v = 64, 5, 32000
+    tgt, dft = _c2_inputs(dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(7)
+    xs = torch.zeros(b, k, dtype=torch.int32)
+    for bi in range(b):
+        for i in range(k):
+            if temperature == 0:
+                xs[bi, i] = int(dft[bi, i].float().argmax())
+            else:
+                xs[bi, i] = orc.draw(orc.probs_from_logits(dft[bi, i].float(), temperature), orc.exp_noise(v, g))
+    u = torch.rand(b, k, generator=g)
+    e = torch.empty(b, v).exponential_(generator=g)
+    k_eff = torch.tensor([k if i % 5 else i % 4 for i in range(b)], dtype=torch.int32)
+    temps = torch.full((b,), float(temperature))
+    rows = torch.cat([tgt, dft], 1).float()                       # (b, 2k+1, v)
+    y = rows * (1.0 / temperature if temperature > 0 else 0.0)
+    mx = y.max(-1).values
+    st = _records(mx, torch.exp((y - mx[..., None]).double()).sum(-1).float(), rows.max(-1).values,
+                  rows.argmax(-1))
+    out, n = ops.spec_accept(tgt.to(DEV), dft.to(DEV), xs.to(DEV), k_eff.to(DEV), temps.to(DEV), u.to(DEV),
+                             e.to(DEV), row_stats=st.to(DEV))
+    out, n = out.cpu(), n.cpu()
+    for bi in range(b):
+        ke = int(k_eff[bi])
+        p = orc.probs_from_logits(tgt[bi, : ke + 1].float() if temperature == 0 else tgt[bi, : ke + 1], temperature)
+        q = orc.probs_from_logits(dft[bi, :ke].float() if temperature == 0 else dft[bi, :ke], temperature)
+        acc, extra = orc.verify_with_noise(p, q, xs[bi, :ke].tolist(), u[bi], e[bi])
+        assert int(n[bi]) == len(acc), bi
+        assert out[bi, : len(acc) + 1].tolist() == acc + [extra], bi
