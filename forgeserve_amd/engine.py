@@ -5,6 +5,16 @@ batched forward; when the pool runs out during decoding the most recently starte
 preempted (its blocks are freed, it is re-prefilled later from prompt + output). Scheduling and the
 order of random draws are the reference's; the forwards, the KV writes and the sampling are HIP
 kernels, and a decode step samples every row in one launch with a single device-to-host copy.
+
+With a draft model (`Engine(..., draft=..., k=...)`) a decode step is one batched draft-then-verify
+round over the running requests instead (speculative.py:53-85 for a batch): each request proposes up
+to k_eff = min(k, remaining - 1) tokens, the k+1 window is reserved in both pools before the round
+(preempting as above when a pool runs out), and EOS, max_new_tokens and max_seq_len stop a request
+exactly where one-token decoding would. The random numbers of a request come from its own stream,
+keyed by (seed, request id, position), so its tokens do not depend on which other requests share
+the batch. (A recompute preemption re-prefills and samples the next token from the prefill logits,
+as one-token decoding does; that moves the request's round boundaries, so at T > 0 a preempted
+request continues with a different, equally valid sample.)
 """
 
 from collections import deque
@@ -17,6 +27,7 @@ from . import ops
 from .model import ForgeModel
 from .paged import PagedKVPool
 from .sampling import exp_noise
+from .speculative import spec_round
 
 
 @dataclass
@@ -30,10 +41,47 @@ class Request:
     blocks: List[int] = field(default_factory=list)
     cached: int = 0
     finished: bool = False
+    blocks_d: List[int] = field(default_factory=list)   # draft pool blocks (speculative engine)
+
+
+def _stream_key(seed: int, rid: int, pos: int) -> int:
+    """Seed of request `rid`'s random stream for the round (or prefill) that starts at position `pos`."""
+    return ((seed * 1_000_003 + rid) * 1_000_033 + pos) % (1 << 62)
+
+
+class _KeyedDraws:
+    """A speculative round's random numbers, one stream per request keyed by (seed, request id,
+    position): the k draft Exp(1) rows, then u, then the final Exp(1) row. Greedy requests draw
+    nothing (their rows are ignored by the kernels)."""
+
+    def __init__(self, reqs, n, temps, seed, k, v, dev):
+        self.k, self.v, self.dev = k, v, dev
+        self.gens = [torch.Generator(device=dev).manual_seed(_stream_key(seed, r.id, ni)) if t > 0 else None
+                     for r, ni, t in zip(reqs, n, temps)]
+
+    def _rows(self, fn):
+        return torch.stack([fn(g) for g in self.gens])
+
+    def draft(self, i):
+        return self._rows(lambda g: torch.empty(self.v, device=self.dev).exponential_(generator=g) if g is not None
+                          else torch.ones(self.v, device=self.dev))
+
+    def accept(self):
+        # per request: u first, then E (one generator, fixed order)
+        u, e = [], []
+        for g in self.gens:
+            if g is None:
+                u.append(torch.zeros(self.k, device=self.dev))
+                e.append(torch.ones(self.v, device=self.dev))
+            else:
+                u.append(torch.rand(self.k, device=self.dev, generator=g))
+                e.append(torch.empty(self.v, device=self.dev).exponential_(generator=g))
+        return torch.stack(u).contiguous(), torch.stack(e)
 
 
 class Engine:
-    def __init__(self, model: ForgeModel, num_blocks: int, block_size: int = 16, max_batch: int = 8, seed: int = 0):
+    def __init__(self, model: ForgeModel, num_blocks: int, block_size: int = 16, max_batch: int = 8, seed: int = 0,
+                 draft: Optional[ForgeModel] = None, k: int = 4, draft_num_blocks: Optional[int] = None):
         self.model, self.cfg = model, model.cfg
         self.pool = PagedKVPool(self.cfg, num_blocks, block_size, tp=model.tp, dtype=model.dtype, device=model.device)
         self.max_batch = max_batch
@@ -42,13 +90,26 @@ class Engine:
         self.running: List[Request] = []
         self.requests: Dict[int, Request] = {}
         self.steps = self.preemptions = self.peak_running = self.peak_blocks = 0
+        # speculative decoding (optional): the draft keeps its own pool, as speculative.py:46 keeps kv_d
+        self.draft, self.k, self.seed = draft, k, seed
+        self.limit = self.cfg.max_seq_len
+        self.stats = {"rounds": 0, "proposed": 0, "accepted": 0}
+        if draft is not None:
+            if draft.cfg.vocab_size != self.cfg.vocab_size:
+                raise ValueError("target and draft must share a vocabulary")
+            if k < 1:
+                raise ValueError("k must be at least 1")
+            self.pool_d = PagedKVPool(draft.cfg, draft_num_blocks or num_blocks, block_size, dtype=model.dtype,
+                                      device=model.device)
+            self.limit = min(self.cfg.max_seq_len, draft.cfg.max_seq_len)
 
     # ---- public API ---------------------------------------------------------------------------------
     def add_request(self, prompt: List[int], max_new_tokens: int, eos_id: Optional[int] = None,
                     temperature: float = 0.0) -> int:
-        if not 0 < len(prompt) < self.cfg.max_seq_len:
-            raise ValueError(f"prompt length must be in 1..{self.cfg.max_seq_len - 1}")
-        if self.pool.blocks_for(len(prompt) + 1) > self.pool.allocator.num_blocks:
+        if not 0 < len(prompt) < self.limit:
+            raise ValueError(f"prompt length must be in 1..{self.limit - 1}")
+        if self.pool.blocks_for(len(prompt) + 1) > self.pool.allocator.num_blocks or (
+                self.draft is not None and self.pool_d.blocks_for(len(prompt) + 1) > self.pool_d.allocator.num_blocks):
             raise ValueError("prompt does not fit in the block pool")
         req = Request(len(self.requests), list(prompt), max_new_tokens, eos_id, temperature)
         self.requests[req.id] = req
@@ -68,7 +129,10 @@ class Engine:
         if self.waiting and len(self.running) < self.max_batch and self._try_prefill():
             pass
         elif self.running:
-            self._decode()
+            if self.draft is not None:
+                self._spec_decode()
+            else:
+                self._decode()
         elif self.waiting:
             raise RuntimeError("the head request cannot be scheduled: the block pool is too small")
         used = self.pool.allocator.num_blocks - self.pool.allocator.num_free
@@ -79,7 +143,9 @@ class Engine:
         req = self.waiting[0]
         tokens = req.prompt + req.output
         need = self.pool.blocks_for(len(tokens))
-        if need > self.pool.allocator.num_free:
+        spec = self.draft is not None
+        need_d = self.pool_d.blocks_for(len(tokens)) if spec else 0
+        if need > self.pool.allocator.num_free or (spec and need_d > self.pool_d.allocator.num_free):
             return False
         self.waiting.popleft()
         req.blocks = self.pool.allocator.allocate(need)
@@ -87,10 +153,97 @@ class Engine:
         views = self.pool.views(torch.tensor([req.blocks]), positions)
         logits = self.model(torch.tensor([tokens]), positions, views, last_only=True)
         req.cached = len(tokens)
-        self._append([req], logits[:, -1])
+        if spec:   # the draft's cache covers the same positions; the first token uses the request's stream
+            req.blocks_d = self.pool_d.allocator.allocate(need_d)
+            self.draft(torch.tensor([tokens]), positions, self.pool_d.views(torch.tensor([req.blocks_d]), positions),
+                       last_only=True)
+            self._append_keyed(req, logits[:, -1])
+        else:
+            self._append([req], logits[:, -1])
         if not req.finished:
             self.running.append(req)
         return True
+
+    # ---- speculative decoding ---------------------------------------------------------------------
+    def _remaining(self, req: Request) -> int:
+        return min(req.max_new_tokens - len(req.output), self.limit - len(req.prompt) - len(req.output))
+
+    def _k_eff(self, req: Request) -> int:
+        return max(0, min(self.k, self._remaining(req) - 1))
+
+    def _release(self, req: Request) -> None:
+        self.pool.allocator.release(req.blocks)
+        req.blocks = []
+        if self.draft is not None:
+            self.pool_d.allocator.release(req.blocks_d)
+            req.blocks_d = []
+
+    def _spec_decode(self) -> None:
+        """One draft-then-verify round over the running requests. Every request first gets the blocks
+        of its k+1 window (positions up to n-1+k_eff) in both pools; when a pool runs out the most
+        recently started request is preempted (engine.py:100-118)."""
+        i = 0
+        while i < len(self.running):
+            req = self.running[i]
+            span = len(req.prompt) + len(req.output) + self._k_eff(req)
+            need_t = self.pool.blocks_for(span) - len(req.blocks)
+            need_d = self.pool_d.blocks_for(span) - len(req.blocks_d)
+            if need_t > self.pool.allocator.num_free or need_d > self.pool_d.allocator.num_free:
+                if len(self.running) == 1:
+                    raise RuntimeError("the block pool is too small to hold even one sequence of this length")
+                victim = self.running.pop()
+                self._release(victim)
+                victim.cached = 0
+                self.waiting.appendleft(victim)
+                self.preemptions += 1
+                continue   # retry (or, if the victim was this request, the loop ends or moves on)
+            if need_t > 0:
+                req.blocks += self.pool.allocator.allocate(need_t)
+            if need_d > 0:
+                req.blocks_d += self.pool_d.allocator.allocate(need_d)
+            i += 1
+        if not self.running:
+            return
+        batch = list(self.running)
+        k_eff = [self._k_eff(r) for r in batch]
+        tokens = [r.prompt + r.output for r in batch]
+        temps = [float(r.temperature) for r in batch]
+        draws = _KeyedDraws(batch, [len(t) for t in tokens], temps, self.seed, max(k_eff), self.cfg.vocab_size,
+                            self.model.device)
+        res = spec_round(self.model, self.draft, self.pool, self.pool_d, tokens, [r.blocks for r in batch],
+                         [r.blocks_d for r in batch], k_eff, temps, draws)
+        self.stats["rounds"] += 1
+        for r, req in enumerate(batch):
+            a = int(res[r, 0])
+            self.stats["proposed"] += k_eff[r]
+            self.stats["accepted"] += a
+            for token in res[r, 1: a + 2].tolist():
+                self._push(req, token)
+                if req.finished:
+                    break
+            req.cached = len(req.prompt) + len(req.output) - 1
+            if req.finished:
+                self.running.remove(req)
+
+    def _append_keyed(self, req: Request, logits: torch.Tensor) -> None:
+        """Sample the token after a (re)prefill from the request's own stream."""
+        v = logits.shape[-1]
+        t = float(req.temperature)
+        noise = None
+        if t > 0:
+            pos = len(req.prompt) + len(req.output)
+            g = torch.Generator(device=logits.device).manual_seed(_stream_key(self.seed, req.id, pos))
+            noise = torch.empty((1, v), device=logits.device).exponential_(generator=g)
+        t_dev = torch.tensor([t], dtype=torch.float32).to(logits.device, non_blocking=True)
+        self._push(req, int(ops.sample_logits(logits, t_dev, noise).tolist()[0]))
+
+    def _push(self, req: Request, token: int) -> None:
+        """Append one token; finish the request at max_new_tokens, EOS or max_seq_len (engine.py:132-139)."""
+        req.output.append(token)
+        total = len(req.prompt) + len(req.output)
+        if len(req.output) >= req.max_new_tokens or token == req.eos_id or total >= self.limit:
+            req.finished = True
+            self._release(req)
 
     def _decode(self) -> None:
         bs = self.pool.block_size
@@ -140,9 +293,4 @@ class Engine:
         t_dev = torch.tensor(temps, dtype=torch.float32).to(logits.device, non_blocking=True)
         toks = ops.sample_logits(logits, t_dev, noise).tolist()
         for req, token in zip(reqs, toks):
-            req.output.append(token)
-            total = len(req.prompt) + len(req.output)
-            if len(req.output) >= req.max_new_tokens or token == req.eos_id or total >= self.cfg.max_seq_len:
-                req.finished = True
-                self.pool.allocator.release(req.blocks)
-                req.blocks = []
+            self._push(req, token)

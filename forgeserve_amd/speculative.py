@@ -115,6 +115,106 @@ def speculative_generate(target, draft, prompt: List[int], max_new_tokens: int, 
 
 
 # ------------------------------------------------------------------------------------------------
+# one round over a batch of sequences held in paged pools
+# ------------------------------------------------------------------------------------------------
+class _GeneratorDraws:
+    """The round's random numbers from one generator, in the batch loop's order: per draft step a
+    (b, V) Exp(1) block, then u (b, k), then the final Exp(1) block."""
+
+    def __init__(self, gen, b, k, v, dev):
+        self.gen, self.b, self.k, self.v, self.dev = gen, b, k, v, dev
+
+    def draft(self, i):
+        return torch.empty((self.b, self.v), dtype=torch.float32, device=self.dev).exponential_(generator=self.gen)
+
+    def accept(self):
+        u = torch.rand((self.b, max(self.k, 1)), dtype=torch.float32, device=self.dev, generator=self.gen)
+        e = torch.empty((self.b, self.v), dtype=torch.float32, device=self.dev).exponential_(generator=self.gen)
+        return u[:, : self.k].contiguous(), e
+
+
+def _tables(lists: List[List[int]], dev) -> torch.Tensor:
+    width = max(1, max(len(x) for x in lists))
+    t = torch.zeros((len(lists), width), dtype=I32)
+    for i, x in enumerate(lists):
+        if x:
+            t[i, : len(x)] = torch.tensor(x, dtype=I32)
+    return t.to(dev, non_blocking=True)
+
+
+@torch.no_grad()
+def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: List[List[int]],
+               blocks_t: List[List[int]], blocks_d: List[List[int]], k_eff: List[int], temps: List[float],
+               draws) -> torch.Tensor:
+    """One draft-then-verify round (speculative.py:53-85) for b sequences whose caches hold positions
+    0..n-2 (n = len(tokens[r])) and whose block lists cover positions up to n-1+k_eff[r].
+
+    Per round: k draft decode steps (step 0 re-feeds (tokens[-2], tokens[-1]) at (n-2, n-1), so a fully
+    accepted round needs no catch-up forward; step i feeds x_{i-1} at n-1+i), one target verify pass
+    over the k+1 window, one fused acceptance. `draws` supplies the randomness: draft(i) -> (b, V)
+    Exp(1) noise of draft step i, accept() -> (u (b, k), E (b, V)); rows of greedy sequences are
+    ignored. Returns (b, k+2) int32 on the host: n_accepted, then the committed tokens (-1 padded)."""
+    b = len(tokens)
+    k = max(k_eff)
+    dev, dtype = target.device, target.dtype
+    n = [len(t) for t in tokens]
+    tab_t = _tables(blocks_t, dev)
+    tab_d = _tables(blocks_d, dev)
+    v = target.cfg.vocab_size
+    temps_dev = torch.tensor(temps, dtype=torch.float32).to(dev, non_blocking=True)
+    sampling = any(t > 0 for t in temps)
+    # The LM heads emit the logits' softmax statistics (sampling.py:13) as they write them, so the
+    # acceptance does not read the 2k+1 logit rows back to normalise them.
+    d = target.cfg.d_model
+    fused = (dtype == torch.bfloat16 and k > 0 and ops.row_stats_parts(b, v, d) > 0
+             and ops.row_stats_parts(b * (k + 1), v, d) > 0)
+    if fused:
+        inv_t = torch.tensor([1.0 / t if t > 0 else 0.0 for t in temps], dtype=torch.float32)
+        inv_t_d = inv_t.to(dev, non_blocking=True)
+        inv_t_t = inv_t.repeat_interleave(k + 1).to(dev, non_blocking=True)
+        # draft step i writes its rows' records into parts_d[:, i]; one merge after the last step
+        parts_d = torch.empty((b, k, ops.row_stats_parts(b, v, d), 4), dtype=I32, device=dev)
+        parts_t = torch.empty((b * (k + 1), ops.row_stats_parts(b * (k + 1), v, d), 4), dtype=I32, device=dev)
+        row_stats = torch.empty((b, 2 * k + 1, 4), dtype=I32, device=dev)
+
+    # 1. draft
+    dft_logits = torch.empty((b, k, v), dtype=dtype, device=dev)
+    draft_tok = torch.empty((b, k), dtype=I32, device=dev)
+    last = torch.tensor([t[-1] for t in tokens], dtype=torch.int64)
+    prev = torch.tensor([t[-2] if len(t) > 1 else 0 for t in tokens], dtype=torch.int64)
+    cur = None
+    for i in range(k):
+        if i == 0:
+            idx = torch.stack([prev, last], 1).to(dev, non_blocking=True)
+            pos = torch.tensor([[ni - 2 if ni > 1 else -1, ni - 1] if k_eff[r] > 0 else [-1, -1]
+                                for r, ni in enumerate(n)])
+        else:
+            idx = cur.to(torch.int64)[:, None]
+            pos = torch.tensor([[ni - 1 + i if i < k_eff[r] else -1] for r, ni in enumerate(n)])
+        logits = draft(idx, pos, pool_d.views(tab_d, pos), last_only=True,
+                       head_stats=(inv_t_d, parts_d[:, i]) if fused else None)[:, 0]
+        dft_logits[:, i].copy_(logits)
+        ops.sample_logits(logits, temps_dev, draws.draft(i) if sampling else None, out32=draft_tok[:, i])
+        cur = draft_tok[:, i]
+    if fused:   # draft row (b, i) is record b*k + i: sequence b's draft rows k+1 .. 2k
+        ops.row_stats_merge(parts_d.view(b * k, -1, 4), row_stats, k, 2 * k + 1, k + 1)
+
+    # 2. target verify over [tokens[-1], x_0 .. x_{k-1}] at n-1 .. n-1+k
+    idx = torch.cat([last.to(dev)[:, None], draft_tok.to(torch.int64)], 1) if k else last[:, None].to(dev)
+    pos = torch.tensor([[ni - 1 + t if t <= k_eff[r] else -1 for t in range(k + 1)] for r, ni in enumerate(n)])
+    tgt_logits = target(idx, pos, pool_t.views(tab_t, pos), head_stats=(inv_t_t, parts_t) if fused else None)
+    if fused:
+        ops.row_stats_merge(parts_t, row_stats, k + 1, 2 * k + 1, 0)
+
+    # 3. acceptance
+    u, noise = draws.accept()
+    keff_dev = torch.tensor(k_eff, dtype=I32).to(dev, non_blocking=True)
+    out_tok, n_acc = ops.spec_accept(tgt_logits, dft_logits, draft_tok, keff_dev, temps_dev, u, noise,
+                                     row_stats=row_stats if fused else None)
+    return torch.cat([n_acc[:, None], out_tok], 1).cpu()
+
+
+# ------------------------------------------------------------------------------------------------
 # batched speculation over paged pools
 # ------------------------------------------------------------------------------------------------
 class _Seq:
@@ -197,14 +297,6 @@ class SpeculativeBatch:
             s.done = True
             self.release(s)
 
-    def _tables(self, lists: List[List[int]]) -> torch.Tensor:
-        width = max(1, max(len(x) for x in lists))
-        t = torch.zeros((len(lists), width), dtype=I32)
-        for i, x in enumerate(lists):
-            if x:
-                t[i, : len(x)] = torch.tensor(x, dtype=I32)
-        return t.to(self.dev, non_blocking=True)
-
     @torch.no_grad()
     def round(self) -> int:
         """One draft-then-verify round for every active sequence. Returns the tokens committed."""
@@ -214,73 +306,12 @@ class SpeculativeBatch:
         b = len(seqs)
         k_eff = [max(0, min(self.k, self._remaining(s) - 1)) for s in seqs]
         k = max(k_eff)
-        n = [len(s.tokens) for s in seqs]
-        for s, ni in zip(seqs, n):
-            self._grow(s, ni + k)
-        tab_t = self._tables([s.blocks_t for s in seqs])
-        tab_d = self._tables([s.blocks_d for s in seqs])
-        v = self.target.cfg.vocab_size
-        temps = torch.tensor([s.temperature for s in seqs], dtype=torch.float32).to(self.dev, non_blocking=True)
-        sampling = any(s.temperature > 0 for s in seqs)
-        # The LM heads emit the logits' softmax statistics (sampling.py:13) as they write them, so the
-        # acceptance does not read the 2k+1 logit rows back to normalise them.
-        d = self.target.cfg.d_model
-        fused = (self.dtype == torch.bfloat16 and k > 0 and ops.row_stats_parts(b, v, d) > 0
-                 and ops.row_stats_parts(b * (k + 1), v, d) > 0)
-        if fused:
-            inv_t = torch.tensor([1.0 / s.temperature if s.temperature > 0 else 0.0 for s in seqs],
-                                 dtype=torch.float32)
-            inv_t_d = inv_t.to(self.dev, non_blocking=True)
-            inv_t_t = inv_t.repeat_interleave(k + 1).to(self.dev, non_blocking=True)
-            # draft step i writes its rows' records into parts_d[:, i]; one merge after the last step
-            parts_d = torch.empty((b, k, ops.row_stats_parts(b, v, d), 4), dtype=I32, device=self.dev)
-            parts_t = torch.empty((b * (k + 1), ops.row_stats_parts(b * (k + 1), v, d), 4), dtype=I32,
-                                  device=self.dev)
-            row_stats = torch.empty((b, 2 * k + 1, 4), dtype=I32, device=self.dev)
-
-        # 1. draft: step 0 re-feeds (tokens[-2], tokens[-1]) at (n-2, n-1); step i feeds x_{i-1} at n-1+i
-        dft_logits = torch.empty((b, k, v), dtype=self.dtype, device=self.dev)
-        draft_tok = torch.empty((b, k), dtype=I32, device=self.dev)
-        last = torch.tensor([s.tokens[-1] for s in seqs], dtype=torch.int64)
-        prev = torch.tensor([s.tokens[-2] if len(s.tokens) > 1 else 0 for s in seqs], dtype=torch.int64)
-        cur = None
-        for i in range(k):
-            if i == 0:
-                idx = torch.stack([prev, last], 1).to(self.dev, non_blocking=True)
-                pos = torch.tensor([[ni - 2 if ni > 1 else -1, ni - 1] if k_eff[r] > 0 else [-1, -1]
-                                    for r, ni in enumerate(n)])
-            else:
-                idx = cur.to(torch.int64)[:, None]
-                pos = torch.tensor([[ni - 1 + i if i < k_eff[r] else -1] for r, ni in enumerate(n)])
-            views = self.pool_d.views(tab_d, pos)
-            logits = self.draft(idx, pos, views, last_only=True,
-                                head_stats=(inv_t_d, parts_d[:, i]) if fused else None)[:, 0]
-            dft_logits[:, i].copy_(logits)
-            noise = None
-            if sampling:
-                noise = torch.empty((b, v), dtype=torch.float32, device=self.dev).exponential_(generator=self.gen)
-            ops.sample_logits(logits, temps, noise, out32=draft_tok[:, i])
-            cur = draft_tok[:, i]
-
-        if fused:   # draft row (b, i) is record b*k + i: sequence b's draft rows k+1 .. 2k
-            ops.row_stats_merge(parts_d.view(b * k, -1, 4), row_stats, k, 2 * k + 1, k + 1)
-
-        # 2. target verify over [tokens[-1], x_0 .. x_{k-1}] at n-1 .. n-1+k
-        idx = torch.cat([last.to(self.dev)[:, None], draft_tok.to(torch.int64)], 1) if k else last[:, None]
-        pos = torch.tensor([[ni - 1 + t if t <= k_eff[r] else -1 for t in range(k + 1)] for r, ni in enumerate(n)])
-        tgt_logits = self.target(idx, pos, self.pool_t.views(tab_t, pos),
-                                 head_stats=(inv_t_t, parts_t) if fused else None)
-        if fused:
-            ops.row_stats_merge(parts_t, row_stats, k + 1, 2 * k + 1, 0)
-
-        # 3. acceptance (+ device-side rollback of the cached lengths)
-        u = torch.rand((b, max(k, 1)), dtype=torch.float32, device=self.dev, generator=self.gen)[:, :k].contiguous()
-        noise = torch.empty((b, v), dtype=torch.float32, device=self.dev).exponential_(generator=self.gen)
-        keff_dev = torch.tensor(k_eff, dtype=I32).to(self.dev, non_blocking=True)
-        out_tok, n_acc = ops.spec_accept(tgt_logits, dft_logits, draft_tok, keff_dev, temps, u, noise,
-                                         row_stats=row_stats if fused else None)
-        res = torch.cat([n_acc[:, None], out_tok], 1).cpu()
-
+        for s in seqs:
+            self._grow(s, len(s.tokens) + k)
+        res = spec_round(self.target, self.draft, self.pool_t, self.pool_d, [s.tokens for s in seqs],
+                         [s.blocks_t for s in seqs], [s.blocks_d for s in seqs], k_eff,
+                         [s.temperature for s in seqs], _GeneratorDraws(self.gen, b, k, self.target.cfg.vocab_size,
+                                                                        self.dev))
         committed = 0
         for r, s in enumerate(seqs):
             a = int(res[r, 0])

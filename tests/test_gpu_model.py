@@ -225,3 +225,83 @@ def test_bf16_batch_perfect_draft_accepts_everything(bf_target):
     got, stats = fa.speculative_generate_batch(bf_target, bf_target, prompts, 25, k=4)
     assert stats["accepted"] == stats["proposed"]
     assert got == [fa.generate(bf_target, torch.tensor([p]), 25)[0].tolist()[len(p):] for p in prompts]
+
+
+# ---- speculative engine (batched speculation inside Engine) ---------------------------------------------
+def test_spec_engine_greedy_matches_the_reference_engine(small):
+    """Greedy: the speculative engine emits the reference Engine's tokens exactly, through a pool small
+    enough to force recompute preemptions (engine_runs.json, run greedy_tight)."""
+    case("spec engine greedy")
+    gold = golden_json("engine_runs.json")
+    run = gold["runs"]["greedy_tight"]
+    draft = fa.early_exit_draft(small, 1)
+    e = fa.Engine(small, num_blocks=run["num_blocks"], block_size=4, max_batch=5, draft=draft, k=4)
+    ids = [e.add_request(p, n) for p, n in gold["requests"]]
+    out = e.run()
+    assert [out[i] for i in ids] == run["outputs"]
+    assert e.preemptions > 0
+    assert e.pool.allocator.num_free == run["num_blocks"] and e.pool_d.allocator.num_free == run["num_blocks"]
+    assert e.stats["rounds"] > 0 and e.stats["accepted"] <= e.stats["proposed"]
+
+
+def test_spec_engine_bf16_greedy_equals_generate(bf_target):
+    case("spec engine bf16")
+    draft = fa.early_exit_draft(bf_target, 1)
+    g = torch.Generator().manual_seed(11)
+    reqs = [(torch.randint(0, 1000, (int(n),), generator=g).tolist(), int(m))
+            for n, m in zip(torch.randint(2, 50, (7,), generator=g), torch.randint(3, 30, (7,), generator=g))]
+    e = fa.Engine(bf_target, num_blocks=200, block_size=16, max_batch=4, draft=draft, k=3)
+    ids = [e.add_request(p, m) for p, m in reqs]
+    out = e.run()
+    for rid, (p, m) in zip(ids, reqs):
+        assert out[rid] == fa.generate(bf_target, torch.tensor([p]), m)[0].tolist()[len(p):], rid
+
+
+def test_spec_engine_stops_at_eos_and_max_seq_len(small):
+    case("spec engine stops")
+    draft = fa.early_exit_draft(small, 1)
+    prompt = [3, 1, 4, 1, 5]
+    full = fa.generate(small, torch.tensor([prompt]), 10)[0].tolist()[len(prompt):]
+    eos = full[3]
+    e = fa.Engine(small, num_blocks=32, block_size=4, draft=draft, k=4)
+    rid = e.add_request(prompt, 10, eos_id=eos)
+    assert e.run()[rid] == full[: full.index(eos) + 1]
+    e = fa.Engine(small, num_blocks=64, block_size=4, draft=draft, k=4)
+    rid = e.add_request(list(range(1, 60)), 100)
+    assert 59 + len(e.run()[rid]) == small.cfg.max_seq_len
+
+
+def test_spec_engine_sampling_does_not_depend_on_the_batch(small):
+    """At T > 0 a request's tokens come from its own keyed stream: alone or batched with others it
+    produces the same tokens. (A recompute preemption re-prefills and samples the next token from the
+    prefill logits, as the reference's engine does, which moves the request's round boundaries: a
+    preempted request's later tokens are a different valid sample.)"""
+    case("spec engine keyed sampling")
+    draft = fa.early_exit_draft(small, 1)
+    reqs = [([1, 2, 3], 20), ([9, 8, 7, 6], 15), ([5, 5], 18), ([30, 31, 32, 33, 34], 12)]
+
+    def run(subset, num_blocks):
+        e = fa.Engine(small, num_blocks=num_blocks, block_size=4, max_batch=4, seed=5, draft=draft, k=3)
+        ids = [e.add_request(p, n, temperature=0.8) for p, n in subset]
+        return [e.run()[i] for i in ids], e
+
+    together, e1 = run(reqs, 64)
+    alone, _ = run(reqs[:1], 64)
+    tight, e2 = run(reqs, 14)
+    assert together[0] == alone[0]
+    assert e2.preemptions > 0
+    for (p, n), out, out2 in zip(reqs, together, tight):
+        assert len(out) == n and all(0 <= t < small.cfg.vocab_size for t in out)
+        assert len(out2) == n and all(0 <= t < small.cfg.vocab_size for t in out2)
+    again, _ = run(reqs, 64)
+    assert again == together
+
+
+def test_spec_engine_errors(small):
+    case("spec engine errors")
+    other = fa.ForgeModel(fa.ModelConfig(vocab_size=32, d_model=64, n_layers=1, n_heads=8, n_kv_heads=4,
+                                         max_seq_len=64))
+    with pytest.raises(ValueError):
+        fa.Engine(small, num_blocks=8, block_size=4, draft=other)
+    with pytest.raises(ValueError):
+        fa.Engine(small, num_blocks=8, block_size=4, draft=fa.early_exit_draft(small, 1), k=0)
