@@ -61,6 +61,50 @@ def build_models(torch, fa):
     return target, draft
 
 
+CFG_1B = dict(vocab_size=32000, d_model=2048, n_layers=16, n_heads=32, n_kv_heads=8, ffn_dim=8192,
+              max_seq_len=2048)
+
+
+def engine_1b(args):
+    """The 1B-shape continuous-batching workload: Engine(max_batch 16, k = 4, T = 0.7) with a 2-layer
+    early-exit draft over 48 requests (prompts U[128, 1024], max_new_tokens U[64, 256]), the pool sized
+    below the peak demand so that recompute preemptions happen. Prints one JSON line."""
+    import torch
+
+    import forgeserve_amd as fa
+
+    cfg = fa.ModelConfig(**CFG_1B)
+    torch.manual_seed(args.seed)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device("cuda"):
+            target = fa.ForgeModel(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    draft = fa.early_exit_draft(target, 2)
+    g = torch.Generator().manual_seed(args.seed + 1)
+    reqs = [(torch.randint(0, cfg.vocab_size, (int(torch.randint(128, 1025, (1,), generator=g)),), generator=g).tolist(),
+             int(torch.randint(64, 257, (1,), generator=g))) for _ in range(48)]
+    eng = fa.Engine(target, num_blocks=600, block_size=16, max_batch=16, seed=args.seed, draft=draft, k=4)
+    for p, n in reqs:
+        eng.add_request(p, n, temperature=0.7)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = eng.run()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    toks = sum(len(v) for v in out.values())
+    assert all(len(out[i]) == n for i, (_, n) in enumerate(reqs))
+    print(json.dumps({"workload": "1B-shape continuous batching: 16L d2048 32/8 heads hd64 ffn8192 V32000 bf16, "
+                                  "2-layer early-exit draft, Engine max_batch 16, k=4, T=0.7, 48 requests, "
+                                  "prompts U[128,1024], max_new U[64,256], 600 blocks of 16",
+                      "generated_tokens": toks, "seconds": round(el, 3), "tok_per_s": round(toks / el, 1),
+                      "engine_steps": eng.steps, "rounds": eng.stats["rounds"], "preemptions": eng.preemptions,
+                      "peak_running": eng.peak_running, "peak_blocks": eng.peak_blocks,
+                      "acceptance": round(eng.stats["accepted"] / max(eng.stats["proposed"], 1), 4)}), flush=True)
+
+
 def attn_bytes(ctxs, t, h, hkv, d, bs):
     kv = sum(ctxs) * hkv * d * 2 * 2
     qo = len(ctxs) * t * h * d * 2 * 2
@@ -326,12 +370,16 @@ def main():
     ap.add_argument("--temperature", type=float, default=0.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--kernel", choices=("round", "attention", "accept", "accept_stats", "copy"), default="round")
+    ap.add_argument("--kernel", choices=("round", "attention", "accept", "accept_stats", "copy", "engine_1b"),
+                    default="round")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         sys.exit(2)
+    if args.kernel == "engine_1b":
+        engine_1b(args)
+        return
     if args.kernel != "round":
         kernel_mode(args)
         return
