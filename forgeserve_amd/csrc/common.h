@@ -56,6 +56,7 @@ template <> struct Elem<FS_F16> {
   static FS_DEVICE void store(T* p, int64_t i, float v) { p[i] = f32_to_f16(v); }
   static FS_DEVICE float round(float v) { return f16_to_f32(f32_to_f16(v)); }
   static FS_DEVICE float to_f32(T v) { return f16_to_f32(v); }
+  static FS_DEVICE T store_bits(float v) { return f32_to_f16(v); }
 };
 
 // ------------------------------------------------------------------------------------------------

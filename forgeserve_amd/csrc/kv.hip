@@ -33,6 +33,95 @@ FS_DEVICE bool slot_of(int pos, const int32_t* table, int64_t table_stride, int 
   return true;
 }
 
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+
+template <int DT>
+FS_DEVICE void unpack8(const u32x4_t& w, float (&v)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = Elem<DT>::to_f32((uint16_t)(w[j] & 0xffffu));
+    v[2 * j + 1] = Elem<DT>::to_f32((uint16_t)(w[j] >> 16));
+  }
+}
+
+template <int DT>
+FS_DEVICE u32x4_t pack8(const float (&v)[8]) {
+  u32x4_t w;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    w[j] = (uint32_t)Elem<DT>::store_bits(v[2 * j]) | ((uint32_t)Elem<DT>::store_bits(v[2 * j + 1]) << 16);
+  return w;
+}
+
+// The same as qkv_rope_write_kernel for 16-bit dtypes whose rows split into 16-byte groups (D/2 % 8 == 0,
+// aligned rows, slot-major keys): a thread rotates 8 pairs at once (two 16-byte loads of the halves,
+// 16-byte loads of cos/sin, 16-byte stores of q and k); values keep the dim-major element stores.
+template <int DT>
+__global__ void __launch_bounds__(256) qkv_rope_write_vec_kernel(
+    const uint16_t* __restrict__ qkv, int64_t qkv_stride, int32_t T, int32_t H, const int32_t* __restrict__ positions,
+    const int32_t* __restrict__ slots, const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
+    int32_t rope_len, const int32_t* __restrict__ table, int64_t table_stride, int32_t max_blocks, fs_kv_layout kv,
+    uint16_t* __restrict__ q_out, int64_t q_stride) {
+  const int64_t m = blockIdx.x;
+  const int b = (int)(m / T);
+  const int D = kv.head_dim, half = D / 2, Hkv = kv.n_kv_heads;
+  const int pos = positions[m];
+  const bool rot_ok = pos >= 0 && pos < rope_len;
+  int64_t blk = 0;
+  int slot = 0;
+  const int wpos = slots ? slots[m] : pos;
+  const bool write_ok = rot_ok && slot_of(wpos, table, table_stride, b, max_blocks, kv, blk, slot);
+  const uint16_t* row = qkv + m * qkv_stride;
+  uint16_t* kp = reinterpret_cast<uint16_t*>(kv.k);
+  uint16_t* vp = reinterpret_cast<uint16_t*>(kv.v);
+  const int ng = half / 8;
+  const int n_groups = (H + Hkv) * ng;
+  const int64_t cs = rot_ok ? (int64_t)pos * half : 0;
+  for (int i = threadIdx.x; i < n_groups; i += blockDim.x) {
+    const int head = i / ng, p0 = 8 * (i - head * ng);
+    float x1[8], x2[8], c[8], sn[8], o1[8], o2[8];
+    unpack8<DT>(*reinterpret_cast<const u32x4_t*>(row + (int64_t)head * D + p0), x1);
+    unpack8<DT>(*reinterpret_cast<const u32x4_t*>(row + (int64_t)head * D + p0 + half), x2);
+    const float4_t c0 = *reinterpret_cast<const float4_t*>(rope_cos + cs + p0);
+    const float4_t c1 = *reinterpret_cast<const float4_t*>(rope_cos + cs + p0 + 4);
+    const float4_t s0 = *reinterpret_cast<const float4_t*>(rope_sin + cs + p0);
+    const float4_t s1 = *reinterpret_cast<const float4_t*>(rope_sin + cs + p0 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c[j] = c0[j]; c[j + 4] = c1[j];
+      sn[j] = s0[j]; sn[j + 4] = s1[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      o1[j] = o2[j] = 0.f;
+      if (rot_ok) rope_pair<DT>(x1[j], x2[j], c[j], sn[j], o1[j], o2[j]);
+    }
+    if (head < H) {
+      uint16_t* qo = q_out + m * q_stride + (int64_t)head * D + p0;
+      *reinterpret_cast<u32x4_t*>(qo) = pack8<DT>(o1);
+      *reinterpret_cast<u32x4_t*>(qo + half) = pack8<DT>(o2);
+    } else if (write_ok) {
+      uint16_t* ko = kp + blk * kv.k_block + (int64_t)(head - H) * kv.k_head + slot * kv.k_slot + p0;
+      *reinterpret_cast<u32x4_t*>(ko) = pack8<DT>(o1);
+      *reinterpret_cast<u32x4_t*>(ko + half) = pack8<DT>(o2);
+    }
+  }
+  if (write_ok) {
+    const int nv = Hkv * D / 8;
+    const uint16_t* vrow = row + (int64_t)(H + Hkv) * D;
+    for (int i = threadIdx.x; i < nv; i += blockDim.x) {
+      const int e0 = 8 * i, h = e0 / D, d0 = e0 - h * D;
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(vrow + e0);
+      uint16_t* vo = vp + blk * kv.v_block + h * kv.v_head + slot * kv.v_slot + d0 * kv.v_dim;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        vo[(2 * j) * kv.v_dim] = (uint16_t)(w[j] & 0xffffu);
+        vo[(2 * j + 1) * kv.v_dim] = (uint16_t)(w[j] >> 16);
+      }
+    }
+  }
+}
+
 // One workgroup per token. Threads cover (q heads + kv heads) * D/2 rotation pairs, then the values.
 template <int DT>
 __global__ void __launch_bounds__(256) qkv_rope_write_kernel(
@@ -170,6 +259,20 @@ extern "C" int fs_qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_
   if (n_tokens == 0) return 0;
   hipStream_t s = fs::as_stream(stream);
   dim3 grid((unsigned)n_tokens);
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (kv->dtype != FS_F32 && (kv->head_dim / 2) % 8 == 0 && kv->head_dim % 2 == 0 && qkv_stride % 8 == 0 &&
+      q_stride % 8 == 0 && kv->k_dim == 1 && kv->k_slot % 8 == 0 && kv->k_head % 8 == 0 && kv->k_block % 8 == 0 &&
+      al16(qkv) && al16(q_out) && al16(kv->k) && al16(rope_cos) && al16(rope_sin)) {
+    if (kv->dtype == FS_BF16)
+      qkv_rope_write_vec_kernel<FS_BF16><<<grid, 256, 0, s>>>((const uint16_t*)qkv, qkv_stride, T, n_heads, positions,
+                                                              slots, rope_cos, rope_sin, rope_len, block_tables,
+                                                              table_stride, max_blocks, *kv, (uint16_t*)q_out, q_stride);
+    else
+      qkv_rope_write_vec_kernel<FS_F16><<<grid, 256, 0, s>>>((const uint16_t*)qkv, qkv_stride, T, n_heads, positions,
+                                                             slots, rope_cos, rope_sin, rope_len, block_tables,
+                                                             table_stride, max_blocks, *kv, (uint16_t*)q_out, q_stride);
+    return fs::launch_status("qkv_rope_write");
+  }
 #define FS_LAUNCH(DT)                                                                                        \
   qkv_rope_write_kernel<DT><<<grid, 256, 0, s>>>(                                                          \
       (const typename Elem<DT>::T*)qkv, qkv_stride, T, n_heads, positions, slots, rope_cos, rope_sin, rope_len, \

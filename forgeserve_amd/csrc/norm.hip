@@ -43,6 +43,104 @@ __global__ void __launch_bounds__(NORM_THREADS) add_rmsnorm_kernel(
   }
 }
 
+// 16-bit rows, 8 elements per 16-byte access, the whole row in registers (N <= NORM_VEC_MAX): one
+// pass over memory. The arithmetic and its order are add_rmsnorm_kernel's, except the sum of squares:
+// each thread adds its 8-element groups in order, then the lanes and waves are added as there.
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+constexpr int NORM_VEC_GROUPS = 4;                                   // 8-element groups per thread
+constexpr int64_t NORM_VEC_MAX = NORM_THREADS * 8 * NORM_VEC_GROUPS;   // 8192 elements
+
+template <int DT>
+FS_DEVICE void unpack8(const u32x4_t& w, float (&v)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = Elem<DT>::to_f32((uint16_t)(w[j] & 0xffffu));
+    v[2 * j + 1] = Elem<DT>::to_f32((uint16_t)(w[j] >> 16));
+  }
+}
+
+template <int DT>
+FS_DEVICE u32x4_t pack8(const float (&v)[8]) {
+  u32x4_t w;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    w[j] = (uint32_t)Elem<DT>::store_bits(v[2 * j]) | ((uint32_t)Elem<DT>::store_bits(v[2 * j + 1]) << 16);
+  return w;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(NORM_THREADS) add_rmsnorm_vec_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ delta, int64_t ldd,
+    uint16_t* __restrict__ x_out, int64_t ldxo, const uint16_t* __restrict__ w, uint16_t* __restrict__ y, int64_t ldy,
+    int64_t N, float eps) {
+  __shared__ float red[NORM_THREADS / 64];
+  const int64_t m = blockIdx.x;
+  const int ng = (int)(N / 8);   // 8-element groups in the row; thread t takes t, t + NORM_THREADS, ...
+  float v[NORM_VEC_GROUPS][8];
+  u32x4_t xr[NORM_VEC_GROUPS], dr[NORM_VEC_GROUPS], wr[NORM_VEC_GROUPS];
+#pragma unroll
+  for (int u = 0; u < NORM_VEC_GROUPS; ++u) {   // every load in flight before any arithmetic
+    const int gi = threadIdx.x + NORM_THREADS * u;
+    if (gi < ng) {
+      xr[u] = *reinterpret_cast<const u32x4_t*>(x + m * ldx + 8 * gi);
+      if (delta) dr[u] = *reinterpret_cast<const u32x4_t*>(delta + m * ldd + 8 * gi);
+      wr[u] = *reinterpret_cast<const u32x4_t*>(w + 8 * gi);
+    }
+  }
+  float sq = 0.f;
+#pragma unroll
+  for (int u = 0; u < NORM_VEC_GROUPS; ++u) {
+    const int gi = threadIdx.x + NORM_THREADS * u;
+    if (gi >= ng) continue;
+    unpack8<DT>(xr[u], v[u]);
+    if (delta) {
+      float d[8];
+      unpack8<DT>(dr[u], d);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[u][j] = Elem<DT>::round(v[u][j] + d[j]);
+      if (x_out) *reinterpret_cast<u32x4_t*>(x_out + m * ldxo + 8 * gi) = pack8<DT>(v[u]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sq += v[u][j] * v[u][j];
+  }
+  sq = wave_sum(sq);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[i];
+  const float r = 1.0f / sqrtf(tot / (float)N + eps);
+#pragma unroll
+  for (int u = 0; u < NORM_VEC_GROUPS; ++u) {
+    const int gi = threadIdx.x + NORM_THREADS * u;
+    if (gi >= ng) continue;
+    float wv[8], o[8];
+    unpack8<DT>(wr[u], wv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = Elem<DT>::round(v[u][j] * r) * wv[j];
+    *reinterpret_cast<u32x4_t*>(y + m * ldy + 8 * gi) = pack8<DT>(o);
+  }
+}
+
+// silu(gate) * up on 16-bit rows, 8 columns per thread and 16-byte accesses (F % 8 == 0); the same
+// per-element arithmetic as silu_mul_kernel.
+template <int DT>
+__global__ void __launch_bounds__(256) silu_mul_vec_kernel(const uint16_t* __restrict__ gu, int64_t ldgu,
+                                                           uint16_t* __restrict__ h, int64_t ldh, int64_t M,
+                                                           int64_t F) {
+  typedef Elem<DT> E;
+  const int64_t groups = F / 8, total = M * groups;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = i / groups, c = 8 * (i - m * groups);
+    float g[8], u[8], o[8];
+    unpack8<DT>(*reinterpret_cast<const u32x4_t*>(gu + m * ldgu + c), g);
+    unpack8<DT>(*reinterpret_cast<const u32x4_t*>(gu + m * ldgu + F + c), u);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = E::round(g[j] / (1.0f + expf(-g[j]))) * u[j];
+    *reinterpret_cast<u32x4_t*>(h + m * ldh + c) = pack8<DT>(o);
+  }
+}
+
 template <int DT>
 __global__ void __launch_bounds__(256) silu_mul_kernel(const typename Elem<DT>::T* __restrict__ gu, int64_t ldgu,
                                                        typename Elem<DT>::T* __restrict__ h, int64_t ldh, int64_t M,
@@ -84,6 +182,19 @@ extern "C" int fs_add_rmsnorm(const void* x, int64_t ldx, const void* delta, int
   FS_CHECK_ARG(M >= 0 && N > 0, "add_rmsnorm: M %lld N %lld", (long long)M, (long long)N);
   if (M == 0) return 0;
   hipStream_t s = fs::as_stream(stream);
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (dtype != FS_F32 && N % 8 == 0 && N <= NORM_VEC_MAX && ldx % 8 == 0 && (!delta || ldd % 8 == 0) &&
+      (!x_out || ldxo % 8 == 0) && ldy % 8 == 0 && al16(x) && (!delta || al16(delta)) && (!x_out || al16(x_out)) &&
+      al16(weight) && al16(y)) {
+#define FS_LAUNCH_VEC(DT)                                                                                      \
+  add_rmsnorm_vec_kernel<DT><<<dim3((unsigned)M), NORM_THREADS, 0, s>>>(                                    \
+      (const uint16_t*)x, ldx, (const uint16_t*)delta, ldd, (uint16_t*)x_out, ldxo, (const uint16_t*)weight,      \
+      (uint16_t*)y, ldy, N, eps)
+    if (dtype == FS_BF16) FS_LAUNCH_VEC(FS_BF16);
+    else FS_LAUNCH_VEC(FS_F16);
+#undef FS_LAUNCH_VEC
+    return fs::launch_status("add_rmsnorm");
+  }
 #define FS_LAUNCH(DT)                                                                                          \
   add_rmsnorm_kernel<DT><<<dim3((unsigned)M), NORM_THREADS, 0, s>>>(                                        \
       (const typename Elem<DT>::T*)x, ldx, (const typename Elem<DT>::T*)delta, ldd, (typename Elem<DT>::T*)x_out, \
@@ -104,6 +215,18 @@ extern "C" int fs_silu_mul(const void* gu, int64_t ldgu, void* h, int64_t ldh, i
   FS_CHECK_ARG(M >= 0 && F > 0 && ldgu >= 2 * F && ldh >= F, "silu_mul: shapes");
   if (M == 0) return 0;
   hipStream_t s = fs::as_stream(stream);
+  if (dtype != FS_F32 && F % 8 == 0 && ldgu % 8 == 0 && ldh % 8 == 0 && (reinterpret_cast<uintptr_t>(gu) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(h) & 15) == 0) {
+    int64_t vblocks = (M * (F / 8) + 255) / 256;
+    if (vblocks > 16384) vblocks = 16384;
+    if (dtype == FS_BF16)
+      silu_mul_vec_kernel<FS_BF16><<<dim3((unsigned)vblocks), 256, 0, s>>>((const uint16_t*)gu, ldgu, (uint16_t*)h, ldh,
+                                                                           M, F);
+    else
+      silu_mul_vec_kernel<FS_F16><<<dim3((unsigned)vblocks), 256, 0, s>>>((const uint16_t*)gu, ldgu, (uint16_t*)h, ldh,
+                                                                          M, F);
+    return fs::launch_status("silu_mul");
+  }
   int64_t blocks = (M * F + 255) / 256;
   if (blocks > 16384) blocks = 16384;
 #define FS_LAUNCH(DT)                                                                                         \

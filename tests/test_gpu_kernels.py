@@ -100,6 +100,22 @@ def test_silu_mul(dtype):
         assert ((h.float() - ref.float()).abs() <= ref.float().abs() * 2 ** -7 * 1.01 + 1e-30).all()
 
 
+def test_rmsnorm_and_silu_general_paths_bf16():
+    """The row kernels' general paths (rows that are not whole 16-byte groups) against the reference,
+    and silu_mul's two paths bit for bit (the same per-element arithmetic)."""
+    case("rmsnorm/silu general paths")
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(9, 4100, generator=g).bfloat16()
+    w = (1 + 0.1 * torch.randn(4100, generator=g)).bfloat16()
+    y = ops.add_rmsnorm(x.to(DEV), w.to(DEV), 1e-5).cpu()
+    ref = orc.rms_norm(x, w, 1e-5)
+    assert ((y.float() - ref.float()).abs() <= ref.float().abs() * 2 ** -7 * 1.01).all()
+    wide = (torch.randn(17, 2 * 688 + 1, generator=g) * 3).bfloat16().to(DEV)
+    strided = wide[:, : 2 * 688]                       # leading dimension 1377: the element-wise path
+    packed = strided.contiguous()                      # leading dimension 1376: the 16-byte path
+    assert torch.equal(ops.silu_mul(strided), ops.silu_mul(packed))
+
+
 def test_embedding():
     case("embedding")
     w = torch.randn(100, 48).bfloat16()
@@ -109,7 +125,7 @@ def test_embedding():
 
 # ---- KV write + rotary ----------------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype,d,bs", [(torch.float32, 8, 4), (torch.float32, 32, 16), (torch.bfloat16, 128, 16),
-                                        (torch.bfloat16, 64, 16)])
+                                        (torch.bfloat16, 64, 16), (torch.bfloat16, 24, 16)])   # 24: element path
 def test_qkv_rope_write(dtype, d, bs):
     case("qkv_rope_write", dtype, d, bs)
     from forgeserve_amd import PagedKVPool, ModelConfig
