@@ -95,6 +95,17 @@ def check(rc: int, what: str) -> None:
         raise FSError(f"{what}: hip error {rc}: {msg}")
 
 
+def to_device(t: torch.Tensor, device, dtype=None) -> torch.Tensor:
+    """A host tensor on `device` without stalling the host: a copy from pageable memory waits until the
+    device has drained its queue, so host tensors are staged through pinned memory and copied
+    asynchronously (the pinned block is held until the copy has run)."""
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    if t.device.type != "cpu":
+        return t.to(device)
+    return t.pin_memory().to(device, non_blocking=True)
+
+
 def require_device(*tensors: torch.Tensor) -> None:
     for t in tensors:
         if t is not None and t.device.type != "cuda":

@@ -24,6 +24,7 @@ from typing import Deque, Dict, List, Optional
 import torch
 
 from . import ops
+from ._lib import to_device
 from .model import ForgeModel
 from .paged import PagedKVPool
 from .sampling import exp_noise
@@ -234,7 +235,7 @@ class Engine:
             pos = len(req.prompt) + len(req.output)
             g = torch.Generator(device=logits.device).manual_seed(_stream_key(self.seed, req.id, pos))
             noise = torch.empty((1, v), device=logits.device).exponential_(generator=g)
-        t_dev = torch.tensor([t], dtype=torch.float32).to(logits.device, non_blocking=True)
+        t_dev = to_device(torch.tensor([t], dtype=torch.float32), logits.device)
         self._push(req, int(ops.sample_logits(logits, t_dev, noise).tolist()[0]))
 
     def _push(self, req: Request, token: int) -> None:
@@ -289,8 +290,8 @@ class Engine:
         noise = None
         if any(t > 0 for t in temps):
             rows = [exp_noise((v,), self.generator, "cpu") if t > 0 else torch.ones(v) for t in temps]
-            noise = torch.stack(rows).to(logits.device, non_blocking=True)
-        t_dev = torch.tensor(temps, dtype=torch.float32).to(logits.device, non_blocking=True)
+            noise = to_device(torch.stack(rows), logits.device)
+        t_dev = to_device(torch.tensor(temps, dtype=torch.float32), logits.device)
         toks = ops.sample_logits(logits, t_dev, noise).tolist()
         for req, token in zip(reqs, toks):
             self._push(req, token)

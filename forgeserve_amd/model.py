@@ -18,6 +18,7 @@ import torch
 import torch.nn as nn
 
 from . import ops
+from ._lib import to_device
 from .config import ModelConfig
 from .parallel import SINGLE, TPContext
 
@@ -173,7 +174,7 @@ class ForgeModel(nn.Module):
         return self._rope_cache[1]
 
     def embed(self, idx):
-        return ops.embedding(idx.to(self.device), self.tok_emb.weight).reshape(*idx.shape, self.cfg.d_model)
+        return ops.embedding(to_device(idx, self.device), self.tok_emb.weight).reshape(*idx.shape, self.cfg.d_model)
 
     def head(self, x, stats=None):
         """Final norm + tied head (model.py:137-138). stats = (inv_temperature (rows,), parts): also emit
@@ -207,9 +208,9 @@ class ForgeModel(nn.Module):
         pmax = int(positions.max())
         if pmax >= self.cfg.max_seq_len:
             raise ValueError(f"position {pmax} exceeds max_seq_len {self.cfg.max_seq_len}")
-        pos32 = positions.to(device=dev, dtype=torch.int32).reshape(b, t).contiguous()
+        pos32 = to_device(positions.reshape(b, t).contiguous(), dev, torch.int32)
         rope = self._rope()
-        x = ops.embedding(idx.to(dev), self.tok_emb.weight)
+        x = ops.embedding(to_device(idx, dev), self.tok_emb.weight)
         for layer, view in zip(self.layers, kv):
             x = layer.step(x, b, t, pos32, view, rope)
         if last_only:

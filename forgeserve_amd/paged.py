@@ -19,6 +19,7 @@ import torch
 from . import ops
 from .config import ModelConfig
 from .parallel import SINGLE, TPContext
+from ._lib import to_device
 
 
 class OutOfBlocks(RuntimeError):
@@ -92,8 +93,8 @@ class _Step:
         if tables.device.type == "cpu" and tables.numel() and (int(tables.min()) < 0 or
                                                               int(tables.max()) >= pool.num_blocks):
             raise IndexError(f"block table entries must be in [0, {pool.num_blocks})")
-        self.tables = tables.to(device=pool.device, dtype=torch.int32, non_blocking=True).contiguous()
-        self.positions = positions.to(device=pool.device, dtype=torch.int32, non_blocking=True).contiguous()
+        self.tables = to_device(tables.contiguous(), pool.device, torch.int32)
+        self.positions = to_device(positions.contiguous(), pool.device, torch.int32)
 
 
 class PagedLayerView:

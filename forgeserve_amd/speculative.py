@@ -21,6 +21,7 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import torch
 
 from . import ops
+from ._lib import to_device
 from .kv import new_contiguous_cache
 from .paged import OutOfBlocks, PagedKVPool
 from .sampling import exp_noise, probs_from_logits
@@ -139,7 +140,7 @@ def _tables(lists: List[List[int]], dev) -> torch.Tensor:
     for i, x in enumerate(lists):
         if x:
             t[i, : len(x)] = torch.tensor(x, dtype=I32)
-    return t.to(dev, non_blocking=True)
+    return to_device(t, dev)
 
 
 @torch.no_grad()
@@ -161,7 +162,7 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     tab_t = _tables(blocks_t, dev)
     tab_d = _tables(blocks_d, dev)
     v = target.cfg.vocab_size
-    temps_dev = torch.tensor(temps, dtype=torch.float32).to(dev, non_blocking=True)
+    temps_dev = to_device(torch.tensor(temps, dtype=torch.float32), dev)
     sampling = any(t > 0 for t in temps)
     # The LM heads emit the logits' softmax statistics (sampling.py:13) as they write them, so the
     # acceptance does not read the 2k+1 logit rows back to normalise them.
@@ -170,8 +171,8 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
              and ops.row_stats_parts(b * (k + 1), v, d) > 0)
     if fused:
         inv_t = torch.tensor([1.0 / t if t > 0 else 0.0 for t in temps], dtype=torch.float32)
-        inv_t_d = inv_t.to(dev, non_blocking=True)
-        inv_t_t = inv_t.repeat_interleave(k + 1).to(dev, non_blocking=True)
+        inv_t_d = to_device(inv_t, dev)
+        inv_t_t = to_device(inv_t.repeat_interleave(k + 1), dev)
         # draft step i writes its rows' records into parts_d[:, i]; one merge after the last step
         parts_d = torch.empty((b, k, ops.row_stats_parts(b, v, d), 4), dtype=I32, device=dev)
         parts_t = torch.empty((b * (k + 1), ops.row_stats_parts(b * (k + 1), v, d), 4), dtype=I32, device=dev)
@@ -185,7 +186,7 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     cur = None
     for i in range(k):
         if i == 0:
-            idx = torch.stack([prev, last], 1).to(dev, non_blocking=True)
+            idx = to_device(torch.stack([prev, last], 1), dev)
             pos = torch.tensor([[ni - 2 if ni > 1 else -1, ni - 1] if k_eff[r] > 0 else [-1, -1]
                                 for r, ni in enumerate(n)])
         else:
@@ -200,7 +201,8 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
         ops.row_stats_merge(parts_d.view(b * k, -1, 4), row_stats, k, 2 * k + 1, k + 1)
 
     # 2. target verify over [tokens[-1], x_0 .. x_{k-1}] at n-1 .. n-1+k
-    idx = torch.cat([last.to(dev)[:, None], draft_tok.to(torch.int64)], 1) if k else last[:, None].to(dev)
+    last_dev = to_device(last, dev)
+    idx = torch.cat([last_dev[:, None], draft_tok.to(torch.int64)], 1) if k else last_dev[:, None]
     pos = torch.tensor([[ni - 1 + t if t <= k_eff[r] else -1 for t in range(k + 1)] for r, ni in enumerate(n)])
     tgt_logits = target(idx, pos, pool_t.views(tab_t, pos), head_stats=(inv_t_t, parts_t) if fused else None)
     if fused:
@@ -208,7 +210,7 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
 
     # 3. acceptance
     u, noise = draws.accept()
-    keff_dev = torch.tensor(k_eff, dtype=I32).to(dev, non_blocking=True)
+    keff_dev = to_device(torch.tensor(k_eff, dtype=I32), dev)
     out_tok, n_acc = ops.spec_accept(tgt_logits, dft_logits, draft_tok, keff_dev, temps_dev, u, noise,
                                      row_stats=row_stats if fused else None)
     return torch.cat([n_acc[:, None], out_tok], 1).cpu()
