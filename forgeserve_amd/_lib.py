@@ -115,7 +115,11 @@ def require_device(*tensors: torch.Tensor) -> None:
 
 
 def stream_ptr(device=None) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current HIP stream of `device` (default: the current device) as a raw pointer."""
+    idx = torch.cuda.current_device() if device is None else torch.device(device).index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 def ptr(t) -> int:

@@ -30,8 +30,19 @@ def precompute_rope(head_dim: int, max_len: int, theta: float):
     return angles.cos(), angles.sin()
 
 
-def _fused_weight(params: List[nn.Parameter]) -> torch.Tensor:
-    """One (sum of rows, cols) weight whose row slices are `params`; re-points them if needed."""
+def _fused_weight(owner: nn.Module, params: List[nn.Parameter]) -> torch.Tensor:
+    """One (sum of rows, cols) weight whose row slices are `params`; re-points them if needed. The
+    result is kept on `owner` and reused while the parameters still hold the same storage."""
+    key = tuple((p.data.data_ptr(), tuple(p.shape), p.dtype) for p in params)
+    hit = owner.__dict__.get("_fused")
+    if hit is not None and hit[1] == key:
+        return hit[0]
+    fused = _build_fused(params)
+    owner.__dict__["_fused"] = (fused, tuple((p.data.data_ptr(), tuple(p.shape), p.dtype) for p in params))
+    return fused
+
+
+def _build_fused(params: List[nn.Parameter]) -> torch.Tensor:
     first = params[0].data
     rows = sum(p.shape[0] for p in params)
     cols = first.shape[1]
@@ -82,7 +93,7 @@ class Attention(nn.Module):
         self.wo = nn.Linear(self.nh * self.hd, cfg.d_model, bias=False)
 
     def qkv_weight(self) -> torch.Tensor:
-        return _fused_weight([self.wq.weight, self.wk.weight, self.wv.weight])
+        return _fused_weight(self, [self.wq.weight, self.wk.weight, self.wv.weight])
 
     def attend(self, h: torch.Tensor, b: int, t: int, pos32: torch.Tensor, view, rope) -> torch.Tensor:
         """h (B*T, d) normed input -> attention output (B*T, n_heads*head_dim), before wo."""
@@ -104,7 +115,7 @@ class SwiGLU(nn.Module):
         self.w_down = nn.Linear(hidden, cfg.d_model, bias=False)
 
     def gate_up_weight(self) -> torch.Tensor:
-        return _fused_weight([self.w_gate.weight, self.w_up.weight])
+        return _fused_weight(self, [self.w_gate.weight, self.w_up.weight])
 
     def forward(self, x, residual: Optional[torch.Tensor] = None):
         shape = x.shape
