@@ -178,10 +178,16 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
   constexpr int ROWB = KB * 2;                 // bytes per stage row (128)
   constexpr int NW = WGM * WGN;                // waves: WGM along M, WGN along N
   constexpr int XB = BM * ROWB, WB = BN * ROWB, STAGE = XB + WB;
-  constexpr int XI = XB / (NW * 1024), WI = WB / (NW * 1024);  // dma instructions per wave per stage
   constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
-  static_assert(XB % (NW * 1024) == 0 && WB % (NW * 1024) == 0, "tile rows must fill whole 1 KB wave copies");
+  // A stage is T copies of 1 KB (one global_load_lds_dwordx4 of 64 lanes): copies q < XQ fill the X
+  // block, the rest the W block. Wave w issues copies w, w + NW, ...: GH of them if w < T % NW,
+  // else GL (tiles of 224 rows do not split evenly over 8 waves).
+  constexpr int XQ = XB / 1024, T = STAGE / 1024, GI = (T + NW - 1) / NW;
+  constexpr int GL = T / NW, GH = (T % NW) ? GL + 1 : GL;
+  static_assert(XB % 1024 == 0 && WB % 1024 == 0, "tile rows must fill whole 1 KB copies");
   static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tiles are whole 16x16 MFMA tiles");
+  static_assert(NS * STAGE <= 160 * 1024, "LDS ring larger than a CU's LDS");
+  static_assert(NS >= 2 && NS <= 4, "wait_stages covers up to two stages in flight behind the awaited one");
   __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE];
 
   // XCD-aware order: workgroup ids go round-robin over the 8 XCDs; give each XCD a contiguous range
@@ -197,25 +203,21 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
   const int wm = wave / WGN, wn = wave % WGN;
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
-  // this lane's source rows/chunks for its share of a stage (fixed across stages but for k0)
-  const uint16_t* xsrc[XI];
-  const uint16_t* wsrc[WI];
+  // this lane's source row/chunk for each of its copies (fixed across stages but for k0). Chunk P of
+  // a block is row P >> 3, physical chunk P & 7, which holds logical chunk (P & 7) ^ (row & 7).
+  const uint16_t* src[GI];
 #pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int P = (i * NW + wave) * 64 + lane;  // 16-byte chunk index inside the X stage
+  for (int i = 0; i < GI; ++i) {
+    const int q0 = i * NW + wave, q = q0 < T ? q0 : 0;
+    const bool in_x = q < XQ;
+    const int P = (in_x ? q : q - XQ) * 64 + lane;
     const int r = P >> 3, c = (P & 7) ^ (r & 7);
-    int64_t gr = m0 + r;
-    gr = gr < M ? gr : M - 1;
-    xsrc[i] = X + gr * ldx + 8 * c;
+    int64_t gr = (in_x ? m0 : n0) + r;
+    const int64_t lim = in_x ? M : N;
+    gr = gr < lim ? gr : lim - 1;
+    src[i] = in_x ? X + gr * ldx + 8 * c : W + gr * ldw + 8 * c;
   }
-#pragma unroll
-  for (int i = 0; i < WI; ++i) {
-    const int P = (i * NW + wave) * 64 + lane;
-    const int r = P >> 3, c = (P & 7) ^ (r & 7);
-    int64_t gr = n0 + r;
-    gr = gr < N ? gr : N - 1;
-    wsrc[i] = W + gr * ldw + 8 * c;
-  }
+  const bool hi = wave < T % NW;
   // split-K: workgroup row blockIdx.y takes the k-range [split*K/S, (split+1)*K/S)
   const int split = blockIdx.y;
   const int nk = (int)(K / KB) / (int)gridDim.y;
@@ -224,9 +226,22 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
     const uint32_t base = lds0 + (uint32_t)((kt % NS) * STAGE);
     const int64_t k0 = kbase + (int64_t)kt * KB;
 #pragma unroll
-    for (int i = 0; i < XI; ++i) dma16(xsrc[i] + k0, base + (uint32_t)((i * NW + wave) * 1024));
-#pragma unroll
-    for (int i = 0; i < WI; ++i) dma16(wsrc[i] + k0, base + XB + (uint32_t)((i * NW + wave) * 1024));
+    for (int i = 0; i < GI; ++i) {
+      const int q = i * NW + wave;
+      if (q < T) dma16(src[i] + k0, base + (uint32_t)(q * 1024));
+    }
+  };
+  // wait until at most `later` stages' copies (issued after the one being waited for) are in flight
+  auto wait_stages = [&](int later) {
+    if (hi || GH == GL) {
+      if (later >= 2) wait_vm<2 * GH>();
+      else if (later == 1) wait_vm<GH>();
+      else wait_vm<0>();
+    } else {
+      if (later >= 2) wait_vm<2 * GL>();
+      else if (later == 1) wait_vm<GL>();
+      else wait_vm<0>();
+    }
   };
 
   float4_t acc[TM][TN];
@@ -241,10 +256,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
 
   for (int kt = 0; kt < nk; ++kt) {
     // stages issued after kt and still allowed in flight: min(NS - 2, nk - 1 - kt)
-    const int later = min(NS - 2, nk - 1 - kt);
-    if (later >= 2) wait_vm<2 * (XI + WI)>();
-    else if (later == 1) wait_vm<XI + WI>();
-    else wait_vm<0>();
+    wait_stages(min(NS - 2, nk - 1 - kt));
     __syncthreads();  // stage kt has landed for every wave; stage kt-1 is no longer being read
     if (kt + NS - 1 < nk) issue(kt + NS - 1);
     const char* st = smem + (kt % NS) * STAGE;
@@ -456,14 +468,21 @@ int split_for(int64_t N, int64_t K) {
   return s;
 }
 
-// The LDS-kernel configuration a shape runs with: the largest tile that still fills the GPU (measured
-// at M = 448 and 128 on the decoder's projections); M <= 64 takes 64x64 tiles.
+// The LDS-kernel configuration a shape runs with. M <= 64 (a decode step) takes 64x64 tiles. Larger
+// M takes 224-row tiles when they pad M less than 128- and 256-row tiles would (the verify pass,
+// M = 64 * 7 = 448, is exactly two), else 256- or 128-row tiles; the width is the widest that still
+// gives most CUs a tile (measured at M = 448 and 128 on the decoder's projections).
 struct LdsCfg {
   int bm, bn, wgm, wgn;
 };
 
 LdsCfg lds_cfg(int64_t M, int64_t N, int splits) {
   if (M <= 64) return LdsCfg{64, 64, 2, 2};
+  auto pad = [&](int64_t bm) { return (M + bm - 1) / bm * bm - M; };
+  if (pad(224) < pad(128) && pad(224) < pad(256)) {
+    const int64_t t256 = ((M + 223) / 224) * ((N + 255) / 256) * splits;
+    return t256 >= 192 ? LdsCfg{224, 256, 2, 4} : LdsCfg{224, 128, 2, 4};
+  }
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256) * splits;
   const int64_t t128 = ((M + 127) / 128) * ((N + 255) / 256) * splits;
   if (t256 >= 192) return LdsCfg{256, 256, 4, 2};
@@ -478,19 +497,16 @@ void launch_lds(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, 
   const LdsCfg cf = lds_cfg(M, N, splits);
   const int tm = (int)((M + cf.bm - 1) / cf.bm), nt = tm * (int)((N + cf.bn - 1) / cf.bn);
   const dim3 grid((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits);
-  if (cf.bm == 64) {
-    gemm_bf16_lds_kernel<64, 64, 4, 2, 2, STATS><<<grid, 256, 0, s>>>(a, lda, b, ldb, c, ldc, r, ldr, M, N, K, 1, nt,
-                                                                     part, rs);
-  } else if (cf.bm == 256) {
-    gemm_bf16_lds_kernel<256, 256, 2, 4, 2, STATS><<<grid, 512, 0, s>>>(a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm,
-                                                                       nt, part, rs);
-  } else if (cf.bn == 256) {
-    gemm_bf16_lds_kernel<128, 256, 3, 2, 4, STATS><<<grid, 512, 0, s>>>(a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm,
-                                                                       nt, part, rs);
-  } else {
-    gemm_bf16_lds_kernel<128, 128, 4, 2, 4, STATS><<<grid, 512, 0, s>>>(a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm,
-                                                                       nt, part, rs);
-  }
+#define FS_LDS_LAUNCH(BM_, BN_, NS_, WGM_, WGN_)                                                              \
+  gemm_bf16_lds_kernel<BM_, BN_, NS_, WGM_, WGN_, STATS><<<grid, 64 * WGM_ * WGN_, 0, s>>>(                  \
+      a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part, rs)
+  if (cf.bm == 64) FS_LDS_LAUNCH(64, 64, 4, 2, 2);
+  else if (cf.bm == 224 && cf.bn == 256) FS_LDS_LAUNCH(224, 256, 2, 2, 4);
+  else if (cf.bm == 224) FS_LDS_LAUNCH(224, 128, 3, 2, 4);
+  else if (cf.bm == 256) FS_LDS_LAUNCH(256, 256, 2, 4, 2);
+  else if (cf.bn == 256) FS_LDS_LAUNCH(128, 256, 3, 2, 4);
+  else FS_LDS_LAUNCH(128, 128, 4, 2, 4);
+#undef FS_LDS_LAUNCH
 }
 
 bool lds_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t K) {

@@ -26,7 +26,7 @@ import torch
 from . import ops
 from ._lib import to_device
 from .model import ForgeModel
-from .paged import PagedKVPool
+from .paged import BlockList, PagedKVPool, block_table
 from .sampling import exp_noise
 from .speculative import spec_round
 
@@ -39,10 +39,10 @@ class Request:
     eos_id: Optional[int] = None
     temperature: float = 0.0
     output: List[int] = field(default_factory=list)
-    blocks: List[int] = field(default_factory=list)
+    blocks: List[int] = field(default_factory=BlockList)
     cached: int = 0
     finished: bool = False
-    blocks_d: List[int] = field(default_factory=list)   # draft pool blocks (speculative engine)
+    blocks_d: List[int] = field(default_factory=BlockList)   # draft pool blocks (speculative engine)
 
 
 def _stream_key(seed: int, rid: int, pos: int) -> int:
@@ -149,13 +149,13 @@ class Engine:
         if need > self.pool.allocator.num_free or (spec and need_d > self.pool_d.allocator.num_free):
             return False
         self.waiting.popleft()
-        req.blocks = self.pool.allocator.allocate(need)
+        req.blocks = BlockList(self.pool.allocator.allocate(need))
         positions = torch.arange(len(tokens))[None]
         views = self.pool.views(torch.tensor([req.blocks]), positions)
         logits = self.model(torch.tensor([tokens]), positions, views, last_only=True)
         req.cached = len(tokens)
         if spec:   # the draft's cache covers the same positions; the first token uses the request's stream
-            req.blocks_d = self.pool_d.allocator.allocate(need_d)
+            req.blocks_d = BlockList(self.pool_d.allocator.allocate(need_d))
             self.draft(torch.tensor([tokens]), positions, self.pool_d.views(torch.tensor([req.blocks_d]), positions),
                        last_only=True)
             self._append_keyed(req, logits[:, -1])
@@ -174,10 +174,10 @@ class Engine:
 
     def _release(self, req: Request) -> None:
         self.pool.allocator.release(req.blocks)
-        req.blocks = []
+        req.blocks = BlockList()
         if self.draft is not None:
             self.pool_d.allocator.release(req.blocks_d)
-            req.blocks_d = []
+            req.blocks_d = BlockList()
 
     def _spec_decode(self) -> None:
         """One draft-then-verify round over the running requests. Every request first gets the blocks
@@ -257,7 +257,7 @@ class Engine:
                         raise RuntimeError("the block pool is too small to hold even one sequence of this length")
                     victim = self.running.pop()
                     self.pool.allocator.release(victim.blocks)
-                    victim.blocks, victim.cached = [], 0
+                    victim.blocks, victim.cached = BlockList(), 0
                     self.waiting.appendleft(victim)
                     self.preemptions += 1
                     if victim is req:
@@ -269,8 +269,7 @@ class Engine:
             i += 1
         if not self.running:
             return
-        max_blocks = max(len(r.blocks) for r in self.running)
-        tables = torch.tensor([r.blocks + [0] * (max_blocks - len(r.blocks)) for r in self.running])
+        tables = block_table([r.blocks for r in self.running], self.pool.device)
         positions = torch.tensor([[r.cached] for r in self.running])
         idx = torch.tensor([[r.output[-1]] for r in self.running])
         logits = self.model(idx, positions, self.pool.views(tables, positions), last_only=True)

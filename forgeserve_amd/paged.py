@@ -12,8 +12,9 @@ The block allocator and the block tables stay on the host, as in the reference; 
 to the GPU (int32) once per step and shared by every layer's view.
 """
 
-from typing import List, Optional, Tuple
+from typing import Iterable, List, Optional, Tuple
 
+import numpy as np
 import torch
 
 from . import ops
@@ -24,6 +25,75 @@ from ._lib import to_device
 
 class OutOfBlocks(RuntimeError):
     pass
+
+
+class BlockList(list):
+    """A sequence's block ids: a list (the allocator's currency) that also keeps an int32 copy of
+    itself, so the per-step block table of a batch is built with one array copy per row instead of
+    converting Python ints. Appends (`+=`, `extend`, `append`) keep the copy current; any other
+    mutation marks the copy stale and the next `array()` rebuilds it."""
+
+    __slots__ = ("_arr", "_n")
+
+    def __init__(self, blocks: Iterable[int] = ()):
+        super().__init__(blocks)
+        self._arr = np.array(self, dtype=np.int32)
+        self._n = len(self)
+
+    def __iadd__(self, other):
+        other = list(other)
+        super().__iadd__(other)
+        n, m = self._n, len(self)
+        if n == m - len(other):   # the copy was current: append to it
+            if self._arr.shape[0] < m:
+                grown = np.empty(max(2 * self._arr.shape[0], m, 16), dtype=np.int32)
+                grown[:n] = self._arr[:n]
+                self._arr = grown
+            self._arr[n:m] = other
+            self._n = m
+        return self
+
+    def extend(self, other) -> None:
+        self.__iadd__(other)
+
+    def append(self, block: int) -> None:
+        self.__iadd__([block])
+
+    def _stale(name):
+        def f(self, *a, **kw):
+            self._n = -1
+            return getattr(list, name)(self, *a, **kw)
+        f.__name__ = name
+        return f
+
+    __setitem__ = _stale("__setitem__")
+    __delitem__ = _stale("__delitem__")
+    __imul__ = _stale("__imul__")
+    insert = _stale("insert")
+    pop = _stale("pop")
+    remove = _stale("remove")
+    clear = _stale("clear")
+    sort = _stale("sort")
+    reverse = _stale("reverse")
+    del _stale
+
+    def array(self) -> np.ndarray:
+        """The ids as an int32 array (a view: valid until the list changes)."""
+        if self._n != len(self):
+            self._arr = np.array(self, dtype=np.int32)
+            self._n = len(self)
+        return self._arr[: self._n]
+
+
+def block_table(lists: List[List[int]], device) -> torch.Tensor:
+    """(B, max_blocks) int32 device table of B block lists, zero padded (engine.py:121-124 pads with
+    block 0, which the positions mask). Rows that are BlockLists are copied as arrays."""
+    arrs = [x.array() if isinstance(x, BlockList) else np.asarray(x, dtype=np.int32) for x in lists]
+    width = max([1] + [a.shape[0] for a in arrs])
+    t = np.zeros((len(arrs), width), dtype=np.int32)
+    for i, a in enumerate(arrs):
+        t[i, : a.shape[0]] = a
+    return to_device(torch.from_numpy(t), device)
 
 
 class BlockAllocator:

@@ -18,12 +18,13 @@ Two entry points:
 
 from typing import Dict, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from . import ops
 from ._lib import to_device
 from .kv import new_contiguous_cache
-from .paged import OutOfBlocks, PagedKVPool
+from .paged import BlockList, OutOfBlocks, PagedKVPool, block_table
 from .sampling import exp_noise, probs_from_logits
 
 I32 = torch.int32
@@ -134,15 +135,6 @@ class _GeneratorDraws:
         return u[:, : self.k].contiguous(), e
 
 
-def _tables(lists: List[List[int]], dev) -> torch.Tensor:
-    width = max(1, max(len(x) for x in lists))
-    t = torch.zeros((len(lists), width), dtype=I32)
-    for i, x in enumerate(lists):
-        if x:
-            t[i, : len(x)] = torch.tensor(x, dtype=I32)
-    return to_device(t, dev)
-
-
 @torch.no_grad()
 def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: List[List[int]],
                blocks_t: List[List[int]], blocks_d: List[List[int]], k_eff: List[int], temps: List[float],
@@ -158,9 +150,10 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     b = len(tokens)
     k = max(k_eff)
     dev, dtype = target.device, target.dtype
-    n = [len(t) for t in tokens]
-    tab_t = _tables(blocks_t, dev)
-    tab_d = _tables(blocks_d, dev)
+    n = np.array([len(t) for t in tokens], dtype=np.int64)
+    keff = np.array(k_eff, dtype=np.int64)
+    tab_t = block_table(blocks_t, dev)
+    tab_d = block_table(blocks_d, dev)
     v = target.cfg.vocab_size
     temps_dev = to_device(torch.tensor(temps, dtype=torch.float32), dev)
     sampling = any(t > 0 for t in temps)
@@ -187,11 +180,11 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     for i in range(k):
         if i == 0:
             idx = to_device(torch.stack([prev, last], 1), dev)
-            pos = torch.tensor([[ni - 2 if ni > 1 else -1, ni - 1] if k_eff[r] > 0 else [-1, -1]
-                                for r, ni in enumerate(n)])
+            p = np.stack([np.where(n > 1, n - 2, -1), n - 1], 1)
+            pos = torch.from_numpy(np.where(keff[:, None] > 0, p, -1))
         else:
             idx = cur.to(torch.int64)[:, None]
-            pos = torch.tensor([[ni - 1 + i if i < k_eff[r] else -1] for r, ni in enumerate(n)])
+            pos = torch.from_numpy(np.where(i < keff, n - 1 + i, -1)[:, None])
         logits = draft(idx, pos, pool_d.views(tab_d, pos), last_only=True,
                        head_stats=(inv_t_d, parts_d[:, i]) if fused else None)[:, 0]
         dft_logits[:, i].copy_(logits)
@@ -203,7 +196,8 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     # 2. target verify over [tokens[-1], x_0 .. x_{k-1}] at n-1 .. n-1+k
     last_dev = to_device(last, dev)
     idx = torch.cat([last_dev[:, None], draft_tok.to(torch.int64)], 1) if k else last_dev[:, None]
-    pos = torch.tensor([[ni - 1 + t if t <= k_eff[r] else -1 for t in range(k + 1)] for r, ni in enumerate(n)])
+    t_ = np.arange(k + 1)[None, :]
+    pos = torch.from_numpy(np.where(t_ <= keff[:, None], n[:, None] - 1 + t_, -1))
     tgt_logits = target(idx, pos, pool_t.views(tab_t, pos), head_stats=(inv_t_t, parts_t) if fused else None)
     if fused:
         ops.row_stats_merge(parts_t, row_stats, k + 1, 2 * k + 1, 0)
@@ -227,8 +221,8 @@ class _Seq:
         self.start = len(tokens)
         self.max_new = max_new
         self.temperature = float(temperature)
-        self.blocks_t: List[int] = []
-        self.blocks_d: List[int] = []
+        self.blocks_t = BlockList()
+        self.blocks_d = BlockList()
         self.done = False
         self.eos_id = eos_id
 
@@ -265,7 +259,7 @@ class SpeculativeBatch:
     def release(self, seq: _Seq) -> None:
         self.pool_t.allocator.release(seq.blocks_t)
         self.pool_d.allocator.release(seq.blocks_d)
-        seq.blocks_t, seq.blocks_d = [], []
+        seq.blocks_t, seq.blocks_d = BlockList(), BlockList()
 
     def add(self, prompt: Sequence[int], max_new_tokens: int, temperature: float = 0.0, eos_id=None,
             prefill: bool = True) -> _Seq:
@@ -315,9 +309,10 @@ class SpeculativeBatch:
                          [s.temperature for s in seqs], _GeneratorDraws(self.gen, b, k, self.target.cfg.vocab_size,
                                                                         self.dev))
         committed = 0
+        rows = res.tolist()
         for r, s in enumerate(seqs):
-            a = int(res[r, 0])
-            new = res[r, 1: a + 2].tolist()
+            a = rows[r][0]
+            new = rows[r][1: a + 2]
             s.tokens += new
             committed += len(new)
             self.stats["proposed"] += k_eff[r]

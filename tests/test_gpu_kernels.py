@@ -24,7 +24,8 @@ def rel_err(got, ref):
 # ---- GEMM -------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("m,n,k", [(1, 48, 64), (7, 256, 688), (64, 1000, 256), (65, 384, 512), (448, 640, 4096),
-                                   (130, 96, 192), (20, 4096, 1024), (100, 2048, 2048)])  # the last two split K
+                                   (130, 96, 192), (20, 4096, 1024), (100, 2048, 2048),   # these two split K
+                                   (448, 24592, 256)])   # 224 x 256 tiles, a partial last column tile
 def test_gemm_matches_fp64(dtype, m, n, k):
     case("gemm", dtype, m, n, k)
     g = torch.Generator().manual_seed(m * 7 + n)
@@ -41,7 +42,7 @@ def test_gemm_matches_fp64(dtype, m, n, k):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("n,k", [(384, 512), (2048, 2048)])   # (2048, 2048) splits K four ways
+@pytest.mark.parametrize("n,k", [(384, 512), (2048, 2048), (24576, 256)])   # (2048, 2048) splits K four ways
 def test_gemm_rows_do_not_depend_on_the_batch(dtype, n, k):
     """A row's result is bit-identical whether it is computed alone, among 64 rows or among 448."""
     case("gemm invariance", dtype, n, k)
@@ -435,7 +436,7 @@ def _records(m, s, av, ai):
     return torch.cat([f, ai.to(torch.int32)[..., None]], -1).contiguous()
 
 
-@pytest.mark.parametrize("m,n,k", [(64, 5003, 256), (100, 4096, 128), (448, 6000, 256)])
+@pytest.mark.parametrize("m,n,k", [(64, 5003, 256), (100, 4096, 128), (448, 6000, 256), (448, 25000, 128)])
 def test_gemm_row_stats(m, n, k):
     """The head GEMM's statistics epilogue, merged per row, against torch on the stored logits:
     max and argmax exact, the sum of exponentials within float rounding."""
