@@ -7,10 +7,13 @@ k = 6, contexts uniform in [2048, 8192] held in a paged pool with block_size 16.
 values are synthetic N(0, 1) bf16 written straight into the pools (no prefill), then `--steps` decode
 rounds are timed: k draft decode steps, one target verify pass over k+1 tokens, one fused acceptance.
 
-One "step" = one speculative round for the whole batch. `value` = committed tokens per second
-(accepted proposals + one target token per sequence per round), inputs resident in HBM.
-`roofline` = the paged verify attention (split-KV kernel + its combine), timed with HIP events on the
-launching stream around every verify-attention launch of the timed rounds, against 8 TB/s.
+One "step" = one speculative round for the whole batch, replayed from the HIP graph captured for its
+shape (the first round of a shape runs eagerly, the second captures). `value` = committed tokens per
+second (accepted proposals + one target token per sequence per round), inputs resident in HBM.
+`roofline` = the paged verify attention (plan + unit kernel, + combine when a query spans chunks),
+timed with HIP events on the launching stream around every verify-attention launch of 8 eager rounds
+of the same batch that follow the timed rounds (a graph replay cannot bracket single launches),
+against 8 TB/s.
 `cpu_baseline` = the CPU oracle (oracle/reference_cpu.py) timed on this host on one target layer's
 verify pass, one draft layer's decode step, the LM head and the acceptance at the same shapes,
 scaled to a round.
@@ -40,6 +43,7 @@ CFG = dict(vocab_size=128256, d_model=4096, n_layers=32, n_heads=32, n_kv_heads=
            max_seq_len=10240)
 DRAFT_LAYERS = 4
 BATCH, K, BLOCK = 64, 6, 16
+ATTN_ROUNDS = 8   # eager rounds after the timed ones, for per-launch attention events
 CTX_LO, CTX_HI = 2048, 8192
 
 
@@ -396,7 +400,7 @@ def main():
 
     g = torch.Generator().manual_seed(args.seed)
     ctxs = torch.randint(CTX_LO, CTX_HI + 1, (BATCH,), generator=g).tolist()
-    rounds = args.warmup + args.steps
+    rounds = args.warmup + args.steps + ATTN_ROUNDS
     per_seq = [-(-(c + 2 + rounds * (K + 1) + K) // BLOCK) for c in ctxs]
     nblocks = sum(per_seq) + 8
     sb = fa.SpeculativeBatch(target, draft, nblocks, BLOCK, K,
@@ -415,27 +419,39 @@ def main():
         log(f"warmup round {i} done")
     torch.cuda.synchronize()
 
-    # verify-attention launches of the timed rounds are bracketed by events on the launching stream
-    events = []
-    ops.ATTN_EVENTS = events
-    ops.ATTN_EVENT_T = K + 1
-    ctx_log = []
+    # timed rounds: each round's kernels replay from the HIP graph captured for its shape
     acc0 = dict(sb.stats)
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     committed = 0
     for i in range(args.steps):
-        ctx_log.append([len(s.tokens) for s in sb.active()])
         committed += sb.round()
         if (i + 1) % 32 == 0:
             log(f"round {i + 1}/{args.steps}: {committed} tokens committed")
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
+    proposed = sb.stats["proposed"] - acc0["proposed"]
+    accepted = sb.stats["accepted"] - acc0["accepted"]
+
+    # verify-attention launch durations: a graph replay cannot bracket single launches with events, so
+    # the next ATTN_ROUNDS rounds of the same batch run eagerly with events on the launching stream
+    # around every verify-attention launch (the kernels are the graph's; the rocprofv3 summary of the
+    # graph rounds gives the same per-launch average)
+    events = []
+    ops.ATTN_EVENTS = events
+    ops.ATTN_EVENT_T = K + 1
+    ctx_log = []
+    sb.graphs = False
+    for i in range(ATTN_ROUNDS):
+        ctx_log.append([len(s.tokens) for s in sb.active()])
+        sb.round()
+    torch.cuda.synchronize()
+    sb.graphs = True
     ops.ATTN_EVENTS = None
 
     # each round's verify pass runs n_layers attention launches over contexts len(tokens) - 1 + k + 1
     layers = CFG["n_layers"]
-    assert len(events) == layers * args.steps, (len(events), layers * args.steps)
+    assert len(events) == layers * ATTN_ROUNDS, (len(events), layers * ATTN_ROUNDS)
     durs = [a.elapsed_time(b) * 1e-3 for a, b in events]
     bytes_total = 0
     for lens in ctx_log:
@@ -444,8 +460,6 @@ def main():
     attn_gbs = bytes_total / sum(durs) / 1e9
     attn_traffic = bytes_total / len(durs)
 
-    proposed = sb.stats["proposed"] - acc0["proposed"]
-    accepted = sb.stats["accepted"] - acc0["accepted"]
     value = committed / elapsed
 
     v = CFG["vocab_size"]

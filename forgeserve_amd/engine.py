@@ -82,7 +82,8 @@ class _KeyedDraws:
 
 class Engine:
     def __init__(self, model: ForgeModel, num_blocks: int, block_size: int = 16, max_batch: int = 8, seed: int = 0,
-                 draft: Optional[ForgeModel] = None, k: int = 4, draft_num_blocks: Optional[int] = None):
+                 draft: Optional[ForgeModel] = None, k: int = 4, draft_num_blocks: Optional[int] = None,
+                 graphs: bool = True):
         self.model, self.cfg = model, model.cfg
         self.pool = PagedKVPool(self.cfg, num_blocks, block_size, tp=model.tp, dtype=model.dtype, device=model.device)
         self.max_batch = max_batch
@@ -93,6 +94,7 @@ class Engine:
         self.steps = self.preemptions = self.peak_running = self.peak_blocks = 0
         # speculative decoding (optional): the draft keeps its own pool, as speculative.py:46 keeps kv_d
         self.draft, self.k, self.seed = draft, k, seed
+        self.graphs = graphs   # speculative rounds: replay each round shape from a captured HIP graph
         self.limit = self.cfg.max_seq_len
         self.stats = {"rounds": 0, "proposed": 0, "accepted": 0}
         if draft is not None:
@@ -212,7 +214,7 @@ class Engine:
         draws = _KeyedDraws(batch, [len(t) for t in tokens], temps, self.seed, max(k_eff), self.cfg.vocab_size,
                             self.model.device)
         res = spec_round(self.model, self.draft, self.pool, self.pool_d, tokens, [r.blocks for r in batch],
-                         [r.blocks_d for r in batch], k_eff, temps, draws)
+                         [r.blocks_d for r in batch], k_eff, temps, draws, graphs=self.graphs)
         self.stats["rounds"] += 1
         for r, req in enumerate(batch):
             a = int(res[r, 0])

@@ -187,15 +187,17 @@ class ForgeModel(nn.Module):
     def embed(self, idx):
         return ops.embedding(to_device(idx, self.device), self.tok_emb.weight).reshape(*idx.shape, self.cfg.d_model)
 
-    def head(self, x, stats=None):
+    def head(self, x, stats=None, out=None):
         """Final norm + tied head (model.py:137-138). stats = (inv_temperature (rows,), parts): also emit
-        the logits' per-row softmax statistics (ops.gemm_row_stats)."""
+        the logits' per-row softmax statistics (ops.gemm_row_stats). out: optional (rows, vocab) view
+        (contiguous rows, any row stride) that receives the logits."""
         shape = x.shape
         y = ops.add_rmsnorm(x.reshape(-1, shape[-1]), self.norm.weight, self.norm.eps)
         if stats is not None:
-            return ops.gemm_row_stats(y, self.lm_head.weight, stats[0], stats[1]).reshape(*shape[:-1],
-                                                                                        self.cfg.vocab_size)
-        return ops.gemm(y, self.lm_head.weight).reshape(*shape[:-1], self.cfg.vocab_size)
+            logits = ops.gemm_row_stats(y, self.lm_head.weight, stats[0], stats[1], out=out)
+        else:
+            logits = ops.gemm(y, self.lm_head.weight, out=out)
+        return logits if out is not None else logits.reshape(*shape[:-1], self.cfg.vocab_size)
 
     @torch.no_grad()
     def forward(self, idx, positions: Optional[torch.Tensor] = None, kv: Optional[List] = None,
@@ -220,12 +222,23 @@ class ForgeModel(nn.Module):
         if pmax >= self.cfg.max_seq_len:
             raise ValueError(f"position {pmax} exceeds max_seq_len {self.cfg.max_seq_len}")
         pos32 = to_device(positions.reshape(b, t).contiguous(), dev, torch.int32)
+        return self._run(to_device(idx, dev), pos32, kv, last_only, head_stats)
+
+    def _run(self, idx: torch.Tensor, pos32: torch.Tensor, kv: List, last_only: bool = False, head_stats=None,
+             out=None):
+        """The forward's kernels alone: idx (B, T) int64 and pos32 (B, T) int32 already on the device,
+        no argument checks and no host synchronisation, so that a caller can capture it in a HIP graph
+        (positions < max_seq_len is the caller's to guarantee). With last_only, `out` (B, vocab) may
+        receive the logits (then it is returned as is)."""
+        b, t = idx.shape
         rope = self._rope()
-        x = ops.embedding(to_device(idx, dev), self.tok_emb.weight)
+        x = ops.embedding(idx, self.tok_emb.weight)
         for layer, view in zip(self.layers, kv):
             x = layer.step(x, b, t, pos32, view, rope)
         if last_only:
             x = x.view(b, t, -1)[:, -1].contiguous()
+            if out is not None:
+                return self.head(x, head_stats, out=out)
             return self.head(x, head_stats).view(b, 1, -1)
         return self.head(x, head_stats).view(b, t, -1)
 

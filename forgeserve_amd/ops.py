@@ -32,14 +32,18 @@ def _ws(nbytes: int, device) -> torch.Tensor:
 
 
 _PERSISTENT = {}
+_RETIRED = []   # outgrown scratch buffers: a captured HIP graph may still hold their addresses
 
 
 def _persistent_ws(name: str, nbytes: int, device) -> torch.Tensor:
     """A per-device scratch buffer reused across calls (calls are ordered on torch's current stream,
-    so consecutive users never overlap); grown when a call needs more."""
+    so consecutive users never overlap); grown when a call needs more. An outgrown buffer is kept
+    alive for the life of the process, since graphs captured earlier launch kernels on it."""
     key = (name, torch.device(device))
     ws = _PERSISTENT.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = torch.empty(max(int(nbytes * 1.25), 1 << 20), dtype=torch.uint8, device=key[1])
         _PERSISTENT[key] = ws
     return ws
@@ -256,7 +260,7 @@ def paged_attention(q: torch.Tensor, layout: KVLayout, tables: torch.Tensor, pos
     lib = _lib.load()
     need = lib.fs_paged_attention_workspace_size(b, t, h, d, nb, layout.block_size)
     ws = _persistent_ws("attention", need, q.device)
-    timing = ATTN_EVENTS is not None and t == ATTN_EVENT_T
+    timing = ATTN_EVENTS is not None and t == ATTN_EVENT_T and not torch.cuda.is_current_stream_capturing()
     if timing:
         ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         ev[0].record()

@@ -16,6 +16,7 @@ Two entry points:
   kernels; the only device-to-host copy per round is (n_accepted, out_tokens).
 """
 
+from collections import OrderedDict
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
@@ -24,7 +25,7 @@ import torch
 from . import ops
 from ._lib import to_device
 from .kv import new_contiguous_cache
-from .paged import BlockList, OutOfBlocks, PagedKVPool, block_table
+from .paged import BlockList, OutOfBlocks, PagedKVPool
 from .sampling import exp_noise, probs_from_logits
 
 I32 = torch.int32
@@ -135,10 +136,142 @@ class _GeneratorDraws:
         return u[:, : self.k].contiguous(), e
 
 
+def _bucket(x: int, q: int) -> int:
+    return max(q, -(-x // q) * q)
+
+
+class _RoundState:
+    """What one shape of round keeps between rounds: the pinned host staging and the device copy of
+    the round's inputs (one host-to-device copy per round), the buffers that pass results between the
+    round's phases, the random-number buffers, and, from its second use on, one HIP graph per phase
+    (each draft step, then the verify pass with the acceptance), replayed on those fixed addresses.
+
+    The shape is (b, k, table widths, sampling, statistics path); b is padded to a multiple of 8 and
+    the table widths to multiples of 64 blocks, so that growing contexts and a changing batch reuse a
+    few graphs. Padding rows have k_eff 0 and only -1 positions (no KV write, no keys), temperature
+    0, and their results are dropped."""
+
+    def __init__(self, dev, dtype, b, k, wt, wd, v, sampling, fused, parts_d, parts_t):
+        self.b, self.k, self.wt, self.wd, self.v = b, k, wt, wd, v
+        self.sampling, self.fused = sampling, fused
+        # staging: int64 ids [b, 2] (prev, last) and last [b]; int32 k_eff [b], draft positions [b, 2] (step 0)
+        # then [k-1, b] (steps 1..k-1), verify positions [b, k+1], tables [b, wt] and [b, wd];
+        # float32 temperature and 1/T [2, b]
+        km = max(k - 1, 0)
+        spans = [("ids", np.int64, (b, 2)), ("last", np.int64, (b,)), ("keff", np.int32, (b,)), ("pos0", np.int32, (b, 2)),
+                 ("posd", np.int32, (km, b)), ("posv", np.int32, (b, k + 1)), ("tab_t", np.int32, (b, wt)),
+                 ("tab_d", np.int32, (b, wd)), ("temps", np.float32, (2, b))]
+        off, lay = 0, {}
+        for name, dt, shape in spans:
+            nbytes = int(np.prod(shape)) * np.dtype(dt).itemsize
+            lay[name] = (off, nbytes, dt, shape)
+            off += -(-nbytes // 16) * 16
+        self.host = torch.empty(max(off, 16), dtype=torch.uint8, pin_memory=True)
+        self.dev = torch.empty(max(off, 16), dtype=torch.uint8, device=dev)
+        hn = self.host.numpy()
+        tdt = {np.int64: torch.int64, np.int32: torch.int32, np.float32: torch.float32}
+        self.h, self.d = {}, {}
+        for name, (o, nbytes, dt, shape) in lay.items():
+            self.h[name] = hn[o: o + nbytes].view(dt).reshape(shape)
+            self.d[name] = self.dev[o: o + nbytes].view(tdt[dt]).view(shape)
+        kk = max(k, 1)
+        self.u = torch.zeros((b, kk), dtype=torch.float32, device=dev)
+        self.e = torch.ones((b, v), dtype=torch.float32, device=dev)
+        self.noise_d = torch.ones((kk, b, v), dtype=torch.float32, device=dev) if sampling else None
+        # results passed between phases
+        self.dft_logits = torch.empty((b, k, v), dtype=dtype, device=dev)
+        self.draft_tok = torch.empty((b, k), dtype=I32, device=dev)
+        if fused:
+            # draft step i writes its rows' records into parts_d[:, i]; one merge after the last step
+            self.parts_d = torch.empty((b, k, parts_d, 4), dtype=I32, device=dev)
+            self.parts_t = torch.empty((b * (k + 1), parts_t, 4), dtype=I32, device=dev)
+            self.row_stats = torch.empty((b, 2 * k + 1, 4), dtype=I32, device=dev)
+        self.res_host = torch.empty((b, k + 2), dtype=torch.int32, pin_memory=True)
+        self.res = None
+        self.graphs = None
+        self.uses = 0
+
+    def stage(self, tokens, k_eff, temps, blocks_t, blocks_d) -> None:
+        """Write one round's inputs into the pinned staging buffer (rows past len(tokens) are padding)."""
+        b, k = len(tokens), self.k
+        h = self.h
+        n = np.array([len(t) for t in tokens], dtype=np.int64)
+        keff = np.array(k_eff, dtype=np.int64)
+        ids = h["ids"]
+        ids.fill(0)
+        ids[:b, 0] = [t[-2] if len(t) > 1 else 0 for t in tokens]
+        ids[:b, 1] = [t[-1] for t in tokens]
+        h["last"][:] = ids[:, 1]
+        h["keff"].fill(0)
+        h["keff"][:b] = keff
+        # step 0 re-feeds (prev, last) at (n-2, n-1); step i feeds x_{i-1} at n-1+i; the verify pass
+        # feeds [last, x_0 .. x_{k-1}] at n-1 .. n-1+k; positions past a row's k_eff are -1
+        h["pos0"].fill(-1)
+        h["pos0"][:b] = np.where(keff[:, None] > 0, np.stack([np.where(n > 1, n - 2, -1), n - 1], 1), -1)
+        h["posd"].fill(-1)
+        for i in range(1, k):
+            h["posd"][i - 1, :b] = np.where(keff > i, n - 1 + i, -1)
+        t_ = np.arange(k + 1)[None, :]
+        h["posv"].fill(-1)
+        h["posv"][:b] = np.where(t_ <= keff[:, None], n[:, None] - 1 + t_, -1)
+        h["temps"].fill(0)
+        h["temps"][0, :b] = temps
+        h["temps"][1, :b] = [np.float32(1.0 / t) if t > 0 else 0.0 for t in temps]
+        for name, lists in (("tab_t", blocks_t), ("tab_d", blocks_d)):
+            tab = h[name]
+            tab.fill(0)
+            for r, x in enumerate(lists):
+                a = x.array() if isinstance(x, BlockList) else np.asarray(x, dtype=np.int32)
+                tab[r, : a.shape[0]] = a
+
+
+def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _RoundState, phase: int):
+    """The kernels of one phase of a round, reading only st's device buffers (no host copies, no host
+    syncs): phase i < k is draft step i, phase k the target's verify pass over the k+1 window and the
+    fused acceptance, which returns (b, k+2) int32: n_accepted, then the committed tokens (-1 padded)."""
+    b, k = st.b, st.k
+    d = st.d
+    temps, inv_t = d["temps"][0], d["temps"][1]
+    if phase < k:
+        i = phase
+        if i == 0:
+            idx, pos = d["ids"], d["pos0"]
+        else:
+            idx, pos = st.draft_tok[:, i - 1].to(torch.int64)[:, None], d["posd"][i - 1][:, None]
+        logits = draft._run(idx, pos, pool_d.views(d["tab_d"], pos), last_only=True,
+                            head_stats=(inv_t, st.parts_d[:, i]) if st.fused else None, out=st.dft_logits[:, i])
+        ops.sample_logits(logits, temps, st.noise_d[i] if st.sampling else None, out32=st.draft_tok[:, i])
+        if st.fused and i == k - 1:   # draft row (b, i) is record b*k + i: sequence b's draft rows k+1 .. 2k
+            ops.row_stats_merge(st.parts_d.view(b * k, -1, 4), st.row_stats, k, 2 * k + 1, k + 1)
+        return None
+    last = d["last"]
+    idx = torch.cat([last[:, None], st.draft_tok.to(torch.int64)], 1) if k else last[:, None]
+    pos = d["posv"]
+    inv_t_t = inv_t.repeat_interleave(k + 1) if st.fused else None
+    tgt_logits = target._run(idx, pos, pool_t.views(d["tab_t"], pos),
+                             head_stats=(inv_t_t, st.parts_t) if st.fused else None)
+    if st.fused:
+        ops.row_stats_merge(st.parts_t, st.row_stats, k + 1, 2 * k + 1, 0)
+    out_tok, n_acc = ops.spec_accept(tgt_logits, st.dft_logits, st.draft_tok, d["keff"], temps, st.u[:, :k], st.e,
+                                     row_stats=st.row_stats if st.fused else None)
+    return torch.cat([n_acc[:, None], out_tok], 1)
+
+
+def _graph_key(model) -> tuple:
+    """Which weights a captured round reads: the model object and a few parameter addresses (a model
+    whose parameters were replaced by new tensors gets new graphs)."""
+    blk = model.layers
+    return (id(model), model.tok_emb.weight.data_ptr(), blk[0].attn.wq.weight.data_ptr(),
+            blk[-1].mlp.w_down.weight.data_ptr())
+
+
+_MAX_GRAPHS = 8
+
+
 @torch.no_grad()
 def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: List[List[int]],
                blocks_t: List[List[int]], blocks_d: List[List[int]], k_eff: List[int], temps: List[float],
-               draws) -> torch.Tensor:
+               draws, graphs: bool = True) -> torch.Tensor:
     """One draft-then-verify round (speculative.py:53-85) for b sequences whose caches hold positions
     0..n-2 (n = len(tokens[r])) and whose block lists cover positions up to n-1+k_eff[r].
 
@@ -146,68 +279,70 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     accepted round needs no catch-up forward; step i feeds x_{i-1} at n-1+i), one target verify pass
     over the k+1 window, one fused acceptance. `draws` supplies the randomness: draft(i) -> (b, V)
     Exp(1) noise of draft step i, accept() -> (u (b, k), E (b, V)); rows of greedy sequences are
-    ignored. Returns (b, k+2) int32 on the host: n_accepted, then the committed tokens (-1 padded)."""
+    ignored, and a round with no sampled row draws nothing. With `graphs`, the round's kernels are
+    captured in a HIP graph on the second round of a shape and replayed from then on (the same kernels
+    on the same inputs: results are identical to running them one by one).
+    Returns (b, k+2) int32 on the host: n_accepted, then the committed tokens (-1 padded)."""
     b = len(tokens)
     k = max(k_eff)
     dev, dtype = target.device, target.dtype
+    v = target.cfg.vocab_size
     n = np.array([len(t) for t in tokens], dtype=np.int64)
     keff = np.array(k_eff, dtype=np.int64)
-    tab_t = block_table(blocks_t, dev)
-    tab_d = block_table(blocks_d, dev)
-    v = target.cfg.vocab_size
-    temps_dev = to_device(torch.tensor(temps, dtype=torch.float32), dev)
+    limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
+    if int((n - 1 + keff).max()) >= limit:
+        raise ValueError(f"a round would write position {int((n - 1 + keff).max())} >= max_seq_len {limit}")
     sampling = any(t > 0 for t in temps)
+    bp = _bucket(b, 8)
+    wt = _bucket(max(len(x) for x in blocks_t), 64)
+    wd = _bucket(max(len(x) for x in blocks_d), 64)
     # The LM heads emit the logits' softmax statistics (sampling.py:13) as they write them, so the
     # acceptance does not read the 2k+1 logit rows back to normalise them.
     d = target.cfg.d_model
-    fused = (dtype == torch.bfloat16 and k > 0 and ops.row_stats_parts(b, v, d) > 0
-             and ops.row_stats_parts(b * (k + 1), v, d) > 0)
-    if fused:
-        inv_t = torch.tensor([1.0 / t if t > 0 else 0.0 for t in temps], dtype=torch.float32)
-        inv_t_d = to_device(inv_t, dev)
-        inv_t_t = to_device(inv_t.repeat_interleave(k + 1), dev)
-        # draft step i writes its rows' records into parts_d[:, i]; one merge after the last step
-        parts_d = torch.empty((b, k, ops.row_stats_parts(b, v, d), 4), dtype=I32, device=dev)
-        parts_t = torch.empty((b * (k + 1), ops.row_stats_parts(b * (k + 1), v, d), 4), dtype=I32, device=dev)
-        row_stats = torch.empty((b, 2 * k + 1, 4), dtype=I32, device=dev)
+    pd, pt = ops.row_stats_parts(bp, v, d), ops.row_stats_parts(bp * (k + 1), v, d)
+    fused = dtype == torch.bfloat16 and k > 0 and pd > 0 and pt > 0
 
-    # 1. draft
-    dft_logits = torch.empty((b, k, v), dtype=dtype, device=dev)
-    draft_tok = torch.empty((b, k), dtype=I32, device=dev)
-    last = torch.tensor([t[-1] for t in tokens], dtype=torch.int64)
-    prev = torch.tensor([t[-2] if len(t) > 1 else 0 for t in tokens], dtype=torch.int64)
-    cur = None
-    for i in range(k):
-        if i == 0:
-            idx = to_device(torch.stack([prev, last], 1), dev)
-            p = np.stack([np.where(n > 1, n - 2, -1), n - 1], 1)
-            pos = torch.from_numpy(np.where(keff[:, None] > 0, p, -1))
-        else:
-            idx = cur.to(torch.int64)[:, None]
-            pos = torch.from_numpy(np.where(i < keff, n - 1 + i, -1)[:, None])
-        logits = draft(idx, pos, pool_d.views(tab_d, pos), last_only=True,
-                       head_stats=(inv_t_d, parts_d[:, i]) if fused else None)[:, 0]
-        dft_logits[:, i].copy_(logits)
-        ops.sample_logits(logits, temps_dev, draws.draft(i) if sampling else None, out32=draft_tok[:, i])
-        cur = draft_tok[:, i]
-    if fused:   # draft row (b, i) is record b*k + i: sequence b's draft rows k+1 .. 2k
-        ops.row_stats_merge(parts_d.view(b * k, -1, 4), row_stats, k, 2 * k + 1, k + 1)
+    cache = pool_t.__dict__.setdefault("_rounds", OrderedDict())
+    key = (bp, k, wt, wd, sampling, fused, _graph_key(target), _graph_key(draft), id(pool_d))
+    st = cache.get(key)
+    if st is None:
+        st = _RoundState(dev, dtype, bp, k, wt, wd, v, sampling, fused, pd, pt)
+        cache[key] = st
+        while len(cache) > _MAX_GRAPHS:
+            cache.popitem(last=False)
+    cache.move_to_end(key)
 
-    # 2. target verify over [tokens[-1], x_0 .. x_{k-1}] at n-1 .. n-1+k
-    last_dev = to_device(last, dev)
-    idx = torch.cat([last_dev[:, None], draft_tok.to(torch.int64)], 1) if k else last_dev[:, None]
-    t_ = np.arange(k + 1)[None, :]
-    pos = torch.from_numpy(np.where(t_ <= keff[:, None], n[:, None] - 1 + t_, -1))
-    tgt_logits = target(idx, pos, pool_t.views(tab_t, pos), head_stats=(inv_t_t, parts_t) if fused else None)
-    if fused:
-        ops.row_stats_merge(parts_t, row_stats, k + 1, 2 * k + 1, 0)
+    # host staging -> one copy; then the random numbers, drawn in the reference loop's order
+    st.stage(tokens, k_eff, temps, blocks_t, blocks_d)
+    st.dev.copy_(st.host, non_blocking=True)
+    if sampling:
+        for i in range(k):
+            st.noise_d[i, :b].copy_(draws.draft(i))
+        u, e = draws.accept()
+        st.u[:b, :k].copy_(u)
+        st.e[:b].copy_(e)
 
-    # 3. acceptance
-    u, noise = draws.accept()
-    keff_dev = to_device(torch.tensor(k_eff, dtype=I32), dev)
-    out_tok, n_acc = ops.spec_accept(tgt_logits, dft_logits, draft_tok, keff_dev, temps_dev, u, noise,
-                                     row_stats=row_stats if fused else None)
-    return torch.cat([n_acc[:, None], out_tok], 1).cpu()
+    if not graphs or st.uses == 0:
+        for phase in range(k + 1):
+            st.res = _round_phase(target, draft, pool_t, pool_d, st, phase)
+    else:
+        if st.graphs is None:
+            torch.cuda.current_stream().synchronize()
+            gs = []
+            for phase in range(k + 1):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    out = _round_phase(target, draft, pool_t, pool_d, st, phase)
+                if out is not None:
+                    st.res = out
+                gs.append(g)
+            st.graphs = gs
+        for g in st.graphs:
+            g.replay()
+    st.uses += 1
+    st.res_host.copy_(st.res, non_blocking=True)
+    torch.cuda.current_stream().synchronize()
+    return st.res_host[:b].clone()
 
 
 # ------------------------------------------------------------------------------------------------
@@ -235,7 +370,8 @@ class SpeculativeBatch:
     1 + (accepted proposals) tokens."""
 
     def __init__(self, target, draft, num_blocks: int, block_size: int = 16, k: int = 4,
-                 draft_num_blocks: Optional[int] = None, generator: Optional[torch.Generator] = None):
+                 draft_num_blocks: Optional[int] = None, generator: Optional[torch.Generator] = None,
+                 graphs: bool = True):
         if target.cfg.vocab_size != draft.cfg.vocab_size:
             raise ValueError("target and draft must share a vocabulary")
         self.target, self.draft, self.k = target, draft, k
@@ -246,6 +382,7 @@ class SpeculativeBatch:
         self.block_size = block_size
         self.limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
         self.gen = generator
+        self.graphs = graphs   # replay each round shape's kernels from a captured HIP graph
         self.seqs: List[_Seq] = []
         self.stats = {"rounds": 0, "proposed": 0, "accepted": 0}
 
@@ -307,7 +444,7 @@ class SpeculativeBatch:
         res = spec_round(self.target, self.draft, self.pool_t, self.pool_d, [s.tokens for s in seqs],
                          [s.blocks_t for s in seqs], [s.blocks_d for s in seqs], k_eff,
                          [s.temperature for s in seqs], _GeneratorDraws(self.gen, b, k, self.target.cfg.vocab_size,
-                                                                        self.dev))
+                                                                        self.dev), graphs=self.graphs)
         committed = 0
         rows = res.tolist()
         for r, s in enumerate(seqs):

@@ -227,6 +227,49 @@ def test_bf16_batch_perfect_draft_accepts_everything(bf_target):
     assert got == [fa.generate(bf_target, torch.tensor([p]), 25)[0].tolist()[len(p):] for p in prompts]
 
 
+def test_graph_rounds_equal_eager_rounds(bf_target):
+    """Rounds replayed from captured HIP graphs commit exactly the eager rounds' tokens. Each shape is
+    replayed many times with new inputs (and eager work, host copies and syncs in between); the batch
+    shrinks as sequences finish, so several shapes are captured; greedy and sampled rows are mixed."""
+    case("graph rounds == eager rounds")
+    draft = fa.early_exit_draft(bf_target, 2)
+    g = torch.Generator().manual_seed(21)
+    prompts = [torch.randint(0, 1000, (int(n),), generator=g).tolist() for n in torch.randint(2, 90, (11,), generator=g)]
+    temps = [0.0, 0.7, 1.0, 0.0, 1.3, 0.9, 0.0, 0.5, 1.0, 0.8, 0.0]
+
+    def run(graphs):
+        sb = fa.SpeculativeBatch(bf_target, draft, 400, 16, k=4,
+                                 generator=torch.Generator(device="cuda").manual_seed(3), graphs=graphs)
+        seqs = [sb.add(p, 30 + 3 * i, t) for i, (p, t) in enumerate(zip(prompts, temps))]
+        sb.run()
+        return [s.tokens for s in seqs], sb.stats
+
+    eager, stats_e = run(False)
+    graph, stats_g = run(True)
+    assert stats_g["rounds"] >= 10
+    assert graph == eager and stats_g == stats_e
+
+
+def test_graph_engine_equals_eager_engine(small):
+    """The speculative engine (f32 model: the generic kernels) gives the same tokens, preemptions and
+    counters with graph-replayed rounds as with eager rounds, at T > 0 through a tight pool."""
+    case("graph engine == eager engine")
+    draft = fa.early_exit_draft(small, 1)
+    reqs = [([1, 2, 3], 20, 0.8), ([9, 8, 7, 6], 15, 0.0), ([5, 5], 18, 1.0), ([30, 31, 32, 33, 34], 12, 0.6),
+            ([7] * 9, 16, 0.9)]
+
+    def run(graphs):
+        e = fa.Engine(small, num_blocks=14, block_size=4, max_batch=4, seed=5, draft=draft, k=3, graphs=graphs)
+        ids = [e.add_request(p, n, temperature=t) for p, n, t in reqs]
+        out = e.run()
+        return [out[i] for i in ids], e.preemptions, e.stats
+
+    eager = run(False)
+    graph = run(True)
+    assert eager[1] > 0
+    assert graph == eager
+
+
 # ---- speculative engine (batched speculation inside Engine) ---------------------------------------------
 def test_spec_engine_greedy_matches_the_reference_engine(small):
     """Greedy: the speculative engine emits the reference Engine's tokens exactly, through a pool small
