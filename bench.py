@@ -10,10 +10,9 @@ rounds are timed: k draft decode steps, one target verify pass over k+1 tokens, 
 One "step" = one speculative round for the whole batch, replayed from the HIP graph captured for its
 shape (the first round of a shape runs eagerly, the second captures). `value` = committed tokens per
 second (accepted proposals + one target token per sequence per round), inputs resident in HBM.
-`roofline` = the paged verify attention (plan + unit kernel, + combine when a query spans chunks),
-timed with HIP events on the launching stream around every verify-attention launch of 8 eager rounds
-of the same batch that follow the timed rounds (a graph replay cannot bracket single launches),
-against 8 TB/s.
+`roofline` = the paged verify attention (plan + unit kernel, + combine when a query spans chunks): the
+last timed round's 32 verify-attention launches (each layer's pool, that round's tables and query
+positions) replayed from one HIP graph between HIP events on the launching stream, against 8 TB/s.
 `cpu_baseline` = the CPU oracle (oracle/reference_cpu.py) timed on this host on one target layer's
 verify pass, one draft layer's decode step, the LM head and the acceptance at the same shapes,
 scaled to a round.
@@ -43,7 +42,6 @@ CFG = dict(vocab_size=128256, d_model=4096, n_layers=32, n_heads=32, n_kv_heads=
            max_seq_len=10240)
 DRAFT_LAYERS = 4
 BATCH, K, BLOCK = 64, 6, 16
-ATTN_ROUNDS = 8   # eager rounds after the timed ones, for per-launch attention events
 CTX_LO, CTX_HI = 2048, 8192
 
 
@@ -118,6 +116,41 @@ def attn_bytes(ctxs, t, h, hkv, d, bs):
 
 def accept_bytes(b, k, v, s_logit=2):
     return s_logit * b * v * (2 * k + 1) + 4 * b * v + 4 * b * k * 2 + 4 * b * (k + 2)
+
+
+def time_verify_attention(torch, fa, ops, sb, lens, reps=4):
+    """Per-launch duration of the verify attention as the timed rounds ran it: the last timed round's
+    32 verify-attention launches (every layer's pool, that round's block tables, and its k+1 query
+    positions per sequence, lens = the sequences' lengths before it) captured in one HIP graph, whose
+    replays are bracketed by events on the launching stream. Returns (seconds per launch, algorithmic
+    bytes per launch)."""
+    dev = sb.dev
+    seqs = sb.active()
+    tables = fa.paged.block_table([s.blocks_t for s in seqs], dev)
+    pos = torch.tensor([[n - 1 + t for t in range(K + 1)] for n in lens], dtype=torch.int32, device=dev)
+    h, d = CFG["n_heads"], CFG["d_model"] // CFG["n_heads"]
+    q = torch.randn(len(seqs), K + 1, h, d, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    layers = range(CFG["n_layers"])
+
+    def launches():
+        for layer in layers:
+            ops.paged_attention(q, sb.pool_t.layout(layer), tables, pos, d ** -0.5, out=out)
+
+    launches()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launches()
+    g.replay()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in ev:
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    sec = sum(a.elapsed_time(b) for a, b in ev) * 1e-3 / (reps * len(layers))
+    return sec, attn_bytes([n + K for n in lens], K + 1, h, CFG["n_kv_heads"], d, BLOCK)
 
 
 def run_rounds(torch, fa, ops, sb, n_rounds, timer=None):
@@ -400,7 +433,7 @@ def main():
 
     g = torch.Generator().manual_seed(args.seed)
     ctxs = torch.randint(CTX_LO, CTX_HI + 1, (BATCH,), generator=g).tolist()
-    rounds = args.warmup + args.steps + ATTN_ROUNDS
+    rounds = args.warmup + args.steps
     per_seq = [-(-(c + 2 + rounds * (K + 1) + K) // BLOCK) for c in ctxs]
     nblocks = sum(per_seq) + 8
     sb = fa.SpeculativeBatch(target, draft, nblocks, BLOCK, K,
@@ -424,7 +457,9 @@ def main():
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     committed = 0
+    last_lens = None
     for i in range(args.steps):
+        last_lens = [len(s.tokens) for s in sb.active()]
         committed += sb.round()
         if (i + 1) % 32 == 0:
             log(f"round {i + 1}/{args.steps}: {committed} tokens committed")
@@ -433,32 +468,9 @@ def main():
     proposed = sb.stats["proposed"] - acc0["proposed"]
     accepted = sb.stats["accepted"] - acc0["accepted"]
 
-    # verify-attention launch durations: a graph replay cannot bracket single launches with events, so
-    # the next ATTN_ROUNDS rounds of the same batch run eagerly with events on the launching stream
-    # around every verify-attention launch (the kernels are the graph's; the rocprofv3 summary of the
-    # graph rounds gives the same per-launch average)
-    events = []
-    ops.ATTN_EVENTS = events
-    ops.ATTN_EVENT_T = K + 1
-    ctx_log = []
-    sb.graphs = False
-    for i in range(ATTN_ROUNDS):
-        ctx_log.append([len(s.tokens) for s in sb.active()])
-        sb.round()
-    torch.cuda.synchronize()
-    sb.graphs = True
-    ops.ATTN_EVENTS = None
-
-    # each round's verify pass runs n_layers attention launches over contexts len(tokens) - 1 + k + 1
-    layers = CFG["n_layers"]
-    assert len(events) == layers * ATTN_ROUNDS, (len(events), layers * ATTN_ROUNDS)
-    durs = [a.elapsed_time(b) * 1e-3 for a, b in events]
-    bytes_total = 0
-    for lens in ctx_log:
-        bytes_total += layers * attn_bytes([n + K for n in lens], K + 1, CFG["n_heads"], CFG["n_kv_heads"], 128, BLOCK)
-    attn_avg = sum(durs) / len(durs)
-    attn_gbs = bytes_total / sum(durs) / 1e9
-    attn_traffic = bytes_total / len(durs)
+    attn_avg, attn_bytes_launch = time_verify_attention(torch, fa, ops, sb, last_lens)
+    attn_gbs = attn_bytes_launch / attn_avg / 1e9
+    attn_traffic = attn_bytes_launch
 
     value = committed / elapsed
 

@@ -167,7 +167,7 @@ struct RowStatsOut {
   int64_t nparts, ld;
 };
 
-template <int BM, int BN, int NS, int WGM = 2, int WGN = 2, bool STATS = false>
+template <int BM, int BN, int NS, int WGM = 2, int WGN = 2, bool STATS = false, bool PRIO = false>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uint16_t* __restrict__ X, int64_t ldx,
                                                             const uint16_t* __restrict__ W, int64_t ldw,
                                                             uint16_t* __restrict__ C, int64_t ldc,
@@ -273,10 +273,13 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
         const int r = wn * WN + 16 * j + l16, c = (4 * ks + g) ^ (r & 7);
         wf[j] = *reinterpret_cast<const bf16x8_t*>(st + XB + r * ROWB + 16 * c);
       }
+      // with 4 waves per SIMD, the wave holding its operands issues its MFMA block ahead of the others
+      if (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], xf[i], acc[i][j], 0, 0, 0);
+      if (PRIO) __builtin_amdgcn_s_setprio(0);
     }
   }
 
@@ -476,12 +479,15 @@ struct LdsCfg {
   int bm, bn, wgm, wgn;
 };
 
-LdsCfg lds_cfg(int64_t M, int64_t N, int splits) {
+LdsCfg lds_cfg(int64_t M, int64_t N, int splits, bool stats = false) {
   if (M <= 64) return LdsCfg{64, 64, 2, 2};
   auto pad = [&](int64_t bm) { return (M + bm - 1) / bm * bm - M; };
   if (pad(224) < pad(128) && pad(224) < pad(256)) {
     const int64_t t256 = ((M + 223) / 224) * ((N + 255) / 256) * splits;
-    return t256 >= 192 ? LdsCfg{224, 256, 2, 4} : LdsCfg{224, 128, 2, 4};
+    // 224 x 256 runs 16 waves (2 x 8, four per SIMD); with the statistics epilogue it keeps 8 waves
+    // (2 x 4), whose 64-column wave blocks halve the number of statistics records per row
+    if (t256 >= 192) return stats ? LdsCfg{224, 256, 2, 4} : LdsCfg{224, 256, 2, 8};
+    return LdsCfg{224, 128, 2, 4};
   }
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256) * splits;
   const int64_t t128 = ((M + 127) / 128) * ((N + 255) / 256) * splits;
@@ -494,13 +500,14 @@ template <bool STATS>
 void launch_lds(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c, int64_t ldc,
                 const uint16_t* r, int64_t ldr, int64_t M, int64_t N, int64_t K, int splits, float* part,
                 RowStatsOut rs, hipStream_t s) {
-  const LdsCfg cf = lds_cfg(M, N, splits);
+  const LdsCfg cf = lds_cfg(M, N, splits, STATS);
   const int tm = (int)((M + cf.bm - 1) / cf.bm), nt = tm * (int)((N + cf.bn - 1) / cf.bn);
   const dim3 grid((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits);
-#define FS_LDS_LAUNCH(BM_, BN_, NS_, WGM_, WGN_)                                                              \
-  gemm_bf16_lds_kernel<BM_, BN_, NS_, WGM_, WGN_, STATS><<<grid, 64 * WGM_ * WGN_, 0, s>>>(                  \
+#define FS_LDS_LAUNCH(BM_, BN_, NS_, WGM_, WGN_, ...)                                                         \
+  gemm_bf16_lds_kernel<BM_, BN_, NS_, WGM_, WGN_, STATS, ##__VA_ARGS__><<<grid, 64 * WGM_ * WGN_, 0, s>>>(     \
       a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part, rs)
   if (cf.bm == 64) FS_LDS_LAUNCH(64, 64, 4, 2, 2);
+  else if (cf.bm == 224 && cf.bn == 256 && cf.wgn == 8) FS_LDS_LAUNCH(224, 256, 2, 2, 8, true);
   else if (cf.bm == 224 && cf.bn == 256) FS_LDS_LAUNCH(224, 256, 2, 2, 4);
   else if (cf.bm == 224) FS_LDS_LAUNCH(224, 128, 3, 2, 4);
   else if (cf.bm == 256) FS_LDS_LAUNCH(256, 256, 2, 4, 2);
@@ -517,7 +524,7 @@ bool lds_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t K) {
 
 extern "C" int64_t fs_gemm_row_stats_parts(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64 || split_for(N, K) != 1) return 0;
-  const LdsCfg cf = lds_cfg(M, N, 1);
+  const LdsCfg cf = lds_cfg(M, N, 1, true);
   const int64_t wn = cf.bn / cf.wgn;
   return (N + wn - 1) / wn;
 }
