@@ -8,7 +8,7 @@ speculative_generate_batch.
 from .config import ModelConfig
 from .engine import Engine, Request
 from .kv import ContiguousKV, new_contiguous_cache
-from .model import ForgeModel, early_exit_draft
+from .model import ForgeModel, early_exit_draft, prefill_packed
 from .paged import BlockAllocator, OutOfBlocks, PagedKVPool
 from .parallel import SINGLE, TPContext
 from .sampling import generate, probs_from_logits, sample
@@ -17,4 +17,4 @@ from .speculative import SpeculativeBatch, speculative_generate, speculative_gen
 __all__ = ["speculative_generate", "verify_draft", "Engine", "Request", "BlockAllocator", "OutOfBlocks",
            "PagedKVPool", "ModelConfig", "ForgeModel", "TPContext", "SINGLE", "ContiguousKV",
            "new_contiguous_cache", "generate", "sample", "probs_from_logits", "early_exit_draft",
-           "SpeculativeBatch", "speculative_generate_batch"]
+           "SpeculativeBatch", "speculative_generate_batch", "prefill_packed"]

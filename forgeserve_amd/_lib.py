@@ -36,11 +36,15 @@ SIGNATURES = {
     "fs_abi_version": (c_i32, []),
     "fs_qkv_rope_write": (c_i32, [c_p, c_i64, c_i64, c_i32, c_i32, c_p, c_p, c_p, c_p, c_i32, c_p, c_i64, c_i32,
                                   ctypes.POINTER(KVLayout), c_p, c_i64, c_p]),
+    "fs_qkv_rope_write_varlen": (c_i32, [c_p, c_i64, c_i64, c_i32, c_p, c_p, c_i32, c_p, c_p, c_i32, c_p, c_i64, c_i32,
+                                         ctypes.POINTER(KVLayout), c_p, c_i64, c_p]),
     "fs_paged_kv_write": (c_i32, [c_p, c_p, c_i64, c_i64, c_i64, c_i32, c_i32, c_p, c_p, c_i64, c_i32,
                                   ctypes.POINTER(KVLayout), c_p]),
     "fs_paged_gather": (c_i32, [ctypes.POINTER(KVLayout), c_p, c_i64, c_i32, c_i32, c_p, c_p, c_p]),
     "fs_paged_attention": (c_i32, [c_p, c_i64, c_i64, c_i64, ctypes.POINTER(KVLayout), c_p, c_i64, c_i32, c_p,
                                    c_i32, c_i32, c_i32, c_f32, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p]),
+    "fs_paged_attention_varlen": (c_i32, [c_p, c_i64, c_i64, ctypes.POINTER(KVLayout), c_p, c_i64, c_i32, c_p, c_p,
+                                          c_i32, c_i32, c_i32, c_f32, c_p, c_i64, c_i64, c_p, c_i64, c_p]),
     "fs_paged_attention_workspace_size": (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
     "fs_gemm": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i32, c_p, c_i64,
                         c_p]),

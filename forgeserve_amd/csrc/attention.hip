@@ -53,6 +53,10 @@ struct AttnParams {
   int32_t direct;
   void* out;
   int64_t o_sb, o_st, o_sh;
+  // packed (varlen) rows: when set, row b's token t is token row_start[b] + t of q and out (strides
+  // q_st/q_sh, o_st/o_sh; q_sb and o_sb unused), and only tokens t < row_start[b+1] - row_start[b]
+  // exist: the others (positions -1) are neither read nor written
+  const int32_t* row_start;
 };
 
 // Reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48) with the gfx950
@@ -84,6 +88,16 @@ FS_DEVICE short4_t bf16_rne4(const float (&v)[4]) {
 }
 
 FS_DEVICE int64_t row_index(const AttnParams& P, int b, int t, int h) { return ((int64_t)b * P.T + t) * P.H + h; }
+
+FS_DEVICE bool token_exists(const AttnParams& P, int b, int t) {
+  return P.row_start == nullptr || t < P.row_start[b + 1] - P.row_start[b];
+}
+FS_DEVICE int64_t q_offset(const AttnParams& P, int b, int t) {
+  return P.row_start ? (int64_t)(P.row_start[b] + t) * P.q_st : (int64_t)b * P.q_sb + (int64_t)t * P.q_st;
+}
+FS_DEVICE int64_t o_offset(const AttnParams& P, int b, int t, int64_t o_sb, int64_t o_st) {
+  return P.row_start ? (int64_t)(P.row_start[b] + t) * o_st : (int64_t)b * o_sb + (int64_t)t * o_st;
+}
 
 // ------------------------------------------------------------------------------------------------
 // work plan: the (query tile, chunk) items that hold visible keys
@@ -288,10 +302,11 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int r = row0 + 16 * nt + l16;
-    const bool ok = (16 * nt + l16) < nrows;
+    const bool in_tile = (16 * nt + l16) < nrows;
+    const bool ok = in_tile && token_exists(P, b, r / P.G);
     const int t = ok ? r / P.G : 0;
     const int h = hkv * P.G + (ok ? r - (r / P.G) * P.G : 0);
-    const u16* qr = qbase + (int64_t)b * P.q_sb + (int64_t)t * P.q_st + (int64_t)h * P.q_sh;
+    const u16* qr = qbase + q_offset(P, b, t) + (int64_t)h * P.q_sh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (ok)
@@ -460,10 +475,10 @@ attn_unit_kernel(AttnParams P) {
     const int rr = row0 + r;
     const int t = rr / P.G, h = hkv * P.G + (rr - t * P.G);
     if (direct) {   // the same normalisation as attn_combine's
+      if (!token_exists(P, b, t)) continue;
       const float f[4] = {L > 0.f ? o[0] / L : 0.f, L > 0.f ? o[1] / L : 0.f, L > 0.f ? o[2] / L : 0.f,
                           L > 0.f ? o[3] / L : 0.f};
-      uint16_t* orow = reinterpret_cast<uint16_t*>(P.out) + (int64_t)b * P.o_sb + (int64_t)t * P.o_st +
-                       (int64_t)h * P.o_sh;
+      uint16_t* orow = reinterpret_cast<uint16_t*>(P.out) + o_offset(P, b, t, P.o_sb, P.o_st) + (int64_t)h * P.o_sh;
       *reinterpret_cast<short4_t*>(orow + 16 * mt + 4 * g) = bf16_rne4(f);
       continue;
     }
@@ -498,7 +513,7 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnParams P) {
   const int kend = min(kbeg + P.split, pos + 1);
   const int D = P.kv.head_dim, BS = P.kv.block_size;
   const int hkv = h / P.G;
-  const T_* qrow = reinterpret_cast<const T_*>(P.q) + (int64_t)b * P.q_sb + (int64_t)t * P.q_st + (int64_t)h * P.q_sh;
+  const T_* qrow = reinterpret_cast<const T_*>(P.q) + q_offset(P, b, t) + (int64_t)h * P.q_sh;
   for (int d = lane; d < D; d += 64) qs[d] = E::load(qrow, d);
   __syncthreads();
   const T_* kp = reinterpret_cast<const T_*>(P.kv.k);
@@ -576,8 +591,9 @@ __global__ void __launch_bounds__(64 * COMBINE_ROWS) attn_combine_kernel(AttnPar
   const int b = bt / P.T, t = bt - b * P.T;
   const int pos = P.pos[bt];
   if (P.direct && (pos < P.split || P.nsplit == 1)) return;   // written by its chunk's workgroup
+  if (!token_exists(P, b, t)) return;
   const int D = P.kv.head_dim;
-  T_* orow = reinterpret_cast<T_*>(out) + (int64_t)b * o_sb + (int64_t)t * o_st + (int64_t)h * o_sh;
+  T_* orow = reinterpret_cast<T_*>(out) + o_offset(P, b, t, o_sb, o_st) + (int64_t)h * o_sh;
   if (pos < 0) {
     for (int d = lane; d < D; d += 64) E::store(orow, d, 0.f);
     return;
@@ -679,11 +695,12 @@ extern "C" int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32
   return WS_HEADER + list + rows * ns * (head_dim + 2) * (int64_t)sizeof(float) + 256;
 }
 
-extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
-                                  const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
-                                  const int32_t* positions, int32_t B, int32_t T, int32_t n_heads, float scale,
-                                  void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, void* workspace,
-                                  int64_t workspace_bytes, void* stream) {
+namespace {
+int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
+                    const int32_t* block_tables, int64_t table_stride, int32_t max_blocks, const int32_t* positions,
+                    const int32_t* row_start, int32_t B, int32_t T, int32_t n_heads, float scale, void* out,
+                    int64_t o_sb, int64_t o_st, int64_t o_sh, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
   FS_CHECK_ARG(kv != nullptr && kv->k && kv->v, "paged_attention: null pool");
   FS_CHECK_ARG(q && block_tables && positions && out && workspace, "paged_attention: null pointer");
   FS_CHECK_ARG(B > 0 && T > 0, "paged_attention: B %d T %d", B, T);
@@ -732,6 +749,7 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
   P.o_sb = o_sb;
   P.o_st = o_st;
   P.o_sh = o_sh;
+  P.row_start = row_start;
 
   hipStream_t st = fs::as_stream(stream);
   if (mfma) {
@@ -766,4 +784,24 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
     default: attn_combine_kernel<FS_F16><<<cgrid, 64 * COMBINE_ROWS, 0, st>>>(P, out, o_sb, o_st, o_sh); break;
   }
   return fs::launch_status("paged_attention_combine");
+}
+}  // namespace
+
+extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
+                                  const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                                  const int32_t* positions, int32_t B, int32_t T, int32_t n_heads, float scale,
+                                  void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  return paged_attention(q, q_sb, q_st, q_sh, kv, block_tables, table_stride, max_blocks, positions, nullptr, B, T,
+                         n_heads, scale, out, o_sb, o_st, o_sh, workspace, workspace_bytes, stream);
+}
+
+extern "C" int fs_paged_attention_varlen(const void* q, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
+                                         const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                                         const int32_t* positions, const int32_t* cu_seqlens, int32_t S,
+                                         int32_t T, int32_t n_heads, float scale, void* out, int64_t o_st,
+                                         int64_t o_sh, void* workspace, int64_t workspace_bytes, void* stream) {
+  FS_CHECK_ARG(cu_seqlens, "paged_attention_varlen: null cu_seqlens");
+  return paged_attention(q, 0, q_st, q_sh, kv, block_tables, table_stride, max_blocks, positions, cu_seqlens, S, T,
+                         n_heads, scale, out, 0, o_st, o_sh, workspace, workspace_bytes, stream);
 }

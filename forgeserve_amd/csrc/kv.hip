@@ -59,13 +59,16 @@ FS_DEVICE u32x4_t pack8(const float (&v)[8]) {
 template <int DT>
 __global__ void __launch_bounds__(256) qkv_rope_write_vec_kernel(
     const uint16_t* __restrict__ qkv, int64_t qkv_stride, int32_t T, int32_t H, const int32_t* __restrict__ positions,
-    const int32_t* __restrict__ slots, const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
+    const int32_t* __restrict__ slots, const int32_t* __restrict__ token_row, int32_t n_rows,
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
     int32_t rope_len, const int32_t* __restrict__ table, int64_t table_stride, int32_t max_blocks, fs_kv_layout kv,
     uint16_t* __restrict__ q_out, int64_t q_stride) {
   const int64_t m = blockIdx.x;
-  const int b = (int)(m / T);
+  int b = token_row ? token_row[m] : (int)(m / T);   // the token's table row
+  const bool row_ok = token_row == nullptr || (b >= 0 && b < n_rows);
+  b = row_ok ? b : 0;
   const int D = kv.head_dim, half = D / 2, Hkv = kv.n_kv_heads;
-  const int pos = positions[m];
+  const int pos = row_ok ? positions[m] : -1;
   const bool rot_ok = pos >= 0 && pos < rope_len;
   int64_t blk = 0;
   int slot = 0;
@@ -126,16 +129,19 @@ __global__ void __launch_bounds__(256) qkv_rope_write_vec_kernel(
 template <int DT>
 __global__ void __launch_bounds__(256) qkv_rope_write_kernel(
     const typename Elem<DT>::T* __restrict__ qkv, int64_t qkv_stride, int32_t T, int32_t H,
-    const int32_t* __restrict__ positions, const int32_t* __restrict__ slots, const float* __restrict__ rope_cos,
-    const float* __restrict__ rope_sin, int32_t rope_len, const int32_t* __restrict__ table,
+    const int32_t* __restrict__ positions, const int32_t* __restrict__ slots, const int32_t* __restrict__ token_row,
+    int32_t n_rows, const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, int32_t rope_len,
+    const int32_t* __restrict__ table,
     int64_t table_stride, int32_t max_blocks, fs_kv_layout kv, typename Elem<DT>::T* __restrict__ q_out,
     int64_t q_stride) {
   typedef Elem<DT> E;
   typedef typename E::T T_;
   const int64_t m = blockIdx.x;
-  const int b = (int)(m / T);
+  int b = token_row ? token_row[m] : (int)(m / T);   // the token's table row
+  const bool row_ok = token_row == nullptr || (b >= 0 && b < n_rows);
+  b = row_ok ? b : 0;
   const int D = kv.head_dim, half = D / 2, Hkv = kv.n_kv_heads;
-  const int pos = positions[m];
+  const int pos = row_ok ? positions[m] : -1;
   const bool rot_ok = pos >= 0 && pos < rope_len;
   int64_t blk = 0;
   int slot = 0;
@@ -241,12 +247,12 @@ int check_layout(const fs_kv_layout* kv) {
 
 }  // namespace
 
-extern "C" int fs_qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_t T, int32_t n_heads,
-                                 const int32_t* positions, const int32_t* slots, const float* rope_cos,
-                                 const float* rope_sin,
-                                 int32_t rope_len, const int32_t* block_tables, int64_t table_stride,
-                                 int32_t max_blocks, const fs_kv_layout* kv, void* q_out, int64_t q_stride,
-                                 void* stream) {
+namespace {
+int qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_t T, int32_t n_heads,
+                   const int32_t* positions, const int32_t* slots, const int32_t* token_row, int32_t n_rows,
+                   const float* rope_cos,
+                   const float* rope_sin, int32_t rope_len, const int32_t* block_tables, int64_t table_stride,
+                   int32_t max_blocks, const fs_kv_layout* kv, void* q_out, int64_t q_stride, void* stream) {
   if (int e = check_layout(kv)) return e;
   FS_CHECK_ARG(qkv && positions && rope_cos && rope_sin && block_tables && q_out, "qkv_rope_write: null pointer");
   FS_CHECK_ARG(T > 0 && n_tokens >= 0 && n_tokens % T == 0, "qkv_rope_write: n_tokens %lld not a multiple of T %d",
@@ -265,17 +271,18 @@ extern "C" int fs_qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_
       al16(qkv) && al16(q_out) && al16(kv->k) && al16(rope_cos) && al16(rope_sin)) {
     if (kv->dtype == FS_BF16)
       qkv_rope_write_vec_kernel<FS_BF16><<<grid, 256, 0, s>>>((const uint16_t*)qkv, qkv_stride, T, n_heads, positions,
-                                                              slots, rope_cos, rope_sin, rope_len, block_tables,
+                                                              slots, token_row, n_rows, rope_cos, rope_sin, rope_len, block_tables,
                                                               table_stride, max_blocks, *kv, (uint16_t*)q_out, q_stride);
     else
       qkv_rope_write_vec_kernel<FS_F16><<<grid, 256, 0, s>>>((const uint16_t*)qkv, qkv_stride, T, n_heads, positions,
-                                                             slots, rope_cos, rope_sin, rope_len, block_tables,
+                                                             slots, token_row, n_rows, rope_cos, rope_sin, rope_len, block_tables,
                                                              table_stride, max_blocks, *kv, (uint16_t*)q_out, q_stride);
     return fs::launch_status("qkv_rope_write");
   }
 #define FS_LAUNCH(DT)                                                                                        \
   qkv_rope_write_kernel<DT><<<grid, 256, 0, s>>>(                                                          \
-      (const typename Elem<DT>::T*)qkv, qkv_stride, T, n_heads, positions, slots, rope_cos, rope_sin, rope_len, \
+      (const typename Elem<DT>::T*)qkv, qkv_stride, T, n_heads, positions, slots, token_row, n_rows, rope_cos,    \
+      rope_sin, rope_len, \
       block_tables, table_stride, max_blocks, *kv, (typename Elem<DT>::T*)q_out, q_stride)
   switch (kv->dtype) {
     case FS_F32: FS_LAUNCH(FS_F32); break;
@@ -284,6 +291,27 @@ extern "C" int fs_qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_
   }
 #undef FS_LAUNCH
   return fs::launch_status("qkv_rope_write");
+}
+}  // namespace
+
+extern "C" int fs_qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_t T, int32_t n_heads,
+                                 const int32_t* positions, const int32_t* slots, const float* rope_cos,
+                                 const float* rope_sin, int32_t rope_len, const int32_t* block_tables,
+                                 int64_t table_stride, int32_t max_blocks, const fs_kv_layout* kv, void* q_out,
+                                 int64_t q_stride, void* stream) {
+  return qkv_rope_write(qkv, qkv_stride, n_tokens, T, n_heads, positions, slots, nullptr, 0, rope_cos, rope_sin,
+                        rope_len, block_tables, table_stride, max_blocks, kv, q_out, q_stride, stream);
+}
+
+extern "C" int fs_qkv_rope_write_varlen(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_t n_heads,
+                                        const int32_t* positions, const int32_t* token_row, int32_t n_rows,
+                                        const float* rope_cos, const float* rope_sin, int32_t rope_len,
+                                        const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                                        const fs_kv_layout* kv, void* q_out, int64_t q_stride, void* stream) {
+  FS_CHECK_ARG(token_row && n_rows > 0, "qkv_rope_write_varlen: token_row / n_rows %d", n_rows);
+  return qkv_rope_write(qkv, qkv_stride, n_tokens, 1, n_heads, positions, nullptr, token_row, n_rows, rope_cos,
+                        rope_sin,
+                        rope_len, block_tables, table_stride, max_blocks, kv, q_out, q_stride, stream);
 }
 
 extern "C" int fs_paged_kv_write(const void* k_new, const void* v_new, int64_t s_b, int64_t s_h, int64_t s_t,

@@ -98,6 +98,13 @@ class Attention(nn.Module):
     def attend(self, h: torch.Tensor, b: int, t: int, pos32: torch.Tensor, view, rope) -> torch.Tensor:
         """h (B*T, d) normed input -> attention output (B*T, n_heads*head_dim), before wo."""
         qkv = ops.gemm(h, self.qkv_weight())
+        if getattr(view, "packed", False):   # packed prefill: rows are the step's tokens, no padding
+            st = view.step
+            q = ops.qkv_rope_write_varlen(qkv, st.pos_tok, st.token_row, self.nh, rope[0], rope[1], st.tables,
+                                          view.layout)
+            o = ops.paged_attention_varlen(q.view(-1, self.nh, self.hd), view.layout, st.tables, st.pos_pad, st.cu,
+                                           1.0 / math.sqrt(self.hd))
+            return o.view(-1, self.nh * self.hd)
         layout, tables, slots, mask = view.prepare(b, t, self.nkv, self.hd, h.dtype, h.device, pos32)
         q = ops.qkv_rope_write(qkv, pos32.reshape(-1), t, self.nh, rope[0], rope[1], tables, layout, slots=slots)
         o = ops.paged_attention(q.view(b, t, self.nh, self.hd), layout, tables, mask, 1.0 / math.sqrt(self.hd))
@@ -241,6 +248,33 @@ class ForgeModel(nn.Module):
                 return self.head(x, head_stats, out=out)
             return self.head(x, head_stats).view(b, 1, -1)
         return self.head(x, head_stats).view(b, t, -1)
+
+
+@torch.no_grad()
+def prefill_packed(model: ForgeModel, pool, tokens: List[List[int]], block_lists: List[List[int]],
+                   starts: Optional[List[int]] = None) -> torch.Tensor:
+    """Run several sequences' new tokens through `model` in one packed forward (no padding rows),
+    writing their keys/values into `pool` (a PagedKVPool of the model's layers) through block_lists.
+    Sequence s's tokens sit at positions starts[s] .. (default 0 ..). Returns the logits of each
+    sequence's last token, (S, vocab). Each sequence's cache contents and logits are bit-identical to
+    prefilling it alone (model(tokens, positions, pool.views(...)), engine.py:80-95)."""
+    from .paged import PackedPrefill
+
+    if len(pool.k) != model.cfg.n_layers:
+        raise ValueError(f"pool has {len(pool.k)} layers, the model {model.cfg.n_layers}")
+    starts = [0] * len(tokens) if starts is None else list(starts)
+    step = PackedPrefill(pool, block_lists, starts, [len(t) for t in tokens])
+    if step.max_position >= model.cfg.max_seq_len:
+        raise ValueError(f"position {step.max_position} exceeds max_seq_len {model.cfg.max_seq_len}")
+    flat = torch.tensor([x for t in tokens for x in t], dtype=torch.int64)
+    if flat.numel() and (int(flat.min()) < 0 or int(flat.max()) >= model.cfg.vocab_size):
+        raise ValueError("token ids must be in [0, vocab_size)")
+    ids = to_device(flat, model.device)
+    rope = model._rope()
+    x = ops.embedding(ids, model.tok_emb.weight)
+    for layer, view in zip(model.layers, step.views()):
+        x = layer.step(x, 1, step.n_tokens, None, view, rope)
+    return model.head(x.index_select(0, step.last_rows))
 
 
 def early_exit_draft(target: ForgeModel, n_layers: int) -> ForgeModel:

@@ -217,6 +217,31 @@ def qkv_rope_write(qkv: torch.Tensor, positions: torch.Tensor, T: int, n_heads: 
     return q_out
 
 
+def qkv_rope_write_varlen(qkv: torch.Tensor, positions: torch.Tensor, token_row: torch.Tensor, n_heads: int,
+                          rope_cos: torch.Tensor, rope_sin: torch.Tensor, tables: torch.Tensor, layout: KVLayout,
+                          q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """qkv_rope_write for packed sequences: token m writes through table row token_row[m].
+
+    qkv: (n_tokens, (n_heads + 2*n_kv_heads) * head_dim); positions, token_row: int32 (n_tokens,);
+    tables: int32 (rows, max_blocks). Returns the rotated queries (n_tokens, n_heads * head_dim)."""
+    require_device(qkv, positions, token_row, tables)
+    m, ld = _rows(qkv)
+    d = layout.head_dim
+    if positions.dtype != I32 or token_row.dtype != I32 or tables.dtype != I32:
+        raise ValueError("qkv_rope_write_varlen: positions, token_row and tables must be int32")
+    if positions.numel() != m or token_row.numel() != m:
+        raise ValueError("qkv_rope_write_varlen: one position and one table row per token")
+    if q_out is None:
+        q_out = torch.empty((m, n_heads * d), dtype=qkv.dtype, device=qkv.device)
+    _, ldq = _rows(q_out)
+    check(_lib.load().fs_qkv_rope_write_varlen(ptr(qkv), ld, m, n_heads, ptr(positions.contiguous()),
+                                               ptr(token_row.contiguous()), tables.shape[0], ptr(rope_cos),
+                                               ptr(rope_sin), rope_cos.shape[0], ptr(tables), tables.stride(0),
+                                               tables.shape[1], layout, ptr(q_out), ldq, stream_ptr()),
+          "qkv_rope_write_varlen")
+    return q_out
+
+
 def paged_kv_write(k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor, tables: torch.Tensor,
                    layout: KVLayout) -> None:
     """Scatter k, v (B, n_kv_heads, T, head_dim) to the pool slots of positions (B, T) (paged.py:74-78)."""
@@ -270,6 +295,33 @@ def paged_attention(q: torch.Tensor, layout: KVLayout, tables: torch.Tensor, pos
     if timing:
         ev[1].record()
         ATTN_EVENTS.append(ev)
+    return out
+
+
+def paged_attention_varlen(q: torch.Tensor, layout: KVLayout, tables: torch.Tensor, positions: torch.Tensor,
+                           cu_seqlens: torch.Tensor, scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """paged_attention over packed sequences: q (n_tokens, n_heads, head_dim); sequence s owns tokens
+    cu_seqlens[s] .. cu_seqlens[s+1]-1 (int32 (S+1,), on the device; the caller guarantees the bounds:
+    cu_seqlens[S] <= n_tokens and no sequence longer than T); positions int32 (S, T), -1 past a
+    sequence's tokens; tables int32 (S, max_blocks). Returns out (n_tokens, n_heads, head_dim)."""
+    require_device(q, tables, positions, cu_seqlens)
+    n, h, d = q.shape
+    if q.stride(2) != 1:
+        raise ValueError("paged_attention_varlen: head_dim must be contiguous")
+    s, t = positions.shape
+    if (positions.dtype != I32 or tables.dtype != I32 or cu_seqlens.dtype != I32 or cu_seqlens.numel() != s + 1
+            or tables.shape[0] != s):
+        raise ValueError("paged_attention_varlen: positions (S, T), tables (S, .) and cu_seqlens (S+1,) int32")
+    positions = positions.contiguous()
+    if out is None:
+        out = torch.empty((n, h, d), dtype=q.dtype, device=q.device)
+    nb = tables.shape[1]
+    lib = _lib.load()
+    ws = _persistent_ws("attention", lib.fs_paged_attention_workspace_size(s, t, h, d, nb, layout.block_size), q.device)
+    check(lib.fs_paged_attention_varlen(ptr(q), q.stride(0), q.stride(1), layout, ptr(tables), tables.stride(0), nb,
+                                        ptr(positions), ptr(cu_seqlens.contiguous()), s, t, h, float(scale), ptr(out),
+                                        out.stride(0), out.stride(1), ptr(ws), ws.numel(), stream_ptr()),
+          "paged_attention_varlen")
     return out
 
 

@@ -196,3 +196,57 @@ class PagedLayerView:
 
     def commit(self, t: int) -> None:
         pass
+
+
+class PackedPrefill:
+    """One prefill step over a pool for several sequences packed back to back, with no padding rows:
+    sequence s has lens[s] new tokens at positions starts[s] .. starts[s] + lens[s] - 1, written through
+    its block list block_lists[s] (which must cover them). The reference prefills one prompt per step
+    with T = its length (engine.py:80-95 through paged.py:71-82); each token's keys, values and
+    attention output here are bit-identical to that (the kernels' per-token arithmetic does not depend
+    on the other tokens of the step)."""
+
+    packed = True
+
+    def __init__(self, pool: "PagedKVPool", block_lists: List[List[int]], starts: List[int], lens: List[int]):
+        if not lens or len(block_lists) != len(lens) or len(starts) != len(lens):
+            raise ValueError("packed prefill: one block list, start and length per sequence")
+        bs = pool.block_size
+        for blocks, st, n in zip(block_lists, starts, lens):
+            if n <= 0 or st < 0:
+                raise ValueError(f"packed prefill: length {n} at start {st}")
+            if len(blocks) * bs < st + n:
+                raise ValueError(f"packed prefill: {len(blocks)} blocks of {bs} do not hold positions < {st + n}")
+            if any(not 0 <= b_ < pool.num_blocks for b_ in blocks):
+                raise IndexError(f"block table entries must be in [0, {pool.num_blocks})")
+        self.pool = pool
+        self.n_seqs, self.n_tokens, self.T = len(lens), int(sum(lens)), int(max(lens))
+        ln = np.asarray(lens, dtype=np.int64)
+        cu = np.zeros(len(lens) + 1, dtype=np.int32)
+        cu[1:] = np.cumsum(ln)
+        pos_tok = np.concatenate([np.arange(st, st + n, dtype=np.int32) for st, n in zip(starts, lens)])
+        token_row = np.repeat(np.arange(len(lens), dtype=np.int32), ln)
+        pos_pad = np.full((len(lens), self.T), -1, dtype=np.int32)
+        for r, (st, n) in enumerate(zip(starts, lens)):
+            pos_pad[r, :n] = np.arange(st, st + n, dtype=np.int32)
+        dev = pool.device
+        self.max_position = int(max(st + n for st, n in zip(starts, lens))) - 1
+        self.tables = block_table(block_lists, dev)
+        self.cu = to_device(torch.from_numpy(cu), dev)
+        self.pos_tok = to_device(torch.from_numpy(pos_tok), dev)
+        self.token_row = to_device(torch.from_numpy(token_row), dev)
+        self.pos_pad = to_device(torch.from_numpy(pos_pad), dev)
+        self.last_rows = to_device(torch.from_numpy(cu[1:].astype(np.int64) - 1), dev)
+
+    def views(self) -> List["PackedLayerView"]:
+        return [PackedLayerView(self, layer) for layer in range(len(self.pool.k))]
+
+
+class PackedLayerView:
+    """What one attention layer sees during a packed prefill step."""
+
+    packed = True
+
+    def __init__(self, step: PackedPrefill, layer: int):
+        self.step, self.layer = step, layer
+        self.layout = step.pool.layout(layer)

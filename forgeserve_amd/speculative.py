@@ -25,6 +25,7 @@ import torch
 from . import ops
 from ._lib import to_device
 from .kv import new_contiguous_cache
+from .model import prefill_packed
 from .paged import BlockList, OutOfBlocks, PagedKVPool
 from .sampling import exp_noise, probs_from_logits
 
@@ -415,6 +416,35 @@ class SpeculativeBatch:
         self.seqs.append(seq)
         return seq
 
+    def add_many(self, prompts: Sequence[Sequence[int]], max_new_tokens, temperature=0.0, eos_id=None,
+                 max_prefill_tokens: int = 32768) -> List[_Seq]:
+        """Add several sequences and prefill their prompts (all but each last token) packed: a few
+        forwards of up to max_prefill_tokens tokens each through both models, instead of one forward per
+        prompt. max_new_tokens, temperature, eos_id: one value, or one per prompt. The caches end up
+        exactly as add() would leave them."""
+        n = len(prompts)
+        per = lambda x: list(x) if isinstance(x, (list, tuple)) else [x] * n
+        max_new, temps, eos = per(max_new_tokens), per(temperature), per(eos_id)
+        for p in prompts:
+            if not 0 < len(p) < self.limit:
+                raise ValueError(f"prompt length must be in 1..{self.limit - 1}")
+        seqs = [_Seq(p, m, t, e) for p, m, t, e in zip(prompts, max_new, temps, eos)]
+        for s in seqs:
+            self._grow(s, len(s.tokens))
+        todo = [s for s in seqs if len(s.tokens) > 1]
+        i = 0
+        while i < len(todo):
+            chunk, total = [], 0
+            while i < len(todo) and (not chunk or total + len(todo[i].tokens) - 1 <= max_prefill_tokens):
+                chunk.append(todo[i])
+                total += len(todo[i].tokens) - 1
+                i += 1
+            toks = [s.tokens[:-1] for s in chunk]
+            prefill_packed(self.target, self.pool_t, toks, [s.blocks_t for s in chunk])
+            prefill_packed(self.draft, self.pool_d, toks, [s.blocks_d for s in chunk])
+        self.seqs.extend(seqs)
+        return seqs
+
     def active(self) -> List[_Seq]:
         return [s for s in self.seqs if not s.done]
 
@@ -475,6 +505,6 @@ def speculative_generate_batch(target, draft, prompts: List[List[int]], max_new_
         limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
         num_blocks = sum(-(-min(len(p) + m + k + 1, limit + k) // block_size) + 1 for p, m in zip(prompts, max_new))
     sb = SpeculativeBatch(target, draft, num_blocks, block_size, k, generator=generator)
-    seqs = [sb.add(p, m, t) for p, m, t in zip(prompts, max_new, temps)]
+    seqs = sb.add_many(prompts, max_new, temps)
     sb.run()
     return [s.tokens[s.start:] for s in seqs], sb.stats

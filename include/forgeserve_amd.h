@@ -77,6 +77,17 @@ int fs_paged_kv_write(const void* k_new, const void* v_new, int64_t s_b, int64_t
                       int32_t B, int32_t T, const int32_t* positions, const int32_t* block_tables,
                       int64_t table_stride, int32_t max_blocks, const fs_kv_layout* kv, void* stream);
 
+/* fs_qkv_rope_write for packed prefill (varlen): n_tokens rows of several sequences back to back, with
+ * no padding; token m uses table row token_row[m] (0 <= token_row[m] < n_rows: other tokens are
+ * neither rotated nor written, and their q rows are zeros) at positions[m]. Replaces the same lines
+ * as fs_qkv_rope_write for a prefill of several prompts at once (engine.py:80-95 prefills one prompt
+ * of T = prompt length per step through paged.py:71-82). */
+int fs_qkv_rope_write_varlen(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_t n_heads,
+                             const int32_t* positions, const int32_t* token_row, int32_t n_rows,
+                             const float* rope_cos, const float* rope_sin, int32_t rope_len,
+                             const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                             const fs_kv_layout* kv, void* q_out, int64_t q_stride, void* stream);
+
 /* Gather every block of every row's table in table order: paged.py:80-81.
  * k_out, v_out: contiguous [B, n_kv_heads, max_blocks*block_size, head_dim]. */
 int fs_paged_gather(const fs_kv_layout* kv, const int32_t* block_tables, int64_t table_stride, int32_t B,
@@ -97,6 +108,19 @@ int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, 
                        const int32_t* positions, int32_t B, int32_t T, int32_t n_heads, float scale,
                        void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, void* workspace,
                        int64_t workspace_bytes, void* stream);
+
+/* fs_paged_attention over packed sequences (varlen prefill): sequence s owns tokens
+ * cu_seqlens[s] .. cu_seqlens[s+1]-1 of q and out (element (token, h, d) at base + token*s_t + h*s_h + d),
+ * at most T of them; positions is [S, T], its first cu_seqlens[s+1]-cu_seqlens[s] entries of row s
+ * the tokens' positions and the rest -1. Rows of q/out past the sequences' tokens are not touched.
+ * Each query's result is bit-identical to fs_paged_attention's for the same query, keys and position.
+ * Replaces model.py:70-76 over paged.py:80-81 for a prefill (T = prompt length, engine.py:80-95) of
+ * several prompts at once. workspace: fs_paged_attention_workspace_size(S, T, ...). */
+int fs_paged_attention_varlen(const void* q, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
+                              const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                              const int32_t* positions, const int32_t* cu_seqlens, int32_t S, int32_t T,
+                              int32_t n_heads, float scale, void* out, int64_t o_st, int64_t o_sh, void* workspace,
+                              int64_t workspace_bytes, void* stream);
 
 int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32_t n_heads, int32_t head_dim,
                                           int32_t max_blocks, int32_t block_size);

@@ -3,6 +3,7 @@ within the stated tolerance for floating point). Every case prints its name befo
 
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -276,6 +277,77 @@ def test_attention_long_verify_equals_decode_bitwise():
         one = ops.paged_attention(q[:, i: i + 1].to(DEV), lay, tab, pos[:, i: i + 1].int().to(DEV),
                                   1.0 / math.sqrt(128))
         assert torch.equal(one[:, 0], full[:, i]), i
+
+
+def _packed(xs, lens, cu):
+    """Dense (S, T, ...) rows -> packed (sum(lens), ...) tokens."""
+    return torch.cat([xs[i, :n] for i, n in enumerate(lens)], 0)
+
+
+@pytest.mark.parametrize("dtype,d,bs,lens,starts", [
+    (torch.bfloat16, 128, 16, [37, 1, 300, 64, 8300], [0, 5, 100, 7, 0]),   # the last one spans two key chunks
+    (torch.bfloat16, 64, 16, [15, 200, 3], [0, 0, 61]),
+    (torch.float32, 32, 4, [9, 600, 1, 40], [3, 0, 0, 500]),
+])
+def test_attention_varlen_equals_dense(dtype, d, bs, lens, starts):
+    """Packed sequences (no padding rows) give every token the bits the dense (S, T) call gives it, and
+    leave the rows of out past the sequences' tokens untouched."""
+    case("attention varlen", dtype, d, bs, lens)
+    h, hkv = 8, 2
+    ctx = [st + n for st, n in zip(starts, lens)]
+    nblocks = sum(-(-c // bs) for c in ctx) + 3
+    q, k, v, tables, _ = _paged_case(len(lens), max(lens), h, hkv, d, bs, ctx, nblocks, dtype, d + len(lens))
+    pos = torch.full((len(lens), max(lens)), -1, dtype=torch.long)
+    for i, (st, n) in enumerate(zip(starts, lens)):
+        pos[i, :n] = torch.arange(st, st + n)
+    dense, pool = _run_attention(q, k, v, tables, pos, dtype, bs)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    n_tok = int(cu[-1])
+    qp = torch.cat([_packed(q, lens, cu), torch.randn(3, h, d).to(dtype)], 0).to(DEV)   # 3 rows past the tokens
+    out = torch.full((n_tok + 3, h, d), 7.0, dtype=dtype, device=DEV)
+    ops.paged_attention_varlen(qp, pool.layout(0), tables.int().to(DEV), pos.int().to(DEV), cu.to(DEV),
+                               1.0 / math.sqrt(d), out=out)
+    assert torch.equal(out[:n_tok], _packed(dense, lens, cu))
+    assert bool((out[n_tok:] == 7.0).all())
+
+
+@pytest.mark.parametrize("dtype,d,bs", [(torch.bfloat16, 128, 16), (torch.float32, 32, 4)])
+def test_qkv_rope_write_varlen_equals_dense(dtype, d, bs):
+    """The packed rotary + KV write stores every token where the dense (S, T) call stores it, returns
+    the same rotated queries, and neither writes nor rotates a token whose table row is out of range."""
+    case("qkv_rope_write varlen", dtype, d, bs)
+    from forgeserve_amd import PagedKVPool, ModelConfig
+    h, hkv = 8, 2
+    lens, starts = [5, 1, 30, 12], [0, 9, 3, 40]
+    cfg = ModelConfig(vocab_size=10, d_model=h * d, n_layers=1, n_heads=h, n_kv_heads=hkv, max_seq_len=128)
+    s = orc.Shape.of(cfg)
+    cos, sin = orc.rope_tables(s)
+    g = torch.Generator().manual_seed(8)
+    nb = -(-max(st + n for st, n in zip(starts, lens)) // bs)
+    perm = torch.randperm(len(lens) * nb, generator=g)
+    tables = perm.reshape(len(lens), nb).int()
+    t = max(lens)
+    qkv = torch.randn(len(lens), t, (h + 2 * hkv) * d, generator=g).to(dtype)
+    pos = torch.full((len(lens), t), -1, dtype=torch.int32)
+    for i, (st, n) in enumerate(zip(starts, lens)):
+        pos[i, :n] = torch.arange(st, st + n, dtype=torch.int32)
+    pos[2, 7] = -1                   # this token gets an out-of-range table row below: it must not be written
+    dense_pool = PagedKVPool(cfg, len(lens) * nb, bs, dtype=dtype, device=DEV)
+    q_dense = ops.qkv_rope_write(qkv.reshape(-1, qkv.shape[-1]).to(DEV), pos.reshape(-1).to(DEV), t, h, cos.to(DEV),
+                                 sin.to(DEV), tables.to(DEV), dense_pool.layout(0)).view(len(lens), t, -1)
+    cu = [0] + list(np.cumsum(lens))
+    rows = torch.cat([torch.full((n,), i, dtype=torch.int32) for i, n in enumerate(lens)])
+    rows[cu[2] + 7] = len(lens)       # out of range
+    ppos = torch.cat([torch.arange(st, st + n, dtype=torch.int32) for st, n in zip(starts, lens)])
+    pool = PagedKVPool(cfg, len(lens) * nb, bs, dtype=dtype, device=DEV)
+    q = ops.qkv_rope_write_varlen(_packed(qkv, lens, cu).to(DEV), ppos.to(DEV), rows.to(DEV), h, cos.to(DEV),
+                                  sin.to(DEV), tables.to(DEV), pool.layout(0))
+    assert torch.equal(pool.k_store, dense_pool.k_store) and torch.equal(pool.v_store, dense_pool.v_store)
+    qd = _packed(q_dense, lens, cu)
+    keep = torch.ones(q.shape[0], dtype=torch.bool)
+    keep[cu[2] + 7] = False
+    assert torch.equal(q[keep.to(DEV)], qd[keep.to(DEV)])
+    assert torch.count_nonzero(q[cu[2] + 7]) == 0
 
 
 def test_attention_c3_shape():

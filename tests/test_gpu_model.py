@@ -227,6 +227,39 @@ def test_bf16_batch_perfect_draft_accepts_everything(bf_target):
     assert got == [fa.generate(bf_target, torch.tensor([p]), 25)[0].tolist()[len(p):] for p in prompts]
 
 
+@pytest.mark.parametrize("which", ["bf16", "f32"])
+def test_packed_prefill_equals_per_sequence_prefill(which, bf_target, small):
+    """Several prompts prefilled in one packed forward (no padding rows) leave the pool holding exactly
+    what one-prompt-per-step prefills (engine.py:80-95) leave, and give the same last-token logits;
+    one prompt starts after a cached prefix."""
+    case("packed prefill", which)
+    model = bf_target if which == "bf16" else small
+    cfg, bs = model.cfg, 16 if which == "bf16" else 4
+    g = torch.Generator().manual_seed(31)
+    prompts = [torch.randint(0, cfg.vocab_size, (int(n),), generator=g).tolist() for n in (23, 1, 40, 9)]
+    prefix = torch.randint(0, cfg.vocab_size, (11,), generator=g).tolist()
+
+    def pools():
+        pool = fa.PagedKVPool(cfg, 64, bs, dtype=model.dtype, device="cuda")
+        lists = [pool.allocator.allocate(pool.blocks_for(len(p) + (11 if i == 2 else 0))) for i, p in enumerate(prompts)]
+        # sequence 2 first caches an 11-token prefix, then prefills its prompt after it
+        pos = torch.arange(11)[None]
+        model(torch.tensor([prefix]), pos, pool.views(torch.tensor([lists[2]]), pos))
+        return pool, lists
+
+    alone_pool, lists = pools()
+    alone = []
+    for i, p in enumerate(prompts):
+        st = 11 if i == 2 else 0
+        pos = torch.arange(st, st + len(p))[None]
+        alone.append(model(torch.tensor([p]), pos, alone_pool.views(torch.tensor([lists[i]]), pos))[0, -1])
+    packed_pool, lists2 = pools()
+    assert lists2 == lists
+    got = fa.prefill_packed(model, packed_pool, prompts, lists, starts=[0, 0, 11, 0])
+    assert torch.equal(got, torch.stack(alone))
+    assert torch.equal(packed_pool.k_store, alone_pool.k_store) and torch.equal(packed_pool.v_store, alone_pool.v_store)
+
+
 def test_graph_rounds_equal_eager_rounds(bf_target):
     """Rounds replayed from captured HIP graphs commit exactly the eager rounds' tokens. Each shape is
     replayed many times with new inputs (and eager work, host copies and syncs in between); the batch
