@@ -3,9 +3,10 @@
 Workload (the reference's largest single-GPU configuration): target = LLaMA-style decoder with 32 layers,
 d_model 4096, 32 query / 8 KV heads, head_dim 128, SwiGLU ffn 14336, vocab 128256, bf16, weights
 N(0, 0.02) from a seed; draft = the target's embedding, head and first 4 layers. 64 running sequences,
-k = 6, contexts uniform in [2048, 8192] held in a paged pool with block_size 16. The contexts' keys and
-values are synthetic N(0, 1) bf16 written straight into the pools (no prefill), then `--steps` decode
-rounds are timed: k draft decode steps, one target verify pass over k+1 tokens, one fused acceptance.
+k = 6, contexts uniform in [2048, 8192] held in a paged pool with block_size 16. The
+contexts come from a packed prefill of uniform random prompt ids through both models (`--synthetic-kv`:
+N(0, 1) bf16 keys/values written straight into the pools instead), then `--steps` decode rounds are
+timed: k draft decode steps, one target verify pass over k+1 tokens, one fused acceptance.
 
 One "step" = one speculative round for the whole batch, replayed from the HIP graph captured for its
 shape (the first round of a shape runs eagerly, the second captures). `value` = committed tokens per
@@ -406,6 +407,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--temperature", type=float, default=0.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--synthetic-kv", action="store_true",
+                    help="fill the pools with N(0,1) keys/values instead of prefilling the prompts")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kernel", choices=("round", "attention", "accept", "accept_stats", "copy", "engine_1b"),
                     default="round")
@@ -438,11 +441,23 @@ def main():
     nblocks = sum(per_seq) + 8
     sb = fa.SpeculativeBatch(target, draft, nblocks, BLOCK, K,
                              generator=torch.Generator(device="cuda").manual_seed(args.seed))
-    for store in (sb.pool_t.k_store, sb.pool_t.v_store, sb.pool_d.k_store, sb.pool_d.v_store):
-        store.normal_()
-    for c in ctxs:
-        toks = torch.randint(0, CFG["vocab_size"], (c + 1,), generator=g).tolist()
-        sb.add(toks, max_new_tokens=10 ** 9, temperature=args.temperature, prefill=False)
+    prompts = [torch.randint(0, CFG["vocab_size"], (c + 1,), generator=g).tolist() for c in ctxs]
+    prefill = None
+    if args.synthetic_kv:   # random keys/values in the pools instead of a prefill
+        for store in (sb.pool_t.k_store, sb.pool_t.v_store, sb.pool_d.k_store, sb.pool_d.v_store):
+            store.normal_()
+        for toks in prompts:
+            sb.add(toks, max_new_tokens=10 ** 9, temperature=args.temperature, prefill=False)
+    else:                   # the contexts come from the models: packed prefill of every prompt
+        torch.cuda.synchronize()
+        tp = time.perf_counter()
+        sb.add_many(prompts, 10 ** 9, args.temperature)
+        torch.cuda.synchronize()
+        tp = time.perf_counter() - tp
+        n_tok = sum(len(p) - 1 for p in prompts)
+        prefill = {"tokens": n_tok, "seconds": round(tp, 3), "tok_per_s": round(n_tok / tp, 1),
+                   "models": "target (32 layers) and draft (4 layers), packed 32K-token forwards"}
+        log(f"prefill: {n_tok} tokens in {tp:.1f}s")
     torch.cuda.synchronize()
     log(f"pools: target {sb.pool_t.k_store.numel() * 4 / 1e9:.1f} GB, draft {sb.pool_d.k_store.numel() * 4 / 1e9:.1f} GB;"
         f" setup {time.time() - t0:.1f}s")
@@ -493,7 +508,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (random-init N(0,0.02) weights; synthetic N(0,1) bf16 context KV)",
+        "data": ("synthetic (random-init N(0,0.02) weights; " +
+                 ("N(0,1) bf16 context KV)" if args.synthetic_kv else
+                  "uniform random prompt ids, contexts prefilled through the models)")),
         "config": {"workload": "8B-shape speculative decode: 32L d4096 32/8 heads hd128 ffn14336 V128256 bf16, "
                                "early-exit draft 4 layers, batch 64, k=6, contexts U[2048,8192], block 16",
                    "global_batch": BATCH, "k": K, "temperature": args.temperature, "parallelism": "none (1 GPU)"},
@@ -514,6 +531,7 @@ def main():
                           # as the round runs it: the rows' statistics come from the LM heads' epilogue
                           "with_head_stats": {"avg_us": round(accs_avg * 1e6, 2),
                                               "effective_GBs": round(accept_bytes(BATCH, K, v) / accs_avg / 1e9, 1)}},
+        "prefill": prefill,
         # MFMA utilisation of the dense GEMMs (bf16 dense peak 2.5 PFLOP/s), event-timed after the rounds
         "gemm_verify_m448": gemm_verify,
         "gemm_draft_m64": gemm_draft,
