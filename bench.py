@@ -456,7 +456,9 @@ def main():
         tp = time.perf_counter() - tp
         n_tok = sum(len(p) - 1 for p in prompts)
         prefill = {"tokens": n_tok, "seconds": round(tp, 3), "tok_per_s": round(n_tok / tp, 1),
-                   "models": "target (32 layers) and draft (4 layers), packed 32K-token forwards"}
+                   "models": ("target (32 layers; the early-exit draft shares its first 4 layers' cache)"
+                              if sb.shared else "target (32 layers) and draft (4 layers)") +
+                             ", packed 32K-token forwards"}
         log(f"prefill: {n_tok} tokens in {tp:.1f}s")
     torch.cuda.synchronize()
     log(f"pools: target {sb.pool_t.k_store.numel() * 4 / 1e9:.1f} GB, draft {sb.pool_d.k_store.numel() * 4 / 1e9:.1f} GB;"

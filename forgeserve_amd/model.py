@@ -232,21 +232,49 @@ class ForgeModel(nn.Module):
         return self._run(to_device(idx, dev), pos32, kv, last_only, head_stats)
 
     def _run(self, idx: torch.Tensor, pos32: torch.Tensor, kv: List, last_only: bool = False, head_stats=None,
-             out=None):
+             out=None, hidden_out=None):
         """The forward's kernels alone: idx (B, T) int64 and pos32 (B, T) int32 already on the device,
         no argument checks and no host synchronisation, so that a caller can capture it in a HIP graph
         (positions < max_seq_len is the caller's to guarantee). With last_only, `out` (B, vocab) may
-        receive the logits (then it is returned as is)."""
+        receive the logits (then it is returned as is) and `hidden_out` (B, d_model) the last
+        position's residual stream after the last layer (the head's input before its norm)."""
         b, t = idx.shape
-        rope = self._rope()
-        x = ops.embedding(idx, self.tok_emb.weight)
-        for layer, view in zip(self.layers, kv):
-            x = layer.step(x, b, t, pos32, view, rope)
+        x = self._layers(ops.embedding(idx, self.tok_emb.weight), 0, len(self.layers), b, t, pos32, kv)
         if last_only:
             x = x.view(b, t, -1)[:, -1].contiguous()
+            if hidden_out is not None:
+                hidden_out.copy_(x)
             if out is not None:
                 return self.head(x, head_stats, out=out)
             return self.head(x, head_stats).view(b, 1, -1)
+        return self.head(x, head_stats).view(b, t, -1)
+
+    def _layers(self, x: torch.Tensor, start: int, stop: int, b: int, t: int, pos32: torch.Tensor,
+                kv: List) -> torch.Tensor:
+        """Blocks start..stop-1 on the residual stream x (B*T, d); kv[i] is block i's cache view."""
+        rope = self._rope()
+        for i in range(start, stop):
+            x = self.layers[i].step(x, b, t, pos32, kv[i], rope)
+        return x
+
+    def _run_verify_reusing(self, n_shared: int, window: torch.Tensor, pos32: torch.Tensor, kv: List,
+                            keff: torch.Tensor, hidden: torch.Tensor, head_stats=None):
+        """The verify pass over window (B, T) at pos32 when blocks 0..n_shared-1 have already run for
+        the first keff[r] tokens of row r (an early-exit draft sharing those blocks and their cache):
+        hidden (B, T-1, d) holds their residual streams after block n_shared-1. Only token keff[r] of
+        each row goes through blocks 0..n_shared-1 here (one row each, at its own position); then
+        all T tokens run the remaining blocks and the head. Every row's result is bit-identical to the
+        full pass: the blocks compute a row the same way whatever else is in the batch."""
+        b, t = window.shape
+        d = self.cfg.d_model
+        k1 = keff.to(torch.int64)[:, None]
+        tail_idx = window.gather(1, k1)
+        tail_pos = pos32.gather(1, k1)
+        h_tail = self._layers(ops.embedding(tail_idx, self.tok_emb.weight), 0, n_shared, b, 1, tail_pos, kv)
+        x = torch.empty((b, t, d), dtype=h_tail.dtype, device=h_tail.device)
+        x[:, : t - 1].copy_(hidden)
+        x.scatter_(1, k1[:, :, None].expand(b, 1, d), h_tail.view(b, 1, d))
+        x = self._layers(x.view(b * t, d), n_shared, len(self.layers), b, t, pos32, kv)
         return self.head(x, head_stats).view(b, t, -1)
 
 

@@ -137,6 +137,19 @@ class _GeneratorDraws:
         return u[:, : self.k].contiguous(), e
 
 
+def shared_layers(target, draft) -> int:
+    """How many leading blocks an early-exit draft shares with its target (the same modules, with the
+    same embedding), 0 if it is not such a draft. Those blocks compute the same keys, values and
+    residual streams for the same tokens in either model, so the draft can read and write the target's
+    cache for them instead of keeping its own (the reference keeps a separate cache, speculative.py:46:
+    the tokens do not change, only the memory and the work)."""
+    n = draft.cfg.n_layers
+    if (n > target.cfg.n_layers or draft.tok_emb is not target.tok_emb or draft.cfg.d_model != target.cfg.d_model
+            or draft.cfg.max_seq_len != target.cfg.max_seq_len):
+        return 0
+    return n if all(draft.layers[i] is target.layers[i] for i in range(n)) else 0
+
+
 def _bucket(x: int, q: int) -> int:
     return max(q, -(-x // q) * q)
 
@@ -152,9 +165,13 @@ class _RoundState:
     few graphs. Padding rows have k_eff 0 and only -1 positions (no KV write, no keys), temperature
     0, and their results are dropped."""
 
-    def __init__(self, dev, dtype, b, k, wt, wd, v, sampling, fused, parts_d, parts_t):
+    def __init__(self, dev, dtype, b, k, wt, wd, v, sampling, fused, parts_d, parts_t, n_shared=0, d_model=0):
         self.b, self.k, self.wt, self.wd, self.v = b, k, wt, wd, v
         self.sampling, self.fused = sampling, fused
+        # a draft sharing the target's first n_shared blocks and their cache leaves its residual
+        # streams after them here, one per fed token (the verify pass continues from them)
+        self.n_shared = n_shared
+        self.hidden = torch.empty((b, max(k, 1), d_model), dtype=dtype, device=dev) if n_shared else None
         # staging: int64 ids [b, 2] (prev, last) and last [b]; int32 k_eff [b], draft positions [b, 2] (step 0)
         # then [k-1, b] (steps 1..k-1), verify positions [b, k+1], tables [b, wt] and [b, wd];
         # float32 temperature and 1/T [2, b]
@@ -240,7 +257,8 @@ def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _R
         else:
             idx, pos = st.draft_tok[:, i - 1].to(torch.int64)[:, None], d["posd"][i - 1][:, None]
         logits = draft._run(idx, pos, pool_d.views(d["tab_d"], pos), last_only=True,
-                            head_stats=(inv_t, st.parts_d[:, i]) if st.fused else None, out=st.dft_logits[:, i])
+                            head_stats=(inv_t, st.parts_d[:, i]) if st.fused else None, out=st.dft_logits[:, i],
+                            hidden_out=st.hidden[:, i] if st.n_shared else None)
         ops.sample_logits(logits, temps, st.noise_d[i] if st.sampling else None, out32=st.draft_tok[:, i])
         if st.fused and i == k - 1:   # draft row (b, i) is record b*k + i: sequence b's draft rows k+1 .. 2k
             ops.row_stats_merge(st.parts_d.view(b * k, -1, 4), st.row_stats, k, 2 * k + 1, k + 1)
@@ -249,8 +267,12 @@ def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _R
     idx = torch.cat([last[:, None], st.draft_tok.to(torch.int64)], 1) if k else last[:, None]
     pos = d["posv"]
     inv_t_t = inv_t.repeat_interleave(k + 1) if st.fused else None
-    tgt_logits = target._run(idx, pos, pool_t.views(d["tab_t"], pos),
-                             head_stats=(inv_t_t, st.parts_t) if st.fused else None)
+    views = pool_t.views(d["tab_t"], pos)
+    stats = (inv_t_t, st.parts_t) if st.fused else None
+    if st.n_shared and k:   # the draft has run the shared blocks for all but token k_eff of each row
+        tgt_logits = target._run_verify_reusing(st.n_shared, idx, pos, views, d["keff"], st.hidden[:, :k], stats)
+    else:
+        tgt_logits = target._run(idx, pos, views, head_stats=stats)
     if st.fused:
         ops.row_stats_merge(st.parts_t, st.row_stats, k + 1, 2 * k + 1, 0)
     out_tok, n_acc = ops.spec_accept(tgt_logits, st.dft_logits, st.draft_tok, d["keff"], temps, st.u[:, :k], st.e,
@@ -294,6 +316,12 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     if int((n - 1 + keff).max()) >= limit:
         raise ValueError(f"a round would write position {int((n - 1 + keff).max())} >= max_seq_len {limit}")
     sampling = any(t > 0 for t in temps)
+    n_shared = 0
+    if pool_d is pool_t:   # the draft reads and writes the target's cache for the blocks they share
+        n_shared = shared_layers(target, draft)
+        if not n_shared:
+            raise ValueError("only an early-exit draft of the target can share the target's pool")
+        blocks_d = blocks_t
     bp = _bucket(b, 8)
     wt = _bucket(max(len(x) for x in blocks_t), 64)
     wd = _bucket(max(len(x) for x in blocks_d), 64)
@@ -307,7 +335,7 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     key = (bp, k, wt, wd, sampling, fused, _graph_key(target), _graph_key(draft), id(pool_d))
     st = cache.get(key)
     if st is None:
-        st = _RoundState(dev, dtype, bp, k, wt, wd, v, sampling, fused, pd, pt)
+        st = _RoundState(dev, dtype, bp, k, wt, wd, v, sampling, fused, pd, pt, n_shared, target.cfg.d_model)
         cache[key] = st
         while len(cache) > _MAX_GRAPHS:
             cache.popitem(last=False)
@@ -364,22 +392,32 @@ class _Seq:
 
 
 class SpeculativeBatch:
-    """Batched draft-then-verify rounds over paged KV pools (one pool for the target, one for the draft).
+    """Batched draft-then-verify rounds over paged KV pools.
 
     Sequence state lives on the host (token lists, block lists); KV, logits, draft tokens, random
     numbers and acceptance results live on the GPU. `round()` advances every active sequence by
-    1 + (accepted proposals) tokens."""
+    1 + (accepted proposals) tokens.
+
+    share_kv: an early-exit draft (`early_exit_draft`) computes exactly the keys and values of the
+    target's first blocks, so by default (None) it uses the target's pool for them instead of a pool of
+    its own, needs no prefill of its own, and the verify pass continues from the draft's residual
+    streams instead of re-running those blocks for the drafted tokens. The tokens are the same either
+    way; False keeps the separate draft pool of the reference (speculative.py:46)."""
 
     def __init__(self, target, draft, num_blocks: int, block_size: int = 16, k: int = 4,
                  draft_num_blocks: Optional[int] = None, generator: Optional[torch.Generator] = None,
-                 graphs: bool = True):
+                 graphs: bool = True, share_kv: Optional[bool] = None):
         if target.cfg.vocab_size != draft.cfg.vocab_size:
             raise ValueError("target and draft must share a vocabulary")
         self.target, self.draft, self.k = target, draft, k
         self.dev, self.dtype = target.device, target.dtype
+        shared = shared_layers(target, draft)
+        if share_kv and not shared:
+            raise ValueError("share_kv needs an early-exit draft of the target (early_exit_draft)")
+        self.shared = bool(shared) if share_kv is None else bool(share_kv)
         self.pool_t = PagedKVPool(target.cfg, num_blocks, block_size, dtype=self.dtype, device=self.dev)
-        self.pool_d = PagedKVPool(draft.cfg, draft_num_blocks or num_blocks, block_size, dtype=self.dtype,
-                                  device=self.dev)
+        self.pool_d = self.pool_t if self.shared else PagedKVPool(draft.cfg, draft_num_blocks or num_blocks,
+                                                                  block_size, dtype=self.dtype, device=self.dev)
         self.block_size = block_size
         self.limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
         self.gen = generator
@@ -389,19 +427,23 @@ class SpeculativeBatch:
 
     # ---- sequences ------------------------------------------------------------------------------
     def _grow(self, seq: _Seq, n_tokens: int) -> None:
-        for pool, blocks in ((self.pool_t, seq.blocks_t), (self.pool_d, seq.blocks_d)):
+        pools = ((self.pool_t, seq.blocks_t),) if self.shared else ((self.pool_t, seq.blocks_t),
+                                                                     (self.pool_d, seq.blocks_d))
+        for pool, blocks in pools:
             need = pool.blocks_for(n_tokens) - len(blocks)
             if need > 0:
                 blocks += pool.allocator.allocate(need)
 
     def release(self, seq: _Seq) -> None:
         self.pool_t.allocator.release(seq.blocks_t)
-        self.pool_d.allocator.release(seq.blocks_d)
+        if not self.shared:
+            self.pool_d.allocator.release(seq.blocks_d)
         seq.blocks_t, seq.blocks_d = BlockList(), BlockList()
 
     def add(self, prompt: Sequence[int], max_new_tokens: int, temperature: float = 0.0, eos_id=None,
             prefill: bool = True) -> _Seq:
-        """Add a sequence; with prefill, its prompt (all but the last token) is run through both models."""
+        """Add a sequence; with prefill, its prompt (all but the last token) is run through the target
+        (and through the draft when it keeps its own pool)."""
         if not 0 < len(prompt) < self.limit:
             raise ValueError(f"prompt length must be in 1..{self.limit - 1}")
         seq = _Seq(prompt, max_new_tokens, temperature, eos_id)
@@ -410,8 +452,10 @@ class SpeculativeBatch:
             n = len(seq.tokens) - 1
             idx = torch.tensor([seq.tokens[:-1]])
             pos = torch.arange(n)[None]
-            for model, pool, blocks in ((self.target, self.pool_t, seq.blocks_t),
-                                        (self.draft, self.pool_d, seq.blocks_d)):
+            runs = [(self.target, self.pool_t, seq.blocks_t)]
+            if not self.shared:   # a shared draft's blocks were written by the target's prefill
+                runs.append((self.draft, self.pool_d, seq.blocks_d))
+            for model, pool, blocks in runs:
                 model(idx, pos, pool.views(torch.tensor([blocks]), pos), last_only=True)
         self.seqs.append(seq)
         return seq
@@ -441,7 +485,8 @@ class SpeculativeBatch:
                 i += 1
             toks = [s.tokens[:-1] for s in chunk]
             prefill_packed(self.target, self.pool_t, toks, [s.blocks_t for s in chunk])
-            prefill_packed(self.draft, self.pool_d, toks, [s.blocks_d for s in chunk])
+            if not self.shared:
+                prefill_packed(self.draft, self.pool_d, toks, [s.blocks_d for s in chunk])
         self.seqs.extend(seqs)
         return seqs
 

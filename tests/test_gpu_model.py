@@ -260,6 +260,33 @@ def test_packed_prefill_equals_per_sequence_prefill(which, bf_target, small):
     assert torch.equal(packed_pool.k_store, alone_pool.k_store) and torch.equal(packed_pool.v_store, alone_pool.v_store)
 
 
+@pytest.mark.parametrize("which", ["bf16", "f32"])
+def test_shared_draft_cache_equals_separate_cache(which, bf_target, small):
+    """An early-exit draft that reads and writes the target's cache for the blocks they share (and a
+    verify pass that continues from the draft's residual streams) commits exactly the tokens of a draft
+    with its own cache: greedy and sampled rows, sequences finishing at different rounds (ragged
+    k_eff), graphs on."""
+    case("shared draft cache", which)
+    model = bf_target if which == "bf16" else small
+    draft = fa.early_exit_draft(model, 2 if which == "bf16" else 1)
+    cfg = model.cfg
+    g = torch.Generator().manual_seed(41)
+    prompts = [torch.randint(0, cfg.vocab_size, (int(n),), generator=g).tolist() for n in (5, 17, 2, 30, 9)]
+    temps = [0.0, 0.9, 1.0, 0.0, 0.6]
+    lim = cfg.max_seq_len
+
+    def run(share):
+        sb = fa.SpeculativeBatch(model, draft, 200, 4, k=3, generator=torch.Generator(device="cuda").manual_seed(2),
+                                 share_kv=share)
+        seqs = sb.add_many(prompts, [min(12 + 5 * i, lim - len(p) - 1) for i, p in enumerate(prompts)], temps)
+        sb.run()
+        return [s.tokens for s in seqs], sb.stats, sb.pool_d is sb.pool_t
+
+    sep, shared = run(False), run(True)
+    assert not sep[2] and shared[2]
+    assert shared[0] == sep[0] and shared[1] == sep[1]
+
+
 def test_graph_rounds_equal_eager_rounds(bf_target):
     """Rounds replayed from captured HIP graphs commit exactly the eager rounds' tokens. Each shape is
     replayed many times with new inputs (and eager work, host copies and syncs in between); the batch
