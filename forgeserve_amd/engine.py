@@ -28,7 +28,7 @@ from ._lib import to_device
 from .model import ForgeModel
 from .paged import BlockList, PagedKVPool, block_table
 from .sampling import exp_noise
-from .speculative import spec_round
+from .speculative import shared_layers, spec_round
 
 
 @dataclass
@@ -83,7 +83,7 @@ class _KeyedDraws:
 class Engine:
     def __init__(self, model: ForgeModel, num_blocks: int, block_size: int = 16, max_batch: int = 8, seed: int = 0,
                  draft: Optional[ForgeModel] = None, k: int = 4, draft_num_blocks: Optional[int] = None,
-                 graphs: bool = True):
+                 graphs: bool = True, share_kv: Optional[bool] = None):
         self.model, self.cfg = model, model.cfg
         self.pool = PagedKVPool(self.cfg, num_blocks, block_size, tp=model.tp, dtype=model.dtype, device=model.device)
         self.max_batch = max_batch
@@ -92,8 +92,11 @@ class Engine:
         self.running: List[Request] = []
         self.requests: Dict[int, Request] = {}
         self.steps = self.preemptions = self.peak_running = self.peak_blocks = 0
-        # speculative decoding (optional): the draft keeps its own pool, as speculative.py:46 keeps kv_d
+        # speculative decoding (optional): the draft keeps its own pool, as speculative.py:46 keeps kv_d,
+        # unless it is an early-exit draft of the model (share_kv None or True): then it uses the model's
+        # pool for the blocks they share (SpeculativeBatch's share_kv; the tokens are the same)
         self.draft, self.k, self.seed = draft, k, seed
+        self.shared = False
         self.graphs = graphs   # speculative rounds: replay each round shape from a captured HIP graph
         self.limit = self.cfg.max_seq_len
         self.stats = {"rounds": 0, "proposed": 0, "accepted": 0}
@@ -102,8 +105,12 @@ class Engine:
                 raise ValueError("target and draft must share a vocabulary")
             if k < 1:
                 raise ValueError("k must be at least 1")
-            self.pool_d = PagedKVPool(draft.cfg, draft_num_blocks or num_blocks, block_size, dtype=model.dtype,
-                                      device=model.device)
+            n_shared = shared_layers(model, draft)
+            if share_kv and not n_shared:
+                raise ValueError("share_kv needs an early-exit draft of the model (early_exit_draft)")
+            self.shared = bool(n_shared) if share_kv is None else bool(share_kv)
+            self.pool_d = self.pool if self.shared else PagedKVPool(
+                draft.cfg, draft_num_blocks or num_blocks, block_size, dtype=model.dtype, device=model.device)
             self.limit = min(self.cfg.max_seq_len, draft.cfg.max_seq_len)
 
     # ---- public API ---------------------------------------------------------------------------------
@@ -147,7 +154,7 @@ class Engine:
         tokens = req.prompt + req.output
         need = self.pool.blocks_for(len(tokens))
         spec = self.draft is not None
-        need_d = self.pool_d.blocks_for(len(tokens)) if spec else 0
+        need_d = self.pool_d.blocks_for(len(tokens)) if spec and not self.shared else 0
         if need > self.pool.allocator.num_free or (spec and need_d > self.pool_d.allocator.num_free):
             return False
         self.waiting.popleft()
@@ -157,9 +164,10 @@ class Engine:
         logits = self.model(torch.tensor([tokens]), positions, views, last_only=True)
         req.cached = len(tokens)
         if spec:   # the draft's cache covers the same positions; the first token uses the request's stream
-            req.blocks_d = BlockList(self.pool_d.allocator.allocate(need_d))
-            self.draft(torch.tensor([tokens]), positions, self.pool_d.views(torch.tensor([req.blocks_d]), positions),
-                       last_only=True)
+            if not self.shared:   # (a shared draft's blocks were written by the model's prefill)
+                req.blocks_d = BlockList(self.pool_d.allocator.allocate(need_d))
+                self.draft(torch.tensor([tokens]), positions,
+                           self.pool_d.views(torch.tensor([req.blocks_d]), positions), last_only=True)
             self._append_keyed(req, logits[:, -1])
         else:
             self._append([req], logits[:, -1])
@@ -177,7 +185,7 @@ class Engine:
     def _release(self, req: Request) -> None:
         self.pool.allocator.release(req.blocks)
         req.blocks = BlockList()
-        if self.draft is not None:
+        if self.draft is not None and not self.shared:
             self.pool_d.allocator.release(req.blocks_d)
             req.blocks_d = BlockList()
 
@@ -190,7 +198,7 @@ class Engine:
             req = self.running[i]
             span = len(req.prompt) + len(req.output) + self._k_eff(req)
             need_t = self.pool.blocks_for(span) - len(req.blocks)
-            need_d = self.pool_d.blocks_for(span) - len(req.blocks_d)
+            need_d = 0 if self.shared else self.pool_d.blocks_for(span) - len(req.blocks_d)
             if need_t > self.pool.allocator.num_free or need_d > self.pool_d.allocator.num_free:
                 if len(self.running) == 1:
                     raise RuntimeError("the block pool is too small to hold even one sequence of this length")

@@ -287,6 +287,28 @@ def test_shared_draft_cache_equals_separate_cache(which, bf_target, small):
     assert shared[0] == sep[0] and shared[1] == sep[1]
 
 
+def test_spec_engine_shared_cache_equals_separate_cache(small):
+    """The speculative engine with the draft on the model's pool gives the separate-pool engine's
+    tokens: sampled rows through a roomy pool, greedy rows through a pool tight enough to preempt."""
+    case("spec engine shared cache")
+    draft = fa.early_exit_draft(small, 1)
+    reqs = [([1, 2, 3], 20, 0.8), ([9, 8, 7, 6], 15, 0.0), ([5, 5], 18, 1.0), ([30, 31, 32, 33, 34], 12, 0.6)]
+
+    def run(share, num_blocks, greedy):
+        e = fa.Engine(small, num_blocks=num_blocks, block_size=4, max_batch=4, seed=5, draft=draft, k=3,
+                      share_kv=share)
+        ids = [e.add_request(p, n, temperature=0.0 if greedy else t) for p, n, t in reqs]
+        out = e.run()
+        return [out[i] for i in ids], e.preemptions, e.pool_d is e.pool
+
+    roomy = run(False, 64, False), run(True, 64, False)
+    assert not roomy[0][2] and roomy[1][2]
+    assert roomy[1][0] == roomy[0][0]
+    tight = run(False, 14, True), run(True, 14, True)
+    assert tight[0][1] > 0 and tight[1][1] > 0
+    assert tight[1][0] == tight[0][0]
+
+
 def test_graph_rounds_equal_eager_rounds(bf_target):
     """Rounds replayed from captured HIP graphs commit exactly the eager rounds' tokens. Each shape is
     replayed many times with new inputs (and eager work, host copies and syncs in between); the batch
