@@ -173,9 +173,12 @@ class _RoundState:
         self.n_shared = n_shared
         self.hidden = torch.empty((b, max(k, 1), d_model), dtype=dtype, device=dev) if n_shared else None
         # staging: int64 ids [b, 2] (prev, last) and last [b]; int32 k_eff [b], draft positions [b, 2] (step 0)
-        # then [k-1, b] (steps 1..k-1), verify positions [b, k+1], tables [b, wt] and [b, wd];
+        # then [k-1, b] (steps 1..k-1; [k, b], steps 0..k-1, with a shared cache), verify positions
+        # [b, k+1], tables [b, wt] and [b, wd];
         # float32 temperature and 1/T [2, b]
-        km = max(k - 1, 0)
+        # a draft on the target's cache feeds only `last` in step 0 (the verify pass has cached every
+        # position before it), so its step 0 is staged with the others
+        km = k if n_shared else max(k - 1, 0)
         spans = [("ids", np.int64, (b, 2)), ("last", np.int64, (b,)), ("keff", np.int32, (b,)), ("pos0", np.int32, (b, 2)),
                  ("posd", np.int32, (km, b)), ("posv", np.int32, (b, k + 1)), ("tab_t", np.int32, (b, wt)),
                  ("tab_d", np.int32, (b, wd)), ("temps", np.float32, (2, b))]
@@ -227,8 +230,9 @@ class _RoundState:
         h["pos0"].fill(-1)
         h["pos0"][:b] = np.where(keff[:, None] > 0, np.stack([np.where(n > 1, n - 2, -1), n - 1], 1), -1)
         h["posd"].fill(-1)
-        for i in range(1, k):
-            h["posd"][i - 1, :b] = np.where(keff > i, n - 1 + i, -1)
+        first = 0 if self.n_shared else 1
+        for i in range(first, k):
+            h["posd"][i - first, :b] = np.where(keff > i, n - 1 + i, -1)
         t_ = np.arange(k + 1)[None, :]
         h["posv"].fill(-1)
         h["posv"][:b] = np.where(t_ <= keff[:, None], n[:, None] - 1 + t_, -1)
@@ -252,10 +256,13 @@ def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _R
     temps, inv_t = d["temps"][0], d["temps"][1]
     if phase < k:
         i = phase
-        if i == 0:
+        if i == 0 and st.n_shared:   # the shared cache holds every position before `last`
+            idx, pos = d["last"][:, None], d["posd"][0][:, None]
+        elif i == 0:                  # re-feed (prev, last): the draft's own cache may lack prev
             idx, pos = d["ids"], d["pos0"]
         else:
-            idx, pos = st.draft_tok[:, i - 1].to(torch.int64)[:, None], d["posd"][i - 1][:, None]
+            idx = st.draft_tok[:, i - 1].to(torch.int64)[:, None]
+            pos = d["posd"][i if st.n_shared else i - 1][:, None]
         logits = draft._run(idx, pos, pool_d.views(d["tab_d"], pos), last_only=True,
                             head_stats=(inv_t, st.parts_d[:, i]) if st.fused else None, out=st.dft_logits[:, i],
                             hidden_out=st.hidden[:, i] if st.n_shared else None)
