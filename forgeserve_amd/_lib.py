@@ -49,6 +49,10 @@ SIGNATURES = {
     "fs_gemm": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i32, c_p, c_i64,
                         c_p]),
     "fs_gemm_workspace_size": (c_i64, [c_i64, c_i64, c_i64, c_i32]),
+    "fs_gemm_splits": (c_i32, [c_i64, c_i64, c_i32]),
+    "fs_gemm_partials": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i32, c_p, c_i64, c_p]),
+    "fs_splitk_add_rmsnorm": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_f32, c_i32,
+                                      c_p]),
     "fs_gemm_row_stats": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_p, c_p, c_i64, c_i64,
                                   c_p]),
     "fs_gemm_row_stats_parts": (c_i64, [c_i64, c_i64, c_i64]),

@@ -549,6 +549,29 @@ extern "C" int fs_gemm_row_stats(const void* A, int64_t lda, const void* B, int6
   return fs::launch_status("gemm_row_stats");
 }
 
+extern "C" int32_t fs_gemm_splits(int64_t N, int64_t K, int32_t dtype) {
+  if (N <= 0 || K <= 0 || dtype != FS_BF16 || N % 4) return 1;
+  return split_for(N, K);
+}
+
+extern "C" int fs_gemm_partials(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                                int32_t dtype, void* partials, int64_t partials_bytes, void* stream) {
+  FS_CHECK_ARG(A && B && partials, "gemm_partials: null pointer");
+  FS_CHECK_ARG(dtype == FS_BF16, "gemm_partials: bf16 only (dtype %d)", dtype);
+  FS_CHECK_ARG(M >= 0 && N > 0 && K > 0 && lda >= K && ldb >= K, "gemm_partials: M %lld N %lld K %lld",
+               (long long)M, (long long)N, (long long)K);
+  FS_CHECK_ARG(lds_ok(A, lda, B, ldb, K) && N % 4 == 0, "gemm_partials: needs K %% 64 == 0, N %% 4 == 0, aligned rows");
+  const int splits = split_for(N, K);
+  FS_CHECK_ARG(splits > 1, "gemm_partials: N %lld K %lld does not split K", (long long)N, (long long)K);
+  const int64_t need = (int64_t)splits * M * N * (int64_t)sizeof(float);
+  FS_CHECK_ARG(partials_bytes >= need && (reinterpret_cast<uintptr_t>(partials) & 15) == 0,
+               "gemm_partials: %lld < %lld bytes (or unaligned)", (long long)partials_bytes, (long long)need);
+  if (M == 0) return 0;
+  launch_lds<false>((const uint16_t*)A, lda, (const uint16_t*)B, ldb, nullptr, 0, nullptr, 0, M, N, K, splits,
+                    reinterpret_cast<float*>(partials), RowStatsOut{}, fs::as_stream(stream));
+  return fs::launch_status("gemm_partials");
+}
+
 extern "C" int64_t fs_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int32_t dtype) {
   if (M <= 0 || N <= 0 || K <= 0 || dtype != FS_BF16) return 0;
   const int s = split_for(N, K);

@@ -122,6 +122,64 @@ __global__ void __launch_bounds__(NORM_THREADS) add_rmsnorm_vec_kernel(
   }
 }
 
+// The same kernel for x = a split-K GEMM's output: x[m] = round(sum over s of parts[s][m], in split
+// order), then the residual: x_out = round(x + residual), y = rmsnorm(x_out) * w. This is the GEMM's
+// reduction (gemm_splitk_reduce_kernel) followed by add_rmsnorm_vec_kernel on its output, in one pass.
+template <int DT>
+__global__ void __launch_bounds__(NORM_THREADS) splitk_add_rmsnorm_kernel(
+    const float* __restrict__ parts, int splits, int64_t part_stride, const uint16_t* __restrict__ residual,
+    int64_t ldr, uint16_t* __restrict__ x_out, int64_t ldxo, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
+    int64_t ldy, int64_t N, float eps) {
+  __shared__ float red[NORM_THREADS / 64];
+  const int64_t m = blockIdx.x;
+  const int ng = (int)(N / 8);
+  float v[NORM_VEC_GROUPS][8];
+  float sq = 0.f;
+#pragma unroll
+  for (int u = 0; u < NORM_VEC_GROUPS; ++u) {
+    const int gi = threadIdx.x + NORM_THREADS * u;
+    if (gi >= ng) continue;
+    const float* p0 = parts + m * N + 8 * gi;
+    float4_t a0 = *reinterpret_cast<const float4_t*>(p0), a1 = *reinterpret_cast<const float4_t*>(p0 + 4);
+    for (int sp = 1; sp < splits; ++sp) {
+      const float4_t b0 = *reinterpret_cast<const float4_t*>(p0 + sp * part_stride);
+      const float4_t b1 = *reinterpret_cast<const float4_t*>(p0 + sp * part_stride + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a0[j] += b0[j];
+        a1[j] += b1[j];
+      }
+    }
+    float d[8];
+    unpack8<DT>(*reinterpret_cast<const u32x4_t*>(residual + m * ldr + 8 * gi), d);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[u][j] = Elem<DT>::round(Elem<DT>::round(a0[j]) + d[j]);
+      v[u][j + 4] = Elem<DT>::round(Elem<DT>::round(a1[j]) + d[j + 4]);
+    }
+    *reinterpret_cast<u32x4_t*>(x_out + m * ldxo + 8 * gi) = pack8<DT>(v[u]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sq += v[u][j] * v[u][j];
+  }
+  sq = wave_sum(sq);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[i];
+  const float r = 1.0f / sqrtf(tot / (float)N + eps);
+#pragma unroll
+  for (int u = 0; u < NORM_VEC_GROUPS; ++u) {
+    const int gi = threadIdx.x + NORM_THREADS * u;
+    if (gi >= ng) continue;
+    float wv[8], o[8];
+    unpack8<DT>(*reinterpret_cast<const u32x4_t*>(w + 8 * gi), wv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = Elem<DT>::round(v[u][j] * r) * wv[j];
+    *reinterpret_cast<u32x4_t*>(y + m * ldy + 8 * gi) = pack8<DT>(o);
+  }
+}
+
 // silu(gate) * up on 16-bit rows, 8 columns per thread and 16-byte accesses (F % 8 == 0); the same
 // per-element arithmetic as silu_mul_kernel.
 template <int DT>
@@ -173,6 +231,29 @@ __global__ void __launch_bounds__(256) embedding_kernel(const int64_t* __restric
 bool dtype_ok(int32_t dt) { return dt == FS_F32 || dt == FS_BF16 || dt == FS_F16; }
 
 }  // namespace
+
+extern "C" int fs_splitk_add_rmsnorm(const float* parts, int32_t splits, const void* residual, int64_t ldr,
+                                     void* x_out, int64_t ldxo, const void* weight, void* y, int64_t ldy, int64_t M,
+                                     int64_t N, float eps, int32_t dtype, void* stream) {
+  FS_CHECK_ARG(parts && residual && x_out && weight && y, "splitk_add_rmsnorm: null pointer");
+  FS_CHECK_ARG(dtype == FS_BF16 || dtype == FS_F16, "splitk_add_rmsnorm: dtype %d (16-bit only)", dtype);
+  FS_CHECK_ARG(splits >= 1 && M >= 0 && N > 0 && N % 8 == 0 && N <= NORM_VEC_MAX,
+               "splitk_add_rmsnorm: splits %d M %lld N %lld", splits, (long long)M, (long long)N);
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  FS_CHECK_ARG(al16(parts) && al16(residual) && al16(x_out) && al16(weight) && al16(y) && ldr % 8 == 0 &&
+                   ldxo % 8 == 0 && ldy % 8 == 0,
+               "splitk_add_rmsnorm: 16-byte aligned rows");
+  if (M == 0) return 0;
+  hipStream_t s = fs::as_stream(stream);
+#define FS_LAUNCH_PARTS(DT)                                                                                     \
+  splitk_add_rmsnorm_kernel<DT><<<dim3((unsigned)M), NORM_THREADS, 0, s>>>(                                  \
+      parts, splits, M * N, (const uint16_t*)residual, ldr, (uint16_t*)x_out, ldxo, (const uint16_t*)weight,      \
+      (uint16_t*)y, ldy, N, eps)
+  if (dtype == FS_BF16) FS_LAUNCH_PARTS(FS_BF16);
+  else FS_LAUNCH_PARTS(FS_F16);
+#undef FS_LAUNCH_PARTS
+  return fs::launch_status("splitk_add_rmsnorm");
+}
 
 extern "C" int fs_add_rmsnorm(const void* x, int64_t ldx, const void* delta, int64_t ldd, void* x_out, int64_t ldxo,
                               const void* weight, void* y, int64_t ldy, int64_t M, int64_t N, float eps,

@@ -140,13 +140,18 @@ class Block(nn.Module):
         self.mlp_norm = RMSNorm(cfg.d_model, cfg.norm_eps)
         self.mlp = SwiGLU(cfg, tp)
 
-    def step(self, x: torch.Tensor, b: int, t: int, pos32: torch.Tensor, view, rope) -> torch.Tensor:
-        """x (B*T, d) -> x + attn(norm(x)), then + mlp(norm(.)) (model.py:104-106)."""
-        h = ops.add_rmsnorm(x, self.attn_norm.weight, self.attn_norm.eps)
+    def step(self, x: torch.Tensor, b: int, t: int, pos32: torch.Tensor, view, rope, h=None, next_norm=None):
+        """x (B*T, d) -> x + attn(norm(x)), then + mlp(norm(.)) (model.py:104-106). h: norm(x) by this
+        block's attention norm when the caller has it. Returns (x_out, next_norm(x_out) or None): a
+        projection that splits K is reduced inside the residual-add + norm kernel that follows it."""
+        if h is None:
+            h = ops.add_rmsnorm(x, self.attn_norm.weight, self.attn_norm.eps)
         a = self.attn.attend(h, b, t, pos32, view, rope)
-        x1 = ops.gemm(a, self.attn.wo.weight, residual=x)
-        h2 = ops.add_rmsnorm(x1, self.mlp_norm.weight, self.mlp_norm.eps)
-        return self.mlp(h2, residual=x1)
+        x1, h2 = ops.gemm_add_rmsnorm(a, self.attn.wo.weight, x, self.mlp_norm.weight, self.mlp_norm.eps)
+        g = ops.silu_mul(ops.gemm(h2, self.mlp.gate_up_weight()))
+        if next_norm is None:
+            return ops.gemm(g, self.mlp.w_down.weight, residual=x1), None
+        return ops.gemm_add_rmsnorm(g, self.mlp.w_down.weight, x1, next_norm.weight, next_norm.eps)
 
 
 class ForgeModel(nn.Module):
@@ -194,6 +199,12 @@ class ForgeModel(nn.Module):
     def embed(self, idx):
         return ops.embedding(to_device(idx, self.device), self.tok_emb.weight).reshape(*idx.shape, self.cfg.d_model)
 
+    def head_normed(self, y, stats=None, out=None):
+        """The tied head (model.py:138) on rows already normalised by the final norm: (rows, vocab)."""
+        if stats is not None:
+            return ops.gemm_row_stats(y, self.lm_head.weight, stats[0], stats[1], out=out)
+        return ops.gemm(y, self.lm_head.weight, out=out)
+
     def head(self, x, stats=None, out=None):
         """Final norm + tied head (model.py:137-138). stats = (inv_temperature (rows,), parts): also emit
         the logits' per-row softmax statistics (ops.gemm_row_stats). out: optional (rows, vocab) view
@@ -239,23 +250,31 @@ class ForgeModel(nn.Module):
         receive the logits (then it is returned as is) and `hidden_out` (B, d_model) the last
         position's residual stream after the last layer (the head's input before its norm)."""
         b, t = idx.shape
-        x = self._layers(ops.embedding(idx, self.tok_emb.weight), 0, len(self.layers), b, t, pos32, kv)
+        x, y = self._layers(ops.embedding(idx, self.tok_emb.weight), 0, len(self.layers), b, t, pos32, kv,
+                            last_norm=self.norm)
         if last_only:
-            x = x.view(b, t, -1)[:, -1].contiguous()
             if hidden_out is not None:
-                hidden_out.copy_(x)
+                hidden_out.copy_(x.view(b, t, -1)[:, -1])
+            y = y.view(b, t, -1)[:, -1].contiguous()
             if out is not None:
-                return self.head(x, head_stats, out=out)
-            return self.head(x, head_stats).view(b, 1, -1)
-        return self.head(x, head_stats).view(b, t, -1)
+                return self.head_normed(y, head_stats, out=out)
+            return self.head_normed(y, head_stats).view(b, 1, -1)
+        return self.head_normed(y, head_stats).view(b, t, -1)
 
-    def _layers(self, x: torch.Tensor, start: int, stop: int, b: int, t: int, pos32: torch.Tensor,
-                kv: List) -> torch.Tensor:
-        """Blocks start..stop-1 on the residual stream x (B*T, d); kv[i] is block i's cache view."""
+    def _layers(self, x: torch.Tensor, start: int, stop: int, b: int, t: int, pos32: torch.Tensor, kv: List,
+                last_norm=None):
+        """Blocks start..stop-1 on the residual stream x (B*T, d); kv[i] is block i's cache view.
+        Returns (x, last_norm(x)): each block's output is normalised by the next block's attention
+        norm in the same kernel as its last projection's reduction; after block stop-1 by last_norm
+        (None: not normalised)."""
         rope = self._rope()
+        h = None
         for i in range(start, stop):
-            x = self.layers[i].step(x, b, t, pos32, kv[i], rope)
-        return x
+            nxt = self.layers[i + 1].attn_norm if i + 1 < stop else last_norm
+            x, h = self.layers[i].step(x, b, t, pos32, kv[i], rope, h=h, next_norm=nxt)
+        if start >= stop and last_norm is not None:   # no block ran (a draft that is the whole model)
+            h = ops.add_rmsnorm(x, last_norm.weight, last_norm.eps)
+        return x, h
 
     def _run_verify_reusing(self, n_shared: int, window: torch.Tensor, pos32: torch.Tensor, kv: List,
                             keff: torch.Tensor, hidden: torch.Tensor, head_stats=None):
@@ -270,12 +289,12 @@ class ForgeModel(nn.Module):
         k1 = keff.to(torch.int64)[:, None]
         tail_idx = window.gather(1, k1)
         tail_pos = pos32.gather(1, k1)
-        h_tail = self._layers(ops.embedding(tail_idx, self.tok_emb.weight), 0, n_shared, b, 1, tail_pos, kv)
+        h_tail, _ = self._layers(ops.embedding(tail_idx, self.tok_emb.weight), 0, n_shared, b, 1, tail_pos, kv)
         x = torch.empty((b, t, d), dtype=h_tail.dtype, device=h_tail.device)
         x[:, : t - 1].copy_(hidden)
         x.scatter_(1, k1[:, :, None].expand(b, 1, d), h_tail.view(b, 1, d))
-        x = self._layers(x.view(b * t, d), n_shared, len(self.layers), b, t, pos32, kv)
-        return self.head(x, head_stats).view(b, t, -1)
+        _, y = self._layers(x.view(b * t, d), n_shared, len(self.layers), b, t, pos32, kv, last_norm=self.norm)
+        return self.head_normed(y, head_stats).view(b, t, -1)
 
 
 @torch.no_grad()
@@ -298,11 +317,9 @@ def prefill_packed(model: ForgeModel, pool, tokens: List[List[int]], block_lists
     if flat.numel() and (int(flat.min()) < 0 or int(flat.max()) >= model.cfg.vocab_size):
         raise ValueError("token ids must be in [0, vocab_size)")
     ids = to_device(flat, model.device)
-    rope = model._rope()
     x = ops.embedding(ids, model.tok_emb.weight)
-    for layer, view in zip(model.layers, step.views()):
-        x = layer.step(x, 1, step.n_tokens, None, view, rope)
-    return model.head(x.index_select(0, step.last_rows))
+    _, y = model._layers(x, 0, len(model.layers), 1, step.n_tokens, None, step.views(), last_norm=model.norm)
+    return model.head_normed(y.index_select(0, step.last_rows))
 
 
 def early_exit_draft(target: ForgeModel, n_layers: int) -> ForgeModel:

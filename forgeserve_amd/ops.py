@@ -95,6 +95,36 @@ def gemm(a: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
     return out
 
 
+def gemm_add_rmsnorm(a: torch.Tensor, w: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor,
+                     eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """x = a @ w.T + residual (nn.Linear then the residual add, model.py:105-106) and y = RMSNorm(x)
+    with norm_weight (model.py:29-31): returns (x, y). When the GEMM splits K, the partials are added
+    by the norm kernel itself (no separate reduction pass); otherwise the GEMM adds the residual and
+    the norm runs on its output. The results are the same either way."""
+    require_device(a, w, residual, norm_weight)
+    m, lda = _rows(a)
+    n, ldb = _rows(w)
+    k = a.shape[1]
+    lib = _lib.load()
+    if (a.dtype in (torch.bfloat16,) and w.dtype == a.dtype and w.shape[1] == k and residual.shape == (m, n)
+            and residual.dtype == a.dtype and n % 8 == 0 and n <= 8192 and lib.fs_gemm_splits(n, k, _dt(a)) > 1
+            and k % 64 == 0 and lda % 8 == 0 and ldb % 8 == 0 and residual.stride(1) == 1
+            and residual.stride(0) % 8 == 0 and norm_weight.is_contiguous() and norm_weight.dtype == a.dtype):
+        splits = lib.fs_gemm_splits(n, k, _dt(a))
+        need = splits * m * n * 4
+        ws = _persistent_ws("gemm", need, a.device)
+        check(lib.fs_gemm_partials(ptr(a), lda, ptr(w), ldb, m, n, k, _dt(a), ptr(ws), ws.numel(), stream_ptr()),
+              "gemm_partials")
+        x = torch.empty((m, n), dtype=a.dtype, device=a.device)
+        y = torch.empty((m, n), dtype=a.dtype, device=a.device)
+        check(lib.fs_splitk_add_rmsnorm(ptr(ws), splits, ptr(residual), residual.stride(0), ptr(x), n,
+                                        ptr(norm_weight), ptr(y), n, m, n, float(eps), _dt(a), stream_ptr()),
+              "splitk_add_rmsnorm")
+        return x, y
+    x = gemm(a, w, residual=residual)
+    return x, add_rmsnorm(x, norm_weight, eps)
+
+
 def row_stats_parts(m: int, n: int, k: int) -> int:
     """Column blocks per row of gemm_row_stats at this shape (0: the shape has no statistics epilogue)."""
     return int(_lib.load().fs_gemm_row_stats_parts(m, n, k))

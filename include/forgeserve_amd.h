@@ -141,6 +141,16 @@ int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int
 
 int64_t fs_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int32_t dtype);
 
+/* How many ways fs_gemm splits K for an (N, K) bf16 product (1: not split). A function of N and K only. */
+int32_t fs_gemm_splits(int64_t N, int64_t K, int32_t dtype);
+
+/* The first half of a split-K fs_gemm: the f32 partial products of each K range, partials[s][M][N]
+ * (s = 0 .. fs_gemm_splits(N, K) - 1), each the sum over its K range in increasing k. For consumers
+ * that add them themselves (fs_splitk_add_rmsnorm). bf16, K % 64 == 0, N % 4 == 0, only for shapes
+ * that split. Replaces the same nn.Linear calls as fs_gemm. */
+int fs_gemm_partials(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                     int32_t dtype, void* partials, int64_t partials_bytes, void* stream);
+
 /* The LM head (model.py:137-138) with the softmax statistics of its logits (sampling.py:13) as a
  * by-product, so that sampling and acceptance need not read the logits back to normalise them.
  * C = A . B^T as fs_gemm (bf16, K % 64 == 0, 16-byte aligned rows, no residual), and for every row m
@@ -154,6 +164,15 @@ int fs_gemm_row_stats(const void* A, int64_t lda, const void* B, int64_t ldb, vo
                       int64_t nparts, void* stream);
 
 int64_t fs_gemm_row_stats_parts(int64_t M, int64_t N, int64_t K);
+
+/* The end of a split-K projection fused with the residual add and RMSNorm that follow it
+ * (model.py:105-106 then model.py:29-31): x = round(sum of parts[s] in increasing s), then
+ * x_out = round(x + residual) and y = rmsnorm(x_out) * weight, exactly as fs_gemm with that residual
+ * followed by fs_add_rmsnorm on its output. parts: splits * M * N f32 (fs_gemm_partials). 16-bit
+ * dtypes, N % 8 == 0, N <= 8192, 16-byte aligned rows. */
+int fs_splitk_add_rmsnorm(const float* parts, int32_t splits, const void* residual, int64_t ldr, void* x_out,
+                          int64_t ldxo, const void* weight, void* y, int64_t ldy, int64_t M, int64_t N, float eps,
+                          int32_t dtype, void* stream);
 
 /* Merge fs_gemm_row_stats' per-block statistics (row m's nparts records at parts + m * parts_ld)
  * into one record per row, in a fixed order: row m goes to out[(m / group) * gstride + m % group +

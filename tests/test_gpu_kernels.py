@@ -70,6 +70,25 @@ def test_gemm_residual_epilogue(n, k):
     assert torch.equal(fused, two_step)
 
 
+@pytest.mark.parametrize("m,n,k", [(70, 2048, 2048), (448, 4096, 4096), (64, 1024, 7168), (1, 2048, 2048)])
+def test_splitk_add_rmsnorm_equals_gemm_then_norm(m, n, k):
+    """A split-K projection reduced inside the residual-add + RMSNorm kernel gives exactly what the
+    GEMM with its residual epilogue followed by add_rmsnorm gives (the reduction's and the norm's
+    arithmetic, in the same order)."""
+    case("splitk add_rmsnorm", m, n, k)
+    from forgeserve_amd import _lib
+    assert _lib.load().fs_gemm_splits(n, k, 1) > 1
+    g = torch.Generator().manual_seed(m + n + k)
+    a = torch.randn(m, k, generator=g).bfloat16().to(DEV)
+    w = (torch.randn(n, k, generator=g) * 0.03).bfloat16().to(DEV)
+    r = torch.randn(m, n, generator=g).bfloat16().to(DEV)
+    nw = (1 + 0.1 * torch.randn(n, generator=g)).bfloat16().to(DEV)
+    x, y = ops.gemm_add_rmsnorm(a, w, r, nw, 1e-5)
+    x_ref = ops.gemm(a, w, residual=r)
+    assert torch.equal(x, x_ref)
+    assert torch.equal(y, ops.add_rmsnorm(x_ref, nw, 1e-5))
+
+
 # ---- row ops ------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_rmsnorm_and_residual(dtype):
