@@ -473,21 +473,42 @@ int split_for(int64_t N, int64_t K) {
 
 // The LDS-kernel configuration a shape runs with. M <= 64 (a decode step) takes 64x64 tiles. Larger
 // M takes 224-row tiles when they pad M less than 128- and 256-row tiles would (the verify pass,
-// M = 64 * 7 = 448, is exactly two), else 256- or 128-row tiles; the width is the widest that still
-// gives most CUs a tile (measured at M = 448 and 128 on the decoder's projections).
+// M = 64 * 7 = 448, is exactly two), else 256- or 128-row tiles. Every configuration runs the same
+// MFMA over the same k order, so the tile shape never changes a result.
 struct LdsCfg {
   int bm, bn, wgm, wgn;
 };
+
+// Share of the CU slots a grid of `tiles` workgroups keeps busy (one tile per CU at a time, 256 CUs).
+double tile_fill(int64_t tiles) {
+  constexpr int64_t kCUs = 256;
+  return (double)tiles / (double)(kCUs * ((tiles + kCUs - 1) / kCUs));
+}
 
 LdsCfg lds_cfg(int64_t M, int64_t N, int splits, bool stats = false) {
   if (M <= 64) return LdsCfg{64, 64, 2, 2};
   auto pad = [&](int64_t bm) { return (M + bm - 1) / bm * bm - M; };
   if (pad(224) < pad(128) && pad(224) < pad(256)) {
-    const int64_t t256 = ((M + 223) / 224) * ((N + 255) / 256) * splits;
-    // 224 x 256 runs 16 waves (2 x 8, four per SIMD); with the statistics epilogue it keeps 8 waves
-    // (2 x 4), whose 64-column wave blocks halve the number of statistics records per row
-    if (t256 >= 192) return stats ? LdsCfg{224, 256, 2, 4} : LdsCfg{224, 256, 2, 8};
-    return LdsCfg{224, 128, 2, 4};
+    const int64_t tm = (M + 223) / 224;
+    if (stats) {   // the statistics epilogue keeps 8 waves of 64-column blocks
+      const int64_t t256 = tm * ((N + 255) / 256);
+      return t256 >= 192 ? LdsCfg{224, 256, 2, 4} : LdsCfg{224, 128, 2, 4};
+    }
+    // the width whose tile count fills the CUs best, weighted by the throughput a tile of that
+    // width reaches (measured on the decoder's projections at M = 448: wider tiles re-read less)
+    struct Cand {
+      LdsCfg cf;
+      double eff;
+    };
+    const Cand cands[] = {{{224, 256, 2, 8}, 1.0}, {{224, 224, 7, 2}, 0.97}, {{224, 128, 2, 4}, 0.85},
+                          {{224, 96, 7, 2}, 0.8}};
+    LdsCfg best = cands[0].cf;
+    double best_score = -1.0;
+    for (const Cand& c : cands) {
+      const double score = tile_fill(tm * ((N + c.cf.bn - 1) / c.cf.bn) * splits) * c.eff;
+      if (score > best_score) best_score = score, best = c.cf;
+    }
+    return best;
   }
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256) * splits;
   const int64_t t128 = ((M + 127) / 128) * ((N + 255) / 256) * splits;
@@ -509,6 +530,8 @@ void launch_lds(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, 
   if (cf.bm == 64) FS_LDS_LAUNCH(64, 64, 4, 2, 2);
   else if (cf.bm == 224 && cf.bn == 256 && cf.wgn == 8) FS_LDS_LAUNCH(224, 256, 2, 2, 8, true);
   else if (cf.bm == 224 && cf.bn == 256) FS_LDS_LAUNCH(224, 256, 2, 2, 4);
+  else if (cf.bm == 224 && cf.bn == 224) FS_LDS_LAUNCH(224, 224, 2, 7, 2);
+  else if (cf.bm == 224 && cf.bn == 96) FS_LDS_LAUNCH(224, 96, 3, 7, 2);
   else if (cf.bm == 224) FS_LDS_LAUNCH(224, 128, 3, 2, 4);
   else if (cf.bm == 256) FS_LDS_LAUNCH(256, 256, 2, 4, 2);
   else if (cf.bn == 256) FS_LDS_LAUNCH(128, 256, 3, 2, 4);

@@ -26,7 +26,8 @@ def rel_err(got, ref):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("m,n,k", [(1, 48, 64), (7, 256, 688), (64, 1000, 256), (65, 384, 512), (448, 640, 4096),
                                    (130, 96, 192), (20, 4096, 1024), (100, 2048, 2048),   # these two split K
-                                   (448, 24592, 256)])   # 224 x 256 tiles, a partial last column tile
+                                   (448, 24592, 256),    # 224 x 256 tiles, a partial last column tile
+                                   (448, 28672, 256), (448, 6144, 512), (448, 6000, 512)])   # 224 x 224, 224 x 96
 def test_gemm_matches_fp64(dtype, m, n, k):
     case("gemm", dtype, m, n, k)
     g = torch.Generator().manual_seed(m * 7 + n)
@@ -43,7 +44,8 @@ def test_gemm_matches_fp64(dtype, m, n, k):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("n,k", [(384, 512), (2048, 2048), (24576, 256)])   # (2048, 2048) splits K four ways
+@pytest.mark.parametrize("n,k", [(384, 512), (2048, 2048), (24576, 256),   # (2048, 2048) splits K four ways
+                                 (28672, 256), (6144, 1024)])   # 448 rows: 224 x 224 tiles; 224 x 96, K split in two
 def test_gemm_rows_do_not_depend_on_the_batch(dtype, n, k):
     """A row's result is bit-identical whether it is computed alone, among 64 rows or among 448."""
     case("gemm invariance", dtype, n, k)
