@@ -11,9 +11,10 @@ timed: k draft decode steps, one target verify pass over k+1 tokens, one fused a
 One "step" = one speculative round for the whole batch, replayed from the HIP graph captured for its
 shape (the first round of a shape runs eagerly, the second captures). `value` = committed tokens per
 second (accepted proposals + one target token per sequence per round), inputs resident in HBM.
-`roofline` = the paged verify attention (plan + unit kernel, + combine when a query spans chunks): the
-last timed round's 32 verify-attention launches (each layer's pool, that round's tables and query
-positions) replayed from one HIP graph between HIP events on the launching stream, against 8 TB/s.
+`roofline` = the paged verify attention (the unit kernel per layer, + combine when a query spans chunks,
+and one work plan per pass): the last timed round's 32 verify-attention launches (each layer's pool,
+that round's tables and query positions) replayed from one HIP graph between HIP events on the
+launching stream, against 8 TB/s.
 `cpu_baseline` = the CPU oracle (oracle/reference_cpu.py) timed on this host on one target layer's
 verify pass, one draft layer's decode step, the LM head and the acceptance at the same shapes,
 scaled to a round.
@@ -122,9 +123,9 @@ def accept_bytes(b, k, v, s_logit=2):
 def time_verify_attention(torch, fa, ops, sb, lens, reps=4):
     """Per-launch duration of the verify attention as the timed rounds ran it: the last timed round's
     32 verify-attention launches (every layer's pool, that round's block tables, and its k+1 query
-    positions per sequence, lens = the sequences' lengths before it) captured in one HIP graph, whose
-    replays are bracketed by events on the launching stream. Returns (seconds per launch, algorithmic
-    bytes per launch)."""
+    positions per sequence, lens = the sequences' lengths before it; one work plan for the 32, as a
+    verify pass builds it) captured in one HIP graph, whose replays are bracketed by events on the
+    launching stream. Returns (seconds per launch, algorithmic bytes per launch)."""
     dev = sb.dev
     seqs = sb.active()
     tables = fa.paged.block_table([s.blocks_t for s in seqs], dev)
@@ -135,8 +136,9 @@ def time_verify_attention(torch, fa, ops, sb, lens, reps=4):
     layers = range(CFG["n_layers"])
 
     def launches():
+        step = object()   # the layers of one verify pass share its positions
         for layer in layers:
-            ops.paged_attention(q, sb.pool_t.layout(layer), tables, pos, d ** -0.5, out=out)
+            ops.paged_attention(q, sb.pool_t.layout(layer), tables, pos, d ** -0.5, out=out, plan_key=step)
 
     launches()
     torch.cuda.synchronize()
@@ -522,9 +524,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic("paged_attention_verify_8b.md"),
-                     "kernel": "paged_attention verify: attn_plan_kernel + attn_unit_kernel<128,16>, one call "
-                               "per layer (8192-key chunks: every query of this workload sees one chunk, so no "
-                               "combine launch)",
+                     "kernel": "paged_attention verify: attn_unit_kernel<128,16>, one call per layer, after one "
+                               "attn_plan_kernel per pass (8192-key chunks: every query of this workload sees one "
+                               "chunk, so no combine launch)",
                      "avg_launch_us": round(attn_avg * 1e6, 2),
                      "algorithmic_bytes_per_launch": int(attn_traffic)},
         "accept_kernel": {"avg_us": round(acc_avg * 1e6, 2), "achieved_GBs": round(acc_gbs, 1),

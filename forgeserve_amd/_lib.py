@@ -45,6 +45,12 @@ SIGNATURES = {
                                    c_i32, c_i32, c_i32, c_f32, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p]),
     "fs_paged_attention_varlen": (c_i32, [c_p, c_i64, c_i64, ctypes.POINTER(KVLayout), c_p, c_i64, c_i32, c_p, c_p,
                                           c_i32, c_i32, c_i32, c_f32, c_p, c_i64, c_i64, c_p, c_i64, c_p]),
+    "fs_paged_attention_reuse_plan": (c_i32, [c_p, c_i64, c_i64, c_i64, ctypes.POINTER(KVLayout), c_p, c_i64, c_i32,
+                                              c_p, c_i32, c_i32, c_i32, c_f32, c_p, c_i64, c_i64, c_i64, c_p, c_i64,
+                                              c_p]),
+    "fs_paged_attention_varlen_reuse_plan": (c_i32, [c_p, c_i64, c_i64, ctypes.POINTER(KVLayout), c_p, c_i64, c_i32,
+                                                     c_p, c_p, c_i32, c_i32, c_i32, c_f32, c_p, c_i64, c_i64, c_p,
+                                                     c_i64, c_p]),
     "fs_paged_attention_workspace_size": (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
     "fs_gemm": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i32, c_p, c_i64,
                         c_p]),

@@ -696,11 +696,28 @@ extern "C" int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32
 }
 
 namespace {
+// What the work plan of a call depends on besides the contents of its positions: a call that asks to
+// reuse the plan already in its workspace skips the plan kernel only when all of these match the call
+// that wrote it (on this host thread); the caller vouches that the positions hold the same values.
+struct PlanKey {
+  const void* ws = nullptr;
+  const int32_t* pos = nullptr;
+  const int32_t* row_start = nullptr;
+  hipStream_t stream = nullptr;
+  int32_t B = 0, T = 0, G = 0, split = 0, nsplit = 0;
+  bool direct = false;
+  bool operator==(const PlanKey& o) const {
+    return ws == o.ws && pos == o.pos && row_start == o.row_start && stream == o.stream && B == o.B && T == o.T &&
+           G == o.G && split == o.split && nsplit == o.nsplit && direct == o.direct;
+  }
+};
+thread_local PlanKey last_plan;
+
 int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
                     const int32_t* block_tables, int64_t table_stride, int32_t max_blocks, const int32_t* positions,
                     const int32_t* row_start, int32_t B, int32_t T, int32_t n_heads, float scale, void* out,
                     int64_t o_sb, int64_t o_st, int64_t o_sh, void* workspace, int64_t workspace_bytes,
-                    void* stream) {
+                    void* stream, bool reuse_plan) {
   FS_CHECK_ARG(kv != nullptr && kv->k && kv->v, "paged_attention: null pool");
   FS_CHECK_ARG(q && block_tables && positions && out && workspace, "paged_attention: null pointer");
   FS_CHECK_ARG(B > 0 && T > 0, "paged_attention: B %d T %d", B, T);
@@ -758,7 +775,19 @@ int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, con
     const int64_t qtiles = ((int64_t)T * P.G + QTILE - 1) / QTILE;
     const int64_t units = (int64_t)B * qtiles * P.nsplit * kv->n_kv_heads;
     FS_CHECK_ARG(units < 0x7fffffff, "paged_attention: %lld work units", (long long)units);
-    attn_plan_kernel<<<1, PLAN_THREADS, 0, st>>>(P);
+    PlanKey key;
+    key.ws = workspace;
+    key.pos = positions;
+    key.row_start = row_start;
+    key.stream = st;
+    key.B = B;
+    key.T = T;
+    key.G = P.G;
+    key.split = P.split;
+    key.nsplit = P.nsplit;
+    key.direct = P.direct;
+    if (!(reuse_plan && last_plan == key)) attn_plan_kernel<<<1, PLAN_THREADS, 0, st>>>(P);
+    last_plan = key;
     const unsigned grid = (unsigned)units, threads = 64 * UNIT_WAVES;
     if (kv->head_dim == 128) {
       if (bs16) attn_unit_kernel<128, 16><<<grid, threads, 0, st>>>(P);
@@ -768,6 +797,7 @@ int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, con
       else attn_unit_kernel<64, 0><<<grid, threads, 0, st>>>(P);
     }
   } else {
+    last_plan = PlanKey{};   // no plan on this path
     dim3 grid((unsigned)rows, (unsigned)P.nsplit);
     switch (kv->dtype) {
       case FS_F32: attn_generic_kernel<FS_F32><<<grid, 64, 0, st>>>(P); break;
@@ -793,7 +823,17 @@ extern "C" int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int
                                   void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, void* workspace,
                                   int64_t workspace_bytes, void* stream) {
   return paged_attention(q, q_sb, q_st, q_sh, kv, block_tables, table_stride, max_blocks, positions, nullptr, B, T,
-                         n_heads, scale, out, o_sb, o_st, o_sh, workspace, workspace_bytes, stream);
+                         n_heads, scale, out, o_sb, o_st, o_sh, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int fs_paged_attention_reuse_plan(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                                             const fs_kv_layout* kv, const int32_t* block_tables,
+                                             int64_t table_stride, int32_t max_blocks, const int32_t* positions,
+                                             int32_t B, int32_t T, int32_t n_heads, float scale, void* out,
+                                             int64_t o_sb, int64_t o_st, int64_t o_sh, void* workspace,
+                                             int64_t workspace_bytes, void* stream) {
+  return paged_attention(q, q_sb, q_st, q_sh, kv, block_tables, table_stride, max_blocks, positions, nullptr, B, T,
+                         n_heads, scale, out, o_sb, o_st, o_sh, workspace, workspace_bytes, stream, true);
 }
 
 extern "C" int fs_paged_attention_varlen(const void* q, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
@@ -803,5 +843,17 @@ extern "C" int fs_paged_attention_varlen(const void* q, int64_t q_st, int64_t q_
                                          int64_t o_sh, void* workspace, int64_t workspace_bytes, void* stream) {
   FS_CHECK_ARG(cu_seqlens, "paged_attention_varlen: null cu_seqlens");
   return paged_attention(q, 0, q_st, q_sh, kv, block_tables, table_stride, max_blocks, positions, cu_seqlens, S, T,
-                         n_heads, scale, out, 0, o_st, o_sh, workspace, workspace_bytes, stream);
+                         n_heads, scale, out, 0, o_st, o_sh, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int fs_paged_attention_varlen_reuse_plan(const void* q, int64_t q_st, int64_t q_sh,
+                                                    const fs_kv_layout* kv, const int32_t* block_tables,
+                                                    int64_t table_stride, int32_t max_blocks,
+                                                    const int32_t* positions, const int32_t* cu_seqlens, int32_t S,
+                                                    int32_t T, int32_t n_heads, float scale, void* out,
+                                                    int64_t o_st, int64_t o_sh, void* workspace,
+                                                    int64_t workspace_bytes, void* stream) {
+  FS_CHECK_ARG(cu_seqlens, "paged_attention_varlen: null cu_seqlens");
+  return paged_attention(q, 0, q_st, q_sh, kv, block_tables, table_stride, max_blocks, positions, cu_seqlens, S, T,
+                         n_heads, scale, out, 0, o_st, o_sh, workspace, workspace_bytes, stream, true);
 }

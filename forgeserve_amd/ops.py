@@ -297,11 +297,26 @@ def paged_gather(layout: KVLayout, tables: torch.Tensor, dtype, device) -> Tuple
     return k_all, v_all
 
 
+# The plan key and positions tensor of the last paged-attention call (held, so that no later object
+# can share their identities).
+_PLAN_KEY = [None, None]
+
+
+def _reuse_plan(plan_key, positions: torch.Tensor) -> bool:
+    """True when the previous paged-attention call carried the same plan key and the same positions
+    tensor (the layers of one step)."""
+    reuse = plan_key is not None and _PLAN_KEY[0] is plan_key and _PLAN_KEY[1] is positions
+    _PLAN_KEY[0], _PLAN_KEY[1] = plan_key, positions
+    return reuse
+
+
 def paged_attention(q: torch.Tensor, layout: KVLayout, tables: torch.Tensor, positions: torch.Tensor,
-                    scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    scale: float, out: Optional[torch.Tensor] = None, plan_key=None) -> torch.Tensor:
     """Causal GQA attention of q (B, T, n_heads, head_dim) over the paged keys (model.py:70-76).
 
-    positions: int32 (B, T); query (b, t) sees the keys at positions 0..positions[b, t]."""
+    positions: int32 (B, T); query (b, t) sees the keys at positions 0..positions[b, t].
+    plan_key: an object that stands for these positions (the forward step): consecutive calls with the
+    same key reuse the work plan of the first (the positions must not change between them)."""
     require_device(q, tables, positions)
     b, t, h, d = q.shape
     if q.stride(3) != 1:
@@ -319,9 +334,10 @@ def paged_attention(q: torch.Tensor, layout: KVLayout, tables: torch.Tensor, pos
     if timing:
         ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         ev[0].record()
-    check(lib.fs_paged_attention(ptr(q), q.stride(0), q.stride(1), q.stride(2), layout, ptr(tables),
-                                 tables.stride(0), nb, ptr(positions), b, t, h, float(scale), ptr(out), out.stride(0),
-                                 out.stride(1), out.stride(2), ptr(ws), ws.numel(), stream_ptr()), "paged_attention")
+    fn = lib.fs_paged_attention_reuse_plan if _reuse_plan(plan_key, positions) else lib.fs_paged_attention
+    check(fn(ptr(q), q.stride(0), q.stride(1), q.stride(2), layout, ptr(tables), tables.stride(0), nb, ptr(positions),
+             b, t, h, float(scale), ptr(out), out.stride(0), out.stride(1), out.stride(2), ptr(ws), ws.numel(),
+             stream_ptr()), "paged_attention")
     if timing:
         ev[1].record()
         ATTN_EVENTS.append(ev)
@@ -329,11 +345,13 @@ def paged_attention(q: torch.Tensor, layout: KVLayout, tables: torch.Tensor, pos
 
 
 def paged_attention_varlen(q: torch.Tensor, layout: KVLayout, tables: torch.Tensor, positions: torch.Tensor,
-                           cu_seqlens: torch.Tensor, scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                           cu_seqlens: torch.Tensor, scale: float, out: Optional[torch.Tensor] = None,
+                           plan_key=None) -> torch.Tensor:
     """paged_attention over packed sequences: q (n_tokens, n_heads, head_dim); sequence s owns tokens
     cu_seqlens[s] .. cu_seqlens[s+1]-1 (int32 (S+1,), on the device; the caller guarantees the bounds:
     cu_seqlens[S] <= n_tokens and no sequence longer than T); positions int32 (S, T), -1 past a
-    sequence's tokens; tables int32 (S, max_blocks). Returns out (n_tokens, n_heads, head_dim)."""
+    sequence's tokens; tables int32 (S, max_blocks). Returns out (n_tokens, n_heads, head_dim).
+    plan_key: as for paged_attention."""
     require_device(q, tables, positions, cu_seqlens)
     n, h, d = q.shape
     if q.stride(2) != 1:
@@ -348,10 +366,11 @@ def paged_attention_varlen(q: torch.Tensor, layout: KVLayout, tables: torch.Tens
     nb = tables.shape[1]
     lib = _lib.load()
     ws = _persistent_ws("attention", lib.fs_paged_attention_workspace_size(s, t, h, d, nb, layout.block_size), q.device)
-    check(lib.fs_paged_attention_varlen(ptr(q), q.stride(0), q.stride(1), layout, ptr(tables), tables.stride(0), nb,
-                                        ptr(positions), ptr(cu_seqlens.contiguous()), s, t, h, float(scale), ptr(out),
-                                        out.stride(0), out.stride(1), ptr(ws), ws.numel(), stream_ptr()),
-          "paged_attention_varlen")
+    fn = (lib.fs_paged_attention_varlen_reuse_plan if _reuse_plan(plan_key, positions)
+          else lib.fs_paged_attention_varlen)
+    check(fn(ptr(q), q.stride(0), q.stride(1), layout, ptr(tables), tables.stride(0), nb, ptr(positions),
+             ptr(cu_seqlens.contiguous()), s, t, h, float(scale), ptr(out), out.stride(0), out.stride(1), ptr(ws),
+             ws.numel(), stream_ptr()), "paged_attention_varlen")
     return out
 
 

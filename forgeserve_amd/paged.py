@@ -179,6 +179,11 @@ class PagedLayerView:
     def length(self) -> int:
         raise NotImplementedError("paged views need explicit positions")
 
+    @property
+    def plan_key(self):
+        """The step this view belongs to: every layer of it attends with the same tables and positions."""
+        return self._step
+
     def update(self, k: torch.Tensor, v: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
         """Write k, v (B, n_kv_heads, T, head_dim) at their positions, then return every table block of
         every row in table order, (B, n_kv_heads, max_blocks*block_size, head_dim)."""

@@ -125,6 +125,23 @@ int fs_paged_attention_varlen(const void* q, int64_t q_st, int64_t q_sh, const f
 int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32_t n_heads, int32_t head_dim,
                                           int32_t max_blocks, int32_t block_size);
 
+/* fs_paged_attention / fs_paged_attention_varlen for the second and later layers of one forward step:
+ * every layer of a step attends with the same positions and tables (model.py:69-76 per Block, under one
+ * engine step), so the work plan the first layer's call left in the workspace is taken as it is. The
+ * plan is recomputed anyway unless the previous call on this host thread used the same workspace,
+ * positions (and cu_seqlens), stream, B (S), T, n_heads and output alignment; the caller guarantees
+ * that the positions still hold the values that call saw. Same arguments and results otherwise. */
+int fs_paged_attention_reuse_plan(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
+                                  const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                                  const int32_t* positions, int32_t B, int32_t T, int32_t n_heads, float scale,
+                                  void* out, int64_t o_sb, int64_t o_st, int64_t o_sh, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
+int fs_paged_attention_varlen_reuse_plan(const void* q, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
+                                         const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                                         const int32_t* positions, const int32_t* cu_seqlens, int32_t S,
+                                         int32_t T, int32_t n_heads, float scale, void* out, int64_t o_st,
+                                         int64_t o_sh, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------------------------- */
 /* Dense ops of the decoder (model.py)                                                              */
 /* ---------------------------------------------------------------------------------------------- */

@@ -300,6 +300,50 @@ def test_attention_long_verify_equals_decode_bitwise():
         assert torch.equal(one[:, 0], full[:, i]), i
 
 
+def test_attention_plan_reuse_equals_fresh_plan():
+    """The layers of a step reuse the first layer's work plan (plan_key): every layer's output is
+    bit-identical to a call that builds its own plan; a call with other positions under the same key,
+    or the reuse entry point called after a call with other positions, builds a new plan."""
+    case("attention plan reuse")
+    from forgeserve_amd import PagedKVPool, ModelConfig, _lib
+    h, hkv, d, bs, t = 8, 2, 128, 16, 7
+    ctx = [300, 9000, 40, 2100]   # 9000 keys span two chunks: the combine path runs too
+    nblocks = sum(-(-c // bs) for c in ctx) + 2
+    q, k, v, tables, pos = _paged_case(len(ctx), t, h, hkv, d, bs, ctx, nblocks, torch.bfloat16, 77)
+    cfg = ModelConfig(vocab_size=8, d_model=h * d, n_layers=3, n_heads=h, n_kv_heads=hkv, max_seq_len=16)
+    pool = PagedKVPool(cfg, nblocks, bs, dtype=torch.bfloat16, device=DEV)
+    g = torch.Generator().manual_seed(5)
+    for layer in range(3):
+        pool.k[layer].copy_((k.float() + layer).bfloat16().to(DEV))
+        pool.v[layer].copy_(torch.randn(v.shape, generator=g).bfloat16().to(DEV))
+    qs = [(q.float() * (layer + 1)).bfloat16().to(DEV) for layer in range(3)]
+    tab, p32 = tables.int().to(DEV), pos.int().to(DEV)
+    sc = 1.0 / math.sqrt(d)
+    fresh = [ops.paged_attention(qs[layer], pool.layout(layer), tab, p32, sc) for layer in range(3)]
+    key = object()
+    reused = [ops.paged_attention(qs[layer], pool.layout(layer), tab, p32, sc, plan_key=key) for layer in range(3)]
+    for a, b in zip(fresh, reused):
+        assert torch.equal(a, b)
+    # same key, other positions (one query per row at the last position): a new plan
+    p1 = p32[:, -1:].contiguous()
+    one = ops.paged_attention(qs[0][:, -1:].contiguous(), pool.layout(0), tab, p1, sc, plan_key=key)
+    assert torch.equal(one, ops.paged_attention(qs[0][:, -1:].contiguous(), pool.layout(0), tab, p1, sc))
+    # the reuse entry point right after a call with other positions builds its own plan
+    p2 = (p32 - 5).contiguous()
+    want = ops.paged_attention(qs[1], pool.layout(1), tab, p2, sc)
+    ops.paged_attention(qs[0], pool.layout(0), tab, p32, sc)
+    lib = _lib.load()
+    out = torch.empty_like(want)
+    nb = tab.shape[1]
+    ws = ops._persistent_ws("attention", lib.fs_paged_attention_workspace_size(len(ctx), t, h, d, nb, bs), DEV)
+    qq = qs[1]
+    ops.check(lib.fs_paged_attention_reuse_plan(ops.ptr(qq), qq.stride(0), qq.stride(1), qq.stride(2), pool.layout(1),
+                                                ops.ptr(tab), tab.stride(0), nb, ops.ptr(p2), len(ctx), t, h, sc,
+                                                ops.ptr(out), out.stride(0), out.stride(1), out.stride(2), ops.ptr(ws),
+                                                ws.numel(), ops.stream_ptr()), "reuse")
+    assert torch.equal(out, want)
+
+
 def _packed(xs, lens, cu):
     """Dense (S, T, ...) rows -> packed (sum(lens), ...) tokens."""
     return torch.cat([xs[i, :n] for i, n in enumerate(lens)], 0)
