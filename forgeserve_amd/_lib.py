@@ -38,6 +38,8 @@ SIGNATURES = {
                                   ctypes.POINTER(KVLayout), c_p, c_i64, c_p]),
     "fs_qkv_rope_write_varlen": (c_i32, [c_p, c_i64, c_i64, c_i32, c_p, c_p, c_i32, c_p, c_p, c_i32, c_p, c_i64, c_i32,
                                          ctypes.POINTER(KVLayout), c_p, c_i64, c_p]),
+    "fs_qkv_rope_write_partials": (c_i32, [c_p, c_i32, c_i64, c_i64, c_i32, c_i32, c_p, c_p, c_p, c_p, c_i32, c_p,
+                                           c_i64, c_i32, ctypes.POINTER(KVLayout), c_p, c_i64, c_p]),
     "fs_paged_kv_write": (c_i32, [c_p, c_p, c_i64, c_i64, c_i64, c_i32, c_i32, c_p, c_p, c_i64, c_i32,
                                   ctypes.POINTER(KVLayout), c_p]),
     "fs_paged_gather": (c_i32, [ctypes.POINTER(KVLayout), c_p, c_i64, c_i32, c_i32, c_p, c_p, c_p]),

@@ -56,9 +56,43 @@ FS_DEVICE u32x4_t pack8(const float (&v)[8]) {
 // The same as qkv_rope_write_kernel for 16-bit dtypes whose rows split into 16-byte groups (D/2 % 8 == 0,
 // aligned rows, slot-major keys): a thread rotates 8 pairs at once (two 16-byte loads of the halves,
 // 16-byte loads of cos/sin, 16-byte stores of q and k); values keep the dim-major element stores.
-template <int DT>
+// Eight consecutive qkv elements as floats: the 16-bit row itself, or (PART) the split-K partials of
+// the QKV projection [splits][rows][cols] added in increasing split order and rounded to DT, exactly the
+// values the GEMM's own reduction would have stored.
+struct QkvPart {
+  const float* part;   // null: read the 16-bit qkv rows
+  int32_t splits;
+  int64_t stride;      // elements between consecutive splits (rows * cols)
+};
+
+template <int DT, bool PART>
+FS_DEVICE void load8(const uint16_t* qkv, const QkvPart& pp, int64_t e, float (&v)[8]) {
+  if (!PART) {
+    unpack8<DT>(*reinterpret_cast<const u32x4_t*>(qkv + e), v);
+    return;
+  }
+  float4_t a = *reinterpret_cast<const float4_t*>(pp.part + e);
+  float4_t b = *reinterpret_cast<const float4_t*>(pp.part + e + 4);
+  for (int sp = 1; sp < pp.splits; ++sp) {
+    const float4_t a2 = *reinterpret_cast<const float4_t*>(pp.part + sp * pp.stride + e);
+    const float4_t b2 = *reinterpret_cast<const float4_t*>(pp.part + sp * pp.stride + e + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[j] += a2[j];
+      b[j] += b2[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] = Elem<DT>::round(a[j]);
+    v[j + 4] = Elem<DT>::round(b[j]);
+  }
+}
+
+template <int DT, bool PART = false>
 __global__ void __launch_bounds__(256) qkv_rope_write_vec_kernel(
-    const uint16_t* __restrict__ qkv, int64_t qkv_stride, int32_t T, int32_t H, const int32_t* __restrict__ positions,
+    const uint16_t* __restrict__ qkv, QkvPart pp, int64_t qkv_stride, int32_t T, int32_t H,
+    const int32_t* __restrict__ positions,
     const int32_t* __restrict__ slots, const int32_t* __restrict__ token_row, int32_t n_rows,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
     int32_t rope_len, const int32_t* __restrict__ table, int64_t table_stride, int32_t max_blocks, fs_kv_layout kv,
@@ -74,7 +108,7 @@ __global__ void __launch_bounds__(256) qkv_rope_write_vec_kernel(
   int slot = 0;
   const int wpos = slots ? slots[m] : pos;
   const bool write_ok = rot_ok && slot_of(wpos, table, table_stride, b, max_blocks, kv, blk, slot);
-  const uint16_t* row = qkv + m * qkv_stride;
+  const int64_t row0 = m * qkv_stride;   // the token's first element (of qkv, or of each partial)
   uint16_t* kp = reinterpret_cast<uint16_t*>(kv.k);
   uint16_t* vp = reinterpret_cast<uint16_t*>(kv.v);
   const int ng = half / 8;
@@ -83,8 +117,8 @@ __global__ void __launch_bounds__(256) qkv_rope_write_vec_kernel(
   for (int i = threadIdx.x; i < n_groups; i += blockDim.x) {
     const int head = i / ng, p0 = 8 * (i - head * ng);
     float x1[8], x2[8], c[8], sn[8], o1[8], o2[8];
-    unpack8<DT>(*reinterpret_cast<const u32x4_t*>(row + (int64_t)head * D + p0), x1);
-    unpack8<DT>(*reinterpret_cast<const u32x4_t*>(row + (int64_t)head * D + p0 + half), x2);
+    load8<DT, PART>(qkv, pp, row0 + (int64_t)head * D + p0, x1);
+    load8<DT, PART>(qkv, pp, row0 + (int64_t)head * D + p0 + half, x2);
     const float4_t c0 = *reinterpret_cast<const float4_t*>(rope_cos + cs + p0);
     const float4_t c1 = *reinterpret_cast<const float4_t*>(rope_cos + cs + p0 + 4);
     const float4_t s0 = *reinterpret_cast<const float4_t*>(rope_sin + cs + p0);
@@ -111,10 +145,17 @@ __global__ void __launch_bounds__(256) qkv_rope_write_vec_kernel(
   }
   if (write_ok) {
     const int nv = Hkv * D / 8;
-    const uint16_t* vrow = row + (int64_t)(H + Hkv) * D;
+    const int64_t vrow = row0 + (int64_t)(H + Hkv) * D;
     for (int i = threadIdx.x; i < nv; i += blockDim.x) {
       const int e0 = 8 * i, h = e0 / D, d0 = e0 - h * D;
-      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(vrow + e0);
+      u32x4_t w;
+      if (PART) {
+        float x[8];
+        load8<DT, true>(qkv, pp, vrow + e0, x);
+        w = pack8<DT>(x);
+      } else {
+        w = *reinterpret_cast<const u32x4_t*>(qkv + vrow + e0);
+      }
       uint16_t* vo = vp + blk * kv.v_block + h * kv.v_head + slot * kv.v_slot + d0 * kv.v_dim;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -252,9 +293,11 @@ int qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_
                    const int32_t* positions, const int32_t* slots, const int32_t* token_row, int32_t n_rows,
                    const float* rope_cos,
                    const float* rope_sin, int32_t rope_len, const int32_t* block_tables, int64_t table_stride,
-                   int32_t max_blocks, const fs_kv_layout* kv, void* q_out, int64_t q_stride, void* stream) {
+                   int32_t max_blocks, const fs_kv_layout* kv, void* q_out, int64_t q_stride, void* stream,
+                   QkvPart pp = QkvPart{nullptr, 0, 0}) {
   if (int e = check_layout(kv)) return e;
-  FS_CHECK_ARG(qkv && positions && rope_cos && rope_sin && block_tables && q_out, "qkv_rope_write: null pointer");
+  FS_CHECK_ARG((qkv || pp.part) && positions && rope_cos && rope_sin && block_tables && q_out,
+               "qkv_rope_write: null pointer");
   FS_CHECK_ARG(T > 0 && n_tokens >= 0 && n_tokens % T == 0, "qkv_rope_write: n_tokens %lld not a multiple of T %d",
                (long long)n_tokens, T);
   FS_CHECK_ARG(n_heads > 0 && n_heads % kv->n_kv_heads == 0, "qkv_rope_write: n_heads %d vs n_kv_heads %d", n_heads,
@@ -266,17 +309,32 @@ int qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_
   hipStream_t s = fs::as_stream(stream);
   dim3 grid((unsigned)n_tokens);
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  if (kv->dtype != FS_F32 && (kv->head_dim / 2) % 8 == 0 && kv->head_dim % 2 == 0 && qkv_stride % 8 == 0 &&
-      q_stride % 8 == 0 && kv->k_dim == 1 && kv->k_slot % 8 == 0 && kv->k_head % 8 == 0 && kv->k_block % 8 == 0 &&
-      al16(qkv) && al16(q_out) && al16(kv->k) && al16(rope_cos) && al16(rope_sin)) {
-    if (kv->dtype == FS_BF16)
-      qkv_rope_write_vec_kernel<FS_BF16><<<grid, 256, 0, s>>>((const uint16_t*)qkv, qkv_stride, T, n_heads, positions,
-                                                              slots, token_row, n_rows, rope_cos, rope_sin, rope_len, block_tables,
-                                                              table_stride, max_blocks, *kv, (uint16_t*)q_out, q_stride);
-    else
-      qkv_rope_write_vec_kernel<FS_F16><<<grid, 256, 0, s>>>((const uint16_t*)qkv, qkv_stride, T, n_heads, positions,
-                                                             slots, token_row, n_rows, rope_cos, rope_sin, rope_len, block_tables,
-                                                             table_stride, max_blocks, *kv, (uint16_t*)q_out, q_stride);
+  const bool vec = kv->dtype != FS_F32 && (kv->head_dim / 2) % 8 == 0 && kv->head_dim % 2 == 0 &&
+                   qkv_stride % 8 == 0 && q_stride % 8 == 0 && kv->k_dim == 1 && kv->k_slot % 8 == 0 &&
+                   kv->k_head % 8 == 0 && kv->k_block % 8 == 0 && al16(pp.part ? (const void*)pp.part : qkv) &&
+                   al16(q_out) && al16(kv->k) && al16(rope_cos) && al16(rope_sin);
+  if (pp.part) {   // the partials are read by the vectorised kernel only
+    FS_CHECK_ARG(vec && pp.splits >= 1 && pp.stride >= n_tokens * qkv_stride,
+                 "qkv_rope_write_partials: needs 16-bit data, head_dim/2 %% 8 == 0, 16-byte aligned rows");
+#define FS_VEC(DT)                                                                                                 \
+  qkv_rope_write_vec_kernel<DT, true><<<grid, 256, 0, s>>>(nullptr, pp, qkv_stride, T, n_heads, positions, slots,     \
+                                                           token_row, n_rows, rope_cos, rope_sin, rope_len,          \
+                                                           block_tables, table_stride, max_blocks, *kv,              \
+                                                           (uint16_t*)q_out, q_stride)
+    if (kv->dtype == FS_BF16) FS_VEC(FS_BF16);
+    else FS_VEC(FS_F16);
+#undef FS_VEC
+    return fs::launch_status("qkv_rope_write_partials");
+  }
+  if (vec) {
+#define FS_VEC(DT)                                                                                                 \
+  qkv_rope_write_vec_kernel<DT><<<grid, 256, 0, s>>>((const uint16_t*)qkv, pp, qkv_stride, T, n_heads, positions,   \
+                                                     slots, token_row, n_rows, rope_cos, rope_sin, rope_len,         \
+                                                     block_tables, table_stride, max_blocks, *kv, (uint16_t*)q_out,  \
+                                                     q_stride)
+    if (kv->dtype == FS_BF16) FS_VEC(FS_BF16);
+    else FS_VEC(FS_F16);
+#undef FS_VEC
     return fs::launch_status("qkv_rope_write");
   }
 #define FS_LAUNCH(DT)                                                                                        \
@@ -301,6 +359,17 @@ extern "C" int fs_qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_
                                  int64_t q_stride, void* stream) {
   return qkv_rope_write(qkv, qkv_stride, n_tokens, T, n_heads, positions, slots, nullptr, 0, rope_cos, rope_sin,
                         rope_len, block_tables, table_stride, max_blocks, kv, q_out, q_stride, stream);
+}
+
+extern "C" int fs_qkv_rope_write_partials(const float* parts, int32_t splits, int64_t n_tokens, int64_t n_cols,
+                                          int32_t T, int32_t n_heads, const int32_t* positions, const int32_t* slots,
+                                          const float* rope_cos, const float* rope_sin, int32_t rope_len,
+                                          const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                                          const fs_kv_layout* kv, void* q_out, int64_t q_stride, void* stream) {
+  FS_CHECK_ARG(parts && splits >= 1 && n_cols > 0, "qkv_rope_write_partials: parts / splits %d", splits);
+  return qkv_rope_write(nullptr, n_cols, n_tokens, T, n_heads, positions, slots, nullptr, 0, rope_cos, rope_sin,
+                        rope_len, block_tables, table_stride, max_blocks, kv, q_out, q_stride, stream,
+                        QkvPart{parts, splits, n_tokens * n_cols});
 }
 
 extern "C" int fs_qkv_rope_write_varlen(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_t n_heads,

@@ -97,16 +97,16 @@ class Attention(nn.Module):
 
     def attend(self, h: torch.Tensor, b: int, t: int, pos32: torch.Tensor, view, rope) -> torch.Tensor:
         """h (B*T, d) normed input -> attention output (B*T, n_heads*head_dim), before wo."""
-        qkv = ops.gemm(h, self.qkv_weight())
         if getattr(view, "packed", False):   # packed prefill: rows are the step's tokens, no padding
             st = view.step
-            q = ops.qkv_rope_write_varlen(qkv, st.pos_tok, st.token_row, self.nh, rope[0], rope[1], st.tables,
-                                          view.layout)
+            q = ops.qkv_rope_write_varlen(ops.gemm(h, self.qkv_weight()), st.pos_tok, st.token_row, self.nh,
+                                          rope[0], rope[1], st.tables, view.layout)
             o = ops.paged_attention_varlen(q.view(-1, self.nh, self.hd), view.layout, st.tables, st.pos_pad, st.cu,
                                            1.0 / math.sqrt(self.hd), plan_key=st)
             return o.view(-1, self.nh * self.hd)
         layout, tables, slots, mask = view.prepare(b, t, self.nkv, self.hd, h.dtype, h.device, pos32)
-        q = ops.qkv_rope_write(qkv, pos32.reshape(-1), t, self.nh, rope[0], rope[1], tables, layout, slots=slots)
+        q = ops.qkv_rope_gemm(h, self.qkv_weight(), pos32.reshape(-1), t, self.nh, rope[0], rope[1], tables, layout,
+                              slots=slots)
         # the layers of one step share its positions: the attention work plan is built once per step
         o = ops.paged_attention(q.view(b, t, self.nh, self.hd), layout, tables, mask, 1.0 / math.sqrt(self.hd),
                                 plan_key=getattr(view, "plan_key", None))

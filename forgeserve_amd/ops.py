@@ -247,6 +247,35 @@ def qkv_rope_write(qkv: torch.Tensor, positions: torch.Tensor, T: int, n_heads: 
     return q_out
 
 
+def qkv_rope_gemm(h: torch.Tensor, w: torch.Tensor, positions: torch.Tensor, T: int, n_heads: int,
+                  rope_cos: torch.Tensor, rope_sin: torch.Tensor, tables: torch.Tensor, layout: KVLayout,
+                  slots: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """qkv_rope_write(gemm(h, w), ...): the fused QKV projection (model.py:57-60, 64-66) followed by the
+    rotary + pool write. When the projection splits K, the rotary kernel adds the partials itself (no
+    separate reduction pass); the results are the same either way."""
+    require_device(h, w, positions, tables)
+    m, lda = _rows(h)
+    n, ldb = _rows(w)
+    k = h.shape[1]
+    lib = _lib.load()
+    d = layout.head_dim
+    if (h.dtype == torch.bfloat16 and w.dtype == h.dtype and w.shape[1] == k and layout.dtype == _dt(h)
+            and k % 64 == 0 and lda % 8 == 0 and ldb % 8 == 0 and n % 8 == 0 and (d // 2) % 8 == 0
+            and lib.fs_gemm_splits(n, k, _dt(h)) > 1 and positions.dtype == I32 and tables.dtype == I32
+            and (slots is None or slots.dtype == I32)):
+        splits = lib.fs_gemm_splits(n, k, _dt(h))
+        ws = _persistent_ws("gemm", splits * m * n * 4, h.device)
+        check(lib.fs_gemm_partials(ptr(h), lda, ptr(w), ldb, m, n, k, _dt(h), ptr(ws), ws.numel(), stream_ptr()),
+              "gemm_partials")
+        q_out = torch.empty((m, n_heads * d), dtype=h.dtype, device=h.device)
+        check(lib.fs_qkv_rope_write_partials(ptr(ws), splits, m, n, T, n_heads, ptr(positions), ptr(slots),
+                                             ptr(rope_cos), ptr(rope_sin), rope_cos.shape[0], ptr(tables),
+                                             tables.stride(0), tables.shape[1], layout, ptr(q_out), q_out.stride(0),
+                                             stream_ptr()), "qkv_rope_write_partials")
+        return q_out
+    return qkv_rope_write(gemm(h, w), positions, T, n_heads, rope_cos, rope_sin, tables, layout, slots=slots)
+
+
 def qkv_rope_write_varlen(qkv: torch.Tensor, positions: torch.Tensor, token_row: torch.Tensor, n_heads: int,
                           rope_cos: torch.Tensor, rope_sin: torch.Tensor, tables: torch.Tensor, layout: KVLayout,
                           q_out: Optional[torch.Tensor] = None) -> torch.Tensor:

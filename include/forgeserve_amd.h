@@ -88,6 +88,18 @@ int fs_qkv_rope_write_varlen(const void* qkv, int64_t qkv_stride, int64_t n_toke
                              const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
                              const fs_kv_layout* kv, void* q_out, int64_t q_stride, void* stream);
 
+/* fs_qkv_rope_write fed by the split-K partials of the QKV projection instead of its output: parts is
+ * [splits][n_tokens][n_cols] f32 as fs_gemm_partials writes it (n_cols = (n_heads + 2*n_kv_heads) *
+ * head_dim); each element is the partials added in increasing split order and rounded to the pool's
+ * dtype, exactly what fs_gemm would have stored, then rotated and written as fs_qkv_rope_write does.
+ * Replaces the same lines (model.py:64-67, 40-45; paged.py:74-78) with the projection's reduction
+ * (model.py:57-60) folded in. 16-bit pools with head_dim/2 % 8 == 0 and 16-byte aligned data only. */
+int fs_qkv_rope_write_partials(const float* parts, int32_t splits, int64_t n_tokens, int64_t n_cols, int32_t T,
+                               int32_t n_heads, const int32_t* positions, const int32_t* slots,
+                               const float* rope_cos, const float* rope_sin, int32_t rope_len,
+                               const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                               const fs_kv_layout* kv, void* q_out, int64_t q_stride, void* stream);
+
 /* Gather every block of every row's table in table order: paged.py:80-81.
  * k_out, v_out: contiguous [B, n_kv_heads, max_blocks*block_size, head_dim]. */
 int fs_paged_gather(const fs_kv_layout* kv, const int32_t* block_tables, int64_t table_stride, int32_t B,

@@ -376,6 +376,34 @@ def test_attention_varlen_equals_dense(dtype, d, bs, lens, starts):
     assert bool((out[n_tok:] == 7.0).all())
 
 
+@pytest.mark.parametrize("b,t,h,hkv,k", [(64, 1, 8, 2, 1024), (64, 7, 8, 2, 1024), (9, 3, 32, 8, 4096)])
+def test_qkv_rope_gemm_equals_gemm_then_rope(b, t, h, hkv, k):
+    """The QKV projection reduced inside the rotary + pool write (split-K partials added by the rotary
+    kernel) stores the same keys/values and returns the same queries as the projection followed by
+    fs_qkv_rope_write; a padding token (position -1) is neither rotated nor written either way."""
+    case("qkv_rope_gemm", b, t, h, hkv, k)
+    from forgeserve_amd import PagedKVPool, ModelConfig, _lib
+    d, bs = 128, 16
+    n = (h + 2 * hkv) * d
+    assert _lib.load().fs_gemm_splits(n, k, _lib.BF16) > 1   # the fused path is the one under test
+    cfg = ModelConfig(vocab_size=10, d_model=h * d, n_layers=1, n_heads=h, n_kv_heads=hkv, max_seq_len=256)
+    cos, sin = orc.rope_tables(orc.Shape.of(cfg))
+    g = torch.Generator().manual_seed(b * 10 + t)
+    x = torch.randn(b * t, k, generator=g).bfloat16().to(DEV)
+    w = (torch.randn(n, k, generator=g) * 0.03).bfloat16().to(DEV)
+    nb = 12
+    tables = torch.randperm(b * nb, generator=g).reshape(b, nb).int().to(DEV)
+    pos = torch.randint(0, nb * bs - t, (b, 1), generator=g) + torch.arange(t)
+    pos[0, -1] = -1                                   # a padding token
+    pos = pos.int().reshape(-1).to(DEV)
+    pools = [PagedKVPool(cfg, b * nb, bs, dtype=torch.bfloat16, device=DEV) for _ in range(2)]
+    q_two = ops.qkv_rope_write(ops.gemm(x, w), pos, t, h, cos.to(DEV), sin.to(DEV), tables, pools[0].layout(0))
+    q_one = ops.qkv_rope_gemm(x, w, pos, t, h, cos.to(DEV), sin.to(DEV), tables, pools[1].layout(0))
+    assert torch.equal(q_one, q_two)
+    assert torch.equal(pools[1].k_store, pools[0].k_store)
+    assert torch.equal(pools[1].v_store, pools[0].v_store)
+
+
 @pytest.mark.parametrize("dtype,d,bs", [(torch.bfloat16, 128, 16), (torch.float32, 32, 4)])
 def test_qkv_rope_write_varlen_equals_dense(dtype, d, bs):
     """The packed rotary + KV write stores every token where the dense (S, T) call stores it, returns
