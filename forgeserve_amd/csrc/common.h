@@ -62,6 +62,14 @@ template <> struct Elem<FS_F16> {
 // ------------------------------------------------------------------------------------------------
 // wavefront (64-lane) reductions
 // ------------------------------------------------------------------------------------------------
+// silu(g) * u as a 16-bit SwiGLU computes it (model.py:93): silu rounded to the dtype, then the
+// product, which the caller rounds when it stores it; g and u are dtype values. Every kernel that
+// forms this product calls this one function, so their results agree bit for bit.
+template <int DT>
+FS_DEVICE float silu_times(float g, float u) {
+  return Elem<DT>::round(g / (1.0f + expf(-g))) * u;
+}
+
 FS_DEVICE float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -167,7 +167,10 @@ struct RowStatsOut {
   int64_t nparts, ld;
 };
 
-template <int BM, int BN, int NS, int WGM = 2, int WGN = 2, bool STATS = false, bool PRIO = false>
+// SWIGLU: W holds [gate; up] (N/2 rows each) and the tile's output columns are interleaved, column
+// 2j = gate row j and 2j + 1 = up row j, so that each lane's four consecutive columns are two (gate, up)
+// pairs; the epilogue stores silu(gate) * up to C[row][j] (model.py:93) instead of the products.
+template <int BM, int BN, int NS, int WGM = 2, int WGN = 2, bool STATS = false, bool PRIO = false, bool SWIGLU = false>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uint16_t* __restrict__ X, int64_t ldx,
                                                             const uint16_t* __restrict__ W, int64_t ldw,
                                                             uint16_t* __restrict__ C, int64_t ldc,
@@ -215,6 +218,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
     int64_t gr = (in_x ? m0 : n0) + r;
     const int64_t lim = in_x ? M : N;
     gr = gr < lim ? gr : lim - 1;
+    if (SWIGLU && !in_x) gr = (gr & 1) ? N / 2 + (gr >> 1) : (gr >> 1);   // interleaved column -> weight row
     src[i] = in_x ? X + gr * ldx + 8 * c : W + gr * ldw + 8 * c;
   }
   const bool hi = wave < T % NW;
@@ -284,6 +288,25 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
   }
 
   // acc[i][j]: lane (l16, g) holds C[m = 16i + l16][n = 16j + 4g + r], r = 0..3 (wave-local)
+  if (SWIGLU) {   // (no split, no residual on this path; N % 4 == 0)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t row = m0 + wm * WM + 16 * i + l16;
+      if (row >= M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t col0 = n0 + wn * WN + 16 * j + 4 * g;
+        if (col0 >= N) continue;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = Elem<FS_BF16>::round(acc[i][j][r]);
+        const uint32_t h0 = f32_to_bf16(silu_times<FS_BF16>(v[0], v[1]));
+        const uint32_t h1 = f32_to_bf16(silu_times<FS_BF16>(v[2], v[3]));
+        *reinterpret_cast<uint32_t*>(C + row * ldc + col0 / 2) = h0 | (h1 << 16);
+      }
+    }
+    return;
+  }
   if (part) {   // split-K: f32 partial of this k-range, summed in split order by gemm_splitk_reduce_kernel
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -517,25 +540,25 @@ LdsCfg lds_cfg(int64_t M, int64_t N, int splits, bool stats = false) {
   return LdsCfg{128, 128, 2, 4};
 }
 
-template <bool STATS>
+template <bool STATS, bool SWIGLU = false>
 void launch_lds(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c, int64_t ldc,
                 const uint16_t* r, int64_t ldr, int64_t M, int64_t N, int64_t K, int splits, float* part,
                 RowStatsOut rs, hipStream_t s) {
   const LdsCfg cf = lds_cfg(M, N, splits, STATS);
   const int tm = (int)((M + cf.bm - 1) / cf.bm), nt = tm * (int)((N + cf.bn - 1) / cf.bn);
   const dim3 grid((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits);
-#define FS_LDS_LAUNCH(BM_, BN_, NS_, WGM_, WGN_, ...)                                                         \
-  gemm_bf16_lds_kernel<BM_, BN_, NS_, WGM_, WGN_, STATS, ##__VA_ARGS__><<<grid, 64 * WGM_ * WGN_, 0, s>>>(     \
+#define FS_LDS_LAUNCH(BM_, BN_, NS_, WGM_, WGN_, PRIO_)                                                       \
+  gemm_bf16_lds_kernel<BM_, BN_, NS_, WGM_, WGN_, STATS, PRIO_, SWIGLU><<<grid, 64 * WGM_ * WGN_, 0, s>>>(      \
       a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part, rs)
-  if (cf.bm == 64) FS_LDS_LAUNCH(64, 64, 4, 2, 2);
+  if (cf.bm == 64) FS_LDS_LAUNCH(64, 64, 4, 2, 2, false);
   else if (cf.bm == 224 && cf.bn == 256 && cf.wgn == 8) FS_LDS_LAUNCH(224, 256, 2, 2, 8, true);
-  else if (cf.bm == 224 && cf.bn == 256) FS_LDS_LAUNCH(224, 256, 2, 2, 4);
-  else if (cf.bm == 224 && cf.bn == 224) FS_LDS_LAUNCH(224, 224, 2, 7, 2);
-  else if (cf.bm == 224 && cf.bn == 96) FS_LDS_LAUNCH(224, 96, 3, 7, 2);
-  else if (cf.bm == 224) FS_LDS_LAUNCH(224, 128, 3, 2, 4);
-  else if (cf.bm == 256) FS_LDS_LAUNCH(256, 256, 2, 4, 2);
-  else if (cf.bn == 256) FS_LDS_LAUNCH(128, 256, 3, 2, 4);
-  else FS_LDS_LAUNCH(128, 128, 4, 2, 4);
+  else if (cf.bm == 224 && cf.bn == 256) FS_LDS_LAUNCH(224, 256, 2, 2, 4, false);
+  else if (cf.bm == 224 && cf.bn == 224) FS_LDS_LAUNCH(224, 224, 2, 7, 2, false);
+  else if (cf.bm == 224 && cf.bn == 96) FS_LDS_LAUNCH(224, 96, 3, 7, 2, false);
+  else if (cf.bm == 224) FS_LDS_LAUNCH(224, 128, 3, 2, 4, false);
+  else if (cf.bm == 256) FS_LDS_LAUNCH(256, 256, 2, 4, 2, false);
+  else if (cf.bn == 256) FS_LDS_LAUNCH(128, 256, 3, 2, 4, false);
+  else FS_LDS_LAUNCH(128, 128, 4, 2, 4, false);
 #undef FS_LDS_LAUNCH
 }
 
@@ -593,6 +616,22 @@ extern "C" int fs_gemm_partials(const void* A, int64_t lda, const void* B, int64
   launch_lds<false>((const uint16_t*)A, lda, (const uint16_t*)B, ldb, nullptr, 0, nullptr, 0, M, N, K, splits,
                     reinterpret_cast<float*>(partials), RowStatsOut{}, fs::as_stream(stream));
   return fs::launch_status("gemm_partials");
+}
+
+extern "C" int fs_gemm_swiglu(const void* A, int64_t lda, const void* B, int64_t ldb, void* H, int64_t ldh, int64_t M,
+                              int64_t F, int64_t K, int32_t dtype, void* stream) {
+  FS_CHECK_ARG(A && B && H, "gemm_swiglu: null pointer");
+  FS_CHECK_ARG(dtype == FS_BF16, "gemm_swiglu: bf16 only (dtype %d)", dtype);
+  FS_CHECK_ARG(M >= 0 && F > 0 && F % 2 == 0 && 2 * F < 0x7fffffff && K > 0 && lda >= K && ldb >= K && ldh >= F &&
+                   ldh % 2 == 0 && (reinterpret_cast<uintptr_t>(H) & 3) == 0,
+               "gemm_swiglu: M %lld F %lld K %lld (F even, ldh even, H 4-byte aligned)", (long long)M, (long long)F,
+               (long long)K);
+  FS_CHECK_ARG(lds_ok(A, lda, B, ldb, K), "gemm_swiglu: needs K %% 64 == 0 and 16-byte aligned rows");
+  FS_CHECK_ARG(split_for(2 * F, K) == 1, "gemm_swiglu: F %lld K %lld splits K", (long long)F, (long long)K);
+  if (M == 0) return 0;
+  launch_lds<false, true>((const uint16_t*)A, lda, (const uint16_t*)B, ldb, (uint16_t*)H, ldh, nullptr, 0, M, 2 * F, K,
+                          1, nullptr, RowStatsOut{}, fs::as_stream(stream));
+  return fs::launch_status("gemm_swiglu");
 }
 
 extern "C" int64_t fs_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int32_t dtype) {

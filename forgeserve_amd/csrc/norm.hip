@@ -194,7 +194,7 @@ __global__ void __launch_bounds__(256) silu_mul_vec_kernel(const uint16_t* __res
     unpack8<DT>(*reinterpret_cast<const u32x4_t*>(gu + m * ldgu + c), g);
     unpack8<DT>(*reinterpret_cast<const u32x4_t*>(gu + m * ldgu + F + c), u);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = E::round(g[j] / (1.0f + expf(-g[j]))) * u[j];
+    for (int j = 0; j < 8; ++j) o[j] = silu_times<DT>(g[j], u[j]);
     *reinterpret_cast<u32x4_t*>(h + m * ldh + c) = pack8<DT>(o);
   }
 }
@@ -209,8 +209,7 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(const typename Elem<DT>::
     const int64_t m = i / F, n = i - m * F;
     const float gv = E::load(gu, m * ldgu + n);
     const float uv = E::load(gu, m * ldgu + F + n);
-    const float sg = E::round(gv / (1.0f + expf(-gv)));
-    E::store(h, m * ldh + n, sg * uv);
+    E::store(h, m * ldh + n, silu_times<DT>(gv, uv));
   }
 }
 

@@ -4,8 +4,9 @@ Same modules, parameter names and state_dict keys as the reference (RMSNorm, Att
 half-split rotary, SwiGLU, pre-norm blocks, tied embedding/head), so weights load interchangeably.
 The forward runs on the GPU only, as one chain of HIP kernels per layer:
 
-    add_rmsnorm -> gemm(qkv) -> qkv_rope_write (rotary + KV write) -> paged_attention
-      -> gemm(wo, + residual) -> add_rmsnorm -> gemm(gate|up) -> silu_mul -> gemm(w_down, + residual)
+    gemm(qkv) -> qkv_rope_write (rotary + KV write; a split-K projection is reduced here)
+      -> paged_attention -> gemm(wo) -> residual add + mlp RMSNorm
+      -> gemm(gate|up) with the SwiGLU gate in its epilogue -> gemm(w_down) -> residual add + next RMSNorm
 
 q/k/v and gate/up use one fused weight each; the per-projection parameters are re-pointed at slices
 of the fused buffer, so no weight is stored twice.
@@ -129,7 +130,7 @@ class SwiGLU(nn.Module):
     def forward(self, x, residual: Optional[torch.Tensor] = None):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        h = ops.silu_mul(ops.gemm(x2, self.gate_up_weight()))
+        h = ops.gemm_swiglu(x2, self.gate_up_weight())
         r = None if residual is None else residual.reshape(-1, shape[-1])
         return ops.gemm(h, self.w_down.weight, residual=r).reshape(shape)
 
@@ -150,7 +151,7 @@ class Block(nn.Module):
             h = ops.add_rmsnorm(x, self.attn_norm.weight, self.attn_norm.eps)
         a = self.attn.attend(h, b, t, pos32, view, rope)
         x1, h2 = ops.gemm_add_rmsnorm(a, self.attn.wo.weight, x, self.mlp_norm.weight, self.mlp_norm.eps)
-        g = ops.silu_mul(ops.gemm(h2, self.mlp.gate_up_weight()))
+        g = ops.gemm_swiglu(h2, self.mlp.gate_up_weight())
         if next_norm is None:
             return ops.gemm(g, self.mlp.w_down.weight, residual=x1), None
         return ops.gemm_add_rmsnorm(g, self.mlp.w_down.weight, x1, next_norm.weight, next_norm.eps)

@@ -195,6 +195,24 @@ def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, delta: Option
     return y
 
 
+def gemm_swiglu(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """silu_mul(gemm(a, w)) for w the [gate; up] weight (2F, K): h (M, F) = silu(a w_gate^T) * (a w_up^T)
+    (model.py:93). One kernel when the shape allows it (bf16, no K split), else the two; the results
+    are the same either way."""
+    require_device(a, w)
+    m, lda = _rows(a)
+    n2, ldb = _rows(w)
+    k = a.shape[1]
+    f = n2 // 2
+    lib = _lib.load()
+    if (a.dtype == torch.bfloat16 and w.dtype == a.dtype and w.shape[1] == k and n2 % 4 == 0 and k % 64 == 0
+            and lda % 8 == 0 and ldb % 8 == 0 and lib.fs_gemm_splits(n2, k, _dt(a)) == 1):
+        h = torch.empty((m, f), dtype=a.dtype, device=a.device)
+        check(lib.fs_gemm_swiglu(ptr(a), lda, ptr(w), ldb, ptr(h), f, m, f, k, _dt(a), stream_ptr()), "gemm_swiglu")
+        return h
+    return silu_mul(gemm(a, w))
+
+
 def silu_mul(gu: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """silu(gu[:, :F]) * gu[:, F:] (model.py:93)."""
     require_device(gu)

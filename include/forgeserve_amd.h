@@ -223,6 +223,15 @@ int fs_add_rmsnorm(const void* x, int64_t ldx, const void* delta, int64_t ldd, v
 int fs_silu_mul(const void* gu, int64_t ldgu, void* h, int64_t ldh, int64_t M, int64_t F, int32_t dtype,
                 void* stream);
 
+/* The gate|up projection and the SwiGLU gate in one kernel: h = silu(A . B[:F]^T) * (A . B[F:2F]^T)
+ * with B the [gate; up] weight (2F rows of K), each product rounded to bf16 as fs_gemm stores it and
+ * the gate then as fs_silu_mul computes it; bit-identical to fs_gemm followed by fs_silu_mul, without
+ * writing the 2F-wide products. Replaces SwiGLU.forward's w_gate/w_up linears and silu * (model.py:93).
+ * bf16, K % 64 == 0, 16-byte aligned rows, F even, and a shape whose GEMM does not split K
+ * (fs_gemm_splits(2F, K, bf16) == 1). */
+int fs_gemm_swiglu(const void* A, int64_t lda, const void* B, int64_t ldb, void* h, int64_t ldh, int64_t M,
+                   int64_t F, int64_t K, int32_t dtype, void* stream);
+
 /* Embedding lookup (model.py:134-135): out[m] = weight[ids[m]]; ids int64. */
 int fs_embedding(const int64_t* ids, int64_t M, const void* weight, int64_t d_model, int64_t vocab,
                  void* out, int64_t ldo, int32_t dtype, void* stream);

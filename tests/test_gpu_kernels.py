@@ -72,6 +72,22 @@ def test_gemm_residual_epilogue(n, k):
     assert torch.equal(fused, two_step)
 
 
+@pytest.mark.parametrize("m,f,k", [(64, 14336, 4096), (448, 14336, 4096), (1, 8192, 2048), (130, 20000, 256),
+                                   (448, 1000, 256)])
+def test_gemm_swiglu_equals_gemm_then_silu_mul(m, f, k):
+    """The gate|up projection with the SwiGLU gate in its epilogue gives exactly gemm then silu_mul."""
+    case("gemm swiglu", m, f, k)
+    from forgeserve_amd import _lib
+    assert _lib.load().fs_gemm_splits(2 * f, k, _lib.BF16) == 1   # the fused kernel is the one under test
+    g = torch.Generator().manual_seed(m + f)
+    a = torch.randn(m, k, generator=g).bfloat16().to(DEV)
+    w = (torch.randn(2 * f, k, generator=g) * 0.05).bfloat16().to(DEV)
+    fused = ops.gemm_swiglu(a, w)
+    two = ops.silu_mul(ops.gemm(a, w))
+    assert fused.shape == (m, f)
+    assert torch.equal(fused, two)
+
+
 @pytest.mark.parametrize("m,n,k", [(70, 2048, 2048), (448, 4096, 4096), (64, 1024, 7168), (1, 2048, 2048)])
 def test_splitk_add_rmsnorm_equals_gemm_then_norm(m, n, k):
     """A split-K projection reduced inside the residual-add + RMSNorm kernel gives exactly what the
