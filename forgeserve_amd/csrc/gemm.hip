@@ -494,7 +494,7 @@ int split_for(int64_t N, int64_t K) {
   return s;
 }
 
-// The LDS-kernel configuration a shape runs with. M <= 64 (a decode step) takes 64x64 tiles. Larger
+// The LDS-kernel configuration a shape runs with. M <= 64 (a decode step) takes 64-row tiles. Larger
 // M takes 224-row tiles when they pad M less than 128- and 256-row tiles would (the verify pass,
 // M = 64 * 7 = 448, is exactly two), else 256- or 128-row tiles. Every configuration runs the same
 // MFMA over the same k order, so the tile shape never changes a result.
@@ -509,7 +509,8 @@ double tile_fill(int64_t tiles) {
 }
 
 LdsCfg lds_cfg(int64_t M, int64_t N, int splits, bool stats = false) {
-  if (M <= 64) return LdsCfg{64, 64, 2, 2};
+  // 64-row tiles; very wide outputs (an LM head) take 128 columns per tile, still 32 per wave
+  if (M <= 64) return N * splits >= 65536 ? LdsCfg{64, 128, 2, 4} : LdsCfg{64, 64, 2, 2};
   auto pad = [&](int64_t bm) { return (M + bm - 1) / bm * bm - M; };
   if (pad(224) < pad(128) && pad(224) < pad(256)) {
     const int64_t tm = (M + 223) / 224;
@@ -550,7 +551,8 @@ void launch_lds(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, 
 #define FS_LDS_LAUNCH(BM_, BN_, NS_, WGM_, WGN_, PRIO_)                                                       \
   gemm_bf16_lds_kernel<BM_, BN_, NS_, WGM_, WGN_, STATS, PRIO_, SWIGLU><<<grid, 64 * WGM_ * WGN_, 0, s>>>(      \
       a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part, rs)
-  if (cf.bm == 64) FS_LDS_LAUNCH(64, 64, 4, 2, 2, false);
+  if (cf.bm == 64 && cf.bn == 128) FS_LDS_LAUNCH(64, 128, 4, 2, 4, false);
+  else if (cf.bm == 64) FS_LDS_LAUNCH(64, 64, 4, 2, 2, false);
   else if (cf.bm == 224 && cf.bn == 256 && cf.wgn == 8) FS_LDS_LAUNCH(224, 256, 2, 2, 8, true);
   else if (cf.bm == 224 && cf.bn == 256) FS_LDS_LAUNCH(224, 256, 2, 2, 4, false);
   else if (cf.bm == 224 && cf.bn == 224) FS_LDS_LAUNCH(224, 224, 2, 7, 2, false);

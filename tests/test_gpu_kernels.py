@@ -45,7 +45,8 @@ def test_gemm_matches_fp64(dtype, m, n, k):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("n,k", [(384, 512), (2048, 2048), (24576, 256),   # (2048, 2048) splits K four ways
-                                 (28672, 256), (6144, 1024)])   # 448 rows: 224 x 224 tiles; 224 x 96, K split in two
+                                 (28672, 256), (6144, 1024),   # 448 rows: 224 x 224 tiles; 224 x 96, K split in two
+                                 (70000, 128)])   # 64 rows: 64 x 128 tiles
 def test_gemm_rows_do_not_depend_on_the_batch(dtype, n, k):
     """A row's result is bit-identical whether it is computed alone, among 64 rows or among 448."""
     case("gemm invariance", dtype, n, k)
@@ -617,7 +618,8 @@ def _records(m, s, av, ai):
     return torch.cat([f, ai.to(torch.int32)[..., None]], -1).contiguous()
 
 
-@pytest.mark.parametrize("m,n,k", [(64, 5003, 256), (100, 4096, 128), (448, 6000, 256), (448, 25000, 128)])
+@pytest.mark.parametrize("m,n,k", [(64, 5003, 256), (100, 4096, 128), (448, 6000, 256), (448, 25000, 128),
+                                   (64, 70003, 128)])   # 64 x 128 tiles
 def test_gemm_row_stats(m, n, k):
     """The head GEMM's statistics epilogue, merged per row, against torch on the stored logits:
     max and argmax exact, the sum of exponentials within float rounding."""
