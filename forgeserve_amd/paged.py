@@ -33,12 +33,14 @@ class BlockList(list):
     converting Python ints. Appends (`+=`, `extend`, `append`) keep the copy current; any other
     mutation marks the copy stale and the next `array()` rebuilds it."""
 
-    __slots__ = ("_arr", "_n")
+    __slots__ = ("_arr", "_n", "_ver")
 
     def __init__(self, blocks: Iterable[int] = ()):
         super().__init__(blocks)
         self._arr = np.array(self, dtype=np.int32)
         self._n = len(self)
+        self._ver = 0   # bumped by every mutation other than an append: a copy of a prefix is still valid
+                        # while the version is unchanged
 
     def __iadd__(self, other):
         other = list(other)
@@ -62,6 +64,7 @@ class BlockList(list):
     def _stale(name):
         def f(self, *a, **kw):
             self._n = -1
+            self._ver += 1
             return getattr(list, name)(self, *a, **kw)
         f.__name__ = name
         return f
@@ -76,6 +79,11 @@ class BlockList(list):
     sort = _stale("sort")
     reverse = _stale("reverse")
     del _stale
+
+    @property
+    def version(self) -> int:
+        """Changes whenever an entry already in the list may have changed (appends keep it)."""
+        return self._ver
 
     def array(self) -> np.ndarray:
         """The ids as an int32 array (a view: valid until the list changes)."""

@@ -181,7 +181,9 @@ class _RoundState:
         km = k if n_shared else max(k - 1, 0)
         spans = [("ids", np.int64, (b, 2)), ("last", np.int64, (b,)), ("keff", np.int32, (b,)), ("pos0", np.int32, (b, 2)),
                  ("posd", np.int32, (km, b)), ("posv", np.int32, (b, k + 1)), ("tab_t", np.int32, (b, wt)),
-                 ("tab_d", np.int32, (b, wd)), ("temps", np.float32, (2, b))]
+                 ("temps", np.float32, (2, b))]
+        if not n_shared:   # a draft on the target's cache reads the target's table
+            spans.append(("tab_d", np.int32, (b, wd)))
         off, lay = 0, {}
         for name, dt, shape in spans:
             nbytes = int(np.prod(shape)) * np.dtype(dt).itemsize
@@ -195,6 +197,13 @@ class _RoundState:
         for name, (o, nbytes, dt, shape) in lay.items():
             self.h[name] = hn[o: o + nbytes].view(dt).reshape(shape)
             self.d[name] = self.dev[o: o + nbytes].view(tdt[dt]).view(shape)
+        if n_shared:
+            self.d["tab_d"] = self.d["tab_t"]
+        self.h["tab_t"].fill(0)
+        if "tab_d" in lay:
+            self.h["tab_d"].fill(0)
+        # what each table row of the host staging holds: (block list, its version, entries copied)
+        self._staged = {}
         kk = max(k, 1)
         self.u = torch.zeros((b, kk), dtype=torch.float32, device=dev)
         self.e = torch.ones((b, v), dtype=torch.float32, device=dev)
@@ -239,12 +248,31 @@ class _RoundState:
         h["temps"].fill(0)
         h["temps"][0, :b] = temps
         h["temps"][1, :b] = [np.float32(1.0 / t) if t > 0 else 0.0 for t in temps]
-        for name, lists in (("tab_t", blocks_t), ("tab_d", blocks_d)):
-            tab = h[name]
-            tab.fill(0)
+        tables = (("tab_t", blocks_t),) if self.n_shared else (("tab_t", blocks_t), ("tab_d", blocks_d))
+        for name, lists in tables:
+            # rows keep last round's entries: a row whose block list only grew gets its new blocks
+            tab, prev, rows = h[name], self._staged.get(name, ()), []
             for r, x in enumerate(lists):
-                a = x.array() if isinstance(x, BlockList) else np.asarray(x, dtype=np.int32)
-                tab[r, : a.shape[0]] = a
+                p = prev[r] if r < len(prev) else None
+                if isinstance(x, BlockList):
+                    a, ver = x.array(), x.version
+                    m = a.shape[0]
+                    if p is not None and p[0] is x and p[1] == ver and p[2] <= m:
+                        if m > p[2]:
+                            tab[r, p[2]: m] = a[p[2]:]
+                    else:
+                        tab[r, :m] = a
+                        tab[r, m:] = 0
+                    rows.append((x, ver, m))
+                else:
+                    a = np.asarray(x, dtype=np.int32)
+                    tab[r, : a.shape[0]] = a
+                    tab[r, a.shape[0]:] = 0
+                    rows.append((None, 0, a.shape[0]))
+            for r in range(len(lists), len(prev)):   # rows of sequences that left the batch
+                if prev[r][2]:
+                    tab[r] = 0
+            self._staged[name] = rows
 
 
 def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _RoundState, phase: int):
