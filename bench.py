@@ -23,7 +23,8 @@ scaled to a round.
 
 Kernel-only modes (one JSON line each, used for the rocprofv3 counter runs):
     python bench.py --kernel attention   the verify attention alone: B=64, T=7, 32/8 heads, head_dim 128,
-                                         bf16, contexts U[2048,8192], block 16, tables a random permutation
+                                         bf16, contexts U[2048,8192], block 16, tables a random permutation;
+                                         the calls share one work plan (built by the first warm-up call)
     python bench.py --kernel accept      the fused acceptance alone: B=64, k=6, V=128256, bf16 logits
     python bench.py --kernel copy        1 GiB device-to-device copies, f32 and bf16 (counter calibration)
 """
@@ -296,24 +297,29 @@ def time_accept(torch, ops, reps, warmup, with_stats=False):
 
 def time_gemms(torch, ops, model, m, reps=10):
     """One layer's four GEMMs and the LM head at M rows (the verify pass: M = B*(k+1); a draft step:
-    M = B), with the model's own weights: {name: (seconds per call, flops)}."""
-    blk = model.layers[0]
+    M = B), as the round runs them: gate|up with the SwiGLU gate in its epilogue, each call on the
+    next layer's weights (so that, as in a round, the weights stream from HBM rather than the 256 MB
+    last-level cache): {name: (seconds per call, flops)}."""
+    layers = model.layers
     d = model.cfg.d_model
-    shapes = {"qkv": (d, blk.attn.qkv_weight()), "o": (d, blk.attn.wo.weight),
-              "gate_up": (d, blk.mlp.gate_up_weight()), "down": (blk.mlp.w_down.weight.shape[1], blk.mlp.w_down.weight),
-              "head": (d, model.lm_head.weight)}
+    shapes = {"qkv": (d, [b.attn.qkv_weight() for b in layers], ops.gemm),
+              "o": (d, [b.attn.wo.weight for b in layers], ops.gemm),
+              "gate_up": (d, [b.mlp.gate_up_weight() for b in layers], ops.gemm_swiglu),
+              "down": (layers[0].mlp.w_down.weight.shape[1], [b.mlp.w_down.weight for b in layers], ops.gemm),
+              "head": (d, [model.lm_head.weight], ops.gemm)}
     out = {}
-    for name, (kdim, w) in shapes.items():
-        x = torch.randn(m, kdim, device="cuda").to(w.dtype)
-        for _ in range(2):
-            ops.gemm(x, w)
+    for name, (kdim, ws, fn) in shapes.items():
+        x = torch.randn(m, kdim, device="cuda").to(ws[0].dtype)
+        for i in range(2):
+            fn(x, ws[i % len(ws)])
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for a, b in ev:
+        for i, (a, b) in enumerate(ev):
+            w = ws[(i + 2) % len(ws)]
             a.record()
-            ops.gemm(x, w)
+            fn(x, w)
             b.record()
         torch.cuda.synchronize()
-        out[name] = (sum(a.elapsed_time(b) for a, b in ev) / reps * 1e-3, 2.0 * m * kdim * w.shape[0])
+        out[name] = (sum(a.elapsed_time(b) for a, b in ev) / reps * 1e-3, 2.0 * m * kdim * ws[0].shape[0])
     return out
 
 
@@ -361,13 +367,14 @@ def kernel_mode(args):
     if args.kernel == "attention":
         ctxs, pool, q, pos, tab = attention_inputs(torch, fa, args.seed)
         lay = pool.layout(0)
-        for _ in range(warmup):
-            ops.paged_attention(q, lay, tab, pos, 128 ** -0.5)
+        step = object()   # the calls share one work plan, as the layers of one verify pass do
+        for _ in range(max(warmup, 1)):
+            ops.paged_attention(q, lay, tab, pos, 128 ** -0.5, plan_key=step)
         torch.cuda.synchronize()
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         for a, b in ev:
             a.record()
-            ops.paged_attention(q, lay, tab, pos, 128 ** -0.5)
+            ops.paged_attention(q, lay, tab, pos, 128 ** -0.5, plan_key=step)
             b.record()
         torch.cuda.synchronize()
         sec = sum(a.elapsed_time(b) for a, b in ev) / steps * 1e-3
