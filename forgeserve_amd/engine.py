@@ -79,6 +79,23 @@ class _KeyedDraws:
                 e.append(torch.empty(self.v, device=self.dev).exponential_(generator=g))
         return torch.stack(u).contiguous(), torch.stack(e)
 
+    # the same numbers drawn straight into the round's buffers (row r of out is request r's)
+    def draft_into(self, i, out):
+        if any(g is None for g in self.gens):
+            out.fill_(1.0)
+        for r, g in enumerate(self.gens):
+            if g is not None:
+                out[r].exponential_(generator=g)
+
+    def accept_into(self, u, e):
+        if any(g is None for g in self.gens):
+            u.zero_()
+            e.fill_(1.0)
+        for r, g in enumerate(self.gens):
+            if g is not None:
+                u[r, : self.k].uniform_(generator=g)
+                e[r].exponential_(generator=g)
+
 
 class Engine:
     def __init__(self, model: ForgeModel, num_blocks: int, block_size: int = 16, max_batch: int = 8, seed: int = 0,

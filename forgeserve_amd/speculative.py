@@ -136,6 +136,14 @@ class _GeneratorDraws:
         e = torch.empty((self.b, self.v), dtype=torch.float32, device=self.dev).exponential_(generator=self.gen)
         return u[:, : self.k].contiguous(), e
 
+    # the same numbers drawn straight into the round's buffers (contiguous (b, V) / (b, max(k, 1)) slices)
+    def draft_into(self, i, out):
+        out.exponential_(generator=self.gen)
+
+    def accept_into(self, u, e):
+        u.uniform_(generator=self.gen)
+        e.exponential_(generator=self.gen)
+
 
 def shared_layers(target, draft) -> int:
     """How many leading blocks an early-exit draft shares with its target (the same modules, with the
@@ -380,11 +388,16 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     st.stage(tokens, k_eff, temps, blocks_t, blocks_d)
     st.dev.copy_(st.host, non_blocking=True)
     if sampling:
-        for i in range(k):
-            st.noise_d[i, :b].copy_(draws.draft(i))
-        u, e = draws.accept()
-        st.u[:b, :k].copy_(u)
-        st.e[:b].copy_(e)
+        if hasattr(draws, "draft_into"):
+            for i in range(k):
+                draws.draft_into(i, st.noise_d[i, :b])
+            draws.accept_into(st.u[:b], st.e[:b])
+        else:
+            for i in range(k):
+                st.noise_d[i, :b].copy_(draws.draft(i))
+            u, e = draws.accept()
+            st.u[:b, :k].copy_(u)
+            st.e[:b].copy_(e)
 
     if not graphs or st.uses == 0:
         for phase in range(k + 1):
