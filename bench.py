@@ -8,8 +8,10 @@ contexts come from a packed prefill of uniform random prompt ids through both mo
 N(0, 1) bf16 keys/values written straight into the pools instead), then `--steps` decode rounds are
 timed: k draft decode steps, one target verify pass over k+1 tokens, one fused acceptance.
 
-One "step" = one speculative round for the whole batch, replayed from the HIP graph captured for its
-shape (the first round of a shape runs eagerly, the second captures). `value` = committed tokens per
+One "step" = one speculative round for the whole batch, replayed from the HIP graphs captured for its
+shape (the first round of a shape runs eagerly, the second captures). The timed rounds are queued back
+to back (`SpeculativeBatch.run_rounds`: each round's inputs are computed on the GPU from the previous
+round's acceptance, and the host reads a round's tokens while the next one runs). `value` = committed tokens per
 second (accepted proposals + one target token per sequence per round), inputs resident in HBM.
 `roofline` = the paged verify attention (the unit kernel per layer, + combine when a query spans chunks,
 and one work plan per pass): the last timed round's 32 verify-attention launches (each layer's pool,
@@ -155,13 +157,6 @@ def time_verify_attention(torch, fa, ops, sb, lens, reps=4):
     torch.cuda.synchronize()
     sec = sum(a.elapsed_time(b) for a, b in ev) * 1e-3 / (reps * len(layers))
     return sec, attn_bytes([n + K for n in lens], K + 1, h, CFG["n_kv_heads"], d, BLOCK)
-
-
-def run_rounds(torch, fa, ops, sb, n_rounds, timer=None):
-    committed = 0
-    for _ in range(n_rounds):
-        committed += sb.round()
-    return committed
 
 
 def cpu_baseline(torch, committed_per_round):
@@ -483,12 +478,19 @@ def main():
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     committed = 0
-    last_lens = None
-    for i in range(args.steps):
-        last_lens = [len(s.tokens) for s in sb.active()]
-        committed += sb.round()
-        if (i + 1) % 32 == 0:
-            log(f"round {i + 1}/{args.steps}: {committed} tokens committed")
+    done_rounds = 0
+    # rounds queued back to back (each one's inputs computed on the GPU from the previous one's
+    # acceptance, the host's bookkeeping one round behind), in chunks of 32 for the progress lines; the
+    # last round on its own, after noting the lengths it starts from
+    while done_rounds < args.steps - 1:
+        n = min(32 - done_rounds % 32, args.steps - 1 - done_rounds)
+        committed += sb.run_rounds(n)
+        done_rounds += n
+        if done_rounds % 32 == 0:
+            log(f"round {done_rounds}/{args.steps}: {committed} tokens committed")
+    last_lens = [len(s.tokens) for s in sb.active()]
+    committed += sb.round()
+    log(f"round {args.steps}/{args.steps}: {committed} tokens committed")
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
     proposed = sb.stats["proposed"] - acc0["proposed"]

@@ -68,6 +68,8 @@ SIGNATURES = {
     "fs_add_rmsnorm": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_f32, c_i32, c_p]),
     "fs_silu_mul": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i32, c_p]),
     "fs_gemm_swiglu": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i32, c_p]),
+    "fs_spec_advance": (c_i32, [c_p, c_i64, c_i32, c_i32, c_i32, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
+                                c_p]),
     "fs_embedding": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_i32, c_p]),
     "fs_probs_from_logits": (c_i32, [c_p, c_i64, c_i64, c_i64, c_f32, c_i32, c_p, c_i64, c_i32, c_p, c_i64, c_p]),
     "fs_sample_logits": (c_i32, [c_p, c_i64, c_i64, c_i64, c_p, c_f32, c_p, c_i64, c_i32, c_p, c_p, c_i64, c_p,

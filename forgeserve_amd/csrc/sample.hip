@@ -982,3 +982,63 @@ extern "C" int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_
     default: return launch_accept<FS_F16>(A, true, s);
   }
 }
+
+namespace {
+// One row of the round-to-round bookkeeping of speculative.py:71-85, on the device: the row's
+// n_accepted a and committed tokens res[1 .. a+1] (an acceptance's output row) advance its length by
+// a + 1 and its token budget by the same; the row is done once the budget is spent or a committed
+// token is its EOS. Then the next round's inputs are written exactly as the host stages them: (prev,
+// last) ids, k_eff = min(k, budget - 1), the draft steps' positions (step i feeds position n-1+i while
+// i < k_eff; steps below `first` are fed by the pair at pos0) and the verify window's positions
+// (n-1+t for t <= k_eff). A done row, and a row that was done already, gets k_eff 0 and only -1
+// positions: it reads no keys, writes no cache entry and its results are ignored.
+__global__ void __launch_bounds__(256) spec_advance_kernel(const int32_t* __restrict__ res, int64_t res_ld, int32_t B,
+                                                           int32_t k, int32_t first, int32_t* __restrict__ n,
+                                                           int32_t* __restrict__ budget, const int32_t* __restrict__ eos,
+                                                           int32_t* __restrict__ done, int64_t* __restrict__ ids,
+                                                           int64_t* __restrict__ last, int32_t* __restrict__ keff,
+                                                           int32_t* __restrict__ pos0, int32_t* __restrict__ posd,
+                                                           int32_t* __restrict__ posv) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= B) return;
+  bool dn = done[r] != 0;
+  int nn = n[r], bud = budget[r];
+  int64_t prev = ids[2 * r], lst = ids[2 * r + 1];
+  if (!dn) {
+    const int32_t* row = res + (int64_t)r * res_ld;
+    const int a = min(max(row[0], 0), k);
+    const int e = eos[r];
+    bool hit = false;
+    for (int j = 0; j <= a; ++j) hit = hit || (e >= 0 && row[1 + j] == e);
+    nn += a + 1;
+    bud -= a + 1;
+    prev = a >= 1 ? (int64_t)row[a] : lst;
+    lst = row[1 + a];
+    dn = hit || bud <= 0;
+  }
+  const int ke = dn ? 0 : min(k, max(bud - 1, 0));
+  n[r] = nn;
+  budget[r] = bud;
+  done[r] = dn ? 1 : 0;
+  ids[2 * r] = prev;
+  ids[2 * r + 1] = lst;
+  last[r] = lst;
+  keff[r] = ke;
+  pos0[2 * r] = ke > 0 ? (nn > 1 ? nn - 2 : -1) : -1;
+  pos0[2 * r + 1] = ke > 0 ? nn - 1 : -1;
+  for (int i = first; i < k; ++i) posd[(int64_t)(i - first) * B + r] = ke > i ? nn - 1 + i : -1;
+  for (int t = 0; t <= k; ++t) posv[(int64_t)r * (k + 1) + t] = (!dn && t <= ke) ? nn - 1 + t : -1;
+}
+}  // namespace
+
+extern "C" int fs_spec_advance(const int32_t* res, int64_t res_ld, int32_t B, int32_t k, int32_t first, int32_t* n,
+                               int32_t* budget, const int32_t* eos, int32_t* done, int64_t* ids, int64_t* last,
+                               int32_t* keff, int32_t* pos0, int32_t* posd, int32_t* posv, void* stream) {
+  FS_CHECK_ARG(res && n && budget && eos && done && ids && last && keff && pos0 && posv, "spec_advance: null pointer");
+  FS_CHECK_ARG(B >= 0 && k >= 0 && (first == 0 || first == 1) && res_ld >= k + 2 && (k <= first || posd),
+               "spec_advance: B %d k %d first %d res_ld %lld", B, k, first, (long long)res_ld);
+  if (B == 0) return 0;
+  spec_advance_kernel<<<dim3((unsigned)((B + 255) / 256)), 256, 0, fs::as_stream(stream)>>>(
+      res, res_ld, B, k, first, n, budget, eos, done, ids, last, keff, pos0, posd, posv);
+  return fs::launch_status("spec_advance");
+}

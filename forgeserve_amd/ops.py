@@ -553,3 +553,23 @@ def verify_probs(p: torch.Tensor, q: torch.Tensor, draft_tokens: torch.Tensor, u
                               ptr(draft_tokens.contiguous()), ptr(u.contiguous()), ptr(noise.contiguous()), ptr(out),
                               ptr(n), ptr(ws), ws.numel(), stream_ptr()), "verify_probs")
     return out, n
+
+
+def spec_advance(res: torch.Tensor, b: int, k: int, first: int, n: torch.Tensor, budget: torch.Tensor,
+                 eos: torch.Tensor, done: torch.Tensor, ids: torch.Tensor, last: torch.Tensor, keff: torch.Tensor,
+                 pos0: torch.Tensor, posd: torch.Tensor, posv: torch.Tensor) -> None:
+    """The next round's inputs from this round's acceptance, in place on the device (the bookkeeping
+    of speculative.py:71-85 for b rows): res (b, k+2) int32 from the acceptance; n, budget, eos, done
+    int32 (b,); ids int64 (b, 2); last int64 (b,); keff int32 (b,); pos0 int32 (b, 2); posd int32
+    (k - first, b); posv int32 (b, k+1)."""
+    require_device(res, n, budget, eos, done, ids, last, keff, pos0, posv)
+    i32 = (res, n, budget, eos, done, keff, pos0, posd, posv)
+    if any(t.dtype != I32 or not t.is_contiguous() for t in i32) or ids.dtype != torch.int64 or last.dtype != torch.int64:
+        raise ValueError("spec_advance: int32 rows and positions, int64 ids, contiguous")
+    shapes_ok = (res.shape[0] >= b and res.shape[1] >= k + 2 and n.numel() >= b and ids.shape == (b, 2)
+                 and posv.shape == (b, k + 1) and pos0.shape == (b, 2) and (k <= first or posd.shape == (k - first, b)))
+    if not shapes_ok:
+        raise ValueError("spec_advance: shapes")
+    check(_lib.load().fs_spec_advance(ptr(res), res.stride(0), b, k, first, ptr(n), ptr(budget), ptr(eos), ptr(done),
+                                      ptr(ids), ptr(last), ptr(keff), ptr(pos0), ptr(posd), ptr(posv), stream_ptr()),
+          "spec_advance")

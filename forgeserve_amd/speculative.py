@@ -187,9 +187,16 @@ class _RoundState:
         # a draft on the target's cache feeds only `last` in step 0 (the verify pass has cached every
         # position before it), so its step 0 is staged with the others
         km = k if n_shared else max(k - 1, 0)
+        self.km = km
+        # The spans up to `temps` are what a round computes from the previous one (fs_spec_advance
+        # writes them on the device when rounds are queued back to back, with each row's length n,
+        # token budget, EOS id and done flag); the tables and temperatures after them always come from
+        # the host. Two pinned host buffers: a queued round's copy may still be pending while the next
+        # is staged.
         spans = [("ids", np.int64, (b, 2)), ("last", np.int64, (b,)), ("keff", np.int32, (b,)), ("pos0", np.int32, (b, 2)),
-                 ("posd", np.int32, (km, b)), ("posv", np.int32, (b, k + 1)), ("tab_t", np.int32, (b, wt)),
-                 ("temps", np.float32, (2, b))]
+                 ("posd", np.int32, (km, b)), ("posv", np.int32, (b, k + 1)), ("n", np.int32, (b,)),
+                 ("budget", np.int32, (b,)), ("eos", np.int32, (b,)), ("done", np.int32, (b,)),
+                 ("temps", np.float32, (2, b)), ("tab_t", np.int32, (b, wt))]
         if not n_shared:   # a draft on the target's cache reads the target's table
             spans.append(("tab_d", np.int32, (b, wd)))
         off, lay = 0, {}
@@ -197,21 +204,23 @@ class _RoundState:
             nbytes = int(np.prod(shape)) * np.dtype(dt).itemsize
             lay[name] = (off, nbytes, dt, shape)
             off += -(-nbytes // 16) * 16
-        self.host = torch.empty(max(off, 16), dtype=torch.uint8, pin_memory=True)
+        self.host_off = lay["temps"][0]
+        self.hosts = [torch.empty(max(off, 16), dtype=torch.uint8, pin_memory=True) for _ in range(2)]
         self.dev = torch.empty(max(off, 16), dtype=torch.uint8, device=dev)
-        hn = self.host.numpy()
         tdt = {np.int64: torch.int64, np.int32: torch.int32, np.float32: torch.float32}
-        self.h, self.d = {}, {}
+        self.hs, self.d = [{}, {}], {}
         for name, (o, nbytes, dt, shape) in lay.items():
-            self.h[name] = hn[o: o + nbytes].view(dt).reshape(shape)
+            for i in range(2):
+                self.hs[i][name] = self.hosts[i].numpy()[o: o + nbytes].view(dt).reshape(shape)
             self.d[name] = self.dev[o: o + nbytes].view(tdt[dt]).view(shape)
         if n_shared:
             self.d["tab_d"] = self.d["tab_t"]
-        self.h["tab_t"].fill(0)
-        if "tab_d" in lay:
-            self.h["tab_d"].fill(0)
-        # what each table row of the host staging holds: (block list, its version, entries copied)
-        self._staged = {}
+        for h in self.hs:
+            h["tab_t"].fill(0)
+            if "tab_d" in lay:
+                h["tab_d"].fill(0)
+        # what each table row of each host buffer holds: (block list, its version, entries copied)
+        self._staged = [{}, {}]
         kk = max(k, 1)
         self.u = torch.zeros((b, kk), dtype=torch.float32, device=dev)
         self.e = torch.ones((b, v), dtype=torch.float32, device=dev)
@@ -224,15 +233,17 @@ class _RoundState:
             self.parts_d = torch.empty((b, k, parts_d, 4), dtype=I32, device=dev)
             self.parts_t = torch.empty((b * (k + 1), parts_t, 4), dtype=I32, device=dev)
             self.row_stats = torch.empty((b, 2 * k + 1, 4), dtype=I32, device=dev)
-        self.res_host = torch.empty((b, k + 2), dtype=torch.int32, pin_memory=True)
+        self.res_hosts = [torch.empty((b, k + 2), dtype=torch.int32, pin_memory=True) for _ in range(2)]
         self.res = None
         self.graphs = None
         self.uses = 0
 
-    def stage(self, tokens, k_eff, temps, blocks_t, blocks_d) -> None:
-        """Write one round's inputs into the pinned staging buffer (rows past len(tokens) are padding)."""
+    def stage(self, tokens, k_eff, temps, blocks_t, blocks_d, slot=0, budget=None, eos=None) -> None:
+        """Write one round's inputs into pinned staging buffer `slot` (rows past len(tokens) are padding,
+        and done). budget, eos: each row's remaining tokens and EOS id (-1: none), for rounds whose
+        successors are advanced on the device."""
         b, k = len(tokens), self.k
-        h = self.h
+        h = self.hs[slot]
         n = np.array([len(t) for t in tokens], dtype=np.int64)
         keff = np.array(k_eff, dtype=np.int64)
         ids = h["ids"]
@@ -253,13 +264,26 @@ class _RoundState:
         t_ = np.arange(k + 1)[None, :]
         h["posv"].fill(-1)
         h["posv"][:b] = np.where(t_ <= keff[:, None], n[:, None] - 1 + t_, -1)
+        h["n"].fill(0)
+        h["n"][:b] = n
+        h["budget"].fill(0)
+        h["budget"][:b] = budget if budget is not None else 0
+        h["eos"].fill(-1)
+        h["eos"][:b] = eos if eos is not None else -1
+        h["done"].fill(1)
+        h["done"][:b] = 0
+        self.stage_host(temps, blocks_t, blocks_d, slot)
+
+    def stage_host(self, temps, blocks_t, blocks_d, slot) -> None:
+        """The host-owned spans of staging buffer `slot`: temperatures and block tables."""
+        h, b = self.hs[slot], len(temps)
         h["temps"].fill(0)
         h["temps"][0, :b] = temps
         h["temps"][1, :b] = [np.float32(1.0 / t) if t > 0 else 0.0 for t in temps]
         tables = (("tab_t", blocks_t),) if self.n_shared else (("tab_t", blocks_t), ("tab_d", blocks_d))
         for name, lists in tables:
             # rows keep last round's entries: a row whose block list only grew gets its new blocks
-            tab, prev, rows = h[name], self._staged.get(name, ()), []
+            tab, prev, rows = h[name], self._staged[slot].get(name, ()), []
             for r, x in enumerate(lists):
                 p = prev[r] if r < len(prev) else None
                 if isinstance(x, BlockList):
@@ -280,7 +304,7 @@ class _RoundState:
             for r in range(len(lists), len(prev)):   # rows of sequences that left the batch
                 if prev[r][2]:
                     tab[r] = 0
-            self._staged[name] = rows
+            self._staged[slot][name] = rows
 
 
 def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _RoundState, phase: int):
@@ -334,31 +358,11 @@ def _graph_key(model) -> tuple:
 _MAX_GRAPHS = 8
 
 
-@torch.no_grad()
-def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: List[List[int]],
-               blocks_t: List[List[int]], blocks_d: List[List[int]], k_eff: List[int], temps: List[float],
-               draws, graphs: bool = True) -> torch.Tensor:
-    """One draft-then-verify round (speculative.py:53-85) for b sequences whose caches hold positions
-    0..n-2 (n = len(tokens[r])) and whose block lists cover positions up to n-1+k_eff[r].
-
-    Per round: k draft decode steps (step 0 re-feeds (tokens[-2], tokens[-1]) at (n-2, n-1), so a fully
-    accepted round needs no catch-up forward; step i feeds x_{i-1} at n-1+i), one target verify pass
-    over the k+1 window, one fused acceptance. `draws` supplies the randomness: draft(i) -> (b, V)
-    Exp(1) noise of draft step i, accept() -> (u (b, k), E (b, V)); rows of greedy sequences are
-    ignored, and a round with no sampled row draws nothing. With `graphs`, the round's kernels are
-    captured in a HIP graph on the second round of a shape and replayed from then on (the same kernels
-    on the same inputs: results are identical to running them one by one).
-    Returns (b, k+2) int32 on the host: n_accepted, then the committed tokens (-1 padded)."""
-    b = len(tokens)
-    k = max(k_eff)
+def _round_state(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, b: int, k: int, blocks_t, blocks_d,
+                 sampling: bool) -> "_RoundState":
+    """The _RoundState of a round's shape (created on first use; at most _MAX_GRAPHS kept per pool)."""
     dev, dtype = target.device, target.dtype
     v = target.cfg.vocab_size
-    n = np.array([len(t) for t in tokens], dtype=np.int64)
-    keff = np.array(k_eff, dtype=np.int64)
-    limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
-    if int((n - 1 + keff).max()) >= limit:
-        raise ValueError(f"a round would write position {int((n - 1 + keff).max())} >= max_seq_len {limit}")
-    sampling = any(t > 0 for t in temps)
     n_shared = 0
     if pool_d is pool_t:   # the draft reads and writes the target's cache for the blocks they share
         n_shared = shared_layers(target, draft)
@@ -373,7 +377,6 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     d = target.cfg.d_model
     pd, pt = ops.row_stats_parts(bp, v, d), ops.row_stats_parts(bp * (k + 1), v, d)
     fused = dtype == torch.bfloat16 and k > 0 and pd > 0 and pt > 0
-
     cache = pool_t.__dict__.setdefault("_rounds", OrderedDict())
     key = (bp, k, wt, wd, sampling, fused, _graph_key(target), _graph_key(draft), id(pool_d))
     st = cache.get(key)
@@ -383,11 +386,18 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
         while len(cache) > _MAX_GRAPHS:
             cache.popitem(last=False)
     cache.move_to_end(key)
+    st.key = key
+    return st
 
-    # host staging -> one copy; then the random numbers, drawn in the reference loop's order
-    st.stage(tokens, k_eff, temps, blocks_t, blocks_d)
-    st.dev.copy_(st.host, non_blocking=True)
-    if sampling:
+
+def _launch_round(target, draft, pool_t, pool_d, st: "_RoundState", b: int, draws, graphs: bool,
+                  advance: bool = False) -> None:
+    """Queue one round on the current stream: the random numbers (drawn in the reference loop's order),
+    then the k+1 phases (eagerly on the shape's first round, captured on its second, replayed after),
+    then, with `advance`, fs_spec_advance, which writes the next round's inputs from this round's
+    acceptance into the same device buffers."""
+    k = st.k
+    if st.sampling:
         if hasattr(draws, "draft_into"):
             for i in range(k):
                 draws.draft_into(i, st.noise_d[i, :b])
@@ -398,7 +408,6 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
             u, e = draws.accept()
             st.u[:b, :k].copy_(u)
             st.e[:b].copy_(e)
-
     if not graphs or st.uses == 0:
         for phase in range(k + 1):
             st.res = _round_phase(target, draft, pool_t, pool_d, st, phase)
@@ -417,9 +426,45 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
         for g in st.graphs:
             g.replay()
     st.uses += 1
-    st.res_host.copy_(st.res, non_blocking=True)
+    if advance:
+        d = st.d
+        ops.spec_advance(st.res, st.b, k, 0 if st.n_shared else 1, d["n"], d["budget"], d["eos"], d["done"], d["ids"],
+                         d["last"], d["keff"], d["pos0"], d["posd"], d["posv"])
+
+
+@torch.no_grad()
+def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: List[List[int]],
+               blocks_t: List[List[int]], blocks_d: List[List[int]], k_eff: List[int], temps: List[float],
+               draws, graphs: bool = True) -> torch.Tensor:
+    """One draft-then-verify round (speculative.py:53-85) for b sequences whose caches hold positions
+    0..n-2 (n = len(tokens[r])) and whose block lists cover positions up to n-1+k_eff[r].
+
+    Per round: k draft decode steps (step 0 re-feeds (tokens[-2], tokens[-1]) at (n-2, n-1), so a fully
+    accepted round needs no catch-up forward; step i feeds x_{i-1} at n-1+i), one target verify pass
+    over the k+1 window, one fused acceptance. `draws` supplies the randomness: draft(i) -> (b, V)
+    Exp(1) noise of draft step i, accept() -> (u (b, k), E (b, V)); rows of greedy sequences are
+    ignored, and a round with no sampled row draws nothing. With `graphs`, the round's kernels are
+    captured in a HIP graph on the second round of a shape and replayed from then on (the same kernels
+    on the same inputs: results are identical to running them one by one).
+    Returns (b, k+2) int32 on the host: n_accepted, then the committed tokens (-1 padded)."""
+    b = len(tokens)
+    k = max(k_eff)
+    n = np.array([len(t) for t in tokens], dtype=np.int64)
+    keff = np.array(k_eff, dtype=np.int64)
+    limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
+    if int((n - 1 + keff).max()) >= limit:
+        raise ValueError(f"a round would write position {int((n - 1 + keff).max())} >= max_seq_len {limit}")
+    sampling = any(t > 0 for t in temps)
+    st = _round_state(target, draft, pool_t, pool_d, b, k, blocks_t, blocks_d, sampling)
+    if st.n_shared:
+        blocks_d = blocks_t
+    # host staging -> one copy, then the round
+    st.stage(tokens, k_eff, temps, blocks_t, blocks_d)
+    st.dev.copy_(st.hosts[0], non_blocking=True)
+    _launch_round(target, draft, pool_t, pool_d, st, b, draws, graphs)
+    st.res_hosts[0].copy_(st.res, non_blocking=True)
     torch.cuda.current_stream().synchronize()
-    return st.res_host[:b].clone()
+    return st.res_hosts[0][:b].clone()
 
 
 # ------------------------------------------------------------------------------------------------
@@ -580,6 +625,106 @@ class SpeculativeBatch:
             self._finish_check(s)
         self.stats["rounds"] += 1
         return committed
+
+    @torch.no_grad()
+    def run_rounds(self, n_rounds: int) -> int:
+        """n_rounds rounds (fewer once every sequence has finished); returns the tokens committed.
+        Tokens and stats are exactly those of n_rounds calls of round(). Where it is safe, each round is
+        queued before the previous round's tokens are read back (fs_spec_advance computes its inputs
+        on the GPU), so the GPU does not wait for the host between rounds: for a greedy batch always,
+        for a sampled one while no sequence can finish inside the queue and none has an EOS id (the
+        random numbers a round draws depend on the batch, which a finishing sequence changes)."""
+        committed, left = 0, n_rounds
+        while left > 0 and self.active():
+            n_run, c = self._queued_rounds(left) if self.graphs else (0, 0)
+            if n_run == 0:
+                c, n_run = self.round(), 1
+            committed += c
+            left -= n_run
+        return committed
+
+    def _queued_rounds(self, max_rounds: int):
+        """Up to max_rounds rounds of the current batch, each queued before the previous one's tokens
+        are read: (rounds run, tokens committed); (0, 0) when the batch does not allow it."""
+        seqs = self.active()
+        b, k = len(seqs), self.k
+        temps = [s.temperature for s in seqs]
+        sampled = any(t > 0 for t in temps)
+        rem = [self._remaining(s) for s in seqs]
+        if k == 0 or min(rem) <= 0:
+            return 0, 0
+        n_max = max_rounds
+        if sampled:
+            if any(s.eos_id is not None for s in seqs):
+                return 0, 0
+            # every queued round must see k_eff = k in every row (the round's k and batch fix its draws):
+            # round j has at least rem - j*(k+1) tokens left
+            n_max = min(n_max, (min(rem) - k - 1) // (k + 1) + 1)
+        if n_max < 2:
+            return 0, 0
+        limit = self.limit
+        eos = [s.eos_id if s.eos_id is not None else -1 for s in seqs]
+        st, pending, run, committed = None, [], 0, 0
+
+        def process(j, ev):
+            nonlocal run, committed
+            ev.synchronize()
+            rows = st.res_hosts[j % 2][:b].tolist()
+            live = False
+            for r, s in enumerate(seqs):
+                if s.done:
+                    continue
+                live = True
+                ke = max(0, min(k, self._remaining(s) - 1))
+                a = rows[r][0]
+                new = rows[r][1: a + 2]
+                s.tokens += new
+                committed += len(new)
+                self.stats["proposed"] += ke
+                self.stats["accepted"] += a
+                self._finish_check(s)
+            if live:
+                self.stats["rounds"] += 1
+                run += 1
+
+        for j in range(n_max):
+            if not any(not s.done for s in seqs):
+                break
+            # blocks for every position round j can write: its rows start at most k+1 tokens past the
+            # lengths the host knows (those of round j-1's start), and write k past their start
+            try:
+                for s in seqs:
+                    if not s.done:
+                        self._grow(s, min(len(s.tokens) + (k if j == 0 else 2 * k + 1), limit))
+            except OutOfBlocks:
+                break
+            blocks_t = [s.blocks_t for s in seqs]
+            blocks_d = blocks_t if self.shared else [s.blocks_d for s in seqs]
+            if j == 0:
+                st = _round_state(self.target, self.draft, self.pool_t, self.pool_d, b, k, blocks_t, blocks_d, sampled)
+                k_eff = [max(0, min(k, r_ - 1)) for r_ in rem]
+                st.stage([s.tokens for s in seqs], k_eff, temps, blocks_t, blocks_d, slot=0, budget=rem, eos=eos)
+                st.dev.copy_(st.hosts[0], non_blocking=True)
+            else:
+                wt = _bucket(max(len(x) for x in blocks_t), 64)
+                wd = _bucket(max(len(x) for x in blocks_d), 64)
+                if (wt, wd) != (st.wt, st.wd):   # the tables outgrew the shape: finish what is queued
+                    break
+                slot = j % 2
+                st.stage_host(temps, blocks_t, blocks_d, slot)
+                o = st.host_off
+                st.dev[o:].copy_(st.hosts[slot][o:], non_blocking=True)
+            draws = _GeneratorDraws(self.gen, b, k, self.target.cfg.vocab_size, self.dev) if sampled else None
+            _launch_round(self.target, self.draft, self.pool_t, self.pool_d, st, b, draws, True, advance=True)
+            st.res_hosts[j % 2].copy_(st.res, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            pending.append((j, ev))
+            if len(pending) == 2:
+                process(*pending.pop(0))
+        while pending:
+            process(*pending.pop(0))
+        return run, committed
 
     def run(self) -> None:
         while self.active():

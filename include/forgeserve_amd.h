@@ -289,6 +289,20 @@ int fs_spec_accept_stats(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const 
                          int64_t ldE, const void* row_stats, int32_t* out_tokens, int32_t* n_accepted,
                          int32_t* seq_len, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The round-to-round bookkeeping of speculative.py:71-85 (emit the accepted tokens and the extra,
+ * advance the cache length, stop at the token limit) for B rows at once, on the device, so that the
+ * next round can be queued before the host has read this round's tokens. res: the acceptance's
+ * [B, res_ld] int32 rows (n_accepted a, then a+1 committed tokens). Per row: n += a+1, budget -= a+1
+ * (budget = min(max_new - generated, max_seq_len - n)), done once budget <= 0 or a committed token
+ * equals eos[row] (-1: none); then the next round's inputs as a host would stage them: ids [B,2]
+ * (prev, last) int64, last [B] int64, k_eff [B] = min(k, budget-1), pos0 [B,2], posd [k-first, B]
+ * (draft step i at n-1+i while i < k_eff), posv [B, k+1] (n-1+t for t <= k_eff); done rows get
+ * k_eff 0 and -1 positions. first: 1 when draft step 0 feeds the (prev, last) pair at pos0, 0 when
+ * it feeds `last` alone (a draft on the target's cache). */
+int fs_spec_advance(const int32_t* res, int64_t res_ld, int32_t B, int32_t k, int32_t first, int32_t* n,
+                    int32_t* budget, const int32_t* eos, int32_t* done, int64_t* ids, int64_t* last, int32_t* keff,
+                    int32_t* pos0, int32_t* posd, int32_t* posv, void* stream);
+
 /* verify_draft (speculative.py:20-33) on probabilities instead of logits: p [K+1, V] rows at
  * p + i*ldp, q [K, V]; one sequence, K proposals; p and q in `dtype` (f32 from a softmax, or the
  * logits dtype for one-hot rows). Same outputs as fs_spec_accept with B = 1. */

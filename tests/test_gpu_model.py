@@ -332,6 +332,47 @@ def test_graph_rounds_equal_eager_rounds(bf_target):
     assert graph == eager and stats_g == stats_e
 
 
+@pytest.mark.parametrize("share", [True, False])
+def test_queued_rounds_equal_rounds(bf_target, share):
+    """run_rounds(n), which queues each round before reading the previous one's tokens (the next
+    round's inputs computed on the GPU), commits exactly what n round() calls commit, with the same
+    stats: a greedy batch whose sequences finish at different rounds by token budget and by EOS (the
+    queue keeps running past them), and a sampled batch (queued while no sequence can finish inside
+    the queue, then round by round)."""
+    case("queued rounds == rounds", share)
+    draft = fa.early_exit_draft(bf_target, 2)
+    g = torch.Generator().manual_seed(31)
+    prompts = [torch.randint(0, 1000, (int(n),), generator=g).tolist() for n in torch.randint(2, 70, (9,), generator=g)]
+
+    def run(queued, temps, max_new, eos, rounds):
+        sb = fa.SpeculativeBatch(bf_target, draft, 900, 16, k=4, share_kv=share,
+                                 generator=torch.Generator(device="cuda").manual_seed(4))
+        seqs = [sb.add(p, m, t, eos_id=e) for p, t, m, e in zip(prompts, temps, max_new, eos)]
+        if queued:
+            c = sb.run_rounds(rounds)
+        else:
+            c = sum(sb.round() for _ in range(rounds))
+        return [s.tokens for s in seqs], [s.done for s in seqs], c, sb.stats
+
+    greedy = [0.0] * 9
+    budgets = [12, 40, 70, 25, 90, 8, 55, 33, 100]
+    free = run(False, greedy, budgets, [None] * 9, 30)
+    # EOS ids for three sequences: tokens their greedy continuation produces
+    eos = [None] * 9
+    for i in (1, 4, 6):
+        gen = free[0][i][len(prompts[i]):]
+        eos[i] = gen[min(7 + i, len(gen) - 1)]
+    a = run(False, greedy, budgets, eos, 30)
+    b = run(True, greedy, budgets, eos, 30)
+    assert b == a
+    assert any(a[1]) and not all(a[1])   # some sequences finished inside the run, some did not
+    temps = [0.8, 1.0, 0.0, 1.2, 0.7, 0.0, 1.0, 0.9, 0.6]
+    budgets = [60, 80, 70, 90, 200, 75, 65, 85, 120]
+    a = run(False, temps, budgets, [None] * 9, 25)
+    b = run(True, temps, budgets, [None] * 9, 25)
+    assert b == a
+
+
 def test_graph_engine_equals_eager_engine(small):
     """The speculative engine (f32 model: the generic kernels) gives the same tokens, preemptions and
     counters with graph-replayed rounds as with eager rounds, at T > 0 through a tight pool."""
