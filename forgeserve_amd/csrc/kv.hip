@@ -65,21 +65,43 @@ struct QkvPart {
   int64_t stride;      // elements between consecutive splits (rows * cols)
 };
 
-template <int DT, bool PART>
+// PART: 0 reads the 16-bit row; > 0 adds that many partials, all loaded before the first add; < 0
+// adds pp.splits partials one at a time.
+template <int DT, int PART>
 FS_DEVICE void load8(const uint16_t* qkv, const QkvPart& pp, int64_t e, float (&v)[8]) {
-  if (!PART) {
+  if (PART == 0) {
     unpack8<DT>(*reinterpret_cast<const u32x4_t*>(qkv + e), v);
     return;
   }
-  float4_t a = *reinterpret_cast<const float4_t*>(pp.part + e);
-  float4_t b = *reinterpret_cast<const float4_t*>(pp.part + e + 4);
-  for (int sp = 1; sp < pp.splits; ++sp) {
-    const float4_t a2 = *reinterpret_cast<const float4_t*>(pp.part + sp * pp.stride + e);
-    const float4_t b2 = *reinterpret_cast<const float4_t*>(pp.part + sp * pp.stride + e + 4);
+  float4_t a, b;
+  if (PART > 0) {
+    constexpr int NS = PART > 0 ? PART : 1;
+    float4_t qa[NS], qb[NS];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      a[j] += a2[j];
-      b[j] += b2[j];
+    for (int sp = 0; sp < NS; ++sp) {
+      qa[sp] = *reinterpret_cast<const float4_t*>(pp.part + sp * pp.stride + e);
+      qb[sp] = *reinterpret_cast<const float4_t*>(pp.part + sp * pp.stride + e + 4);
+    }
+    a = qa[0];
+    b = qb[0];
+#pragma unroll
+    for (int sp = 1; sp < NS; ++sp)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a[j] += qa[sp][j];
+        b[j] += qb[sp][j];
+      }
+  } else {
+    a = *reinterpret_cast<const float4_t*>(pp.part + e);
+    b = *reinterpret_cast<const float4_t*>(pp.part + e + 4);
+    for (int sp = 1; sp < pp.splits; ++sp) {
+      const float4_t a2 = *reinterpret_cast<const float4_t*>(pp.part + sp * pp.stride + e);
+      const float4_t b2 = *reinterpret_cast<const float4_t*>(pp.part + sp * pp.stride + e + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a[j] += a2[j];
+        b[j] += b2[j];
+      }
     }
   }
 #pragma unroll
@@ -89,8 +111,11 @@ FS_DEVICE void load8(const uint16_t* qkv, const QkvPart& pp, int64_t e, float (&
   }
 }
 
-template <int DT, bool PART = false>
-__global__ void __launch_bounds__(256) qkv_rope_write_vec_kernel(
+// Grid (token, group block): each thread takes one 8-pair rotation group of a q or k head, or one
+// 8-element group of the values (grid.y blocks of blockDim.x groups cover both), so a token's work is
+// spread over several workgroups and every thread issues its loads at once.
+template <int DT, int PART = 0>
+__global__ void __launch_bounds__(128) qkv_rope_write_vec_kernel(
     const uint16_t* __restrict__ qkv, QkvPart pp, int64_t qkv_stride, int32_t T, int32_t H,
     const int32_t* __restrict__ positions,
     const int32_t* __restrict__ slots, const int32_t* __restrict__ token_row, int32_t n_rows,
@@ -114,7 +139,9 @@ __global__ void __launch_bounds__(256) qkv_rope_write_vec_kernel(
   const int ng = half / 8;
   const int n_groups = (H + Hkv) * ng;
   const int64_t cs = rot_ok ? (int64_t)pos * half : 0;
-  for (int i = threadIdx.x; i < n_groups; i += blockDim.x) {
+  const int gi = blockIdx.y * blockDim.x + threadIdx.x;
+  if (gi < n_groups) {
+    const int i = gi;
     const int head = i / ng, p0 = 8 * (i - head * ng);
     float x1[8], x2[8], c[8], sn[8], o1[8], o2[8];
     load8<DT, PART>(qkv, pp, row0 + (int64_t)head * D + p0, x1);
@@ -143,15 +170,16 @@ __global__ void __launch_bounds__(256) qkv_rope_write_vec_kernel(
       *reinterpret_cast<u32x4_t*>(ko + half) = pack8<DT>(o2);
     }
   }
-  if (write_ok) {
-    const int nv = Hkv * D / 8;
+  const int nv = Hkv * D / 8;
+  if (write_ok && gi >= n_groups && gi < n_groups + nv) {
     const int64_t vrow = row0 + (int64_t)(H + Hkv) * D;
-    for (int i = threadIdx.x; i < nv; i += blockDim.x) {
+    {
+      const int i = gi - n_groups;
       const int e0 = 8 * i, h = e0 / D, d0 = e0 - h * D;
       u32x4_t w;
-      if (PART) {
+      if (PART != 0) {
         float x[8];
-        load8<DT, true>(qkv, pp, vrow + e0, x);
+        load8<DT, PART>(qkv, pp, vrow + e0, x);
         w = pack8<DT>(x);
       } else {
         w = *reinterpret_cast<const u32x4_t*>(qkv + vrow + e0);
@@ -313,22 +341,33 @@ int qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_
                    qkv_stride % 8 == 0 && q_stride % 8 == 0 && kv->k_dim == 1 && kv->k_slot % 8 == 0 &&
                    kv->k_head % 8 == 0 && kv->k_block % 8 == 0 && al16(pp.part ? (const void*)pp.part : qkv) &&
                    al16(q_out) && al16(kv->k) && al16(rope_cos) && al16(rope_sin);
+  // the vectorised kernel: one thread per 8-element group (q/k rotation groups, then value groups)
+  const int vec_groups = (n_heads + kv->n_kv_heads) * (kv->head_dim / 16) + kv->n_kv_heads * kv->head_dim / 8;
+  const dim3 vgrid((unsigned)n_tokens, (unsigned)((vec_groups + 127) / 128));
   if (pp.part) {   // the partials are read by the vectorised kernel only
     FS_CHECK_ARG(vec && pp.splits >= 1 && pp.stride >= n_tokens * qkv_stride,
                  "qkv_rope_write_partials: needs 16-bit data, head_dim/2 %% 8 == 0, 16-byte aligned rows");
-#define FS_VEC(DT)                                                                                                 \
-  qkv_rope_write_vec_kernel<DT, true><<<grid, 256, 0, s>>>(nullptr, pp, qkv_stride, T, n_heads, positions, slots,     \
-                                                           token_row, n_rows, rope_cos, rope_sin, rope_len,          \
-                                                           block_tables, table_stride, max_blocks, *kv,              \
-                                                           (uint16_t*)q_out, q_stride)
-    if (kv->dtype == FS_BF16) FS_VEC(FS_BF16);
-    else FS_VEC(FS_F16);
+#define FS_VEC(DT, P)                                                                                              \
+  qkv_rope_write_vec_kernel<DT, P><<<vgrid, 128, 0, s>>>(nullptr, pp, qkv_stride, T, n_heads, positions, slots,      \
+                                                         token_row, n_rows, rope_cos, rope_sin, rope_len,            \
+                                                         block_tables, table_stride, max_blocks, *kv,                \
+                                                         (uint16_t*)q_out, q_stride)
+#define FS_VEC_DT(DT)                                                                                              \
+  switch (pp.splits) {                                                                                         \
+    case 2: FS_VEC(DT, 2); break;                                                                              \
+    case 4: FS_VEC(DT, 4); break;                                                                              \
+    case 8: FS_VEC(DT, 8); break;                                                                              \
+    default: FS_VEC(DT, -1); break;                                                                            \
+  }
+    if (kv->dtype == FS_BF16) FS_VEC_DT(FS_BF16)
+    else FS_VEC_DT(FS_F16)
+#undef FS_VEC_DT
 #undef FS_VEC
     return fs::launch_status("qkv_rope_write_partials");
   }
   if (vec) {
 #define FS_VEC(DT)                                                                                                 \
-  qkv_rope_write_vec_kernel<DT><<<grid, 256, 0, s>>>((const uint16_t*)qkv, pp, qkv_stride, T, n_heads, positions,   \
+  qkv_rope_write_vec_kernel<DT><<<vgrid, 128, 0, s>>>((const uint16_t*)qkv, pp, qkv_stride, T, n_heads, positions, \
                                                      slots, token_row, n_rows, rope_cos, rope_sin, rope_len,         \
                                                      block_tables, table_stride, max_blocks, *kv, (uint16_t*)q_out,  \
                                                      q_stride)

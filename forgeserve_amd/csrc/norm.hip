@@ -125,7 +125,8 @@ __global__ void __launch_bounds__(NORM_THREADS) add_rmsnorm_vec_kernel(
 // The same kernel for x = a split-K GEMM's output: x[m] = round(sum over s of parts[s][m], in split
 // order), then the residual: x_out = round(x + residual), y = rmsnorm(x_out) * w. This is the GEMM's
 // reduction (gemm_splitk_reduce_kernel) followed by add_rmsnorm_vec_kernel on its output, in one pass.
-template <int DT>
+// SPLITS > 0: that many partials, all loaded before the first add; 0: `splits` of them, one at a time.
+template <int DT, int SPLITS>
 __global__ void __launch_bounds__(NORM_THREADS) splitk_add_rmsnorm_kernel(
     const float* __restrict__ parts, int splits, int64_t part_stride, const uint16_t* __restrict__ residual,
     int64_t ldr, uint16_t* __restrict__ x_out, int64_t ldxo, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
@@ -140,14 +141,34 @@ __global__ void __launch_bounds__(NORM_THREADS) splitk_add_rmsnorm_kernel(
     const int gi = threadIdx.x + NORM_THREADS * u;
     if (gi >= ng) continue;
     const float* p0 = parts + m * N + 8 * gi;
-    float4_t a0 = *reinterpret_cast<const float4_t*>(p0), a1 = *reinterpret_cast<const float4_t*>(p0 + 4);
-    for (int sp = 1; sp < splits; ++sp) {
-      const float4_t b0 = *reinterpret_cast<const float4_t*>(p0 + sp * part_stride);
-      const float4_t b1 = *reinterpret_cast<const float4_t*>(p0 + sp * part_stride + 4);
+    float4_t a0, a1;
+    if (SPLITS > 0) {
+      float4_t q0[SPLITS > 0 ? SPLITS : 1], q1[SPLITS > 0 ? SPLITS : 1];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        a0[j] += b0[j];
-        a1[j] += b1[j];
+      for (int sp = 0; sp < SPLITS; ++sp) {
+        q0[sp] = *reinterpret_cast<const float4_t*>(p0 + sp * part_stride);
+        q1[sp] = *reinterpret_cast<const float4_t*>(p0 + sp * part_stride + 4);
+      }
+      a0 = q0[0];
+      a1 = q1[0];
+#pragma unroll
+      for (int sp = 1; sp < SPLITS; ++sp)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          a0[j] += q0[sp][j];
+          a1[j] += q1[sp][j];
+        }
+    } else {
+      a0 = *reinterpret_cast<const float4_t*>(p0);
+      a1 = *reinterpret_cast<const float4_t*>(p0 + 4);
+      for (int sp = 1; sp < splits; ++sp) {
+        const float4_t b0 = *reinterpret_cast<const float4_t*>(p0 + sp * part_stride);
+        const float4_t b1 = *reinterpret_cast<const float4_t*>(p0 + sp * part_stride + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          a0[j] += b0[j];
+          a1[j] += b1[j];
+        }
       }
     }
     float d[8];
@@ -244,12 +265,20 @@ extern "C" int fs_splitk_add_rmsnorm(const float* parts, int32_t splits, const v
                "splitk_add_rmsnorm: 16-byte aligned rows");
   if (M == 0) return 0;
   hipStream_t s = fs::as_stream(stream);
-#define FS_LAUNCH_PARTS(DT)                                                                                     \
-  splitk_add_rmsnorm_kernel<DT><<<dim3((unsigned)M), NORM_THREADS, 0, s>>>(                                  \
+#define FS_LAUNCH_PARTS(DT, S)                                                                                  \
+  splitk_add_rmsnorm_kernel<DT, S><<<dim3((unsigned)M), NORM_THREADS, 0, s>>>(                               \
       parts, splits, M * N, (const uint16_t*)residual, ldr, (uint16_t*)x_out, ldxo, (const uint16_t*)weight,      \
       (uint16_t*)y, ldy, N, eps)
-  if (dtype == FS_BF16) FS_LAUNCH_PARTS(FS_BF16);
-  else FS_LAUNCH_PARTS(FS_F16);
+#define FS_LAUNCH_DT(DT)                                                                                        \
+  switch (splits) {                                                                                           \
+    case 2: FS_LAUNCH_PARTS(DT, 2); break;                                                                    \
+    case 4: FS_LAUNCH_PARTS(DT, 4); break;                                                                    \
+    case 8: FS_LAUNCH_PARTS(DT, 8); break;                                                                    \
+    default: FS_LAUNCH_PARTS(DT, 0); break;                                                                   \
+  }
+  if (dtype == FS_BF16) FS_LAUNCH_DT(FS_BF16)
+  else FS_LAUNCH_DT(FS_F16)
+#undef FS_LAUNCH_DT
 #undef FS_LAUNCH_PARTS
   return fs::launch_status("splitk_add_rmsnorm");
 }
