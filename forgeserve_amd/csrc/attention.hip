@@ -63,6 +63,10 @@ struct AttnParams {
 // row swaps: permlane16_swap of (x, x) yields {rows 0,0,2,2 ; rows 1,1,3,3} of x, permlane32_swap
 // yields {lanes 0-31 twice ; lanes 32-63 twice}. Both steps are symmetric, so every lane ends with
 // the same value, and the sum adds (g0 + g1) + (g2 + g3) in every lane.
+// 2^x with the bare v_exp_f32 (no denormal-result scaling): the same value as exp2f wherever the
+// result is a normal float.
+FS_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 FS_DEVICE float max_across_groups(float x) {
   auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
@@ -364,12 +368,14 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
       }
       tmax = max_across_groups(tmax);
       const float m_new = fmaxf(m_run[nt], tmax);
-      alpha[nt] = (m_new == -INFINITY) ? 1.f : exp2f(m_run[nt] - m_new);
+      // v_exp_f32 directly (fast_exp2): exp2f adds a range scaling that only changes results below
+      // 2^-126, which neither the bf16 P operand nor the f32 row sum can resolve, for ~4 VALU each
+      alpha[nt] = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run[nt] - m_new);
       float psum = 0.f;
       float pv[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pv[e] = (sv[e] == -INFINITY) ? 0.f : exp2f(sv[e] - m_new);
+        pv[e] = (sv[e] == -INFINITY) ? 0.f : fast_exp2(sv[e] - m_new);
         psum += pv[e];
       }
       pf[nt] = bf16_rne4(pv);
@@ -464,7 +470,7 @@ attn_unit_kernel(AttnParams P) {
 #pragma unroll
     for (int v = 0; v < UNIT_WAVES; ++v) {
       const float mv = red_m[v][r];
-      const float c = (mv == -INFINITY) ? 0.f : exp2f(mv - M);
+      const float c = (mv == -INFINITY) ? 0.f : fast_exp2(mv - M);
       L += c * red_l[v][r];
       const float4_t a = red_acc[v][gi][lane];
       o[0] += c * a[0];
