@@ -18,10 +18,13 @@ and one work plan per pass): the last timed round's 32 verify-attention launches
 that round's tables and query positions) replayed from one HIP graph between HIP events on the
 launching stream, against 8 TB/s.
 `cpu_baseline` = the CPU oracle (oracle/reference_cpu.py) timed on this host on one target layer's
-verify pass, one draft layer's decode step, the LM head and the acceptance at the same shapes,
-scaled to a round.
+verify pass, one draft layer's decode step, the LM head and the acceptance at the same shapes (one
+warm-up, then the median of three runs of each), scaled to a round.
+`t1_variant` = the same workload at temperature 1.0 (fresh prefill, same timing), whose acceptance
+exercises the residual draws; `verify_pass` = the target's verify pass alone (its k+1-token forward,
+head, statistics merge and fused acceptance) and one draft step, replayed from the round's graphs.
 
-    python bench.py [--gpus 1] [--steps 128] [--warmup 4] [--temperature 0.0]
+    python bench.py [--gpus 1] [--steps 128] [--warmup 4] [--temperature 0.0] [--no-t1-variant]
 
 Kernel-only modes (one JSON line each, used for the rocprofv3 counter runs):
     python bench.py --kernel attention   the verify attention alone: B=64, T=7, 32/8 heads, head_dim 128,
@@ -201,10 +204,15 @@ def cpu_baseline(torch, committed_per_round):
         return x + (torch.nn.functional.silu(h @ w[p + "mlp.w_gate.weight"].T) * (h @ w[p + "mlp.w_up.weight"].T)) \
             @ w[p + "mlp.w_down.weight"].T
 
-    def timed(fn):
-        t0 = time.perf_counter()
+    def timed(fn, runs=3):
+        """One warm-up, then the median of `runs` timed calls."""
         fn()
-        return time.perf_counter() - t0
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2]
 
     t_verify = timed(lambda: layer(K + 1))
     t_decode = timed(lambda: layer(1))
@@ -229,7 +237,8 @@ def cpu_baseline(torch, committed_per_round):
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"CPU oracle at the bench shapes: 1 target layer verify (B={BATCH}, T={K + 1}, per-row "
+        "sample": (f"CPU oracle at the bench shapes, each piece warmed up once then the median of 3 runs: "
+                   f"1 target layer verify (B={BATCH}, T={K + 1}, per-row "
                    f"contexts U[{CTX_LO},{CTX_HI}]) {t_verify:.2f}s, 1 draft layer decode {t_decode:.2f}s, "
                    f"LM head {t_head_v:.2f}s/{t_head_d:.2f}s, acceptance {t_acc:.2f}s; scaled to one round "
                    f"({n_t} verify layers + {K}x{n_d} draft layers + heads) = {round_s:.1f}s for "
@@ -351,6 +360,103 @@ def attention_inputs(torch, fa, seed=0):
     return ctxs, pool, q, pos, tables.cuda()
 
 
+def phase_times(torch, sb, reps=8):
+    """The round's phases as captured for its shape, replayed alone between HIP events on the launching
+    stream: the target's verify phase (k+1-token forward through the reused draft residual streams,
+    LM head with its statistics epilogue, statistics merges, fused acceptance) and the draft steps. The
+    replays rewrite what the last round wrote (same keys, values, logits and outputs)."""
+    st = next(reversed(sb.pool_t.__dict__.get("_rounds", {}).values()), None)
+    if st is None or st.graphs is None:
+        return None
+    out = {}
+    for name, idx in (("verify_ms", [st.k]), ("draft_step_ms", list(range(st.k)))):
+        for i in idx:
+            st.graphs[i].replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            for i in idx:
+                st.graphs[i].replay()
+        b.record()
+        torch.cuda.synchronize()
+        out[name] = round(a.elapsed_time(b) / reps / len(idx), 3)
+    out["what"] = ("verify_ms: the verify phase (28 blocks over the k+1 window from the draft's residual "
+                   "streams, 4 shared blocks for the last proposal, head + statistics, merges, acceptance); "
+                   "draft_step_ms: one draft decode step (4 blocks, head + statistics, sample), mean of the k")
+    return out
+
+
+def run_rounds(torch, fa, ops, target, draft, args, temperature, timing):
+    """Prefill the benchmark's 64 contexts into a fresh SpeculativeBatch at `temperature`, run the warm-up
+    rounds, then time args.steps rounds (queued back to back). With timing: also the verify-attention
+    launch time of the last round and the round's phases."""
+    g = torch.Generator().manual_seed(args.seed)
+    ctxs = torch.randint(CTX_LO, CTX_HI + 1, (BATCH,), generator=g).tolist()
+    rounds = args.warmup + args.steps
+    per_seq = [-(-(c + 2 + rounds * (K + 1) + K) // BLOCK) for c in ctxs]
+    nblocks = sum(per_seq) + 8
+    sb = fa.SpeculativeBatch(target, draft, nblocks, BLOCK, K,
+                             generator=torch.Generator(device="cuda").manual_seed(args.seed))
+    prompts = [torch.randint(0, CFG["vocab_size"], (c + 1,), generator=g).tolist() for c in ctxs]
+    prefill = None
+    if args.synthetic_kv:   # random keys/values in the pools instead of a prefill
+        for store in (sb.pool_t.k_store, sb.pool_t.v_store, sb.pool_d.k_store, sb.pool_d.v_store):
+            store.normal_()
+        for toks in prompts:
+            sb.add(toks, max_new_tokens=10 ** 9, temperature=temperature, prefill=False)
+    else:                   # the contexts come from the models: packed prefill of every prompt
+        torch.cuda.synchronize()
+        tp = time.perf_counter()
+        sb.add_many(prompts, 10 ** 9, temperature)
+        torch.cuda.synchronize()
+        tp = time.perf_counter() - tp
+        n_tok = sum(len(p) - 1 for p in prompts)
+        prefill = {"tokens": n_tok, "seconds": round(tp, 3), "tok_per_s": round(n_tok / tp, 1),
+                   "models": ("target (32 layers; the early-exit draft shares its first 4 layers' cache)"
+                              if sb.shared else "target (32 layers) and draft (4 layers)") +
+                             ", packed 32K-token forwards"}
+        log(f"T={temperature}: prefill {n_tok} tokens in {tp:.1f}s")
+    torch.cuda.synchronize()
+    for i in range(args.warmup):
+        sb.round()
+    log(f"T={temperature}: {args.warmup} warm-up rounds done")
+    torch.cuda.synchronize()
+
+    # timed rounds: each round's kernels replay from the HIP graph captured for its shape, queued back
+    # to back (each one's inputs computed on the GPU from the previous one's acceptance, the host's
+    # bookkeeping one round behind), in chunks of 32 for the progress lines; the last round on its own,
+    # after noting the lengths it starts from
+    acc0 = dict(sb.stats)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    committed = 0
+    done_rounds = 0
+    while done_rounds < args.steps - 1:
+        n = min(32 - done_rounds % 32, args.steps - 1 - done_rounds)
+        committed += sb.run_rounds(n)
+        done_rounds += n
+        if done_rounds % 32 == 0:
+            log(f"T={temperature}: round {done_rounds}/{args.steps}: {committed} tokens committed")
+    last_lens = [len(s.tokens) for s in sb.active()]
+    committed += sb.round()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    log(f"T={temperature}: round {args.steps}/{args.steps}: {committed} tokens committed in {elapsed:.2f}s")
+    out = {"elapsed": elapsed, "committed": committed, "prefill": prefill,
+           "proposed": sb.stats["proposed"] - acc0["proposed"], "accepted": sb.stats["accepted"] - acc0["accepted"]}
+    if timing:
+        out["attn_avg"], out["attn_bytes"] = time_verify_attention(torch, fa, ops, sb, last_lens)
+        past = sum(1 for n in last_lens for t in range(K + 1) if n - 1 + t >= 8192)
+        out["combine_note"] = (f"{past} of {len(last_lens) * (K + 1)} query positions of the measured round "
+                               f"reach past key 8191, so attn_combine_kernel also runs" if past else
+                               "every query of the measured round sees one chunk, so no combine launch")
+        out["phases"] = phase_times(torch, sb)
+    del sb
+    torch.cuda.empty_cache()
+    return out
+
+
 def kernel_mode(args):
     import torch
 
@@ -411,6 +517,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--temperature", type=float, default=0.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-t1-variant", action="store_true", help="skip the temperature-1.0 run")
     ap.add_argument("--synthetic-kv", action="store_true",
                     help="fill the pools with N(0,1) keys/values instead of prefilling the prompts")
     ap.add_argument("--seed", type=int, default=0)
@@ -438,69 +545,22 @@ def main():
     target, draft = build_models(torch, fa)
     log(f"models built in {time.time() - t0:.1f}s")
 
-    g = torch.Generator().manual_seed(args.seed)
-    ctxs = torch.randint(CTX_LO, CTX_HI + 1, (BATCH,), generator=g).tolist()
-    rounds = args.warmup + args.steps
-    per_seq = [-(-(c + 2 + rounds * (K + 1) + K) // BLOCK) for c in ctxs]
-    nblocks = sum(per_seq) + 8
-    sb = fa.SpeculativeBatch(target, draft, nblocks, BLOCK, K,
-                             generator=torch.Generator(device="cuda").manual_seed(args.seed))
-    prompts = [torch.randint(0, CFG["vocab_size"], (c + 1,), generator=g).tolist() for c in ctxs]
-    prefill = None
-    if args.synthetic_kv:   # random keys/values in the pools instead of a prefill
-        for store in (sb.pool_t.k_store, sb.pool_t.v_store, sb.pool_d.k_store, sb.pool_d.v_store):
-            store.normal_()
-        for toks in prompts:
-            sb.add(toks, max_new_tokens=10 ** 9, temperature=args.temperature, prefill=False)
-    else:                   # the contexts come from the models: packed prefill of every prompt
-        torch.cuda.synchronize()
-        tp = time.perf_counter()
-        sb.add_many(prompts, 10 ** 9, args.temperature)
-        torch.cuda.synchronize()
-        tp = time.perf_counter() - tp
-        n_tok = sum(len(p) - 1 for p in prompts)
-        prefill = {"tokens": n_tok, "seconds": round(tp, 3), "tok_per_s": round(n_tok / tp, 1),
-                   "models": ("target (32 layers; the early-exit draft shares its first 4 layers' cache)"
-                              if sb.shared else "target (32 layers) and draft (4 layers)") +
-                             ", packed 32K-token forwards"}
-        log(f"prefill: {n_tok} tokens in {tp:.1f}s")
-    torch.cuda.synchronize()
-    log(f"pools: target {sb.pool_t.k_store.numel() * 4 / 1e9:.1f} GB, draft {sb.pool_d.k_store.numel() * 4 / 1e9:.1f} GB;"
-        f" setup {time.time() - t0:.1f}s")
-
-    for i in range(args.warmup):
-        sb.round()
-        log(f"warmup round {i} done")
-    torch.cuda.synchronize()
-
-    # timed rounds: each round's kernels replay from the HIP graph captured for its shape
-    acc0 = dict(sb.stats)
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    committed = 0
-    done_rounds = 0
-    # rounds queued back to back (each one's inputs computed on the GPU from the previous one's
-    # acceptance, the host's bookkeeping one round behind), in chunks of 32 for the progress lines; the
-    # last round on its own, after noting the lengths it starts from
-    while done_rounds < args.steps - 1:
-        n = min(32 - done_rounds % 32, args.steps - 1 - done_rounds)
-        committed += sb.run_rounds(n)
-        done_rounds += n
-        if done_rounds % 32 == 0:
-            log(f"round {done_rounds}/{args.steps}: {committed} tokens committed")
-    last_lens = [len(s.tokens) for s in sb.active()]
-    committed += sb.round()
-    log(f"round {args.steps}/{args.steps}: {committed} tokens committed")
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t_start
-    proposed = sb.stats["proposed"] - acc0["proposed"]
-    accepted = sb.stats["accepted"] - acc0["accepted"]
-
-    attn_avg, attn_bytes_launch = time_verify_attention(torch, fa, ops, sb, last_lens)
+    main_run = run_rounds(torch, fa, ops, target, draft, args, args.temperature, timing=True)
+    elapsed, committed = main_run["elapsed"], main_run["committed"]
+    proposed, accepted = main_run["proposed"], main_run["accepted"]
+    attn_avg, attn_bytes_launch = main_run["attn_avg"], main_run["attn_bytes"]
     attn_gbs = attn_bytes_launch / attn_avg / 1e9
     attn_traffic = attn_bytes_launch
-
+    prefill = main_run["prefill"]
     value = committed / elapsed
+    t1 = None
+    if not args.no_t1_variant and args.temperature != 1.0:
+        r = run_rounds(torch, fa, ops, target, draft, args, 1.0, timing=False)
+        t1 = {"value": round(r["committed"] / r["elapsed"], 2), "unit": "tok/s", "temperature": 1.0,
+              "ms_per_step": round(r["elapsed"] / args.steps * 1e3, 3),
+              "acceptance": {"proposed": r["proposed"], "accepted": r["accepted"],
+                             "rate": round(r["accepted"] / max(r["proposed"], 1), 4),
+                             "committed_per_round": round(r["committed"] / args.steps, 2)}}
 
     v = CFG["vocab_size"]
     acc_avg = time_accept(torch, ops, 20, 3)
@@ -534,8 +594,7 @@ def main():
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic("paged_attention_verify_8b.md"),
                      "kernel": "paged_attention verify: attn_unit_kernel<128,16>, one call per layer, after one "
-                               "attn_plan_kernel per pass (8192-key chunks: every query of this workload sees one "
-                               "chunk, so no combine launch)",
+                               "attn_plan_kernel per pass (8192-key chunks); " + main_run["combine_note"],
                      "avg_launch_us": round(attn_avg * 1e6, 2),
                      "algorithmic_bytes_per_launch": int(attn_traffic)},
         "accept_kernel": {"avg_us": round(acc_avg * 1e6, 2), "achieved_GBs": round(acc_gbs, 1),
@@ -545,6 +604,8 @@ def main():
                           "with_head_stats": {"avg_us": round(accs_avg * 1e6, 2),
                                               "effective_GBs": round(accept_bytes(BATCH, K, v) / accs_avg / 1e9, 1)}},
         "prefill": prefill,
+        "verify_pass": main_run["phases"],
+        "t1_variant": t1,
         # MFMA utilisation of the dense GEMMs (bf16 dense peak 2.5 PFLOP/s), event-timed after the rounds
         "gemm_verify_m448": gemm_verify,
         "gemm_draft_m64": gemm_draft,

@@ -76,12 +76,13 @@ SIGNATURES = {
                                  c_i64, c_p]),
     "fs_sampling_workspace_size": (c_i64, [c_i64, c_i64]),
     "fs_spec_accept": (c_i32, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i32, c_i32, c_i64, c_i32, c_p, c_p, c_p,
-                               c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_i64, c_p]),
+                               c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p]),
     "fs_spec_accept_stats": (c_i32, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i32, c_i32, c_i64, c_i32, c_p, c_p, c_p,
-                                     c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_i64, c_p]),
+                                     c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p]),
     "fs_verify_probs": (c_i32, [c_p, c_i64, c_p, c_i64, c_i32, c_i64, c_i32, c_p, c_p, c_p, c_p, c_p, c_p, c_i64,
                                 c_p]),
     "fs_spec_accept_workspace_size": (c_i64, [c_i32, c_i32, c_i64]),
+    "fs_keyed_noise": (c_i32, [c_p, c_i32, c_i32, c_i32, c_i64, c_i32, c_p, c_i64, c_i64, c_p]),
 }
 
 _lib = None

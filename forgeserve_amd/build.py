@@ -28,7 +28,7 @@ FLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
 
-SOURCES = ["abi.hip", "kv.hip", "attention.hip", "norm.hip", "gemm.hip", "sample.hip"]
+SOURCES = ["abi.hip", "kv.hip", "attention.hip", "norm.hip", "gemm.hip", "sample.hip", "rng.hip"]
 
 
 def _run(cmd):

@@ -160,9 +160,10 @@ FS_DEVICE void wait_vm() {
 
 // Row statistics epilogue (the LM head feeding sampling and acceptance, sampling.py:13): for every
 // output row and every WN-column block of a wave, the softmax statistics of the stored (bf16-rounded)
-// values at that row's 1/T, written to stats[row * ld + column / WN].
+// values x at that row's temperature (y = x / T, a true division; y = x at T == 1 and at T == 0,
+// whose rows use only the argmax), written to stats[row * ld + column / WN].
 struct RowStatsOut {
-  const float* inv_t;   // [M], or null for T = 1
+  const float* temp;    // [M], or null for T = 1
   SoftmaxStat* stats;   // row m's nparts records at stats + m * ld
   int64_t nparts, ld;
 };
@@ -353,7 +354,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
       // the four lanes l16 + 16g share a row: their shuffles never mix rows, so rows past M are
       // harmless and are simply not written
       const int64_t row = m0 + wm * WM + 16 * i + l16;
-      const float inv_t = (rs.inv_t && row < M) ? rs.inv_t[row] : 1.f;
+      const float temp = (rs.temp && row < M) ? rs.temp[row] : 1.f;
+      // y = x / T in place of the products (the logits are stored already); the division only where
+      // some row of the wave has a temperature other than 0 and 1
+      const bool div = __any(temp != 1.f && temp > 0.f);
       float ym = -INFINITY, av = -INFINITY;
       int ai = 0x7fffffff;
 #pragma unroll
@@ -361,9 +365,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
         const int64_t col0 = n0 + wn * WN + 16 * j + 4 * g;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          if (col0 + r >= N) continue;
           const float v = Elem<FS_BF16>::round(acc[i][j][r]);
-          ym = fmaxf(ym, v * inv_t);
+          const float y = (div && temp != 1.f && temp > 0.f) ? v / temp : v;
+          acc[i][j][r] = y;
+          if (col0 + r >= N) continue;
+          ym = fmaxf(ym, y);
           argmax_merge(av, ai, v, (int)(col0 + r));
         }
       }
@@ -381,7 +387,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
         const int64_t col0 = n0 + wn * WN + 16 * j + 4 * g;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (col0 + r < N) se += __builtin_amdgcn_exp2f(fmaf(Elem<FS_BF16>::round(acc[i][j][r]) * inv_t, L2E, -ml));
+          if (col0 + r < N) se += __builtin_amdgcn_exp2f(fmaf(acc[i][j][r], L2E, -ml));
       }
       se += __shfl_xor(se, 16, 64);   // (g0 + g1) + (g2 + g3) in every lane
       se += __shfl_xor(se, 32, 64);
@@ -578,7 +584,7 @@ extern "C" int64_t fs_gemm_row_stats_parts(int64_t M, int64_t N, int64_t K) {
 }
 
 extern "C" int fs_gemm_row_stats(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
-                                 int64_t M, int64_t N, int64_t K, const float* inv_temperature, void* stats,
+                                 int64_t M, int64_t N, int64_t K, const float* temperature, void* stats,
                                  int64_t stats_ld, int64_t nparts, void* stream) {
   FS_CHECK_ARG(A && B && C && stats, "gemm_row_stats: null pointer");
   FS_CHECK_ARG(M >= 0 && N > 0 && N < 0x7fffffff && K > 0, "gemm_row_stats: M %lld N %lld K %lld", (long long)M,
@@ -592,7 +598,7 @@ extern "C" int fs_gemm_row_stats(const void* A, int64_t lda, const void* B, int6
                "gemm_row_stats: stats_ld %lld < nparts (or stats not 16-byte aligned)", (long long)stats_ld);
   if (M == 0) return 0;
   launch_lds<true>((const uint16_t*)A, lda, (const uint16_t*)B, ldb, (uint16_t*)C, ldc, nullptr, 0, M, N, K, 1, nullptr,
-                   RowStatsOut{inv_temperature, reinterpret_cast<SoftmaxStat*>(stats), nparts, stats_ld},
+                   RowStatsOut{temperature, reinterpret_cast<SoftmaxStat*>(stats), nparts, stats_ld},
                    fs::as_stream(stream));
   return fs::launch_status("gemm_row_stats");
 }

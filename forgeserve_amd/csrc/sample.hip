@@ -4,9 +4,11 @@
 // rollback arithmetic of speculative.py:77.
 //
 // Every row of V logits is cut into chunks of CH columns. Launch 1 reduces each (row, chunk) to
-// (max of x/T, sum of exp(x/T - max), first argmax of x). Later launches merge a row's chunk partials
+// (max of y = x/T, sum of exp(y - max), first argmax of x). Later launches merge a row's chunk partials
 // in increasing chunk order, so every workgroup that needs a row's softmax gets bit-identical
-// (M, S) and therefore bit-identical probabilities p_v = exp(x_v/T - M) / S.
+// (M, S), and every probability is evaluated by one function (ProbFn): p_v = exp(y_v - M) * (1/S),
+// y_v = x_v / T a true float32 division, the order in which torch's softmax forms it (sampling.py:13).
+// M is torch's max bit for bit; exp and S (a sum in another order) differ from torch's by a few ulps.
 //
 // torch.multinomial(w, 1) draws argmax_v(w_v / E_v) with E ~ Exp(1) (first index on ties); the
 // caller supplies E, so the draw is a deterministic function of (logits, E) and can be compared
@@ -141,13 +143,25 @@ FS_DEVICE Stat merge_row(const Stat* st, int nch) {
   return r;
 }
 
-// p_v of a row from logits and merged stats (T > 0): softmax(f32(x) / T) (sampling.py:13).
-FS_DEVICE float softmax_at(float x, float T, const Stat& st) { return expf(x / T - st.m) / st.s; }
+// The probability of logit x in a row with merged statistics (M, S) at temperature T > 0
+// (sampling.py:13): y = x / T (a true division; exact and skipped at T == 1), then exp(y - M) times the
+// correctly rounded 1/S, the order torch's softmax uses. Every kernel that needs a probability on the
+// logits path calls this one function, so the accept test, the residual sums, the candidate keys and
+// the exact keys all see the same p_v.
+struct ProbFn {
+  float T, M, invS;
+  FS_DEVICE ProbFn() : T(1.f), M(0.f), invS(1.f) {}
+  FS_DEVICE ProbFn(float t, const Stat& st) : T(t), M(st.m), invS(1.f / st.s) {}
+  FS_DEVICE float operator()(float x) const {
+    const float y = T == 1.f ? x : x / T;
+    return expf(y - M) * invS;
+  }
+};
 
 // One chunk of one row. T == 0: the first argmax of x. T > 0: (m, s) = (max of y, sum of exp(y - m))
-// with y = x * (1/T) (exact at T == 1; elsewhere within an ulp of sampling.py:13's x / T, a shift the
-// softmax absorbs). The chunk's loads are all issued up front; the values stay in registers for the
-// max pass and the exp pass.
+// with y = x / T, a true division (sampling.py:13), so m is the max torch's softmax subtracts. The
+// chunk's loads are all issued up front; the values stay in registers for the max pass and the exp
+// pass (the sum's exp is the bare exp2; S differs from torch's sum by rounding either way).
 template <int DT>
 FS_DEVICE Stat chunk_stat(const typename Elem<DT>::T* row, int c, int64_t V, float T, float* shf, int* shi) {
   const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
@@ -173,11 +187,10 @@ FS_DEVICE Stat chunk_stat(const typename Elem<DT>::T* row, int c, int64_t V, flo
     return st;
   }
   if (T != 1.f) {
-    const float invT = 1.f / T;
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[u][j] = x[u][j] * invT;  // padding stays -inf
+      for (int j = 0; j < 8; ++j) x[u][j] = x[u][j] / T;  // padding stays -inf
   }
   float m = -INFINITY;
 #pragma unroll
@@ -197,16 +210,6 @@ FS_DEVICE Stat chunk_stat(const typename Elem<DT>::T* row, int c, int64_t V, flo
   st.ai = 0;
   return st;
 }
-
-// Softmax value of one column for the vocab-wide passes: exp(y - M) / S evaluated as
-// exp2(y*log2e - M*log2e) * (1/S) with y = x * (1/T) (exact at T = 1). The accept/reject test itself
-// uses softmax_at (expf, true divides).
-struct FastSoftmax {
-  float invT, ML, invS;
-  FS_DEVICE FastSoftmax() : invT(1.f), ML(0.f), invS(1.f) {}
-  FS_DEVICE FastSoftmax(float t, const Stat& st) : invT(1.f / t), ML(st.m * LOG2E_F), invS(1.f / st.s) {}
-  FS_DEVICE float operator()(float x) const { return __builtin_amdgcn_exp2f(fmaf(x * invT, LOG2E_F, -ML)) * invS; }
-};
 
 // ------------------------------------------------------------------------------------------------
 // launch 1: per-(row, chunk) statistics
@@ -248,7 +251,7 @@ __global__ void __launch_bounds__(THREADS) sample_argmax_kernel(RowSet rs, int64
   if (T <= 0.f) return;
   if (threadIdx.x == 0) shs = merge_row(stats + (int64_t)r * nch, nch);
   __syncthreads();
-  const FastSoftmax fs(T, shs);
+  const ProbFn fs(T, shs);
   const auto* row = row_ptr<DT>(rs, r, 0);
   const float* er = E + (int64_t)r * ldE;
   const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0) &&
@@ -319,6 +322,9 @@ struct AcceptArgs {
   int32_t* out_tokens;   // [B, K+1]
   int32_t* n_acc;        // [B]
   int32_t* seq_len;      // [B] or null
+  float* dbg_p;          // [B, K] or null: p_i(x_i) of the proposals i < k_eff (the accept test's p)
+  float* dbg_q;          // [B, K] or null: q_i(x_i)
+  float* dbg_s;          // [B] or null: the residual sum of the rejected position (0: none, or greedy)
 };
 
 FS_DEVICE int keff_of(const AcceptArgs& A, int b) { return A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K; }
@@ -418,14 +424,18 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* ms) {
           px = xp;
           qx = xq;
         } else if (T > 0.f) {
-          px = softmax_at(xp, T, ms[i]);
-          qx = softmax_at(xq, T, ms[A.rs.n0 + i]);
+          px = ProbFn(T, ms[i])(xp);
+          qx = ProbFn(T, ms[A.rs.n0 + i])(xq);
         } else {  // one-hot rows of the first argmax (sampling.py:11-12)
           px = ms[i].ai == x ? 1.f : 0.f;
           qx = ms[A.rs.n0 + i].ai == x ? 1.f : 0.f;
         }
         const float ratio = qx > 0.f ? Elem<ProbType<DT, PROBS>::value>::round(px / qx) : 1.0f;  // speculative.py:26
         accept = u < fminf(1.0f, ratio);
+        if (A.dbg_p) {
+          A.dbg_p[(int64_t)b * A.K + i] = px;
+          A.dbg_q[(int64_t)b * A.K + i] = qx;
+        }
       }
     }
     const uint64_t rejected = __ballot(w == 0 && i < ke && !accept);
@@ -433,7 +443,10 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* ms) {
   }
   if (threadIdx.x == 0) {
     A.jpos[b] = j;
-    if (!PROBS && T <= 0.f) write_outputs(A, b, j, ms[j].ai);
+    if (!PROBS && T <= 0.f) {
+      write_outputs(A, b, j, ms[j].ai);
+      if (A.dbg_s) A.dbg_s[b] = 0.f;
+    }
   }
 }
 
@@ -464,10 +477,12 @@ __global__ void __launch_bounds__(64 * STEP_WAVES) accept_step_kernel(AcceptArgs
 // The extra token is argmax_v fl(w_v / E_v) (multinomial as the argmax over Exp(1) noise), with
 // w = p for the bonus token or when Σr = 0, and w = fl(r / S) otherwise (speculative.py:30-33); S = Σ r
 // is known only once every chunk has summed its part. One pass therefore ranks the columns by cheap
-// keys, p_v · rcp(E_v) and r_v · rcp(E_v), which differ from the final keys (times S) by a few float32
-// roundings plus, for the residual, the rounding of r / S to the probability dtype. A column whose
-// cheap key is below max · (1 - margin) cannot win, with the margin 8 or more times that error (2^-18
-// for float32 arithmetic, 2^-6 for bf16 probabilities, 2^-8 for f16). Each chunk keeps the columns
+// keys, p_v · rcp(E_v) and r_v · rcp(E_v). p_v, q_v and r_v = max(p_v - q_v, 0) are the exact values
+// the final keys use (the same ProbFn, the same subtraction), so the cheap keys differ from the final
+// keys (times S) only by the reciprocal and the last two roundings (under 3 float32 ulps, also where
+// p_v and q_v nearly cancel) plus, for bf16/f16 probabilities, the rounding of r / S to that dtype. A
+// column whose cheap key is below max · (1 - margin) cannot win, with the margin 8 or more times that
+// error (2^-18 for float32 arithmetic, 2^-6 for bf16 probabilities, 2^-8 for f16). Each chunk keeps the columns
 // within the margin of its own max (its candidates, nearly always one per set), and the final pass
 // scores them exactly. Chunks whose list overflowed, and sequences whose max is too small for a
 // relative bound, are rescanned exactly.
@@ -487,7 +502,7 @@ template <int DT, bool PROBS>
 struct PairRow {
   const typename Elem<DT>::T* pr;
   const typename Elem<DT>::T* qr;
-  FastSoftmax sp, sq;
+  ProbFn sp, sq;
   FS_DEVICE float p_at(float x) const { return PROBS ? x : sp(x); }
   FS_DEVICE float q_at(float x) const { return PROBS ? x : sq(x); }
   FS_DEVICE float resid(float xp, float xq) const {   // (p - q).clamp(min=0)
@@ -524,10 +539,10 @@ __global__ void __launch_bounds__(THREADS) accept_pair_kernel(AcceptArgs A) {
   const Stat* ms = A.mstats + (int64_t)b * per;
   const int j = A.jpos[b];
   const bool bonus = j >= ke;
-  FastSoftmax sp, sq;
+  ProbFn sp, sq;
   if (!PROBS) {
-    sp = FastSoftmax(T, ms[j]);
-    if (!bonus) sq = FastSoftmax(T, ms[A.rs.n0 + j]);
+    sp = ProbFn(T, ms[j]);
+    if (!bonus) sq = ProbFn(T, ms[A.rs.n0 + j]);
   }
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j);
@@ -633,10 +648,10 @@ __global__ void __launch_bounds__(64) accept_final_kernel(AcceptArgs A) {
   const bool trust = gmax >= CAND_MIN;
   const float th = cand_threshold(gmax, set ? CandMargin<PD>::value : MARGIN_F32);
   const int per = A.rs.n0 + A.rs.n1;
-  FastSoftmax sp, sq;
+  ProbFn sp, sq;
   if (!PROBS) {
-    sp = FastSoftmax(T, A.mstats[(int64_t)b * per + j]);
-    if (!bonus) sq = FastSoftmax(T, A.mstats[(int64_t)b * per + A.rs.n0 + j]);
+    sp = ProbFn(T, A.mstats[(int64_t)b * per + j]);
+    if (!bonus) sq = ProbFn(T, A.mstats[(int64_t)b * per + A.rs.n0 + j]);
   }
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const PairRow<DT, PROBS> pair{pr, bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j), sp, sq};
@@ -668,7 +683,10 @@ __global__ void __launch_bounds__(64) accept_final_kernel(AcceptArgs A) {
     }
   }
   wave_argmax(v, extra);
-  if (lane == 0) write_outputs(A, b, j, extra);
+  if (lane == 0) {
+    write_outputs(A, b, j, extra);
+    if (A.dbg_s) A.dbg_s[b] = s;
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -688,7 +706,7 @@ __global__ void __launch_bounds__(THREADS) probs_kernel(RowSet rs, int64_t V, in
     const int64_t v = (int64_t)c * CH + (int64_t)u * THREADS + threadIdx.x;
     if (v >= V) break;
     if (T > 0.f) {
-      reinterpret_cast<float*>(out)[(int64_t)r * ldo + v] = softmax_at(Elem<DT>::load(row, v), T, st);
+      reinterpret_cast<float*>(out)[(int64_t)r * ldo + v] = ProbFn(T, st)(Elem<DT>::load(row, v));
     } else {
       Elem<DT>::store(reinterpret_cast<typename Elem<DT>::T*>(out), (int64_t)r * ldo + v, v == st.ai ? 1.f : 0.f);
     }
@@ -873,9 +891,11 @@ namespace {
 int spec_accept_impl(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb, int64_t dft_si,
                      int32_t B, int32_t K, int64_t V, int32_t dtype, const int32_t* draft_tokens, const int32_t* k_eff,
                      const float* temperature, const float* u, const float* E, int64_t ldE, int32_t* out_tokens,
-                     int32_t* n_accepted, int32_t* seq_len, const void* row_stats, void* workspace,
-                     int64_t workspace_bytes, void* stream) {
+                     int32_t* n_accepted, int32_t* seq_len, float* p_x, float* q_x, float* res_sum,
+                     const void* row_stats, void* workspace, int64_t workspace_bytes, void* stream) {
   FS_CHECK_ARG(tgt && temperature && out_tokens && n_accepted && workspace, "spec_accept: null pointer");
+  FS_CHECK_ARG((p_x == nullptr) == (q_x == nullptr) && (p_x == nullptr) == (res_sum == nullptr),
+               "spec_accept: p_x, q_x and res_sum are given together or not at all");
   FS_CHECK_ARG(K == 0 || (dft && draft_tokens && u), "spec_accept: null draft inputs");
   FS_CHECK_ARG(E != nullptr, "spec_accept: E (Exp(1) noise) is required");
   FS_CHECK_ARG(dtype_ok(dtype), "spec_accept: dtype %d", dtype);
@@ -900,6 +920,9 @@ int spec_accept_impl(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void
   A.out_tokens = out_tokens;
   A.n_acc = n_accepted;
   A.seq_len = seq_len;
+  A.dbg_p = p_x;
+  A.dbg_q = q_x;
+  A.dbg_s = res_sum;
   carve_accept(A, workspace, B, K, nch, A.nchr);
   if (row_stats) {
     FS_CHECK_ARG((reinterpret_cast<uintptr_t>(row_stats) & 15) == 0, "spec_accept: row statistics not 16-byte aligned");
@@ -919,20 +942,24 @@ extern "C" int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, c
                               int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype,
                               const int32_t* draft_tokens, const int32_t* k_eff, const float* temperature,
                               const float* u, const float* E, int64_t ldE, int32_t* out_tokens, int32_t* n_accepted,
-                              int32_t* seq_len, void* workspace, int64_t workspace_bytes, void* stream) {
+                              int32_t* seq_len, float* p_x, float* q_x, float* res_sum, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
   return spec_accept_impl(tgt, tgt_sb, tgt_si, dft, dft_sb, dft_si, B, K, V, dtype, draft_tokens, k_eff, temperature, u,
-                          E, ldE, out_tokens, n_accepted, seq_len, nullptr, workspace, workspace_bytes, stream);
+                          E, ldE, out_tokens, n_accepted, seq_len, p_x, q_x, res_sum, nullptr, workspace,
+                          workspace_bytes, stream);
 }
 
 extern "C" int fs_spec_accept_stats(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
                                     int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype,
                                     const int32_t* draft_tokens, const int32_t* k_eff, const float* temperature,
                                     const float* u, const float* E, int64_t ldE, const void* row_stats,
-                                    int32_t* out_tokens, int32_t* n_accepted, int32_t* seq_len, void* workspace,
-                                    int64_t workspace_bytes, void* stream) {
+                                    int32_t* out_tokens, int32_t* n_accepted, int32_t* seq_len, float* p_x,
+                                    float* q_x, float* res_sum, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
   FS_CHECK_ARG(row_stats != nullptr, "spec_accept_stats: null row statistics");
   return spec_accept_impl(tgt, tgt_sb, tgt_si, dft, dft_sb, dft_si, B, K, V, dtype, draft_tokens, k_eff, temperature, u,
-                          E, ldE, out_tokens, n_accepted, seq_len, row_stats, workspace, workspace_bytes, stream);
+                          E, ldE, out_tokens, n_accepted, seq_len, p_x, q_x, res_sum, row_stats, workspace,
+                          workspace_bytes, stream);
 }
 
 extern "C" int fs_row_stats_merge(const void* parts, int64_t parts_ld, int64_t nparts, int64_t M, void* out,
@@ -974,6 +1001,7 @@ extern "C" int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_
   A.out_tokens = out_tokens;
   A.n_acc = n_accepted;
   A.seq_len = nullptr;
+  A.dbg_p = A.dbg_q = A.dbg_s = nullptr;
   carve_accept(A, workspace, 1, K, nch, A.nchr);
   hipStream_t s = fs::as_stream(stream);
   switch (dtype) {

@@ -11,10 +11,12 @@ round over the running requests instead (speculative.py:53-85 for a batch): each
 to k_eff = min(k, remaining - 1) tokens, the k+1 window is reserved in both pools before the round
 (preempting as above when a pool runs out), and EOS, max_new_tokens and max_seq_len stop a request
 exactly where one-token decoding would. The random numbers of a request come from its own stream,
-keyed by (seed, request id, position), so its tokens do not depend on which other requests share
-the batch. (A recompute preemption re-prefills and samples the next token from the prefill logits,
-as one-token decoding does; that moves the request's round boundaries, so at T > 0 a preempted
-request continues with a different, equally valid sample.)
+keyed by (seed, request id, position) and drawn on the device by a counter-based generator
+(ops.keyed_noise): each use has a fixed slot (draft step i, the uniforms, the final draw, the
+prefill draw), so a request's tokens do not depend on which other requests share the batch nor on
+the round's k. (A recompute preemption re-prefills and samples the next token from the prefill
+logits, as one-token decoding does; that moves the request's round boundaries, so at T > 0 a
+preempted request continues with a different, equally valid sample.)
 """
 
 from collections import deque
@@ -43,58 +45,39 @@ class Request:
     cached: int = 0
     finished: bool = False
     blocks_d: List[int] = field(default_factory=BlockList)   # draft pool blocks (speculative engine)
+    preempted: int = 0                                        # times this request was preempted
+    stream: int = -1                                          # id of its random stream (speculative engine)
 
 
 def _stream_key(seed: int, rid: int, pos: int) -> int:
-    """Seed of request `rid`'s random stream for the round (or prefill) that starts at position `pos`."""
+    """Key of request `rid`'s random stream for the round (or prefill) that starts at position `pos`."""
     return ((seed * 1_000_003 + rid) * 1_000_033 + pos) % (1 << 62)
+
+
+# Slots of a key's stream: draft step i uses slot i; the acceptance's uniforms and its final Exp(1)
+# row, and the draw after a (re)prefill, have slots of their own past any draft step.
+SLOT_U, SLOT_FINAL, SLOT_PREFILL = 1 << 20, (1 << 20) + 1, (1 << 20) + 2
 
 
 class _KeyedDraws:
     """A speculative round's random numbers, one stream per request keyed by (seed, request id,
-    position): the k draft Exp(1) rows, then u, then the final Exp(1) row. Greedy requests draw
-    nothing (their rows are ignored by the kernels)."""
+    position), drawn on the device (ops.keyed_noise) straight into the round's buffers: the draft
+    steps' Exp(1) rows (slot i for step i), the uniforms u (slot SLOT_U, column i for proposal i) and
+    the final Exp(1) row (SLOT_FINAL). Every value depends only on the request's key, the slot and
+    the column, never on the batch or the round's k. Greedy requests get numbers too; the kernels
+    ignore them."""
 
     def __init__(self, reqs, n, temps, seed, k, v, dev):
         self.k, self.v, self.dev = k, v, dev
-        self.gens = [torch.Generator(device=dev).manual_seed(_stream_key(seed, r.id, ni)) if t > 0 else None
-                     for r, ni, t in zip(reqs, n, temps)]
+        keys = torch.tensor([_stream_key(seed, r.stream, ni) for r, ni in zip(reqs, n)], dtype=torch.int64)
+        self.keys = to_device(keys, dev)
 
-    def _rows(self, fn):
-        return torch.stack([fn(g) for g in self.gens])
-
-    def draft(self, i):
-        return self._rows(lambda g: torch.empty(self.v, device=self.dev).exponential_(generator=g) if g is not None
-                          else torch.ones(self.v, device=self.dev))
-
-    def accept(self):
-        # per request: u first, then E (one generator, fixed order)
-        u, e = [], []
-        for g in self.gens:
-            if g is None:
-                u.append(torch.zeros(self.k, device=self.dev))
-                e.append(torch.ones(self.v, device=self.dev))
-            else:
-                u.append(torch.rand(self.k, device=self.dev, generator=g))
-                e.append(torch.empty(self.v, device=self.dev).exponential_(generator=g))
-        return torch.stack(u).contiguous(), torch.stack(e)
-
-    # the same numbers drawn straight into the round's buffers (row r of out is request r's)
-    def draft_into(self, i, out):
-        if any(g is None for g in self.gens):
-            out.fill_(1.0)
-        for r, g in enumerate(self.gens):
-            if g is not None:
-                out[r].exponential_(generator=g)
-
-    def accept_into(self, u, e):
-        if any(g is None for g in self.gens):
-            u.zero_()
-            e.fill_(1.0)
-        for r, g in enumerate(self.gens):
-            if g is not None:
-                u[r, : self.k].uniform_(generator=g)
-                e[r].exponential_(generator=g)
+    def fill_round(self, noise_d, u, e):
+        """noise_d (k, b, V) draft Exp(1) rows, u (b, >= k) uniforms, e (b, V) final Exp(1) rows."""
+        if noise_d.shape[0]:
+            ops.keyed_noise(self.keys, 0, noise_d, ops.RNG_EXP)
+        ops.keyed_noise(self.keys, SLOT_U, u, ops.RNG_UNIFORM)
+        ops.keyed_noise(self.keys, SLOT_FINAL, e, ops.RNG_EXP)
 
 
 class Engine:
@@ -132,13 +115,17 @@ class Engine:
 
     # ---- public API ---------------------------------------------------------------------------------
     def add_request(self, prompt: List[int], max_new_tokens: int, eos_id: Optional[int] = None,
-                    temperature: float = 0.0) -> int:
+                    temperature: float = 0.0, stream_id: Optional[int] = None) -> int:
+        """Queue a request (engine.py:48-55); returns its id. stream_id (speculative engine, optional):
+        the id its random numbers are keyed by, default the request id; two requests with the same
+        stream id, prompt and settings sample the same tokens in any engine (absent preemption)."""
         if not 0 < len(prompt) < self.limit:
             raise ValueError(f"prompt length must be in 1..{self.limit - 1}")
         if self.pool.blocks_for(len(prompt) + 1) > self.pool.allocator.num_blocks or (
                 self.draft is not None and self.pool_d.blocks_for(len(prompt) + 1) > self.pool_d.allocator.num_blocks):
             raise ValueError("prompt does not fit in the block pool")
         req = Request(len(self.requests), list(prompt), max_new_tokens, eos_id, temperature)
+        req.stream = req.id if stream_id is None else int(stream_id)
         self.requests[req.id] = req
         self.waiting.append(req)
         return req.id
@@ -222,6 +209,7 @@ class Engine:
                 victim = self.running.pop()
                 self._release(victim)
                 victim.cached = 0
+                victim.preempted += 1
                 self.waiting.appendleft(victim)
                 self.preemptions += 1
                 continue   # retry (or, if the victim was this request, the loop ends or moves on)
@@ -260,8 +248,8 @@ class Engine:
         noise = None
         if t > 0:
             pos = len(req.prompt) + len(req.output)
-            g = torch.Generator(device=logits.device).manual_seed(_stream_key(self.seed, req.id, pos))
-            noise = torch.empty((1, v), device=logits.device).exponential_(generator=g)
+            key = to_device(torch.tensor([_stream_key(self.seed, req.stream, pos)], dtype=torch.int64), logits.device)
+            noise = ops.keyed_noise(key, SLOT_PREFILL, torch.empty((1, v), device=logits.device), ops.RNG_EXP)
         t_dev = to_device(torch.tensor([t], dtype=torch.float32), logits.device)
         self._push(req, int(ops.sample_logits(logits, t_dev, noise).tolist()[0]))
 
@@ -285,6 +273,7 @@ class Engine:
                     victim = self.running.pop()
                     self.pool.allocator.release(victim.blocks)
                     victim.blocks, victim.cached = BlockList(), 0
+                    victim.preempted += 1
                     self.waiting.appendleft(victim)
                     self.preemptions += 1
                     if victim is req:

@@ -209,7 +209,7 @@ class ForgeModel(nn.Module):
         return ops.gemm(y, self.lm_head.weight, out=out)
 
     def head(self, x, stats=None, out=None):
-        """Final norm + tied head (model.py:137-138). stats = (inv_temperature (rows,), parts): also emit
+        """Final norm + tied head (model.py:137-138). stats = (temperature (rows,), parts): also emit
         the logits' per-row softmax statistics (ops.gemm_row_stats). out: optional (rows, vocab) view
         (contiguous rows, any row stride) that receives the logits."""
         shape = x.shape
@@ -228,7 +228,7 @@ class ForgeModel(nn.Module):
         positions (B, T): absolute positions; default continues after what `kv` holds.
         kv: one cache view per layer (ContiguousKV or PagedLayerView); None uses a fresh cache.
         last_only: return only the logits of the last position, (B, 1, vocab).
-        head_stats: (inv_temperature, parts) for the head's rows: see head()."""
+        head_stats: (temperature, parts) for the head's rows: see head()."""
         dev = self.device
         if dev.type != "cuda":
             raise RuntimeError("ForgeModel runs on the GPU: move it with .to('cuda') first")

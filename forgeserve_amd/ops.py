@@ -130,10 +130,11 @@ def row_stats_parts(m: int, n: int, k: int) -> int:
     return int(_lib.load().fs_gemm_row_stats_parts(m, n, k))
 
 
-def gemm_row_stats(a: torch.Tensor, w: torch.Tensor, inv_temperature: Optional[torch.Tensor],
+def gemm_row_stats(a: torch.Tensor, w: torch.Tensor, temperature: Optional[torch.Tensor],
                    stats: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out = a @ w.T (the LM head, model.py:137-138) and, per row and column block, the softmax
-    statistics of the stored logits at 1/T = inv_temperature[row] (sampling.py:13). stats: int32
+    statistics of the stored logits x at y = x / temperature[row] (a true division, sampling.py:13;
+    rows at T = 0 keep only a meaningful argmax). stats: int32
     (M, nparts, 4) records (max, sum, argmax value as float bits, argmax index); rows may be strided."""
     require_device(a, w, stats)
     m, lda = _rows(a)
@@ -145,12 +146,12 @@ def gemm_row_stats(a: torch.Tensor, w: torch.Tensor, inv_temperature: Optional[t
     if (stats.dtype != I32 or tuple(stats.shape) != (m, nparts, 4) or stats.stride(2) != 1 or stats.stride(1) != 4
             or stats.stride(0) % 4):
         raise ValueError(f"gemm_row_stats: stats must be int32 ({m}, {nparts}, 4) with whole records per row")
-    if inv_temperature is not None and (inv_temperature.dtype != torch.float32 or inv_temperature.shape != (m,)):
-        raise ValueError("gemm_row_stats: inv_temperature must be float32 (M,)")
+    if temperature is not None and (temperature.dtype != torch.float32 or temperature.shape != (m,)):
+        raise ValueError("gemm_row_stats: temperature must be float32 (M,)")
     if out is None:
         out = torch.empty((m, n), dtype=a.dtype, device=a.device)
     _, ldc = _rows(out)
-    check(_lib.load().fs_gemm_row_stats(ptr(a), lda, ptr(w), ldb, ptr(out), ldc, m, n, k, ptr(inv_temperature),
+    check(_lib.load().fs_gemm_row_stats(ptr(a), lda, ptr(w), ldb, ptr(out), ldc, m, n, k, ptr(temperature),
                                         ptr(stats), stats.stride(0) // 4, nparts, stream_ptr()), "gemm_row_stats")
     return out
 
@@ -489,15 +490,17 @@ def spec_accept(tgt: torch.Tensor, dft: torch.Tensor, draft_tokens: torch.Tensor
                 temperature: torch.Tensor, u: torch.Tensor, noise: torch.Tensor,
                 seq_len: Optional[torch.Tensor] = None, out_tokens: Optional[torch.Tensor] = None,
                 n_accepted: Optional[torch.Tensor] = None,
-                row_stats: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                row_stats: Optional[torch.Tensor] = None, debug: bool = False):
     """Batched verify_draft from logits (speculative.py:20-33, sampling.py:9-13).
 
     tgt (B, K+1, V), dft (B, K, V) logits; draft_tokens int32 (B, K); k_eff int32 (B,) or None (= K);
     temperature float32 (B,); u float32 (B, K) uniforms; noise float32 (B, V) Exp(1);
     seq_len int32 (B,) cached lengths, advanced in place by 1 + n_accepted;
     row_stats: int32 (B, 2K+1, 4) softmax statistics of the rows (row_stats_merge of the LM heads'
-    gemm_row_stats at 1/temperature), which skips the statistics pass.
-    Returns out_tokens int32 (B, K+1) (accepted, extra, then -1) and n_accepted int32 (B,)."""
+    gemm_row_stats at the temperatures), which skips the statistics pass.
+    Returns out_tokens int32 (B, K+1) (accepted, extra, then -1) and n_accepted int32 (B,); with debug,
+    also {"p_x", "q_x": float32 (B, K), p_i(x_i) and q_i(x_i) of the proposals i < k_eff (NaN past it),
+    "res_sum": float32 (B,), the residual sum at the first rejection (0: none)}."""
     require_device(tgt, dft, draft_tokens, temperature, u, noise)
     b, k1, v = tgt.shape
     k = k1 - 1
@@ -518,6 +521,12 @@ def spec_accept(tgt: torch.Tensor, dft: torch.Tensor, draft_tokens: torch.Tensor
         n_accepted = torch.empty((b,), dtype=I32, device=tgt.device)
     lib = _lib.load()
     ws = _persistent_ws("accept", lib.fs_spec_accept_workspace_size(b, k, v), tgt.device)
+    dbg = None
+    if debug:
+        dbg = {"p_x": torch.full((b, k), float("nan"), dtype=torch.float32, device=tgt.device),
+               "q_x": torch.full((b, k), float("nan"), dtype=torch.float32, device=tgt.device),
+               "res_sum": torch.zeros((b,), dtype=torch.float32, device=tgt.device)}
+    px, qx, rs = (ptr(dbg["p_x"]), ptr(dbg["q_x"]), ptr(dbg["res_sum"])) if dbg else (0, 0, 0)
     if row_stats is not None:
         if row_stats.dtype != I32 or tuple(row_stats.shape) != (b, 2 * k + 1, 4) or not row_stats.is_contiguous():
             raise ValueError(f"spec_accept: row_stats must be contiguous int32 ({b}, {2 * k + 1}, 4)")
@@ -525,14 +534,15 @@ def spec_accept(tgt: torch.Tensor, dft: torch.Tensor, draft_tokens: torch.Tensor
         check(lib.fs_spec_accept_stats(ptr(tgt), tgt.stride(0), tgt.stride(1), ptr(dft), dft.stride(0),
                                        dft.stride(1) if k else 0, b, k, v, _dt(tgt), ptr(draft_tokens), ptr(k_eff),
                                        ptr(temperature), ptr(u), ptr(noise), noise.stride(0), ptr(row_stats),
-                                       ptr(out_tokens), ptr(n_accepted), ptr(seq_len), ptr(ws), ws.numel(),
-                                       stream_ptr()), "spec_accept")
-        return out_tokens, n_accepted
-    check(lib.fs_spec_accept(ptr(tgt), tgt.stride(0), tgt.stride(1), ptr(dft), dft.stride(0), dft.stride(1) if k else 0,
-                             b, k, v, _dt(tgt), ptr(draft_tokens), ptr(k_eff), ptr(temperature), ptr(u), ptr(noise),
-                             noise.stride(0), ptr(out_tokens), ptr(n_accepted), ptr(seq_len), ptr(ws), ws.numel(),
-                             stream_ptr()), "spec_accept")
-    return out_tokens, n_accepted
+                                       ptr(out_tokens), ptr(n_accepted), ptr(seq_len), px, qx, rs, ptr(ws),
+                                       ws.numel(), stream_ptr()), "spec_accept")
+    else:
+        check(lib.fs_spec_accept(ptr(tgt), tgt.stride(0), tgt.stride(1), ptr(dft), dft.stride(0),
+                                 dft.stride(1) if k else 0, b, k, v, _dt(tgt), ptr(draft_tokens), ptr(k_eff),
+                                 ptr(temperature), ptr(u), ptr(noise), noise.stride(0), ptr(out_tokens),
+                                 ptr(n_accepted), ptr(seq_len), px, qx, rs, ptr(ws), ws.numel(), stream_ptr()),
+              "spec_accept")
+    return (out_tokens, n_accepted, dbg) if debug else (out_tokens, n_accepted)
 
 
 def verify_probs(p: torch.Tensor, q: torch.Tensor, draft_tokens: torch.Tensor, u: torch.Tensor,
@@ -573,3 +583,22 @@ def spec_advance(res: torch.Tensor, b: int, k: int, first: int, n: torch.Tensor,
     check(_lib.load().fs_spec_advance(ptr(res), res.stride(0), b, k, first, ptr(n), ptr(budget), ptr(eos), ptr(done),
                                       ptr(ids), ptr(last), ptr(keff), ptr(pos0), ptr(posd), ptr(posv), stream_ptr()),
           "spec_advance")
+
+
+RNG_UNIFORM, RNG_EXP = 0, 1
+
+
+def keyed_noise(keys: torch.Tensor, slot0: int, out: torch.Tensor, kind: int) -> torch.Tensor:
+    """Counter-based draws keyed per row: out (n_slots, B, n) or (B, n) float32 (last dim contiguous)
+    receives, for slot s and row b, the variates of (keys[b], slot0 + s, column j): uniforms in
+    [0, 1) (kind RNG_UNIFORM) or Exp(1) (RNG_EXP). keys: int64 (B,) on the device."""
+    require_device(keys, out)
+    if keys.dtype != torch.int64 or keys.dim() != 1 or not keys.is_contiguous():
+        raise ValueError("keyed_noise: keys must be a contiguous int64 (B,) tensor")
+    o = out if out.dim() == 3 else out.unsqueeze(0)
+    s, b, n = o.shape
+    if o.dtype != torch.float32 or (n > 1 and o.stride(2) != 1) or b != keys.numel():
+        raise ValueError("keyed_noise: out must be float32 (n_slots, B, n) with B = len(keys), last dim contiguous")
+    check(_lib.load().fs_keyed_noise(ptr(keys), b, slot0, s, n, kind, ptr(o), o.stride(1), o.stride(0), stream_ptr()),
+          "keyed_noise")
+    return out

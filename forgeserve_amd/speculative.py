@@ -183,7 +183,7 @@ class _RoundState:
         # staging: int64 ids [b, 2] (prev, last) and last [b]; int32 k_eff [b], draft positions [b, 2] (step 0)
         # then [k-1, b] (steps 1..k-1; [k, b], steps 0..k-1, with a shared cache), verify positions
         # [b, k+1], tables [b, wt] and [b, wd];
-        # float32 temperature and 1/T [2, b]
+        # float32 temperatures [b]
         # a draft on the target's cache feeds only `last` in step 0 (the verify pass has cached every
         # position before it), so its step 0 is staged with the others
         km = k if n_shared else max(k - 1, 0)
@@ -196,7 +196,7 @@ class _RoundState:
         spans = [("ids", np.int64, (b, 2)), ("last", np.int64, (b,)), ("keff", np.int32, (b,)), ("pos0", np.int32, (b, 2)),
                  ("posd", np.int32, (km, b)), ("posv", np.int32, (b, k + 1)), ("n", np.int32, (b,)),
                  ("budget", np.int32, (b,)), ("eos", np.int32, (b,)), ("done", np.int32, (b,)),
-                 ("temps", np.float32, (2, b)), ("tab_t", np.int32, (b, wt))]
+                 ("temps", np.float32, (b,)), ("tab_t", np.int32, (b, wt))]
         if not n_shared:   # a draft on the target's cache reads the target's table
             spans.append(("tab_d", np.int32, (b, wd)))
         off, lay = 0, {}
@@ -278,8 +278,7 @@ class _RoundState:
         """The host-owned spans of staging buffer `slot`: temperatures and block tables."""
         h, b = self.hs[slot], len(temps)
         h["temps"].fill(0)
-        h["temps"][0, :b] = temps
-        h["temps"][1, :b] = [np.float32(1.0 / t) if t > 0 else 0.0 for t in temps]
+        h["temps"][:b] = temps
         tables = (("tab_t", blocks_t),) if self.n_shared else (("tab_t", blocks_t), ("tab_d", blocks_d))
         for name, lists in tables:
             # rows keep last round's entries: a row whose block list only grew gets its new blocks
@@ -313,7 +312,7 @@ def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _R
     fused acceptance, which returns (b, k+2) int32: n_accepted, then the committed tokens (-1 padded)."""
     b, k = st.b, st.k
     d = st.d
-    temps, inv_t = d["temps"][0], d["temps"][1]
+    temps = d["temps"]
     if phase < k:
         i = phase
         if i == 0 and st.n_shared:   # the shared cache holds every position before `last`
@@ -324,7 +323,7 @@ def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _R
             idx = st.draft_tok[:, i - 1].to(torch.int64)[:, None]
             pos = d["posd"][i if st.n_shared else i - 1][:, None]
         logits = draft._run(idx, pos, pool_d.views(d["tab_d"], pos), last_only=True,
-                            head_stats=(inv_t, st.parts_d[:, i]) if st.fused else None, out=st.dft_logits[:, i],
+                            head_stats=(temps, st.parts_d[:, i]) if st.fused else None, out=st.dft_logits[:, i],
                             hidden_out=st.hidden[:, i] if st.n_shared else None)
         ops.sample_logits(logits, temps, st.noise_d[i] if st.sampling else None, out32=st.draft_tok[:, i])
         if st.fused and i == k - 1:   # draft row (b, i) is record b*k + i: sequence b's draft rows k+1 .. 2k
@@ -333,9 +332,9 @@ def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _R
     last = d["last"]
     idx = torch.cat([last[:, None], st.draft_tok.to(torch.int64)], 1) if k else last[:, None]
     pos = d["posv"]
-    inv_t_t = inv_t.repeat_interleave(k + 1) if st.fused else None
+    temps_t = temps.repeat_interleave(k + 1) if st.fused else None
     views = pool_t.views(d["tab_t"], pos)
-    stats = (inv_t_t, st.parts_t) if st.fused else None
+    stats = (temps_t, st.parts_t) if st.fused else None
     if st.n_shared and k:   # the draft has run the shared blocks for all but token k_eff of each row
         tgt_logits = target._run_verify_reusing(st.n_shared, idx, pos, views, d["keff"], st.hidden[:, :k], stats)
     else:
@@ -398,7 +397,9 @@ def _launch_round(target, draft, pool_t, pool_d, st: "_RoundState", b: int, draw
     acceptance into the same device buffers."""
     k = st.k
     if st.sampling:
-        if hasattr(draws, "draft_into"):
+        if hasattr(draws, "fill_round"):   # every row's numbers in one launch per kind
+            draws.fill_round(st.noise_d[:k, :b], st.u[:b], st.e[:b])
+        elif hasattr(draws, "draft_into"):
             for i in range(k):
                 draws.draft_into(i, st.noise_d[i, :b])
             draws.accept_into(st.u[:b], st.e[:b])

@@ -185,11 +185,12 @@ int fs_gemm_partials(const void* A, int64_t lda, const void* B, int64_t ldb, int
  * C = A . B^T as fs_gemm (bf16, K % 64 == 0, 16-byte aligned rows, no residual), and for every row m
  * and every column block p of the kernel's tiling, stats[m * stats_ld + p] = {max of y, sum of
  * exp(y - max), max of x, first index of that max} over the block's stored (bf16) values x, with
- * y = x * inv_temperature[m] (inv_temperature NULL: 1). nparts must equal
- * fs_gemm_row_stats_parts(M, N, K) (0: the shape has no such kernel). No counterpart in the
- * reference: it computes softmax(logits.float() / T) from the stored logits. */
+ * y = x / temperature[m], a true float32 division as in sampling.py:13 (temperature NULL, 1 or 0:
+ * y = x; at 0 only the argmax is meaningful). nparts must equal fs_gemm_row_stats_parts(M, N, K)
+ * (0: the shape has no such kernel). No counterpart in the reference: it computes
+ * softmax(logits.float() / T) from the stored logits. */
 int fs_gemm_row_stats(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int64_t M,
-                      int64_t N, int64_t K, const float* inv_temperature, void* stats, int64_t stats_ld,
+                      int64_t N, int64_t K, const float* temperature, void* stats, int64_t stats_ld,
                       int64_t nparts, void* stream);
 
 int64_t fs_gemm_row_stats_parts(int64_t M, int64_t N, int64_t K);
@@ -272,22 +273,30 @@ int64_t fs_sampling_workspace_size(int64_t R, int64_t V);
  * Outputs: out_tokens int32 [B, K+1] (accepted proposals, then the extra token, then -1),
  * n_accepted int32 [B]. If seq_len != NULL it is the device-side rollback: on entry seq_len[b] is
  * the number of cached tokens before the verify window, on exit cached + 1 + n_accepted
- * (speculative.py:77). */
+ * (speculative.py:77).
+ * Probabilities are p_v = exp(x_v/T - M) * (1/S) (x_v/T a true float32 division, M the row's max of
+ * x/T, S the sum of exp(x/T - M)): the order torch's softmax forms them (sampling.py:13). One function
+ * computes them for the test, the residual and the draws.
+ * Optional debug outputs (all three or none, f32): p_x [B, K] and q_x [B, K] receive p_i(x_i) and
+ * q_i(x_i) of the proposals i < k_eff (speculative.py:26; others untouched); res_sum [B] the sum of
+ * the residual max(p_j - q_j, 0) at the first rejection j (speculative.py:30), 0 when every proposal
+ * was accepted or the row is greedy. They let a caller measure how near a decision was to a tie. */
 int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
                    int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype, const int32_t* draft_tokens,
                    const int32_t* k_eff, const float* temperature, const float* u, const float* E,
-                   int64_t ldE, int32_t* out_tokens, int32_t* n_accepted, int32_t* seq_len, void* workspace,
-                   int64_t workspace_bytes, void* stream);
+                   int64_t ldE, int32_t* out_tokens, int32_t* n_accepted, int32_t* seq_len, float* p_x,
+                   float* q_x, float* res_sum, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* fs_spec_accept with the rows' softmax statistics given (row_stats: [B][2K+1] records of
- * fs_row_stats_merge at 1/temperature, target rows 0..K then draft rows; 16-byte aligned): the
+ * fs_row_stats_merge at the rows' temperatures, target rows 0..K then draft rows; 16-byte aligned): the
  * vocab-wide statistics pass is skipped. Replaces the same seam as fs_spec_accept (speculative.py:20-33
  * with probs_from_logits), for callers whose LM head produced the statistics (fs_gemm_row_stats). */
 int fs_spec_accept_stats(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
                          int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype, const int32_t* draft_tokens,
                          const int32_t* k_eff, const float* temperature, const float* u, const float* E,
                          int64_t ldE, const void* row_stats, int32_t* out_tokens, int32_t* n_accepted,
-                         int32_t* seq_len, void* workspace, int64_t workspace_bytes, void* stream);
+                         int32_t* seq_len, float* p_x, float* q_x, float* res_sum, void* workspace,
+                         int64_t workspace_bytes, void* stream);
 
 /* The round-to-round bookkeeping of speculative.py:71-85 (emit the accepted tokens and the extra,
  * advance the cache length, stop at the token limit) for B rows at once, on the device, so that the
@@ -313,6 +322,24 @@ int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_t ldq, int3
 
 /* Workspace of fs_spec_accept / fs_verify_probs (256-byte aligned, any contents). */
 int64_t fs_spec_accept_workspace_size(int32_t B, int32_t K, int64_t V);
+
+/* ---------------------------------------------------------------------------------------------- */
+/* Keyed random numbers                                                                             */
+/* ---------------------------------------------------------------------------------------------- */
+#define FS_RNG_UNIFORM 0
+#define FS_RNG_EXP 1
+
+/* Per-request random streams for batched speculation in the Engine (engine.py:41, 126-133 draw
+ * from one shared generator in running-row order instead; this replaces those draws for the
+ * speculative engine, the per-request RNG keyed by (request, position) of the batched Engine).
+ * out[s*ld_slot + b*ld_row + j] for s < n_slots, b < B, j < n is the variate of (keys[b],
+ * slot0 + s, j): Philox4x32-10 with key keys[b] and counter (j/2, slot, 0, 0); kind FS_RNG_UNIFORM:
+ * u = (w >> 8) * 2^-24 in [0, 1) (torch.rand's float32 grid, speculative.py:27); FS_RNG_EXP: Exp(1)
+ * E = -log1p(-t), t uniform in (0, 1) with 2^-23 relative resolution down to 2^-33, never 0 (the
+ * noise of multinomial as argmax(w / E), sampling.py:21, speculative.py:32-33, 62). At most 65535
+ * rows x slots per call. */
+int fs_keyed_noise(const uint64_t* keys, int32_t B, int32_t slot0, int32_t n_slots, int64_t n, int32_t kind,
+                   float* out, int64_t ld_row, int64_t ld_slot, void* stream);
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,9 @@ reference algorithms the GPU kernels must reproduce:
                                                                      speculative_generate
   engine.py:36-139    continuous batching with preemption         -> Engine
 
+and, in oracle.keyed_noise, the counter-based (Philox4x32-10) per-request random stream that the
+speculative Engine draws instead of the reference's shared generator (engine.py:41, 126-133).
+
 Pinning (tests/test_oracle.py): every function is checked against golden vectors written by the
 reference itself (tests/golden/make_golden.py) and/or closed forms and library identities
 (torch.multinomial == argmax(p / Exp(1) noise), softmax in float64, brute-force attention).

@@ -41,15 +41,21 @@ def test_python_binding_covers_the_header(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fs_abi_version() == 1
+    assert lib.fs_abi_version() == 2
 
 
 def test_argument_errors_are_reported_not_launched(lib):
     rc = lib.fs_gemm(None, 0, None, 0, None, 0, None, 0, 4, 4, 4, 1, None, 0, None)
     assert rc == -1 and b"null" in lib.fs_last_error()
     rc = lib.fs_spec_accept(None, 0, 0, None, 0, 0, 1, 1, 10, 1, None, None, None, None, None, 0, None, None, None,
-                            None, 0, None)
+                            None, None, None, None, 0, None)
     assert rc == -1
+    rc = lib.fs_keyed_noise(None, 1, 0, 1, 10, 1, None, 10, 10, None)
+    assert rc == -1 and b"keyed_noise" in lib.fs_last_error()
+    # a debug output without its two companions is refused before anything is launched
+    rc = lib.fs_spec_accept(1, 0, 0, 1, 0, 0, 1, 1, 10, 1, 1, None, 1, 1, 1, 10, 1, 1, None, 1, None, None, 1, 1 << 20,
+                            None)
+    assert rc == -1 and b"together" in lib.fs_last_error()
     lay = _lib.KVLayout()
     rc = lib.fs_paged_attention(None, 0, 0, 0, ctypes.byref(lay), None, 0, 1, None, 1, 1, 1, 1.0, None, 0, 0, 0, None,
                                 0, None)

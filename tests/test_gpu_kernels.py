@@ -627,15 +627,16 @@ def test_gemm_row_stats(m, n, k):
     g = torch.Generator().manual_seed(m + n)
     a = (torch.randn(m, k, generator=g) * 0.5).bfloat16().to(DEV)
     w = (torch.randn(n, k, generator=g) * 0.5).bfloat16().to(DEV)
-    inv_t = torch.tensor([0.0 if r % 5 == 0 else 1.0 / (0.5 + (r % 3) * 0.25) for r in range(m)], dtype=torch.float32)
+    temps = torch.tensor([0.0 if r % 5 == 0 else 0.5 + (r % 3) * 0.25 for r in range(m)], dtype=torch.float32)
     nparts = ops.row_stats_parts(m, n, k)
     assert nparts > 0
     parts = torch.empty((m, nparts, 4), dtype=torch.int32, device=DEV)
-    out = ops.gemm_row_stats(a, w, inv_t.to(DEV), parts)
+    out = ops.gemm_row_stats(a, w, temps.to(DEV), parts)
     assert torch.equal(out, ops.gemm(a, w))            # the logits are the plain GEMM's
     rs = ops.row_stats_merge(parts, torch.empty((m, 4), dtype=torch.int32, device=DEV)).cpu()
     x = out.cpu().float()
-    y = x * inv_t[:, None]
+    # y = x / T as sampling.py:13 divides (T = 0 rows: y = x, only their argmax is used)
+    y = torch.where(temps[:, None] > 0, x / temps.clamp(min=1e-30)[:, None], x)
     mx = y.max(-1).values
     fl = rs[:, :3].contiguous().view(torch.float32)
     assert torch.equal(fl[:, 0], mx)
@@ -664,7 +665,7 @@ def test_spec_accept_with_row_stats_bit_exact(temperature):
     k_eff = torch.tensor([k if i % 5 else i % 4 for i in range(b)], dtype=torch.int32)
     temps = torch.full((b,), float(temperature))
     rows = torch.cat([tgt, dft], 1).float()                       # (b, 2k+1, v)
-    y = rows * (1.0 / temperature if temperature > 0 else 0.0)
+    y = rows / temperature if temperature > 0 else rows   # sampling.py:13's logits.float() / T
     mx = y.max(-1).values
     st = _records(mx, torch.exp((y - mx[..., None]).double()).sum(-1).float(), rows.max(-1).values,
                   rows.argmax(-1))
@@ -678,3 +679,42 @@ def test_spec_accept_with_row_stats_bit_exact(temperature):
         acc, extra = orc.verify_with_noise(p, q, xs[bi, :ke].tolist(), u[bi], e[bi])
         assert int(n[bi]) == len(acc), bi
         assert out[bi, : len(acc) + 1].tolist() == acc + [extra], bi
+
+
+# ---- keyed random numbers (the speculative Engine's per-request streams) --------------------------------
+def test_keyed_noise_matches_the_philox_stream():
+    """Uniforms bit-exact and Exp(1) variates within a few ulps of the numpy restatement of the Philox
+    stream, on strided rows and several slots; columns past n are not written; a row's values depend
+    only on its key (the same with other rows beside it or alone)."""
+    from oracle import keyed_noise as kn
+    case("keyed noise")
+    keys = torch.tensor([0, 1, 12345, (1 << 62) - 1, 987654321123], dtype=torch.int64)
+    n = 1001
+    for kind in (ops.RNG_UNIFORM, ops.RNG_EXP):
+        buf = torch.full((3, 5, 1004), -1.0, device=DEV)
+        ops.keyed_noise(keys.to(DEV), 7, buf[:, :, :n], kind)
+        got = buf.cpu()
+        assert (got[:, :, n:] == -1).all()
+        for s in range(3):
+            for b, key in enumerate(keys.tolist()):
+                if kind == ops.RNG_UNIFORM:
+                    assert np.array_equal(got[s, b, :n].numpy(), kn.uniform(key, 7 + s, n)), (s, b)
+                else:
+                    want = kn.exponential(key, 7 + s, n)
+                    assert (np.abs(got[s, b, :n].numpy() - want) / want).max() < 5e-7, (s, b)
+        alone = torch.empty(1, 1, n, device=DEV)
+        ops.keyed_noise(keys[2:3].to(DEV), 8, alone, kind)
+        assert torch.equal(alone[0, 0].cpu(), got[1, 2, :n])
+
+
+def test_keyed_noise_distribution_at_vocab_size():
+    """One 128256-column Exp(1) row per key for 64 keys (a round's final draws at the 8B shape): the
+    pooled values follow Exp(1) (Kolmogorov-Smirnov), none is 0 or infinite."""
+    from scipy import stats
+    case("keyed noise distribution")
+    keys = torch.arange(64, dtype=torch.int64).mul_(1_000_033).add_(17)
+    e = ops.keyed_noise(keys.to(DEV), 1 << 20, torch.empty(64, 128256, device=DEV), ops.RNG_EXP).cpu().numpy()
+    assert (e > 0).all() and np.isfinite(e).all()
+    assert stats.kstest(e.reshape(-1)[::7], "expon").statistic < 2e-3
+    u = ops.keyed_noise(keys.to(DEV), 5, torch.empty(64, 4096, device=DEV), ops.RNG_UNIFORM).cpu().numpy()
+    assert u.min() >= 0 and u.max() < 1 and stats.kstest(u.reshape(-1), "uniform").statistic < 3e-3

@@ -253,3 +253,34 @@ def test_a_planted_mistake_is_caught():
     finally:
         orc.rotate = original
     assert not np.allclose(bad, gold["logits"], atol=1e-3)
+
+
+def test_philox_known_answers():
+    """The Philox4x32-10 restatement against the known-answer vectors published with Random123
+    (counter and key all zeros, all ones, and the digits of pi)."""
+    from oracle.keyed_noise import philox4x32_10
+    kat = [((0, 0, 0, 0, 0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+           ((0xFFFFFFFF,) * 6, (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+           ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344, 0xA4093822, 0x299F31D0),
+            (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1))]
+    for args, want in kat:
+        assert tuple(int(w) for w in philox4x32_10(*args)) == want
+
+
+def test_keyed_noise_distributions():
+    """Uniforms on [0, 1) and Exp(1) variates of the keyed stream: Kolmogorov-Smirnov distances small,
+    the Exp(1) values never 0 and finite, different slots and keys independent-looking."""
+    import numpy as np
+    from scipy import stats
+    from oracle import keyed_noise as kn
+    u = kn.uniform(12345, 7, 200_000)
+    e = kn.exponential(12345, 8, 200_000)
+    assert u.min() >= 0 and u.max() < 1
+    assert (e > 0).all() and np.isfinite(e).all()
+    assert stats.kstest(u, "uniform").statistic < 0.005
+    assert stats.kstest(e, "expon").statistic < 0.005
+    # small values keep their resolution: the exponential's lower tail follows 1 - exp(-x)
+    assert abs((e < 1e-3).mean() - (1 - np.exp(-1e-3))) < 3e-4
+    other = kn.uniform(12346, 7, 200_000)
+    assert abs(np.corrcoef(u, other)[0, 1]) < 0.01
+    assert abs(np.corrcoef(u, kn.uniform(12345, 9, 200_000))[0, 1]) < 0.01
