@@ -152,11 +152,22 @@ struct ProbFn {
   float T, M, invS;
   FS_DEVICE ProbFn() : T(1.f), M(0.f), invS(1.f) {}
   FS_DEVICE ProbFn(float t, const Stat& st) : T(t), M(st.m), invS(1.f / st.s) {}
-  FS_DEVICE float operator()(float x) const {
-    const float y = T == 1.f ? x : x / T;
-    return expf(y - M) * invS;
-  }
+  // from y = x / T (vocab-wide passes divide a whole register block under one uniform branch)
+  FS_DEVICE float of_y(float y) const { return expf(y - M) * invS; }
+  FS_DEVICE float operator()(float x) const { return of_y(T == 1.f ? x : x / T); }
 };
+
+// y = x / T in place for a block of registers, under a branch uniform over the workgroup (T is the
+// row's or the sequence's), so T == 1 costs nothing; padding (-inf or 0) stays what it was.
+template <int U>
+FS_DEVICE void divide_by_t(float (&x)[U][8], float T) {
+  if (T != 1.f) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[u][j] = x[u][j] / T;
+  }
+}
 
 // One chunk of one row. T == 0: the first argmax of x. T > 0: (m, s) = (max of y, sum of exp(y - m))
 // with y = x / T, a true division (sampling.py:13), so m is the max torch's softmax subtracts. The
@@ -258,15 +269,20 @@ __global__ void __launch_bounds__(THREADS) sample_argmax_kernel(RowSet rs, int64
                       ((reinterpret_cast<uintptr_t>(er) & 15) == 0);
   float bv = -INFINITY;
   int bi = 0x7fffffff;
+  float x[UNROLL][8], e[UNROLL][8];
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
     const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
-    float x[8], e[8];
-    load8<DT>(row, v0, V, vec_ok, -INFINITY, x);
-    load8_f32(er, v0, V, vec_ok, e);
+    load8<DT>(row, v0, V, vec_ok, -INFINITY, x[u]);
+    load8_f32(er, v0, V, vec_ok, e[u]);
+  }
+  divide_by_t(x, T);
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      if (v0 + j < V) argmax_merge(bv, bi, fs(x[j]) / e[j], (int)(v0 + j));
+      if (v0 + j < V) argmax_merge(bv, bi, fs.of_y(x[u][j]) / e[u][j], (int)(v0 + j));
     }
   }
   block_argmax(bv, bi, shf, shi);
@@ -483,9 +499,10 @@ __global__ void __launch_bounds__(64 * STEP_WAVES) accept_step_kernel(AcceptArgs
 // p_v and q_v nearly cancel) plus, for bf16/f16 probabilities, the rounding of r / S to that dtype. A
 // column whose cheap key is below max · (1 - margin) cannot win, with the margin 8 or more times that
 // error (2^-18 for float32 arithmetic, 2^-6 for bf16 probabilities, 2^-8 for f16). Each chunk keeps the columns
-// within the margin of its own max (its candidates, nearly always one per set), and the final pass
-// scores them exactly. Chunks whose list overflowed, and sequences whose max is too small for a
-// relative bound, are rescanned exactly.
+// within the margin of its own max (its candidates, nearly always one), and the final pass scores
+// them exactly. Chunks whose list overflowed, sequences whose max is too small for a relative bound,
+// and a rejection whose residual sums to 0 (its draw falls back to p / E, which the pass does not
+// rank) are rescanned exactly.
 constexpr int NCAND = 8;
 constexpr float CAND_MIN = 7.888609052210118e-31f;  // 2^-100: below it the bound is not relied on
 constexpr float MARGIN_F32 = 1.0f / 262144.0f;     // 2^-18
@@ -524,13 +541,14 @@ FS_DEVICE void collect(float key, int col, float th, int* n, int* list) {
 }
 
 // launch 3: one pass over the rejected position's two rows and E, per chunk of CHR columns: the
-// residual partial sum, and the max and candidates of both draws (p / E and r / E)
+// residual partial sum and the max and candidates of the draw's keys (r / E at a rejection, p / E for
+// the bonus token)
 template <int DT, bool PROBS>
 __global__ void __launch_bounds__(THREADS) accept_pair_kernel(AcceptArgs A) {
   constexpr int PD = ProbType<DT, PROBS>::value;
   __shared__ float shf[THREADS / 64];
-  __shared__ int sh_n[2];
-  __shared__ int sh_c[2][NCAND];
+  __shared__ int sh_n[1];
+  __shared__ int sh_c[1][NCAND];
   const int c = blockIdx.x, b = blockIdx.y;
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
@@ -546,7 +564,6 @@ __global__ void __launch_bounds__(THREADS) accept_pair_kernel(AcceptArgs A) {
   }
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j);
-  const PairRow<DT, PROBS> pair{pr, qr, sp, sq};
   const float* er = A.E + (int64_t)b * A.ldE;
   const bool vec_ok = (A.V % VEC) == 0 &&
                       (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr) |
@@ -559,8 +576,15 @@ __global__ void __launch_bounds__(THREADS) accept_pair_kernel(AcceptArgs A) {
     if (!bonus) load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq[u]);
     load8_f32(er, v0, A.V, vec_ok, e[u]);
   }
-  float ls = 0.f, mp = 0.f, mr = 0.f;
-  float ap[UNROLL_R][8], ar[UNROLL_R][8];   // cheap keys (0 past the row)
+  if (!PROBS) {   // y = x / T once per element (the ProbFn arithmetic, divided ahead)
+    divide_by_t(xp, T);
+    if (!bonus) divide_by_t(xq, T);
+  }
+  // One set of cheap keys: p / E for the bonus token, r / E at a rejection. The p / E set of a
+  // rejection is needed only when the residual sums to 0; its chunks are then marked for an exact
+  // rescan instead of being collected here.
+  float ls = 0.f, mk = 0.f;
+  float ak[UNROLL_R][8];   // cheap keys (0 past the row)
 #pragma unroll
   for (int u = 0; u < UNROLL_R; ++u) {
     const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
@@ -568,46 +592,40 @@ __global__ void __launch_bounds__(THREADS) accept_pair_kernel(AcceptArgs A) {
     for (int jj = 0; jj < 8; ++jj) {
       const bool in = v0 + jj < A.V;
       const float re = __builtin_amdgcn_rcpf(e[u][jj]);
-      ap[u][jj] = in ? pair.p_at(xp[u][jj]) * re : 0.f;
-      mp = fmaxf(mp, ap[u][jj]);
-      ar[u][jj] = 0.f;
-      if (!bonus) {
-        const float r = in ? pair.resid(xp[u][jj], xq[u][jj]) : 0.f;
+      const float p = PROBS ? xp[u][jj] : sp.of_y(xp[u][jj]);
+      if (bonus) {
+        ak[u][jj] = in ? p * re : 0.f;
+      } else {   // (p - q).clamp(min=0), rounded to the probability dtype
+        const float q = PROBS ? xq[u][jj] : sq.of_y(xq[u][jj]);
+        const float r = in ? fmaxf(Elem<PD>::round(p - q), 0.f) : 0.f;
         ls += r;
-        ar[u][jj] = r * re;
-        mr = fmaxf(mr, ar[u][jj]);
+        ak[u][jj] = r * re;
       }
+      mk = fmaxf(mk, ak[u][jj]);
     }
   }
   const float tot = bonus ? 0.f : block_sum(ls, shf);
-  const float cmp = block_max(mp, shf);
-  const float cmr = bonus ? 0.f : block_max(mr, shf);
-  if (threadIdx.x < 2) sh_n[threadIdx.x] = 0;
+  const float cm = block_max(mk, shf);
+  if (threadIdx.x == 0) sh_n[0] = 0;
   __syncthreads();
-  const float thp = cmp > 0.f ? cand_threshold(cmp, MARGIN_F32) : INFINITY;
-  const float thr = cmr > 0.f ? cand_threshold(cmr, CandMargin<PD>::value) : INFINITY;
+  const float th = cm > 0.f ? cand_threshold(cm, bonus ? MARGIN_F32 : CandMargin<PD>::value) : INFINITY;
 #pragma unroll
   for (int u = 0; u < UNROLL_R; ++u) {
     const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      collect(ap[u][jj], (int)(v0 + jj), thp, &sh_n[0], sh_c[0]);
-      collect(ar[u][jj], (int)(v0 + jj), thr, &sh_n[1], sh_c[1]);
-    }
+    for (int jj = 0; jj < 8; ++jj) collect(ak[u][jj], (int)(v0 + jj), th, &sh_n[0], sh_c[0]);
   }
   __syncthreads();
   const int64_t o = (int64_t)b * A.nchr + c;
+  const int set = bonus ? 0 : 1;
   if (threadIdx.x == 0) {
     A.resid[o] = tot;
-    A.cmax[2 * o] = cmp;
-    A.cmax[2 * o + 1] = cmr;
-    A.ncand[2 * o] = cmp > 0.f ? sh_n[0] : 0;
-    A.ncand[2 * o + 1] = cmr > 0.f ? sh_n[1] : 0;
+    A.cmax[2 * o + set] = cm;
+    A.ncand[2 * o + set] = cm > 0.f ? sh_n[0] : 0;
+    A.cmax[2 * o + 1 - set] = bonus ? 0.f : INFINITY;      // rejection: p / E not collected, rescan
+    A.ncand[2 * o + 1 - set] = bonus ? 0 : NCAND + 1;
   }
-  if (threadIdx.x < 2 * NCAND) {
-    const int set = threadIdx.x / NCAND, k = threadIdx.x % NCAND;
-    if (k < sh_n[set]) A.cand[(2 * o + set) * NCAND + k] = sh_c[set][k];
-  }
+  if (threadIdx.x < NCAND && threadIdx.x < sh_n[0]) A.cand[(2 * o + set) * NCAND + threadIdx.x] = sh_c[0][threadIdx.x];
 }
 
 // launch 4: one wave per sampled sequence draws the extra token and writes the outputs and rollback:
