@@ -79,6 +79,8 @@ SIGNATURES = {
                                c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p]),
     "fs_spec_accept_stats": (c_i32, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i32, c_i32, c_i64, c_i32, c_p, c_p, c_p,
                                      c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p]),
+    "fs_spec_accept_noalloc": (c_i32, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i32, c_i32, c_i64, c_i32, c_p, c_p,
+                                       c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p]),
     "fs_verify_probs": (c_i32, [c_p, c_i64, c_p, c_i64, c_i32, c_i64, c_i32, c_p, c_p, c_p, c_p, c_p, c_p, c_i64,
                                 c_p]),
     "fs_spec_accept_workspace_size": (c_i64, [c_i32, c_i32, c_i64]),

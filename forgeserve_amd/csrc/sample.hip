@@ -15,6 +15,8 @@
 // bit for bit with the CPU reference on the same noise.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -978,6 +980,66 @@ extern "C" int fs_spec_accept_stats(const void* tgt, int64_t tgt_sb, int64_t tgt
   return spec_accept_impl(tgt, tgt_sb, tgt_si, dft, dft_sb, dft_si, B, K, V, dtype, draft_tokens, k_eff, temperature, u,
                           E, ldE, out_tokens, n_accepted, seq_len, p_x, q_x, res_sum, row_stats, workspace,
                           workspace_bytes, stream);
+}
+
+// ------------------------------------------------------------------------------------------------
+// the acceptance without a caller workspace (for callers that cannot allocate)
+// ------------------------------------------------------------------------------------------------
+// Scratch of fs_spec_accept_noalloc: a fixed device array that each GPU holds for the life of the
+// process. Its size bounds the shapes that entry point takes (batch 512 at k = 8 and a 128256-token
+// vocabulary needs 3.6 MiB). Calls on one GPU share it: calls that overlap on one device race.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = (int64_t)4 << 20;
+static __device__ __align__(256) char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[MAX_DEVICES] = {};   // the array's device address on each GPU, looked up once per device
+
+// The scratch address on the current device: hipGetSymbolAddress the first time a device calls, with
+// that device current; the cached pointer afterwards. In host code `scratch` only names a host-side
+// stand-in for the array, so kernels always receive this pointer.
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fs::set_error("spec_accept_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  if (dev < 0 || dev >= MAX_DEVICES) return fs::arg_error("spec_accept_noalloc: device %d (at most %d)", dev, MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      fs::set_error("spec_accept_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+    }
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int fs_spec_accept_noalloc(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
+                                      int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype,
+                                      const int32_t* draft_tokens, const int32_t* k_eff, const float* temperature,
+                                      const float* u, const float* E, int64_t ldE, const void* row_stats,
+                                      int32_t* out_tokens, int32_t* n_accepted, int32_t* seq_len, void* stream) {
+  FS_CHECK_ARG(B > 0 && B <= 65535 && K >= 0 && K <= 65535 && V > 0 && V < 0x7fffffff,
+               "spec_accept_noalloc: B %d K %d V %lld", B, K, (long long)V);
+  const int64_t need = accept_ws(B, K, V);
+  FS_CHECK_ARG(need <= NOALLOC_SCRATCH_BYTES,
+               "spec_accept_noalloc: B %d K %d V %lld needs %lld bytes of scratch, more than the %lld this entry "
+               "point holds per device; use fs_spec_accept with a workspace",
+               B, K, (long long)V, (long long)need, (long long)NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (int rc = scratch_on_current_device(&ws)) return rc;
+  // the acceptance rewrites every byte of its scratch that it reads later, so nothing is cleared
+  return spec_accept_impl(tgt, tgt_sb, tgt_si, dft, dft_sb, dft_si, B, K, V, dtype, draft_tokens, k_eff, temperature, u,
+                          E, ldE, out_tokens, n_accepted, seq_len, nullptr, nullptr, nullptr, row_stats, ws,
+                          NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int fs_row_stats_merge(const void* parts, int64_t parts_ld, int64_t nparts, int64_t M, void* out,

@@ -298,6 +298,21 @@ int fs_spec_accept_stats(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const 
                          int32_t* seq_len, float* p_x, float* q_x, float* res_sum, void* workspace,
                          int64_t workspace_bytes, void* stream);
 
+/* fs_spec_accept (row_stats NULL) or fs_spec_accept_stats (row_stats given) without a workspace
+ * argument and without any allocation: the scratch is a fixed 4 MiB device array of the library, one
+ * per GPU, held until the process ends (its address is looked up once per device, on that device's
+ * first call). No counterpart in the reference; it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops and harnesses that forbid allocation). Shapes whose
+ * scratch exceeds 4 MiB (fs_spec_accept_workspace_size(B, K, V) > 4 MiB; batch 512 with k = 8 and a
+ * 128256-token vocabulary fits) are refused with FS_ERR_ARG before anything is launched. Every call on
+ * one GPU shares that GPU's scratch, so calls that overlap on one device (different streams, or host
+ * threads) race; calls ordered on one stream do not. No debug outputs. */
+int fs_spec_accept_noalloc(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
+                           int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype, const int32_t* draft_tokens,
+                           const int32_t* k_eff, const float* temperature, const float* u, const float* E,
+                           int64_t ldE, const void* row_stats, int32_t* out_tokens, int32_t* n_accepted,
+                           int32_t* seq_len, void* stream);
+
 /* The round-to-round bookkeeping of speculative.py:71-85 (emit the accepted tokens and the extra,
  * advance the cache length, stop at the token limit) for B rows at once, on the device, so that the
  * next round can be queued before the host has read this round's tokens. res: the acceptance's
