@@ -32,6 +32,9 @@ Kernel-only modes (one JSON line each, used for the rocprofv3 counter runs):
                                          the calls share one work plan (built by the first warm-up call)
     python bench.py --kernel accept      the fused acceptance alone: B=64, k=6, V=128256, bf16 logits
     python bench.py --kernel copy        1 GiB device-to-device copies, f32 and bf16 (counter calibration)
+    python bench.py --kernel prefill_attention
+                                         packed causal prefill attention: 8 prompts of 4096 tokens back to
+                                         back, 32/8 heads, head_dim 128, bf16, block 16, TFLOP/s vs 2.5 PFLOP/s
 """
 
 import argparse
@@ -488,6 +491,34 @@ def kernel_mode(args):
         byts = accept_bytes(BATCH, K, CFG["vocab_size"])
         out = {"kernel": "spec_accept" + (" (row statistics given)" if stats else ""), "calls": steps,
                "avg_us": round(sec * 1e6, 2), "algorithmic_bytes": byts, "achieved_GBs": round(byts / sec / 1e9, 1)}
+    elif args.kernel == "prefill_attention":
+        n_seq, L, h, hkv, d = 8, 4096, CFG["n_heads"], CFG["n_kv_heads"], 128
+        g = torch.Generator(device="cuda").manual_seed(args.seed)
+        cfg = fa.ModelConfig(vocab_size=8, d_model=h * d, n_layers=1, n_heads=h, n_kv_heads=hkv, max_seq_len=16)
+        nb = -(-L // BLOCK)
+        pool = fa.PagedKVPool(cfg, n_seq * nb + 8, BLOCK, dtype=torch.bfloat16, device="cuda")
+        pool.k_store.normal_(generator=g)
+        pool.v_store.normal_(generator=g)
+        perm = torch.randperm(n_seq * nb, generator=torch.Generator().manual_seed(args.seed))
+        tab = perm.view(n_seq, nb).int().cuda()
+        pos = torch.arange(L, dtype=torch.int32).repeat(n_seq, 1).cuda()
+        cu = torch.arange(0, (n_seq + 1) * L, L, dtype=torch.int32).cuda()
+        q = torch.randn(n_seq * L, h, d, device="cuda", generator=g).bfloat16()
+        lay = pool.layout(0)
+        for _ in range(max(warmup, 1)):
+            ops.paged_attention_varlen(q, lay, tab, pos, cu, d ** -0.5)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            ops.paged_attention_varlen(q, lay, tab, pos, cu, d ** -0.5)
+        b.record()
+        torch.cuda.synchronize()
+        sec = a.elapsed_time(b) / steps * 1e-3
+        flops = 4.0 * d * h * n_seq * L * (L + 1) / 2   # QK^T and PV over the causal triangle
+        out = {"kernel": "paged_attention_varlen prefill", "calls": steps, "prompts": n_seq, "tokens_each": L,
+               "avg_us": round(sec * 1e6, 1), "tflops": round(flops / sec / 1e12, 1),
+               "frac_of_bf16_peak": round(flops / sec / 1e12 / MFMA_PEAK_TFLOPS, 4)}
     else:
         # 1 GiB device copies: f32 (16 bytes per lane per load) and bf16 (8 bytes per lane per load)
         out = {"kernel": "copy 1 GiB", "calls": steps}
@@ -521,7 +552,8 @@ def main():
     ap.add_argument("--synthetic-kv", action="store_true",
                     help="fill the pools with N(0,1) keys/values instead of prefilling the prompts")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--kernel", choices=("round", "attention", "accept", "accept_stats", "copy", "engine_1b"),
+    ap.add_argument("--kernel", choices=("round", "attention", "accept", "accept_stats", "copy", "engine_1b",
+                                         "prefill_attention"),
                     default="round")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -280,6 +280,28 @@ def test_attention_verify_equals_decode_bitwise():
     assert torch.equal(one_row[0], full[3])
 
 
+@pytest.mark.parametrize("d", [128, 64])
+def test_attention_prefill_equals_decode_bitwise(d):
+    """A prefill-shaped call (many query tiles per row, the kernel's prefill variant) gives every token
+    the bits a one-token decode at its position gives it: prompts of 300 and 37 tokens after cached
+    prefixes of 0 and 500, against 337 one-token calls."""
+    case("attention prefill == decode", d)
+    lens, starts = [300, 37], [0, 500]
+    t = max(lens)
+    ctx = [st + n for st, n in zip(starts, lens)]
+    q, k, v, tables, _ = _paged_case(2, t, 32, 8, d, 16, ctx, 80, torch.bfloat16, 5 + d)
+    pos = torch.full((2, t), -1, dtype=torch.long)
+    for i, (st, n) in enumerate(zip(starts, lens)):
+        pos[i, :n] = torch.arange(st, st + n)
+    full, pool = _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
+    lay, tab = pool.layout(0), tables.int().to(DEV)
+    for i, n in enumerate(lens):
+        for j in range(n):
+            one = ops.paged_attention(q[i: i + 1, j: j + 1].to(DEV), lay, tab[i: i + 1], pos[i: i + 1, j: j + 1].int().to(DEV),
+                                      1.0 / math.sqrt(d))
+            assert torch.equal(one[0, 0], full[i, j]), (i, j)
+
+
 def test_attention_padding_rows_are_zero():
     case("attention padding")
     q, k, v, tables, pos = _paged_case(3, 3, 8, 2, 128, 16, [50, 70, 30], 20, torch.bfloat16, 4)
