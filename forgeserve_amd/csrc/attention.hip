@@ -239,10 +239,7 @@ __global__ void __launch_bounds__(PLAN_THREADS) attn_plan_kernel(AttnParams P) {
 // positions, and a tile wholly above a query's position leaves that query's partial exactly as it
 // was; a query's result therefore does not depend on the other queries of its tile.
 
-// PF (prefill: several query tiles per row): two register tile buffers instead of three, and the
-// accumulator rescale skipped when no row's running max moved in a tile (alpha == 1 for every row, so
-// the multiply is an identity): the same arithmetic, so the same bits, as the decode/verify variant.
-template <int D, int BSZ, bool PF>
+template <int D, int BSZ>
 __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const AttnParams& P, int b, int kbeg, int kend,
                                                                       int qmax, int row0, int nrows,
                                                                       const int (&rpos)[2], int hkv, int w,
@@ -271,10 +268,10 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
   const int64_t k_head_off = (int64_t)hkv * P.kv.k_head;
   const int64_t v_head_off = (int64_t)hkv * P.kv.v_head;
 
-  // Three tile buffers in registers (two for PF): while tile i is consumed, tiles i+1 and i+2 (i+1)
-  // are in flight. Every load is unconditional (a prefetch past the end re-reads the last tile, an
-  // unmapped block reads block 0 and is masked in consume) so that each wait before a consume counts
-  // exactly the loads issued after that tile, on every path through the loop.
+  // Three tile buffers in registers: while tile i is consumed, tiles i+1 and i+2 are in flight.
+  // Every load is unconditional (a prefetch past the end re-reads the last tile, an unmapped block
+  // reads block 0 and is masked in consume) so that each wait before a consume counts exactly the
+  // loads issued after that tile, on every path through the loop.
   bf16x8_t kb0[KS], kb1[KS], kb2[KS];
   short4_t vb0[MT], vb1[MT], vb2[MT];
 
@@ -385,19 +382,16 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
       l_run[nt] = l_run[nt] * alpha[nt] + psum;
       m_run[nt] = m_new;
     }
-    // decode/verify: unconditional rescale (a branch here splits the accumulators' live ranges and
-    // spills with three tile buffers); prefill: skipped when every row's alpha is exactly 1
-    if (!PF || __any(alpha[0] != 1.f || alpha[1] != 1.f)) {
+    // unconditional rescale: a branch here splits the accumulators' live ranges and spills
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          acc[mt][nt][0] *= alpha[nt];
-          acc[mt][nt][1] *= alpha[nt];
-          acc[mt][nt][2] *= alpha[nt];
-          acc[mt][nt][3] *= alpha[nt];
-        }
-    }
+      for (int nt = 0; nt < 2; ++nt) {
+        acc[mt][nt][0] *= alpha[nt];
+        acc[mt][nt][1] *= alpha[nt];
+        acc[mt][nt][2] *= alpha[nt];
+        acc[mt][nt][3] *= alpha[nt];
+      }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[mt], pf[0], acc[mt][0], 0, 0, 0);
@@ -405,25 +399,15 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
     }
   };
 
-  if (PF) {   // tile i+1 in flight while tile i is consumed (load(1) was issued above)
-    for (int i = 0; i < nt_w; i += 2) {
-      consume(i, kb0, vb0);
-      if (i + 1 >= nt_w) break;
-      load_tile(i + 2, kb0, vb0);
-      consume(i + 1, kb1, vb1);
-      load_tile(i + 3, kb1, vb1);
-    }
-  } else {
-    for (int i = 0; i < nt_w; i += 3) {
-      load_tile(i + 2, kb2, vb2);
-      consume(i, kb0, vb0);
-      if (i + 1 >= nt_w) break;
-      load_tile(i + 3, kb0, vb0);
-      consume(i + 1, kb1, vb1);
-      if (i + 2 >= nt_w) break;
-      load_tile(i + 4, kb1, vb1);
-      consume(i + 2, kb2, vb2);
-    }
+  for (int i = 0; i < nt_w; i += 3) {
+    load_tile(i + 2, kb2, vb2);
+    consume(i, kb0, vb0);
+    if (i + 1 >= nt_w) break;
+    load_tile(i + 3, kb0, vb0);
+    consume(i + 1, kb1, vb1);
+    if (i + 2 >= nt_w) break;
+    load_tile(i + 4, kb1, vb1);
+    consume(i + 2, kb2, vb2);
   }
   // this wave's partial to LDS: acc by (query half, dim tile, lane), m and l by query row
 #pragma unroll
@@ -438,7 +422,7 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
   }
 }
 
-template <int D, int BSZ, bool PF>
+template <int D, int BSZ>
 __global__ void __launch_bounds__(64 * UNIT_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 attn_unit_kernel(AttnParams P) {
   constexpr int MT = D / 16;
@@ -465,7 +449,7 @@ attn_unit_kernel(AttnParams P) {
   const int kbeg = s * P.split;
   const int kend = min(kbeg + P.split, qmax + 1);
 
-  attn_wave_tiles<D, BSZ, PF>(P, b, kbeg, kend, qmax, row0, nrows, rpos, hkv, w, red_acc[w], red_m[w], red_l[w]);
+  attn_wave_tiles<D, BSZ>(P, b, kbeg, kend, qmax, row0, nrows, rpos, hkv, w, red_acc[w], red_m[w], red_l[w]);
   __syncthreads();
 
   // merge the waves' partials in wave order; wave w takes the (query half, 16-dim tile) pairs w,
@@ -811,18 +795,13 @@ int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, con
     if (!(reuse_plan && last_plan == key)) attn_plan_kernel<<<1, PLAN_THREADS, 0, st>>>(P);
     last_plan = key;
     const unsigned grid = (unsigned)units, threads = 64 * UNIT_WAVES;
-    // several query tiles per row (a prefill): the prefill variant; its outputs are the same bits
-    const bool pf = qtiles > 1;
-#define FS_UNIT(D_, BS_) \
-    (pf ? attn_unit_kernel<D_, BS_, true><<<grid, threads, 0, st>>>(P) : attn_unit_kernel<D_, BS_, false><<<grid, threads, 0, st>>>(P))
     if (kv->head_dim == 128) {
-      if (bs16) FS_UNIT(128, 16);
-      else FS_UNIT(128, 0);
+      if (bs16) attn_unit_kernel<128, 16><<<grid, threads, 0, st>>>(P);
+      else attn_unit_kernel<128, 0><<<grid, threads, 0, st>>>(P);
     } else {
-      if (bs16) FS_UNIT(64, 16);
-      else FS_UNIT(64, 0);
+      if (bs16) attn_unit_kernel<64, 16><<<grid, threads, 0, st>>>(P);
+      else attn_unit_kernel<64, 0><<<grid, threads, 0, st>>>(P);
     }
-#undef FS_UNIT
   } else {
     last_plan = PlanKey{};   // no plan on this path
     dim3 grid((unsigned)rows, (unsigned)P.nsplit);
