@@ -161,6 +161,29 @@ __global__ void __launch_bounds__(PLAN_THREADS) attn_plan_kernel(AttnParams P) {
   const int tid = threadIdx.x;
   const int qtiles = (P.T * P.G + QTILE - 1) / QTILE;
   const int U = P.B * qtiles;
+  if (qtiles > 1) {
+    // A prefill (several query tiles per row): the tiles of one row are listed together, longest
+    // first, so the workgroups running at any time on an XCD (one KV head each) read one row's keys
+    // and values and share them in that XCD's L2; across rows the reads would not fit it. The order
+    // decides only which workgroup runs an item, never what the item computes.
+    int base = 0;
+    for (int u0 = 0; u0 < U; u0 += PLAN_THREADS) {
+      const int u = u0 + tid;
+      int qm = -1, nch = 0, b = 0, z = 0;
+      if (u < U) {
+        b = u / qtiles;
+        z = qtiles - 1 - (u - b * qtiles);
+        qm = tile_qmax(P, b, z);
+        nch = tile_chunks(P, qm);
+      }
+      int n_round;
+      const int e0 = base + block_scan(nch, sh, n_round) - nch;
+      for (int c = 0; c < nch; ++c) P.items[e0 + c] = AttnItem{b, z, c, qm};
+      base += n_round;
+    }
+    if (tid == 0) P.n_items[0] = base;
+    return;
+  }
   const int nlen = P.split / 16;   // a last chunk holds 1..nlen tiles (an empty one counts as 1)
   for (int i = tid; i <= nlen; i += PLAN_THREADS) cursor[i] = 0;
   // the thread's first tile (u = tid) stays in registers; tiles past the first PLAN_THREADS are
