@@ -32,6 +32,8 @@ Kernel-only modes (one JSON line each, used for the rocprofv3 counter runs):
                                          the calls share one work plan (built by the first warm-up call)
     python bench.py --kernel accept      the fused acceptance alone: B=64, k=6, V=128256, bf16 logits
     python bench.py --kernel copy        1 GiB device-to-device copies, f32 and bf16 (counter calibration)
+    python bench.py --kernel gemm        the 8B model's four layer GEMMs and the LM head at M = 448 (a verify
+                                         pass) and M = 64 (a draft step), each call on the next layer's weights
     python bench.py --kernel prefill_attention
                                          packed causal prefill attention: 8 prompts of 4096 tokens back to
                                          back, 32/8 heads, head_dim 128, bf16, block 16, TFLOP/s vs 2.5 PFLOP/s
@@ -491,6 +493,11 @@ def kernel_mode(args):
         byts = accept_bytes(BATCH, K, CFG["vocab_size"])
         out = {"kernel": "spec_accept" + (" (row statistics given)" if stats else ""), "calls": steps,
                "avg_us": round(sec * 1e6, 2), "algorithmic_bytes": byts, "achieved_GBs": round(byts / sec / 1e9, 1)}
+    elif args.kernel == "gemm":
+        target, draft = build_models(torch, fa)
+        out = {"kernel": "gemm", "m448": gemm_summary(time_gemms(torch, ops, target, BATCH * (K + 1)), CFG["n_layers"],
+                                                      MFMA_PEAK_TFLOPS),
+               "m64": gemm_summary(time_gemms(torch, ops, draft, BATCH), draft.cfg.n_layers, MFMA_PEAK_TFLOPS)}
     elif args.kernel == "prefill_attention":
         n_seq, L, h, hkv, d = 8, 4096, CFG["n_heads"], CFG["n_kv_heads"], 128
         g = torch.Generator(device="cuda").manual_seed(args.seed)
@@ -553,7 +560,7 @@ def main():
                     help="fill the pools with N(0,1) keys/values instead of prefilling the prompts")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kernel", choices=("round", "attention", "accept", "accept_stats", "copy", "engine_1b",
-                                         "prefill_attention"),
+                                         "prefill_attention", "gemm"),
                     default="round")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -151,6 +151,12 @@ FS_DEVICE void dma16(const void* g, uint32_t lds) {
   const uint32_t l = __builtin_amdgcn_readfirstlane(lds);  // the LDS base is the same for the whole wave
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(l) : "memory", "m0");
 }
+// the same copy marked non-temporal: the weights stream through once, and keeping them out of the way
+// in L2 leaves the activation panel (re-read by every column tile) resident (about 3% at M = 448)
+FS_DEVICE void dma16_nt(const void* g, uint32_t lds) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "s"(l) : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 template <int N>
@@ -233,7 +239,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
 #pragma unroll
     for (int i = 0; i < GI; ++i) {
       const int q = i * NW + wave;
-      if (q < T) dma16(src[i] + k0, base + (uint32_t)(q * 1024));
+      if (q < T) {
+        if (q >= XQ) dma16_nt(src[i] + k0, base + (uint32_t)(q * 1024));   // a weight copy
+        else dma16(src[i] + k0, base + (uint32_t)(q * 1024));
+      }
     }
   };
   // wait until at most `later` stages' copies (issued after the one being waited for) are in flight
