@@ -529,9 +529,9 @@ LdsCfg lds_cfg(int64_t M, int64_t N, int splits, bool stats = false) {
   auto pad = [&](int64_t bm) { return (M + bm - 1) / bm * bm - M; };
   if (pad(224) < pad(128) && pad(224) < pad(256)) {
     const int64_t tm = (M + 223) / 224;
-    if (stats) {   // the statistics epilogue keeps 8 waves of 64-column blocks
+    if (stats) {   // 16 waves of 32-column blocks: the blocks a 64-row head's statistics use too
       const int64_t t256 = tm * ((N + 255) / 256);
-      return t256 >= 192 ? LdsCfg{224, 256, 2, 4} : LdsCfg{224, 128, 2, 4};
+      return t256 >= 192 ? LdsCfg{224, 256, 2, 8} : LdsCfg{224, 128, 2, 4};
     }
     // the width whose tile count fills the CUs best, weighted by the throughput a tile of that
     // width reaches (measured on the decoder's projections at M = 448: wider tiles re-read less)
@@ -566,7 +566,9 @@ void launch_lds(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, 
 #define FS_LDS_LAUNCH(BM_, BN_, NS_, WGM_, WGN_, PRIO_)                                                       \
   gemm_bf16_lds_kernel<BM_, BN_, NS_, WGM_, WGN_, STATS, PRIO_, SWIGLU><<<grid, 64 * WGM_ * WGN_, 0, s>>>(      \
       a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part, rs)
-  if (cf.bm == 64 && cf.bn == 128) FS_LDS_LAUNCH(64, 128, 4, 2, 4, false);
+  // 64 x 128 with a 3-stage ring (72 KB of LDS): two workgroups share a CU, so one's epilogue (the
+  // head's statistics) overlaps the other's weight stream
+  if (cf.bm == 64 && cf.bn == 128) FS_LDS_LAUNCH(64, 128, 3, 2, 4, false);
   else if (cf.bm == 64) FS_LDS_LAUNCH(64, 64, 4, 2, 2, false);
   else if (cf.bm == 224 && cf.bn == 256 && cf.wgn == 8) FS_LDS_LAUNCH(224, 256, 2, 2, 8, true);
   else if (cf.bm == 224 && cf.bn == 256) FS_LDS_LAUNCH(224, 256, 2, 2, 4, false);
