@@ -366,23 +366,25 @@ def attention_inputs(torch, fa, seed=0):
 
 
 def phase_times(torch, sb, reps=8):
-    """The round's phases as captured for its shape, replayed alone between HIP events on the launching
+    """The round's phases, each captured in a graph of its own, replayed alone between HIP events on the launching
     stream: the target's verify phase (k+1-token forward through the reused draft residual streams,
     LM head with its statistics epilogue, statistics merges, fused acceptance) and the draft steps. The
     replays rewrite what the last round wrote (same keys, values, logits and outputs)."""
     st = next(reversed(sb.pool_t.__dict__.get("_rounds", {}).values()), None)
-    if st is None or st.graphs is None:
+    if st is None or not st.graphs:
         return None
+    from forgeserve_amd.speculative import capture_phase_graphs
+    graphs = capture_phase_graphs(sb.target, sb.draft, sb.pool_t, sb.pool_d, st)
     out = {}
     for name, idx in (("verify_ms", [st.k]), ("draft_step_ms", list(range(st.k)))):
         for i in idx:
-            st.graphs[i].replay()
+            graphs[i].replay()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(reps):
             for i in idx:
-                st.graphs[i].replay()
+                graphs[i].replay()
         b.record()
         torch.cuda.synchronize()
         out[name] = round(a.elapsed_time(b) / reps / len(idx), 3)

@@ -234,8 +234,9 @@ class _RoundState:
             self.parts_t = torch.empty((b * (k + 1), parts_t, 4), dtype=I32, device=dev)
             self.row_stats = torch.empty((b, 2 * k + 1, 4), dtype=I32, device=dev)
         self.res_hosts = [torch.empty((b, k + 2), dtype=torch.int32, pin_memory=True) for _ in range(2)]
-        self.res = None
-        self.graphs = None
+        self.res = torch.empty((b, k + 2), dtype=I32, device=dev)   # the verify phase's output
+        self.graphs = {}           # the round's k+1 phases (and, keyed True, fs_spec_advance) in one graph
+        self.phase_graphs = None   # one graph per phase, captured on request (phase timing)
         self.uses = 0
 
     def stage(self, tokens, k_eff, temps, blocks_t, blocks_d, slot=0, budget=None, eos=None) -> None:
@@ -343,7 +344,7 @@ def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _R
         ops.row_stats_merge(st.parts_t, st.row_stats, k + 1, 2 * k + 1, 0)
     out_tok, n_acc = ops.spec_accept(tgt_logits, st.dft_logits, st.draft_tok, d["keff"], temps, st.u[:, :k], st.e,
                                      row_stats=st.row_stats if st.fused else None)
-    return torch.cat([n_acc[:, None], out_tok], 1)
+    return torch.cat([n_acc[:, None], out_tok], 1, out=st.res)
 
 
 def _graph_key(model) -> tuple:
@@ -392,9 +393,10 @@ def _round_state(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, b: int
 def _launch_round(target, draft, pool_t, pool_d, st: "_RoundState", b: int, draws, graphs: bool,
                   advance: bool = False) -> None:
     """Queue one round on the current stream: the random numbers (drawn in the reference loop's order),
-    then the k+1 phases (eagerly on the shape's first round, captured on its second, replayed after),
-    then, with `advance`, fs_spec_advance, which writes the next round's inputs from this round's
-    acceptance into the same device buffers."""
+    then the k+1 phases and, with `advance`, fs_spec_advance, which writes the next round's inputs from
+    this round's acceptance into the same device buffers. The kernels run eagerly on the shape's first
+    round and are captured in one graph on its second (one graph per value of `advance`), replayed after.
+    The round's result is st.res: (b, k+2) int32, n_accepted then the committed tokens."""
     k = st.k
     if st.sampling:
         if hasattr(draws, "fill_round"):   # every row's numbers in one launch per kind
@@ -409,28 +411,43 @@ def _launch_round(target, draft, pool_t, pool_d, st: "_RoundState", b: int, draw
             u, e = draws.accept()
             st.u[:b, :k].copy_(u)
             st.e[:b].copy_(e)
-    if not graphs or st.uses == 0:
+
+    def kernels():
         for phase in range(k + 1):
-            st.res = _round_phase(target, draft, pool_t, pool_d, st, phase)
+            _round_phase(target, draft, pool_t, pool_d, st, phase)
+        if advance:
+            d = st.d
+            ops.spec_advance(st.res, st.b, k, 0 if st.n_shared else 1, d["n"], d["budget"], d["eos"], d["done"],
+                             d["ids"], d["last"], d["keff"], d["pos0"], d["posd"], d["posv"])
+
+    if not graphs or st.uses == 0:
+        kernels()
     else:
-        if st.graphs is None:
+        g = st.graphs.get(advance)
+        if g is None:   # the whole round in one graph: no launch gap between its phases
             torch.cuda.current_stream().synchronize()
-            gs = []
-            for phase in range(k + 1):
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g):
-                    out = _round_phase(target, draft, pool_t, pool_d, st, phase)
-                if out is not None:
-                    st.res = out
-                gs.append(g)
-            st.graphs = gs
-        for g in st.graphs:
-            g.replay()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                kernels()
+            st.graphs[advance] = g
+        g.replay()
     st.uses += 1
-    if advance:
-        d = st.d
-        ops.spec_advance(st.res, st.b, k, 0 if st.n_shared else 1, d["n"], d["budget"], d["eos"], d["done"], d["ids"],
-                         d["last"], d["keff"], d["pos0"], d["posd"], d["posv"])
+
+
+def capture_phase_graphs(target, draft, pool_t, pool_d, st: "_RoundState") -> list:
+    """One HIP graph per phase of st's round (draft steps 0..k-1, then the verify phase), for timing a
+    phase alone. Their replays rewrite what the round graph's last replay wrote: the same inputs give
+    the same keys, values, logits and outputs (st.res included)."""
+    if st.phase_graphs is None:
+        torch.cuda.current_stream().synchronize()
+        gs = []
+        for phase in range(st.k + 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                _round_phase(target, draft, pool_t, pool_d, st, phase)
+            gs.append(g)
+        st.phase_graphs = gs
+    return st.phase_graphs
 
 
 @torch.no_grad()
