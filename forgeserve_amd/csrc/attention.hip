@@ -57,6 +57,9 @@ struct AttnParams {
   // q_st/q_sh, o_st/o_sh; q_sb and o_sb unused), and only tokens t < row_start[b+1] - row_start[b]
   // exist: the others (positions -1) are neither read nor written
   const int32_t* row_start;
+  // query tiles per plan item: 1 for the unit kernel, PF_WAVES for the prefill kernel (item.z is then
+  // the index of a group of zgroup consecutive tiles, item.qmax the group's furthest query)
+  int32_t zgroup;
 };
 
 // Reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48) with the gfx950
@@ -110,15 +113,17 @@ struct AttnItem {
   int32_t b, z, s, qmax;   // batch row, query tile, chunk, furthest query position of the tile
 };
 
-FS_DEVICE int tile_qmax(const AttnParams& P, int b, int z) {
-  const int row0 = z * QTILE;
-  const int nrows = min(QTILE, P.T * P.G - row0);
-  const int t0 = row0 / P.G, t1 = (row0 + nrows - 1) / P.G;
+// furthest query position of query rows [row0, row0 + n) of batch row b (-1 if none)
+FS_DEVICE int rows_qmax(const AttnParams& P, int b, int row0, int n) {
+  n = min(n, P.T * P.G - row0);
+  if (n <= 0) return -1;
+  const int t0 = row0 / P.G, t1 = (row0 + n - 1) / P.G;
   const int* posb = P.pos + (int64_t)b * P.T;
   int q = -1;
   for (int t = t0; t <= t1; ++t) q = max(q, posb[t]);
   return q;
 }
+FS_DEVICE int tile_qmax(const AttnParams& P, int b, int z) { return rows_qmax(P, b, z * QTILE, QTILE); }
 
 // Chunks a query tile reads. With direct outputs a tile of padding queries still gets chunk 0, whose
 // workgroup writes their zero outputs.
@@ -162,18 +167,20 @@ __global__ void __launch_bounds__(PLAN_THREADS) attn_plan_kernel(AttnParams P) {
   const int qtiles = (P.T * P.G + QTILE - 1) / QTILE;
   const int U = P.B * qtiles;
   if (qtiles > 1) {
-    // A prefill (several query tiles per row): the tiles of one row are listed together, longest
-    // first, so the workgroups running at any time on an XCD (one KV head each) read one row's keys
-    // and values and share them in that XCD's L2; across rows the reads would not fit it. The order
-    // decides only which workgroup runs an item, never what the item computes.
+    // A prefill (several query tiles per row): the tiles (or groups of zgroup tiles) of one row are
+    // listed together, longest first, so the workgroups running at any time on an XCD (one KV head
+    // each) read one row's keys and values and share them in that XCD's L2; across rows the reads
+    // would not fit it. The order decides only which workgroup runs an item, never what it computes.
+    const int qg = (qtiles + P.zgroup - 1) / P.zgroup;
+    const int UG = P.B * qg;
     int base = 0;
-    for (int u0 = 0; u0 < U; u0 += PLAN_THREADS) {
+    for (int u0 = 0; u0 < UG; u0 += PLAN_THREADS) {
       const int u = u0 + tid;
       int qm = -1, nch = 0, b = 0, z = 0;
-      if (u < U) {
-        b = u / qtiles;
-        z = qtiles - 1 - (u - b * qtiles);
-        qm = tile_qmax(P, b, z);
+      if (u < UG) {
+        b = u / qg;
+        z = qg - 1 - (u - b * qg);
+        qm = rows_qmax(P, b, z * P.zgroup * QTILE, P.zgroup * QTILE);
         nch = tile_chunks(P, qm);
       }
       int n_round;
@@ -261,6 +268,152 @@ __global__ void __launch_bounds__(PLAN_THREADS) attn_plan_kernel(AttnParams P) {
 // LDS in wave order. Which tiles a wave sees, and in what order, depends only on absolute key
 // positions, and a tile wholly above a query's position leaves that query's partial exactly as it
 // was; a query's result therefore does not depend on the other queries of its tile.
+
+// One 16-key tile into a wave's online-softmax partial of up to 32 query rows (two 16-row halves; the
+// second only when `two`). kf holds the tile's keys as A operands of S^T = K.Q^T, vf its values as A
+// operands of O^T += V^T.P^T (zeroed in place where a key must not reach the product: an unmapped
+// block, or a key past qmax, the furthest query of the 32 rows, which may never have been written).
+// j0 is the tile's first key, rpos the positions of the lane's two rows (-1: no query), rmin the
+// smallest position over all 32 rows (-1 if any row is missing). A key above a row's position gets
+// score -inf.
+//
+// The partial is (m, l, acc) with p = 2^(s - m): m is a reference maximum that moves only when a
+// tile's maximum exceeds it by more than 8 (then to that maximum, and acc and l are rescaled), so
+// p <= 2^8 and the rescale is rare once a row has seen a few tiles. A tile wholly above a row leaves
+// that row's partial exactly as it was (m unchanged, alpha = 1, p = 0). A tile whose keys every row
+// sees takes a path without the per-key masks; its arithmetic is the same. LAZY skips the rescale
+// when no row of the wave moved (multiplying by alpha = 1 is exact, so the bits do not change). Every
+// kernel that builds a partial calls this function, so a row's partial does not depend on which
+// kernel ran it.
+// Smallest position over the rows r < nrows of a wave's 32-row tile (-1 if nrows <= 0); the rows of
+// lane l16 are l16 and 16 + l16, whose positions are rpos[0] and rpos[1].
+FS_DEVICE int rows_min_pos(const int (&rpos)[2], int nrows) {
+  if (nrows <= 0) return -1;
+  const int l16 = threadIdx.x & 15;
+  int v = min(l16 < nrows ? rpos[0] : 0x7fffffff, 16 + l16 < nrows ? rpos[1] : 0x7fffffff);
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v = min(v, __shfl_xor(v, o, 64));
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+constexpr float REF_SLACK = 8.f;   // log2 units a tile's maximum may exceed the reference by
+
+template <int D, bool LAZY, bool BOTH = false>
+FS_DEVICE void attn_tile(const bf16x8_t (&kf)[D / 32], short4_t (&vf)[D / 16], int j0, bool tile_valid, int qmax,
+                         const int (&rpos)[2], int rmin, bool two, const bf16x8_t (&qf)[2][D / 32],
+                         float scale_log2, float4_t (&acc)[D / 16][2], float (&m_run)[2], float (&l_run)[2]) {
+  constexpr int KS = D / 32;
+  constexpr int MT = D / 16;
+  const int g = (threadIdx.x & 63) >> 4;
+  const bool full = tile_valid && j0 + 15 <= rmin;   // wave-uniform
+  if (!full && (!tile_valid || j0 + 15 > qmax)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (!tile_valid || j0 + 4 * g + e > qmax) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) vf[mt][e] = 0;
+      }
+    }
+  }
+  // BOTH: the second half's products are formed whatever `two` says (rows past the tile's end hold
+  // values that are never written out), so the two halves' MFMA chains interleave without a branch
+  float4_t sc[2];
+  if (BOTH) {
+    sc[0] = float4_t{0.f, 0.f, 0.f, 0.f};
+    sc[1] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      sc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[0][ks], sc[0], 0, 0, 0);
+      sc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[1][ks], sc[1], 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      sc[nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+      if (nt == 0 || two) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[nt][ks], sc[nt], 0, 0, 0);
+      }
+    }
+  }
+  short4_t pf[2];
+  float alpha[2];
+  bool moved = false;
+  if (full) {   // every key visible to every row: scores are finite, no masks
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      float sv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sv[e] = sc[nt][e] * scale_log2;
+      const float tmax = max_across_groups(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+      const bool mv = tmax > m_run[nt] + REF_SLACK;
+      const float m_new = mv ? tmax : m_run[nt];
+      alpha[nt] = mv ? fast_exp2(m_run[nt] - m_new) : 1.f;
+      moved |= mv;
+      float pv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pv[e] = fast_exp2(sv[e] - m_new);
+      pf[nt] = bf16_rne4(pv);
+      l_run[nt] = l_run[nt] * alpha[nt] + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+      m_run[nt] = m_new;
+    }
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      float sv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = j0 + 4 * g + e;
+        const bool vis = tile_valid && key <= rpos[nt];
+        sv[e] = vis ? sc[nt][e] * scale_log2 : -INFINITY;
+      }
+      const float tmax = max_across_groups(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+      // (-inf > x is false: a row that sees nothing here keeps its reference)
+      const bool mv = tmax > m_run[nt] + REF_SLACK;
+      const float m_new = mv ? tmax : m_run[nt];
+      alpha[nt] = mv ? fast_exp2(m_run[nt] - m_new) : 1.f;
+      moved |= mv;
+      float pv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pv[e] = (sv[e] == -INFINITY) ? 0.f : fast_exp2(sv[e] - m_new);
+      pf[nt] = bf16_rne4(pv);
+      l_run[nt] = l_run[nt] * alpha[nt] + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+      m_run[nt] = m_new;
+    }
+  }
+  // The unit kernel rescales unconditionally (a branch there splits the accumulators' live ranges
+  // and spills at its register budget).
+  if (!LAZY || __any(moved)) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        acc[mt][nt][0] *= alpha[nt];
+        acc[mt][nt][1] *= alpha[nt];
+        acc[mt][nt][2] *= alpha[nt];
+        acc[mt][nt][3] *= alpha[nt];
+      }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[mt], pf[0], acc[mt][0], 0, 0, 0);
+    if (BOTH || two) acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[mt], pf[1], acc[mt][1], 0, 0, 0);
+  }
+}
+
+// A chunk's result for one query row is its 8 partials (tiles t with t % 8 == v, v = 0..7) folded in
+// increasing v: (M, L, O) <- (max(M, m), L*2^(M-M') + l*2^(m-M'), O*2^(M-M') + a*2^(m-M')). An empty
+// partial (m = -inf: no visible key) leaves the state as it is; the first non-empty one gets weight 1
+// and the empty state weight 2^-inf = 0. fold_weights returns false for an empty partial.
+FS_DEVICE bool fold_weights(float M, float m, float& Mn, float& cM, float& cm) {
+  if (m == -INFINITY) return false;
+  Mn = fmaxf(M, m);
+  cM = fast_exp2(M - Mn);
+  cm = fast_exp2(m - Mn);
+  return true;
+}
+FS_DEVICE float fold_value(float x, float cM, float y, float cm) { return x * cM + y * cm; }
 
 template <int D, int BSZ>
 __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const AttnParams& P, int b, int kbeg, int kend,
@@ -352,74 +505,10 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_run[2] = {0.f, 0.f};
 
+  const int rmin = rows_min_pos(rpos, nrows);
   auto consume = [&](int i, const bf16x8_t (&kf)[KS], short4_t (&vf)[MT]) {
-    const int j0 = key0(i);
-    const bool tile_valid = block_of(i) >= 0;
-    // keys of an unmapped block, and keys past the furthest query (possibly never written), must not
-    // reach the PV product: their values may be anything
-    if (!tile_valid || j0 + 15 > qmax) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (!tile_valid || j0 + 4 * g + e > qmax) {
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) vf[mt][e] = 0;
-        }
-      }
-    }
-    float4_t sc[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      sc[nt] = float4_t{0.f, 0.f, 0.f, 0.f};
-      if (nt == 0 || two) {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[nt][ks], sc[nt], 0, 0, 0);
-      }
-    }
-    short4_t pf[2];
-    float alpha[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      float sv[4];
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = j0 + 4 * g + e;
-        const bool vis = tile_valid && key <= rpos[nt];
-        sv[e] = vis ? sc[nt][e] * P.scale_log2 : -INFINITY;
-        tmax = fmaxf(tmax, sv[e]);
-      }
-      tmax = max_across_groups(tmax);
-      const float m_new = fmaxf(m_run[nt], tmax);
-      // v_exp_f32 directly (fast_exp2): exp2f adds a range scaling that only changes results below
-      // 2^-126, which neither the bf16 P operand nor the f32 row sum can resolve, for ~4 VALU each
-      alpha[nt] = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run[nt] - m_new);
-      float psum = 0.f;
-      float pv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pv[e] = (sv[e] == -INFINITY) ? 0.f : fast_exp2(sv[e] - m_new);
-        psum += pv[e];
-      }
-      pf[nt] = bf16_rne4(pv);
-      l_run[nt] = l_run[nt] * alpha[nt] + psum;
-      m_run[nt] = m_new;
-    }
-    // unconditional rescale: a branch here splits the accumulators' live ranges and spills
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        acc[mt][nt][0] *= alpha[nt];
-        acc[mt][nt][1] *= alpha[nt];
-        acc[mt][nt][2] *= alpha[nt];
-        acc[mt][nt][3] *= alpha[nt];
-      }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[mt], pf[0], acc[mt][0], 0, 0, 0);
-      if (two) acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[mt], pf[1], acc[mt][1], 0, 0, 0);
-    }
+    attn_tile<D, false>(kf, vf, key0(i), block_of(i) >= 0, qmax, rpos, rmin, two, qf, P.scale_log2, acc, m_run,
+                        l_run);
   };
 
   for (int i = 0; i < nt_w; i += 3) {
@@ -442,6 +531,34 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
       red_m[16 * nt + l16] = m_run[nt];
       red_l[16 * nt + l16] = lsum;
     }
+  }
+}
+
+// Row `rr` of the query rows (token rr / G, head hkv*G + rr % G), dims 16*mt + 4g .. +4, from its
+// folded chunk-s state (M, L, O): a query that sees one chunk only is finished here (a padding query,
+// position < 0, gets zeros from chunk 0); any other query gets this chunk's partial for attn_combine
+// if the chunk holds keys it sees.
+template <int D>
+FS_DEVICE void attn_emit(const AttnParams& P, int b, int s, int kbeg, int hkv, int rr, int rp, int mt, float M,
+                         float L, const float4_t& o) {
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  const bool direct = P.direct && (rp < P.split || P.nsplit == 1);
+  if (direct ? s != 0 : rp < kbeg) return;
+  const int t = rr / P.G, h = hkv * P.G + (rr - t * P.G);
+  if (direct) {   // the same normalisation as attn_combine's
+    if (!token_exists(P, b, t)) return;
+    const float f[4] = {L > 0.f ? o[0] / L : 0.f, L > 0.f ? o[1] / L : 0.f, L > 0.f ? o[2] / L : 0.f,
+                        L > 0.f ? o[3] / L : 0.f};
+    uint16_t* orow = reinterpret_cast<uint16_t*>(P.out) + o_offset(P, b, t, P.o_sb, P.o_st) + (int64_t)h * P.o_sh;
+    *reinterpret_cast<short4_t*>(orow + 16 * mt + 4 * g) = bf16_rne4(f);
+    return;
+  }
+  const int64_t R = row_index(P, b, t, h);
+  *reinterpret_cast<float4_t*>(P.ws_acc + (R * P.nsplit + s) * D + 16 * mt + 4 * g) = o;
+  if (mt == 0 && g == 0) {
+    float* pm = P.ws_ml + (R * P.nsplit + s) * 2;
+    pm[0] = M;
+    pm[1] = L;
   }
 }
 
@@ -475,49 +592,275 @@ attn_unit_kernel(AttnParams P) {
   attn_wave_tiles<D, BSZ>(P, b, kbeg, kend, qmax, row0, nrows, rpos, hkv, w, red_acc[w], red_m[w], red_l[w]);
   __syncthreads();
 
-  // merge the waves' partials in wave order; wave w takes the (query half, 16-dim tile) pairs w,
+  // fold the waves' partials in wave order; wave w takes the (query half, 16-dim tile) pairs w,
   // w + UNIT_WAVES, ...
   for (int gi = w; gi < 2 * MT; gi += UNIT_WAVES) {
     const int nt = gi / MT, mt = gi - nt * MT;
     const int r = 16 * nt + l16;
     if (r >= nrows) continue;
-    // a query that sees one chunk only is finished here (a padding query, position < 0, gets zeros
-    // from chunk 0); any other query gets this chunk's partial if the chunk holds keys it sees
-    const bool direct = P.direct && (rpos[nt] < P.split || P.nsplit == 1);
-    if (direct ? s != 0 : rpos[nt] < kbeg) continue;
-    float M = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < UNIT_WAVES; ++v) M = fmaxf(M, red_m[v][r]);
-    float L = 0.f;
+    float M = -INFINITY, L = 0.f;
     float4_t o = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int v = 0; v < UNIT_WAVES; ++v) {
-      const float mv = red_m[v][r];
-      const float c = (mv == -INFINITY) ? 0.f : fast_exp2(mv - M);
-      L += c * red_l[v][r];
+      float Mn, cM, cm;
+      if (!fold_weights(M, red_m[v][r], Mn, cM, cm)) continue;
+      L = fold_value(L, cM, red_l[v][r], cm);
       const float4_t a = red_acc[v][gi][lane];
-      o[0] += c * a[0];
-      o[1] += c * a[1];
-      o[2] += c * a[2];
-      o[3] += c * a[3];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = fold_value(o[c], cM, a[c], cm);
+      M = Mn;
     }
-    const int rr = row0 + r;
-    const int t = rr / P.G, h = hkv * P.G + (rr - t * P.G);
-    if (direct) {   // the same normalisation as attn_combine's
-      if (!token_exists(P, b, t)) continue;
-      const float f[4] = {L > 0.f ? o[0] / L : 0.f, L > 0.f ? o[1] / L : 0.f, L > 0.f ? o[2] / L : 0.f,
-                          L > 0.f ? o[3] / L : 0.f};
-      uint16_t* orow = reinterpret_cast<uint16_t*>(P.out) + o_offset(P, b, t, P.o_sb, P.o_st) + (int64_t)h * P.o_sh;
-      *reinterpret_cast<short4_t*>(orow + 16 * mt + 4 * g) = bf16_rne4(f);
-      continue;
+    attn_emit<D>(P, b, s, kbeg, hkv, row0 + r, rpos[nt], mt, M, L, o);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// prefill kernel: one workgroup of PF_WAVES waves per (plan item of PF_WAVES query tiles, KV head)
+// ------------------------------------------------------------------------------------------------
+// A prompt's queries are many 32-row tiles per row. Here the PF_WAVES tiles of an item (256 query rows:
+// wave w owns tile PF_WAVES * item.z + w) share every key and value tile through an LDS ring that
+// direct global->LDS copies fill, so a key tile is read from memory once per 256 query rows instead of
+// once per 32. Each wave computes, for its own rows, exactly what the unit kernel computes for them:
+// the partial of tiles v, v + 8, v + 16, ... (v = 0..7, increasing), with attn_tile, folded in
+// increasing v with fold_weights/fold_value. The ring therefore carries the chunk's tiles in that
+// order (all tiles t % 8 == 0, then t % 8 == 1, ...), and a wave skips the tiles wholly above its
+// furthest query (no-ops for every row of the wave). Output bits equal the unit kernel's.
+constexpr int PF_WAVES = 8;      // query tiles (waves) per workgroup
+constexpr int PF_TILES = 4;      // 16-key tiles per ring stage
+constexpr int PF_NS = 4;         // ring stages (two in flight behind the one awaited)
+constexpr int PF_MIN_QTILES = 5; // a call with at least this many query tiles per row takes this kernel
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// One 16-byte copy per lane straight into LDS (lane l lands at lds + 16 * l; the base is the same for
+// the whole wave). The copy is counted by vmcnt like any vector load; the waits below are explicit.
+FS_DEVICE void pf_dma16(const void* src, uint32_t lds) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+FS_DEVICE void pf_wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// The chunk's tiles in the ring's order: class v = t % 8 in increasing v, increasing t inside a class.
+// The tile after t (of a chunk of n tiles) is t + 8, or the next class's first tile (t % 8) + 1.
+FS_DEVICE int pf_next_tile(int t, int n) {
+  t += 8;
+  return t < n ? t : (t & 7) + 1;
+}
+
+template <int D, int BSZ>
+__global__ void __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+attn_prefill_kernel(AttnParams P) {
+  constexpr int KS = D / 32, MT = D / 16;
+  constexpr int TK = 16 * D * 2;                    // bytes of a tile's keys (and of its values)
+  constexpr int TB = 2 * TK;                        // a tile in LDS: keys, then values
+  constexpr int CPT = TB / 1024;                    // 1 KB copies per tile
+  constexpr int CPW = PF_TILES * CPT / PF_WAVES;    // copies per wave per stage
+  constexpr int CPR = D / 8;                        // 16-byte chunks per key row
+  constexpr int STAGE = PF_TILES * TB;
+  static_assert(PF_WAVES % CPT == 0 && CPW >= 1, "every wave copies the same part of its tiles");
+  static_assert(PF_NS == 4, "the waits below cover two stages in flight behind the awaited one");
+  __shared__ __attribute__((aligned(1024))) char ring[PF_NS * STAGE];
+  __shared__ int tbl[MAX_SPLIT / 16 + 1];           // the chunk's physical blocks (-1: unmapped)
+
+  const int nkv = P.kv.n_kv_heads;
+  const int64_t e_idx = blockIdx.x / nkv;
+  const int hkv = (int)(blockIdx.x - e_idx * nkv);
+  if (e_idx >= P.n_items[0]) return;   // uniform over the workgroup
+  typedef __attribute__((address_space(4))) const AttnItem ConstItem;
+  ConstItem* ep = (ConstItem*)(uintptr_t)(P.items + e_idx);
+  const int b = ep->b, zb = ep->z, s = ep->s, qmax_item = ep->qmax;
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int BS = BSZ ? BSZ : P.kv.block_size;
+  const int64_t v_dim = BSZ ? BSZ : P.kv.v_dim;   // == block_size (dim-major values)
+  const int kbeg = s * P.split;
+  const int kend = min(kbeg + P.split, qmax_item + 1);
+  const int ntiles = max((kend - kbeg + 15) >> 4, 0);
+  const int nst = (ntiles + PF_TILES - 1) / PF_TILES;
+
+  // this wave's query tile: the unit kernel's tile z, with its rows, positions and furthest query
+  const int z = zb * PF_WAVES + w;
+  const int row0 = z * QTILE;
+  const int nrows = min(QTILE, P.T * P.G - row0);   // <= 0: a wave past the last tile (copies only)
+  const bool two = nrows > 16;
+  const int* posb = P.pos + (int64_t)b * P.T;
+  int rpos[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int r = 16 * nt + l16;
+    rpos[nt] = (r < nrows) ? posb[(row0 + r) / P.G] : -1;
+  }
+  const int qmax = nrows > 0 ? tile_qmax(P, b, z) : -1;
+  const int rmin = rows_min_pos(rpos, nrows);
+  const int ntiles_w = nrows > 0 ? min(max((min(kbeg + P.split, qmax + 1) - kbeg + 15) >> 4, 0), ntiles) : 0;
+
+  typedef uint16_t u16;
+  const u16* qbase = reinterpret_cast<const u16*>(P.q);
+  bf16x8_t qf[2][KS];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int r = row0 + 16 * nt + l16;
+    const bool in_tile = nrows > 0 && (16 * nt + l16) < nrows;
+    const bool ok = in_tile && token_exists(P, b, r / P.G);
+    const int t = ok ? r / P.G : 0;
+    const int h = hkv * P.G + (ok ? r - (r / P.G) * P.G : 0);
+    const u16* qr = qbase + q_offset(P, b, t) + (int64_t)h * P.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[nt][ks] = ok ? *reinterpret_cast<const bf16x8_t*>(qr + 32 * ks + 8 * g) : bf16x8_t{};
+  }
+
+  // the chunk's table entries
+  const int blk0 = kbeg / BS;
+  const int nblk = ntiles > 0 ? (kbeg + 16 * ntiles - 1) / BS - blk0 + 1 : 0;
+  int unmapped = 0;
+  for (int i = tid; i < nblk; i += 64 * PF_WAVES) {
+    const int blk = blk0 + i;
+    int v = blk < P.max_blocks ? P.table[(int64_t)b * P.table_stride + blk] : -1;
+    v = (v >= 0 && v < P.kv.num_blocks) ? v : -1;
+    unmapped |= v < 0;
+    tbl[i] = v;
+  }
+  // every load above has landed (the copies below are counted by the explicit waits only)
+  __builtin_amdgcn_s_waitcnt(0);
+  const bool all_mapped = !__syncthreads_or(unmapped);   // (the common case: no lookups per tile)
+
+  // This wave copies part p = w % CPT of every tile it copies (keys for p < CPT/2, else values).
+  // LDS layouts (16-byte slots; 16 consecutive slots are read without bank conflicts):
+  //  * keys: row r's 16-byte chunk c at slot r * CPR + (c ^ f(r)), f(r) = r & 15 for 16 chunks per
+  //    row, (r >> 1) & 7 for 8, so the 16 rows of an MFMA operand read 16 different slots mod 16;
+  //  * values: dim d's keys 8h .. 8h+7 at slot 2d + (h ^ ((d >> 3) & 1)), so dims d and d + 8 of an
+  //    operand read different slots mod 16.
+  const int p = w % CPT;
+  const bool kpart = p < CPT / 2;
+  int64_t src_off;
+  {
+    const int P16 = (kpart ? p : p - CPT / 2) * 64 + lane;
+    if (kpart) {
+      const int row = P16 / CPR, f = CPR == 16 ? (row & 15) : ((row >> 1) & 7);
+      const int c = (P16 % CPR) ^ f;
+      src_off = (int64_t)row * D + 8 * c;
+    } else {
+      const int d = P16 >> 1, h = (P16 & 1) ^ ((d >> 3) & 1);
+      src_off = (int64_t)d * v_dim + 8 * h;
     }
-    const int64_t R = row_index(P, b, t, h);
-    *reinterpret_cast<float4_t*>(P.ws_acc + (R * P.nsplit + s) * D + 16 * mt + 4 * g) = o;
-    if (mt == 0 && g == 0) {
-      float* pm = P.ws_ml + (R * P.nsplit + s) * 2;
-      pm[0] = M;
-      pm[1] = L;
+  }
+  const u16* pool = reinterpret_cast<const u16*>(kpart ? P.kv.k : P.kv.v);
+  const int64_t blk_stride = kpart ? P.kv.k_block : P.kv.v_block;
+  const int64_t lane_off = (int64_t)hkv * (kpart ? P.kv.k_head : P.kv.v_head) + src_off;
+  const int slot_mul = kpart ? D : 1;
+  const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
+  // this lane's operand reads inside a tile (bytes)
+  const int fk = CPR == 16 ? (l16 & 15) : ((l16 >> 1) & 7);
+  int koff[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = (l16 * CPR + ((4 * ks + g) ^ fk)) * 16;
+  const int voff = TK + (2 * l16 + ((g >> 1) ^ ((l16 >> 3) & 1))) * 16 + 8 * (g & 1);
+
+  // copies walk the tiles PF_TILES at a time; a stage past the last tile copies the last tile again
+  int ct = 0, copied = 0;
+  auto issue = [&](int k) {
+    const uint32_t base = ring0 + (uint32_t)((k % PF_NS) * STAGE) + (uint32_t)(p * 1024);
+    int tt[PF_TILES];
+#pragma unroll
+    for (int u = 0; u < PF_TILES; ++u) {
+      tt[u] = ct;
+      if (++copied < ntiles) ct = pf_next_tile(ct, ntiles);
     }
+    // every table read of the stage before the first copy (each copy orders all memory accesses)
+    const u16* src[CPW];
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+      const int key0 = kbeg + 16 * tt[(w + PF_WAVES * i) / CPT];
+      const int bi = key0 / BS;
+      const int ph = tbl[bi - blk0];
+      const int64_t pb = ph >= 0 ? ph : 0;       // unmapped: block 0, masked in attn_tile
+      src[i] = pool + pb * blk_stride + (int64_t)(key0 - bi * BS) * slot_mul;
+    }
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) pf_dma16(src[i] + lane_off, base + (uint32_t)(((w + PF_WAVES * i) / CPT) * TB));
+  };
+  auto wait_stages = [&](int later) {
+    if (later >= 2) pf_wait_vm<2 * CPW>();
+    else if (later == 1) pf_wait_vm<CPW>();
+    else pf_wait_vm<0>();
+  };
+
+  float4_t acc[MT][2], O[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      acc[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+      O[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  float Ms[2] = {-INFINITY, -INFINITY}, Ls[2] = {0.f, 0.f};
+  // the finished partial of class v into the row state, then an empty partial for the next class
+  auto fold = [&]() {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const float l = sum_across_groups(l_run[nt]);
+      float Mn, cM, cm;
+      if (fold_weights(Ms[nt], m_run[nt], Mn, cM, cm)) {
+        Ls[nt] = fold_value(Ls[nt], cM, l, cm);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) O[mt][nt][c] = fold_value(O[mt][nt][c], cM, acc[mt][nt][c], cm);
+        Ms[nt] = Mn;
+      }
+      m_run[nt] = -INFINITY;
+      l_run[nt] = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+#pragma unroll
+  for (int k = 0; k < PF_NS - 1; ++k)
+    if (k < nst) issue(k);
+  int rt = 0;   // the tile consumed next
+  int cur_v = 0;
+  for (int k = 0; k < nst; ++k) {
+    wait_stages(min(PF_NS - 2, nst - 1 - k));
+    __syncthreads();   // stage k has landed for every wave; stage k-1 is no longer being read
+    if (k + PF_NS - 1 < nst) issue(k + PF_NS - 1);
+    const char* st = ring + (k % PF_NS) * STAGE;
+#pragma unroll 1
+    for (int u = 0; u < PF_TILES; ++u) {
+      if (k * PF_TILES + u >= ntiles) break;
+      const int t = rt;
+      rt = pf_next_tile(rt, ntiles);
+      if (nrows <= 0) continue;
+      if ((t & 7) != cur_v) {   // a new class: fold the last one into the row state
+        fold();
+        cur_v = t & 7;
+      }
+      if (t >= ntiles_w) continue;   // wholly above every query of the wave
+      const char* tk = st + u * TB;
+      bf16x8_t kf[KS];
+      short4_t vf[MT];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const bf16x8_t*>(tk + koff[ks]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) vf[mt] = *reinterpret_cast<const short4_t*>(tk + voff + mt * 16 * 32);
+      const int key0 = kbeg + 16 * t;
+      const bool tv = all_mapped || tbl[key0 / BS - blk0] >= 0;
+      attn_tile<D, true, true>(kf, vf, key0, tv, qmax, rpos, rmin, two, qf, P.scale_log2, acc, m_run, l_run);
+    }
+  }
+  if (nrows <= 0) return;
+  fold();
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int r = 16 * nt + l16;
+    if (r >= nrows) continue;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) attn_emit<D>(P, b, s, kbeg, hkv, row0 + r, rpos[nt], mt, Ms[nt], Ls[nt], O[mt][nt]);
   }
 }
 
@@ -733,11 +1076,11 @@ struct PlanKey {
   const int32_t* pos = nullptr;
   const int32_t* row_start = nullptr;
   hipStream_t stream = nullptr;
-  int32_t B = 0, T = 0, G = 0, split = 0, nsplit = 0;
+  int32_t B = 0, T = 0, G = 0, split = 0, nsplit = 0, zgroup = 0;
   bool direct = false;
   bool operator==(const PlanKey& o) const {
     return ws == o.ws && pos == o.pos && row_start == o.row_start && stream == o.stream && B == o.B && T == o.T &&
-           G == o.G && split == o.split && nsplit == o.nsplit && direct == o.direct;
+           G == o.G && split == o.split && nsplit == o.nsplit && direct == o.direct && zgroup == o.zgroup;
   }
 };
 thread_local PlanKey last_plan;
@@ -796,13 +1139,16 @@ int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, con
   P.o_st = o_st;
   P.o_sh = o_sh;
   P.row_start = row_start;
+  const int64_t qtiles = ((int64_t)T * P.G + QTILE - 1) / QTILE;
+  // many query tiles per row (a prompt): groups of PF_WAVES tiles share their key/value reads
+  const bool prefill = mfma && qtiles >= PF_MIN_QTILES;
+  P.zgroup = prefill ? PF_WAVES : 1;
 
   hipStream_t st = fs::as_stream(stream);
   if (mfma) {
     const bool bs16 = kv->block_size == 16;
     // one workgroup per (plan item, KV head); items past the plan's length exit at once
-    const int64_t qtiles = ((int64_t)T * P.G + QTILE - 1) / QTILE;
-    const int64_t units = (int64_t)B * qtiles * P.nsplit * kv->n_kv_heads;
+    const int64_t units = (int64_t)B * ((qtiles + P.zgroup - 1) / P.zgroup) * P.nsplit * kv->n_kv_heads;
     FS_CHECK_ARG(units < 0x7fffffff, "paged_attention: %lld work units", (long long)units);
     PlanKey key;
     key.ws = workspace;
@@ -815,15 +1161,28 @@ int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, con
     key.split = P.split;
     key.nsplit = P.nsplit;
     key.direct = P.direct;
+    key.zgroup = P.zgroup;
     if (!(reuse_plan && last_plan == key)) attn_plan_kernel<<<1, PLAN_THREADS, 0, st>>>(P);
     last_plan = key;
-    const unsigned grid = (unsigned)units, threads = 64 * UNIT_WAVES;
-    if (kv->head_dim == 128) {
-      if (bs16) attn_unit_kernel<128, 16><<<grid, threads, 0, st>>>(P);
-      else attn_unit_kernel<128, 0><<<grid, threads, 0, st>>>(P);
+    const unsigned grid = (unsigned)units;
+    if (prefill) {
+      const unsigned threads = 64 * PF_WAVES;
+      if (kv->head_dim == 128) {
+        if (bs16) attn_prefill_kernel<128, 16><<<grid, threads, 0, st>>>(P);
+        else attn_prefill_kernel<128, 0><<<grid, threads, 0, st>>>(P);
+      } else {
+        if (bs16) attn_prefill_kernel<64, 16><<<grid, threads, 0, st>>>(P);
+        else attn_prefill_kernel<64, 0><<<grid, threads, 0, st>>>(P);
+      }
     } else {
-      if (bs16) attn_unit_kernel<64, 16><<<grid, threads, 0, st>>>(P);
-      else attn_unit_kernel<64, 0><<<grid, threads, 0, st>>>(P);
+      const unsigned threads = 64 * UNIT_WAVES;
+      if (kv->head_dim == 128) {
+        if (bs16) attn_unit_kernel<128, 16><<<grid, threads, 0, st>>>(P);
+        else attn_unit_kernel<128, 0><<<grid, threads, 0, st>>>(P);
+      } else {
+        if (bs16) attn_unit_kernel<64, 16><<<grid, threads, 0, st>>>(P);
+        else attn_unit_kernel<64, 0><<<grid, threads, 0, st>>>(P);
+      }
     }
   } else {
     last_plan = PlanKey{};   // no plan on this path

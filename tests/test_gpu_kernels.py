@@ -302,6 +302,45 @@ def test_attention_prefill_equals_decode_bitwise(d):
             assert torch.equal(one[0, 0], full[i, j]), (i, j)
 
 
+@pytest.mark.parametrize("d,g,bs,lens,starts", [
+    (128, 4, 16, [9000], [0]),              # the prompt crosses key 8192: two chunks and the combine
+    (128, 4, 32, [700, 1500], [0, 300]),    # block size 32; row 0 has 800 padding tokens
+    (64, 8, 16, [513, 90], [40, 0]),
+    (128, 1, 16, [260], [3]),               # one head per KV head: 9 query tiles
+    (128, 2, 48, [8400], [0]),              # blocks of 48 keys: the 8192-key chunk starts mid-block
+])
+def test_attention_prefill_kernel_equals_unit_kernel_bitwise(d, g, bs, lens, starts):
+    """The prefill kernel (groups of 8 query tiles sharing each key tile through LDS) gives every token
+    the bits the unit kernel gives it: the same prompts cut into windows of 32 // g tokens (one query
+    tile each, so the unit kernel runs), every window a batch row on the same table row."""
+    case("attention prefill kernel == unit kernel", d, g, bs, lens)
+    hkv = 2
+    h = hkv * g
+    ctx = [st + n for st, n in zip(starts, lens)]
+    nblocks = sum(-(-c // bs) for c in ctx) + 3
+    t = max(lens)
+    q, k, v, tables, _ = _paged_case(len(lens), t, h, hkv, d, bs, ctx, nblocks, torch.bfloat16, 100 + d + g + bs)
+    pos = torch.full((len(lens), t), -1, dtype=torch.long)
+    for i, (st, n) in enumerate(zip(starts, lens)):
+        pos[i, :n] = torch.arange(st, st + n)
+    full, pool = _run_attention(q, k, v, tables, pos, torch.bfloat16, bs)
+    full = full.cpu()
+    win = 32 // g
+    lay = pool.layout(0)
+    for i, n in enumerate(lens):
+        nw = -(-n // win)
+        qw = torch.zeros(nw, win, h, d, dtype=torch.bfloat16)
+        pw = torch.full((nw, win), -1, dtype=torch.long)
+        qw.view(-1, h, d)[:n] = q[i, :n]
+        pw.view(-1)[:n] = pos[i, :n]
+        tw = tables[i: i + 1].expand(nw, -1).contiguous()
+        one = ops.paged_attention(qw.to(DEV), lay, tw.int().to(DEV), pw.int().to(DEV), 1.0 / math.sqrt(d)).cpu()
+        got = one.view(-1, h, d)[:n]
+        bad = (got != full[i, :n]).any(-1).any(-1).nonzero()
+        assert bad.numel() == 0, f"row {i}: {bad.numel()} tokens differ, first {bad[:5].flatten().tolist()}"
+        assert torch.count_nonzero(full[i, n:]) == 0   # padding tokens
+
+
 def test_attention_padding_rows_are_zero():
     case("attention padding")
     q, k, v, tables, pos = _paged_case(3, 3, 8, 2, 128, 16, [50, 70, 30], 20, torch.bfloat16, 4)
