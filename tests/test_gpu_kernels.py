@@ -302,24 +302,28 @@ def test_attention_prefill_equals_decode_bitwise(d):
             assert torch.equal(one[0, 0], full[i, j]), (i, j)
 
 
-@pytest.mark.parametrize("d,g,bs,lens,starts", [
-    (128, 4, 16, [9000], [0]),              # the prompt crosses key 8192: two chunks and the combine
-    (128, 4, 32, [700, 1500], [0, 300]),    # block size 32; row 0 has 800 padding tokens
-    (64, 8, 16, [513, 90], [40, 0]),
-    (128, 1, 16, [260], [3]),               # one head per KV head: 9 query tiles
-    (128, 2, 48, [8400], [0]),              # blocks of 48 keys: the 8192-key chunk starts mid-block
+@pytest.mark.parametrize("d,g,bs,lens,starts,qscale", [
+    (128, 4, 16, [9000], [0], 1.0),              # the prompt crosses key 8192: two chunks and the combine
+    (128, 4, 32, [700, 1500], [0, 300], 1.0),    # block size 32; row 0 has 800 padding tokens
+    (64, 8, 16, [513, 90], [40, 0], 1.0),
+    (128, 1, 16, [260], [3], 1.0),               # one head per KV head: 9 query tiles
+    (128, 2, 48, [8400], [0], 1.0),              # blocks of 48 keys: the 8192-key chunk starts mid-block
+    (128, 4, 16, [1100, 333], [0, 64], 12.0),    # scores spread over ~2^30: references move often
+    (64, 4, 16, [700], [5], 12.0),
 ])
-def test_attention_prefill_kernel_equals_unit_kernel_bitwise(d, g, bs, lens, starts):
+def test_attention_prefill_kernel_equals_unit_kernel_bitwise(d, g, bs, lens, starts, qscale):
     """The prefill kernel (groups of 8 query tiles sharing each key tile through LDS) gives every token
     the bits the unit kernel gives it: the same prompts cut into windows of 32 // g tokens (one query
-    tile each, so the unit kernel runs), every window a batch row on the same table row."""
-    case("attention prefill kernel == unit kernel", d, g, bs, lens)
+    tile each, so the unit kernel runs), every window a batch row on the same table row. qscale
+    stretches the scores so that a tile often lifts a row's reference maximum (the rescale paths)."""
+    case("attention prefill kernel == unit kernel", d, g, bs, lens, qscale)
     hkv = 2
     h = hkv * g
     ctx = [st + n for st, n in zip(starts, lens)]
     nblocks = sum(-(-c // bs) for c in ctx) + 3
     t = max(lens)
     q, k, v, tables, _ = _paged_case(len(lens), t, h, hkv, d, bs, ctx, nblocks, torch.bfloat16, 100 + d + g + bs)
+    q = (q.float() * qscale).bfloat16()
     pos = torch.full((len(lens), t), -1, dtype=torch.long)
     for i, (st, n) in enumerate(zip(starts, lens)):
         pos[i, :n] = torch.arange(st, st + n)
