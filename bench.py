@@ -304,36 +304,65 @@ def time_accept(torch, ops, reps, warmup, with_stats=False):
     return sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e-3
 
 
-def time_gemms(torch, ops, model, m, reps=10):
+def time_gemms(torch, ops, model, m, passes=3):
     """One layer's four GEMMs and the LM head at M rows (the verify pass: M = B*(k+1); a draft step:
-    M = B), as the round runs them: gate|up with the SwiGLU gate in its epilogue, each call on the
-    next layer's weights (so that, as in a round, the weights stream from HBM rather than the 256 MB
-    last-level cache): {name: (seconds per call, flops)}."""
+    M = B), each as the round runs it: qkv, wo and w_down as split-K partials where their (N, K)
+    splits K (the round adds the partials inside the rotary + KV write and the residual-add + RMSNorm
+    that follow, kernels counted apart), gate|up with the SwiGLU gate in its epilogue, the head with
+    its softmax-statistics epilogue. A shape's calls run back to back over successive layers' weights
+    (so that, as in a round, the weights stream from HBM rather than the 256 MB last-level cache),
+    `passes` times over the layers, between one pair of events: {name: (seconds per call, flops)}."""
+    from forgeserve_amd import _lib
+    lib = _lib.load()
     layers = model.layers
     d = model.cfg.d_model
-    shapes = {"qkv": (d, [b.attn.qkv_weight() for b in layers], ops.gemm),
-              "o": (d, [b.attn.wo.weight for b in layers], ops.gemm),
-              "gate_up": (d, [b.mlp.gate_up_weight() for b in layers], ops.gemm_swiglu),
-              "down": (layers[0].mlp.w_down.weight.shape[1], [b.mlp.w_down.weight for b in layers], ops.gemm),
-              "head": (d, [model.lm_head.weight], ops.gemm)}
+    shapes = {"qkv": (d, [b.attn.qkv_weight() for b in layers], "gemm"),
+              "o": (d, [b.attn.wo.weight for b in layers], "gemm"),
+              "gate_up": (d, [b.mlp.gate_up_weight() for b in layers], "swiglu"),
+              "down": (layers[0].mlp.w_down.weight.shape[1], [b.mlp.w_down.weight for b in layers], "gemm"),
+              "head": (d, [model.lm_head.weight], "head")}
     out = {}
-    for name, (kdim, ws, fn) in shapes.items():
+    for name, (kdim, ws, kind) in shapes.items():
+        n = ws[0].shape[0]
         x = torch.randn(m, kdim, device="cuda").to(ws[0].dtype)
+        if kind == "swiglu":
+            def fn(w):
+                ops.gemm_swiglu(x, w)
+        elif kind == "head":
+            stats = torch.empty((m, ops.row_stats_parts(m, n, kdim), 4), dtype=torch.int32, device="cuda")
+            logits = torch.empty((m, n), dtype=x.dtype, device="cuda")
+
+            def fn(w):
+                ops.gemm_row_stats(x, w, None, stats, out=logits)
+        elif lib.fs_gemm_splits(n, kdim, _lib.BF16) > 1:
+            part = torch.empty(lib.fs_gemm_splits(n, kdim, _lib.BF16) * m * n, dtype=torch.float32, device="cuda")
+
+            def fn(w):
+                ops.check(lib.fs_gemm_partials(ops.ptr(x), x.stride(0), ops.ptr(w), w.stride(0), m, n, kdim,
+                                               _lib.BF16, ops.ptr(part), part.numel() * 4, ops.stream_ptr()),
+                          "gemm_partials")
+        else:
+            c = torch.empty((m, n), dtype=x.dtype, device="cuda")
+
+            def fn(w):
+                ops.gemm(x, w, out=c)
+        calls = max(passes * len(ws), 8)
         for i in range(2):
-            fn(x, ws[i % len(ws)])
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for i, (a, b) in enumerate(ev):
-            w = ws[(i + 2) % len(ws)]
-            a.record()
-            fn(x, w)
-            b.record()
+            fn(ws[i % len(ws)])
         torch.cuda.synchronize()
-        out[name] = (sum(a.elapsed_time(b) for a, b in ev) / reps * 1e-3, 2.0 * m * kdim * ws[0].shape[0])
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(calls):
+            fn(ws[i % len(ws)])
+        b.record()
+        torch.cuda.synchronize()
+        out[name] = (a.elapsed_time(b) * 1e-3 / calls, 2.0 * m * kdim * n)
     return out
 
 
 def gemm_summary(times, layers, peak_tflops):
-    """Σ flops / Σ time over a pass's GEMMs (the layer GEMMs `layers` times, the head once)."""
+    """Σ flops / Σ time over a pass's GEMMs (the layer GEMMs `layers` times, the head once; the verify
+    pass runs blocks L_d..L-1 at M = B*(k+1), a draft step its L_d blocks at M = B)."""
     t = sum(v[0] for k, v in times.items() if k != "head") * layers + times["head"][0]
     f = sum(v[1] for k, v in times.items() if k != "head") * layers + times["head"][1]
     return {"tflops": round(f / t / 1e12, 1), "frac": round(f / t / 1e12 / peak_tflops, 4),
@@ -497,8 +526,8 @@ def kernel_mode(args):
                "avg_us": round(sec * 1e6, 2), "algorithmic_bytes": byts, "achieved_GBs": round(byts / sec / 1e9, 1)}
     elif args.kernel == "gemm":
         target, draft = build_models(torch, fa)
-        out = {"kernel": "gemm", "m448": gemm_summary(time_gemms(torch, ops, target, BATCH * (K + 1)), CFG["n_layers"],
-                                                      MFMA_PEAK_TFLOPS),
+        out = {"kernel": "gemm", "m448": gemm_summary(time_gemms(torch, ops, target, BATCH * (K + 1)),
+                                                      CFG["n_layers"] - draft.cfg.n_layers, MFMA_PEAK_TFLOPS),
                "m64": gemm_summary(time_gemms(torch, ops, draft, BATCH), draft.cfg.n_layers, MFMA_PEAK_TFLOPS)}
     elif args.kernel == "prefill_attention":
         n_seq, L, h, hkv, d = 8, 4096, CFG["n_heads"], CFG["n_kv_heads"], 128
@@ -607,7 +636,8 @@ def main():
     acc_avg = time_accept(torch, ops, 20, 3)
     acc_gbs = accept_bytes(BATCH, K, v) / acc_avg / 1e9
     accs_avg = time_accept(torch, ops, 20, 3, with_stats=True)
-    gemm_verify = gemm_summary(time_gemms(torch, ops, target, BATCH * (K + 1)), CFG["n_layers"], MFMA_PEAK_TFLOPS)
+    gemm_verify = gemm_summary(time_gemms(torch, ops, target, BATCH * (K + 1)), CFG["n_layers"] - draft.cfg.n_layers,
+                               MFMA_PEAK_TFLOPS)
     gemm_draft = gemm_summary(time_gemms(torch, ops, draft, BATCH), draft.cfg.n_layers, MFMA_PEAK_TFLOPS)
 
     result = {
@@ -647,7 +677,9 @@ def main():
         "prefill": prefill,
         "verify_pass": main_run["phases"],
         "t1_variant": t1,
-        # MFMA utilisation of the dense GEMMs (bf16 dense peak 2.5 PFLOP/s), event-timed after the rounds
+        # MFMA utilisation of the GEMM kernels (bf16 dense peak 2.5 PFLOP/s), each shape run as the round
+        # runs it (split-K partials, the SwiGLU and statistics epilogues) back to back over the layers'
+        # weights, event-timed after the rounds
         "gemm_verify_m448": gemm_verify,
         "gemm_draft_m64": gemm_draft,
     }
