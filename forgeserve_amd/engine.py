@@ -229,11 +229,11 @@ class Engine:
         res = spec_round(self.model, self.draft, self.pool, self.pool_d, tokens, [r.blocks for r in batch],
                          [r.blocks_d for r in batch], k_eff, temps, draws, graphs=self.graphs)
         self.stats["rounds"] += 1
-        for r, req in enumerate(batch):
-            a = int(res[r, 0])
+        for r, (req, row) in enumerate(zip(batch, res.tolist())):
+            a = row[0]
             self.stats["proposed"] += k_eff[r]
             self.stats["accepted"] += a
-            for token in res[r, 1: a + 2].tolist():
+            for token in row[1: a + 2]:
                 self._push(req, token)
                 if req.finished:
                     break
