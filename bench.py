@@ -101,7 +101,8 @@ def engine_1b(args):
     g = torch.Generator().manual_seed(args.seed + 1)
     reqs = [(torch.randint(0, cfg.vocab_size, (int(torch.randint(128, 1025, (1,), generator=g)),), generator=g).tolist(),
              int(torch.randint(64, 257, (1,), generator=g))) for _ in range(48)]
-    eng = fa.Engine(target, num_blocks=600, block_size=16, max_batch=16, seed=args.seed, draft=draft, k=4)
+    eng = fa.Engine(target, num_blocks=600, block_size=16, max_batch=16, seed=args.seed, draft=draft, k=4,
+                    key_layout="groups")
     for p, n in reqs:
         eng.add_request(p, n, temperature=0.7)
     torch.cuda.synchronize()
@@ -113,7 +114,7 @@ def engine_1b(args):
     assert all(len(out[i]) == n for i, (_, n) in enumerate(reqs))
     print(json.dumps({"workload": "1B-shape continuous batching: 16L d2048 32/8 heads hd64 ffn8192 V32000 bf16, "
                                   "2-layer early-exit draft, Engine max_batch 16, k=4, T=0.7, 48 requests, "
-                                  "prompts U[128,1024], max_new U[64,256], 600 blocks of 16",
+                                  "prompts U[128,1024], max_new U[64,256], 600 blocks of 16 (keys in 8-dim groups)",
                       "generated_tokens": toks, "seconds": round(el, 3), "tok_per_s": round(toks / el, 1),
                       "engine_steps": eng.steps, "rounds": eng.stats["rounds"], "preemptions": eng.preemptions,
                       "peak_running": eng.peak_running, "peak_blocks": eng.peak_blocks,
@@ -373,7 +374,8 @@ def gemm_summary(times, layers, peak_tflops):
 def attention_inputs(torch, fa, seed=0):
     """Verify-attention inputs at the benchmark shape: contexts U[2048,8192] (the round benchmark's
     seed), the k+1 = 7 query positions at the end of each context, block tables a random permutation
-    of the pool, N(0,1) bf16 queries, keys and values."""
+    of the pool, N(0,1) bf16 queries, keys and values; keys in 8-dim groups, as the rounds' pools hold
+    them."""
     g = torch.Generator().manual_seed(seed)
     ctxs = torch.randint(CTX_LO, CTX_HI + 1, (BATCH,), generator=g).tolist()
     nb = [-(-c // BLOCK) for c in ctxs]
@@ -386,7 +388,7 @@ def attention_inputs(torch, fa, seed=0):
         at += n
     cfg = fa.ModelConfig(vocab_size=8, d_model=CFG["n_heads"] * 128, n_layers=1, n_heads=CFG["n_heads"],
                          n_kv_heads=CFG["n_kv_heads"], max_seq_len=16)
-    pool = fa.PagedKVPool(cfg, n_pool, BLOCK, dtype=torch.bfloat16, device="cuda")
+    pool = fa.PagedKVPool(cfg, n_pool, BLOCK, dtype=torch.bfloat16, device="cuda", key_layout="groups")
     pool.k_store.normal_()
     pool.v_store.normal_()
     q = torch.randn(BATCH, K + 1, CFG["n_heads"], 128, device="cuda").bfloat16()
@@ -534,7 +536,7 @@ def kernel_mode(args):
         g = torch.Generator(device="cuda").manual_seed(args.seed)
         cfg = fa.ModelConfig(vocab_size=8, d_model=h * d, n_layers=1, n_heads=h, n_kv_heads=hkv, max_seq_len=16)
         nb = -(-L // BLOCK)
-        pool = fa.PagedKVPool(cfg, n_seq * nb + 8, BLOCK, dtype=torch.bfloat16, device="cuda")
+        pool = fa.PagedKVPool(cfg, n_seq * nb + 8, BLOCK, dtype=torch.bfloat16, device="cuda", key_layout="groups")
         pool.k_store.normal_(generator=g)
         pool.v_store.normal_(generator=g)
         perm = torch.randperm(n_seq * nb, generator=torch.Generator().manual_seed(args.seed))

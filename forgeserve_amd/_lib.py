@@ -26,7 +26,7 @@ class KVLayout(ctypes.Structure):
         ("k_block", c_i64), ("k_head", c_i64), ("k_slot", c_i64), ("k_dim", c_i64),
         ("v_block", c_i64), ("v_head", c_i64), ("v_slot", c_i64), ("v_dim", c_i64),
         ("block_size", c_i32), ("n_kv_heads", c_i32), ("head_dim", c_i32), ("dtype", c_i32),
-        ("num_blocks", c_i64),
+        ("num_blocks", c_i64), ("k_group", c_i64),
     ]
 
 

@@ -37,4 +37,4 @@ int launch_status(const char* what) {
 }  // namespace fs
 
 extern "C" const char* fs_last_error(void) { return g_error; }
-extern "C" int fs_abi_version(void) { return 2; }
+extern "C" int fs_abi_version(void) { return 3; }

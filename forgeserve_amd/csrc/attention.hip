@@ -443,6 +443,9 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
   const u16* vpool = reinterpret_cast<const u16*>(P.kv.v);
   const int64_t k_head_off = (int64_t)hkv * P.kv.k_head;
   const int64_t v_head_off = (int64_t)hkv * P.kv.v_head;
+  // key (slot, dims 8c .. 8c+7) at slot * k_slot + c * kgs: slot-major (k_slot = D, kgs = 8) or grouped
+  // (k_slot = 8, kgs = 8 * block_size: one load of a tile's 32 dims is a contiguous 1 KB)
+  const int64_t k_slot = P.kv.k_slot, kgs = key_group_stride(P.kv);
 
   // Three tile buffers in registers: while tile i is consumed, tiles i+1 and i+2 are in flight.
   // Every load is unconditional (a prefetch past the end re-reads the last tile, an unmapped block
@@ -463,10 +466,10 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
     const int phys = block_of(ic);
     const int64_t pb = phys >= 0 ? phys : 0;
     const int slot0 = j0 - (j0 / BS) * BS;
-    const u16* kt_ = kpool + pb * P.kv.k_block + k_head_off + (int64_t)(slot0 + l16) * D;
+    const u16* kt_ = kpool + pb * P.kv.k_block + k_head_off + (int64_t)(slot0 + l16) * k_slot + g * kgs;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)   // read once per launch: nontemporal
-      kd[ks] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(kt_ + 32 * ks + 8 * g));
+      kd[ks] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(kt_ + 4 * ks * kgs));
     const u16* vt_ = vpool + pb * P.kv.v_block + v_head_off + slot0 + 4 * g;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -730,16 +733,22 @@ attn_prefill_kernel(AttnParams P) {
 
   // This wave copies part p = w % CPT of every tile it copies (keys for p < CPT/2, else values).
   // LDS layouts (16-byte slots; 16 consecutive slots are read without bank conflicts):
-  //  * keys: row r's 16-byte chunk c at slot r * CPR + (c ^ f(r)), f(r) = r & 15 for 16 chunks per
-  //    row, (r >> 1) & 7 for 8, so the 16 rows of an MFMA operand read 16 different slots mod 16;
+  //  * slot-major keys: row r's 16-byte chunk c at slot r * CPR + (c ^ f(r)), f(r) = r & 15 for 16
+  //    chunks per row, (r >> 1) & 7 for 8, so the 16 rows of an MFMA operand read 16 different slots
+  //    mod 16; grouped keys: chunk c of row r at slot 16 * c + r, the pool's own order (each copy is
+  //    then one contiguous 1 KB of the pool, and an operand's 16 rows are 16 consecutive slots);
   //  * values: dim d's keys 8h .. 8h+7 at slot 2d + (h ^ ((d >> 3) & 1)), so dims d and d + 8 of an
   //    operand read different slots mod 16.
   const int p = w % CPT;
   const bool kpart = p < CPT / 2;
+  const bool kgrp = P.kv.k_group != 0;
+  const int64_t kgs = key_group_stride(P.kv);
   int64_t src_off;
   {
     const int P16 = (kpart ? p : p - CPT / 2) * 64 + lane;
-    if (kpart) {
+    if (kpart && kgrp) {
+      src_off = (int64_t)(P16 & 15) * 8 + (int64_t)(P16 >> 4) * kgs;
+    } else if (kpart) {
       const int row = P16 / CPR, f = CPR == 16 ? (row & 15) : ((row >> 1) & 7);
       const int c = (P16 % CPR) ^ f;
       src_off = (int64_t)row * D + 8 * c;
@@ -751,13 +760,13 @@ attn_prefill_kernel(AttnParams P) {
   const u16* pool = reinterpret_cast<const u16*>(kpart ? P.kv.k : P.kv.v);
   const int64_t blk_stride = kpart ? P.kv.k_block : P.kv.v_block;
   const int64_t lane_off = (int64_t)hkv * (kpart ? P.kv.k_head : P.kv.v_head) + src_off;
-  const int slot_mul = kpart ? D : 1;
+  const int64_t slot_mul = kpart ? P.kv.k_slot : 1;
   const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
   // this lane's operand reads inside a tile (bytes)
   const int fk = CPR == 16 ? (l16 & 15) : ((l16 >> 1) & 7);
   int koff[KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) koff[ks] = (l16 * CPR + ((4 * ks + g) ^ fk)) * 16;
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = (kgrp ? (4 * ks + g) * 16 + l16 : l16 * CPR + ((4 * ks + g) ^ fk)) * 16;
   const int voff = TK + (2 * l16 + ((g >> 1) ^ ((l16 >> 3) & 1))) * 16 + 8 * (g & 1);
 
   // copies walk the tiles PF_TILES at a time; a stage past the last tile copies the last tile again
@@ -903,7 +912,7 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnParams P) {
       if (blk >= 0 && blk < P.kv.num_blocks) {
         const T_* kr = kp + blk * P.kv.k_block + hkv * P.kv.k_head + (int64_t)(j - bi * BS) * P.kv.k_slot;
         float dot = 0.f;
-        for (int d = 0; d < D; ++d) dot = fmaf(qs[d], E::load(kr, (int64_t)d * P.kv.k_dim), dot);
+        for (int d = 0; d < D; ++d) dot = fmaf(qs[d], E::load(kr, key_dim_off(P.kv, d)), dot);
         sv = dot * P.scale_log2;
       }
     }
@@ -1019,7 +1028,10 @@ bool mfma_eligible(const fs_kv_layout& kv, const void* q, int64_t q_sb, int64_t 
   if (kv.dtype != FS_BF16) return false;
   if (kv.head_dim != 64 && kv.head_dim != 128) return false;
   if (kv.block_size % 16 != 0) return false;  // a 16-key tile never straddles two blocks
-  if (kv.k_slot != kv.head_dim || kv.k_dim != 1 || kv.v_slot != 1 || kv.v_dim != kv.block_size) return false;
+  if (kv.k_dim != 1 || kv.v_slot != 1 || kv.v_dim != kv.block_size) return false;
+  const bool slot_major = kv.k_group == 0 && kv.k_slot == kv.head_dim;
+  const bool grouped = kv.k_group == 8 * (int64_t)kv.block_size && kv.k_slot == 8;
+  if (!slot_major && !grouped) return false;
   if (kv.k_block % 8 || kv.k_head % 8 || kv.v_block % 8 || kv.v_head % 8) return false;
   if ((reinterpret_cast<uintptr_t>(kv.k) | reinterpret_cast<uintptr_t>(kv.v) | reinterpret_cast<uintptr_t>(q)) & 15)
     return false;
@@ -1101,6 +1113,8 @@ int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, con
   FS_CHECK_ARG(kv->num_blocks > 0, "paged_attention: num_blocks");
   FS_CHECK_ARG(kv->dtype == FS_F32 || kv->dtype == FS_BF16 || kv->dtype == FS_F16, "paged_attention: dtype %d",
                kv->dtype);
+  FS_CHECK_ARG(kv->k_group == 0 || (kv->k_group > 0 && kv->k_dim == 1 && kv->head_dim % 8 == 0),
+               "paged_attention: grouped keys need k_group > 0, k_dim == 1 and head_dim %% 8 == 0");
   const int64_t need = fs_paged_attention_workspace_size(B, T, n_heads, kv->head_dim, max_blocks, kv->block_size);
   FS_CHECK_ARG(workspace_bytes >= need, "paged_attention: workspace %lld < %lld bytes", (long long)workspace_bytes,
                (long long)need);

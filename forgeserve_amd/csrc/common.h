@@ -14,6 +14,13 @@
 
 #define FS_DEVICE __device__ __forceinline__
 
+// Offset of key dim d within a key (fs_kv_layout: plain k_dim stride, or 8-dim groups k_group apart).
+FS_DEVICE int64_t key_dim_off(const fs_kv_layout& kv, int d) {
+  return kv.k_group ? (int64_t)(d >> 3) * kv.k_group + (d & 7) : (int64_t)d * kv.k_dim;
+}
+// Distance between a key's 8-dim groups when its dims are contiguous within a group (k_dim == 1).
+FS_DEVICE int64_t key_group_stride(const fs_kv_layout& kv) { return kv.k_group ? kv.k_group : 8; }
+
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(short)))) short short4_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float float4_t;

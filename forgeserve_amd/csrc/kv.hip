@@ -2,8 +2,8 @@
 //
 // Reference: paged.py:71-82 (PagedLayerView.update) and model.py:40-45 (apply_rope).
 // Pool layout is described by fs_kv_layout; one (block, kv-head) tile of keys is block_size*head_dim
-// contiguous elements, and values are stored dim-major so the attention kernel reads 16 keys of one
-// dim as one contiguous run.
+// contiguous elements (slot-major, or as 8-dim groups of every slot), and values are stored dim-major
+// so the attention kernel reads 16 keys of one dim as one contiguous run.
 #include "common.h"
 
 namespace {
@@ -54,7 +54,7 @@ FS_DEVICE u32x4_t pack8(const float (&v)[8]) {
 }
 
 // The same as qkv_rope_write_kernel for 16-bit dtypes whose rows split into 16-byte groups (D/2 % 8 == 0,
-// aligned rows, slot-major keys): a thread rotates 8 pairs at once (two 16-byte loads of the halves,
+// aligned rows, each 8-dim group of a key contiguous): a thread rotates 8 pairs at once (two 16-byte loads of the halves,
 // 16-byte loads of cos/sin, 16-byte stores of q and k); values keep the dim-major element stores.
 // Eight consecutive qkv elements as floats: the 16-bit row itself, or (PART) the split-K partials of
 // the QKV projection [splits][rows][cols] added in increasing split order and rounded to DT, exactly the
@@ -165,9 +165,10 @@ __global__ void __launch_bounds__(128) qkv_rope_write_vec_kernel(
       *reinterpret_cast<u32x4_t*>(qo) = pack8<DT>(o1);
       *reinterpret_cast<u32x4_t*>(qo + half) = pack8<DT>(o2);
     } else if (write_ok) {
-      uint16_t* ko = kp + blk * kv.k_block + (int64_t)(head - H) * kv.k_head + slot * kv.k_slot + p0;
-      *reinterpret_cast<u32x4_t*>(ko) = pack8<DT>(o1);
-      *reinterpret_cast<u32x4_t*>(ko + half) = pack8<DT>(o2);
+      const int64_t kgs = key_group_stride(kv);
+      uint16_t* ko = kp + blk * kv.k_block + (int64_t)(head - H) * kv.k_head + slot * kv.k_slot;
+      *reinterpret_cast<u32x4_t*>(ko + (p0 >> 3) * kgs) = pack8<DT>(o1);
+      *reinterpret_cast<u32x4_t*>(ko + ((p0 + half) >> 3) * kgs) = pack8<DT>(o2);
     }
   }
   const int nv = Hkv * D / 8;
@@ -234,8 +235,8 @@ __global__ void __launch_bounds__(256) qkv_rope_write_kernel(
     } else if (write_ok) {
       const int h = head - H;
       const int64_t base = blk * kv.k_block + h * kv.k_head + slot * kv.k_slot;
-      E::store(kp, base + p * kv.k_dim, o1);
-      E::store(kp, base + (p + half) * kv.k_dim, o2);
+      E::store(kp, base + key_dim_off(kv, p), o1);
+      E::store(kp, base + key_dim_off(kv, p + half), o2);
     }
   }
   if (write_ok) {
@@ -268,7 +269,7 @@ __global__ void __launch_bounds__(256) kv_write_kernel(const typename Elem<DT>::
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const int h = i / D, d = i - h * D;
     const int64_t src = (int64_t)b * s_b + (int64_t)h * s_h + (int64_t)t * s_t + d;
-    kp[blk * kv.k_block + h * kv.k_head + slot * kv.k_slot + d * kv.k_dim] = k_new[src];
+    kp[blk * kv.k_block + h * kv.k_head + slot * kv.k_slot + key_dim_off(kv, d)] = k_new[src];
     vp[blk * kv.v_block + h * kv.v_head + slot * kv.v_slot + d * kv.v_dim] = v_new[src];
   }
 }
@@ -295,7 +296,7 @@ __global__ void __launch_bounds__(256) gather_kernel(fs_kv_layout kv, const int3
     const int slot = (int)(j % BS);
     T_ kv_k = T_(0), kv_v = T_(0);
     if (blk >= 0 && blk < kv.num_blocks) {
-      kv_k = kp[blk * kv.k_block + h * kv.k_head + slot * kv.k_slot + d * kv.k_dim];
+      kv_k = kp[blk * kv.k_block + h * kv.k_head + slot * kv.k_slot + key_dim_off(kv, d)];
       kv_v = vp[blk * kv.v_block + h * kv.v_head + slot * kv.v_slot + d * kv.v_dim];
     }
     k_out[i] = kv_k;
@@ -311,6 +312,9 @@ int check_layout(const fs_kv_layout* kv) {
                "kv layout: block_size %d, n_kv_heads %d, head_dim %d", kv->block_size, kv->n_kv_heads,
                kv->head_dim);
   FS_CHECK_ARG(kv->num_blocks > 0, "kv layout: num_blocks %lld", (long long)kv->num_blocks);
+  FS_CHECK_ARG(kv->k_group == 0 || (kv->k_group > 0 && kv->k_dim == 1 && kv->head_dim % 8 == 0),
+               "kv layout: grouped keys need k_group > 0, k_dim == 1 and head_dim %% 8 == 0 (k_group %lld)",
+               (long long)kv->k_group);
   return 0;
 }
 
@@ -339,6 +343,7 @@ int qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   const bool vec = kv->dtype != FS_F32 && (kv->head_dim / 2) % 8 == 0 && kv->head_dim % 2 == 0 &&
                    qkv_stride % 8 == 0 && q_stride % 8 == 0 && kv->k_dim == 1 && kv->k_slot % 8 == 0 &&
+                   kv->k_group % 8 == 0 &&
                    kv->k_head % 8 == 0 && kv->k_block % 8 == 0 && al16(pp.part ? (const void*)pp.part : qkv) &&
                    al16(q_out) && al16(kv->k) && al16(rope_cos) && al16(rope_sin);
   // the vectorised kernel: one thread per 8-element group (q/k rotation groups, then value groups)

@@ -81,11 +81,15 @@ class _KeyedDraws:
 
 
 class Engine:
+    """key_layout: the pools' key storage (`PagedKVPool`): "slots" keeps `pool.k` in the reference's
+    shape; "groups" streams faster in attention, with the same tokens."""
+
     def __init__(self, model: ForgeModel, num_blocks: int, block_size: int = 16, max_batch: int = 8, seed: int = 0,
                  draft: Optional[ForgeModel] = None, k: int = 4, draft_num_blocks: Optional[int] = None,
-                 graphs: bool = True, share_kv: Optional[bool] = None):
+                 graphs: bool = True, share_kv: Optional[bool] = None, key_layout: str = "slots"):
         self.model, self.cfg = model, model.cfg
-        self.pool = PagedKVPool(self.cfg, num_blocks, block_size, tp=model.tp, dtype=model.dtype, device=model.device)
+        self.pool = PagedKVPool(self.cfg, num_blocks, block_size, tp=model.tp, dtype=model.dtype, device=model.device,
+                                key_layout=key_layout)
         self.max_batch = max_batch
         self.generator = torch.Generator().manual_seed(seed)
         self.waiting: Deque[Request] = deque()
@@ -110,7 +114,8 @@ class Engine:
                 raise ValueError("share_kv needs an early-exit draft of the model (early_exit_draft)")
             self.shared = bool(n_shared) if share_kv is None else bool(share_kv)
             self.pool_d = self.pool if self.shared else PagedKVPool(
-                draft.cfg, draft_num_blocks or num_blocks, block_size, dtype=model.dtype, device=model.device)
+                draft.cfg, draft_num_blocks or num_blocks, block_size, dtype=model.dtype, device=model.device,
+                key_layout=key_layout)
             self.limit = min(self.cfg.max_seq_len, draft.cfg.max_seq_len)
 
     # ---- public API ---------------------------------------------------------------------------------

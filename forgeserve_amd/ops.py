@@ -60,11 +60,20 @@ def _rows(t: torch.Tensor) -> Tuple[int, int]:
 # KV pool layout
 # ------------------------------------------------------------------------------------------------
 def kv_layout(k: torch.Tensor, v: torch.Tensor) -> KVLayout:
-    """Layout of one layer: k, v are (num_blocks, n_kv_heads, block_size, head_dim) views (any strides)."""
-    if k.shape != v.shape or k.dim() != 4 or k.dtype != v.dtype:
+    """Layout of one layer: v is a (num_blocks, n_kv_heads, block_size, head_dim) view (any strides); k
+    is the same, or (num_blocks, n_kv_heads, block_size, head_dim // 8, 8) with unit stride inside a
+    group for keys stored as 8-dim groups (fs_kv_layout.k_group)."""
+    if k.dim() == 5 and k.shape[-1] == 8 and k.stride(-1) == 1:
+        kb, kh, ks, kg, _ = k.stride()
+        k_strides, k_group, kshape = (kb, kh, ks, 1), kg, (*k.shape[:3], 8 * k.shape[3])
+    elif k.dim() == 4:
+        k_strides, k_group, kshape = k.stride(), 0, tuple(k.shape)
+    else:
+        raise ValueError(f"k pool view must be 4-D or grouped 5-D (..., head_dim // 8, 8): {tuple(k.shape)}")
+    if kshape != tuple(v.shape) or v.dim() != 4 or k.dtype != v.dtype:
         raise ValueError(f"k/v pool views must match: {tuple(k.shape)} vs {tuple(v.shape)}")
-    nb, h, bs, d = k.shape
-    return KVLayout(k.data_ptr(), v.data_ptr(), *k.stride(), *v.stride(), bs, h, d, _dt(k), nb)
+    nb, h, bs, d = v.shape
+    return KVLayout(k.data_ptr(), v.data_ptr(), *k_strides, *v.stride(), bs, h, d, _dt(k), nb, k_group)
 
 
 # ------------------------------------------------------------------------------------------------

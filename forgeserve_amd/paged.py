@@ -8,6 +8,14 @@ tile of keys is block_size*head_dim contiguous elements (4 KB at 16 x 128 bf16),
 block for one dim are block_size contiguous elements: the attention kernel streams both with 16-byte
 and 8-byte loads and never gathers.
 
+`key_layout="groups"` stores each (block, kv-head) tile of keys as head_dim/8 groups of 8 dims, each
+group holding every slot's 8 dims back to back (n_layers, num_blocks, n_kv_heads, head_dim/8,
+block_size, 8). Each 16-byte-per-lane load of a key tile is then one contiguous 1 KB instead of
+sixteen 64-byte pieces, which the attention kernels stream faster; the values, the arithmetic and
+every result are the same.
+`pool.k[layer]` is then a (num_blocks, n_kv_heads, block_size, head_dim/8, 8) view
+(`.flatten(-2)` gives the reference's shape, as a copy).
+
 The block allocator and the block tables stay on the host, as in the reference; tables are copied
 to the GPU (int32) once per step and shared by every layer's view.
 """
@@ -130,7 +138,7 @@ class PagedKVPool:
     """The block pool of every layer (paged.py:42-58)."""
 
     def __init__(self, cfg: ModelConfig, num_blocks: int, block_size: int = 16, tp: TPContext = SINGLE,
-                 dtype=torch.float32, device=None):
+                 dtype=torch.float32, device=None, key_layout: str = "slots"):
         if device is None:
             device = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() else "cuda"
         h = cfg.n_kv_heads // tp.size
@@ -140,9 +148,19 @@ class PagedKVPool:
         self.num_blocks = num_blocks
         self.dtype = dtype
         self.device = torch.device(device)
-        self.k_store = torch.zeros((cfg.n_layers, num_blocks, h, block_size, d), dtype=dtype, device=self.device)
+        if key_layout == "slots":
+            self.k_store = torch.zeros((cfg.n_layers, num_blocks, h, block_size, d), dtype=dtype, device=self.device)
+            self.k = [self.k_store[i] for i in range(cfg.n_layers)]
+        elif key_layout == "groups":
+            if d % 8:
+                raise ValueError(f"grouped keys need head_dim % 8 == 0 (head_dim {d})")
+            self.k_store = torch.zeros((cfg.n_layers, num_blocks, h, d // 8, block_size, 8), dtype=dtype,
+                                       device=self.device)
+            self.k = [self.k_store[i].transpose(2, 3) for i in range(cfg.n_layers)]
+        else:
+            raise ValueError(f"key_layout must be 'slots' or 'groups', not {key_layout!r}")
+        self.key_layout = key_layout
         self.v_store = torch.zeros((cfg.n_layers, num_blocks, h, d, block_size), dtype=dtype, device=self.device)
-        self.k = [self.k_store[i] for i in range(cfg.n_layers)]
         self.v = [self.v_store[i].transpose(-1, -2) for i in range(cfg.n_layers)]
         self.allocator = BlockAllocator(num_blocks)
         self._layouts = None

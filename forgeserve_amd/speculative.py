@@ -513,11 +513,14 @@ class SpeculativeBatch:
     target's first blocks, so by default (None) it uses the target's pool for them instead of a pool of
     its own, needs no prefill of its own, and the verify pass continues from the draft's residual
     streams instead of re-running those blocks for the drafted tokens. The tokens are the same either
-    way; False keeps the separate draft pool of the reference (speculative.py:46)."""
+    way; False keeps the separate draft pool of the reference (speculative.py:46).
+
+    key_layout: the pools' key storage (`PagedKVPool`); "groups" (the default here: the pools are
+    internal) streams faster in attention than the reference-shaped "slots", with the same results."""
 
     def __init__(self, target, draft, num_blocks: int, block_size: int = 16, k: int = 4,
                  draft_num_blocks: Optional[int] = None, generator: Optional[torch.Generator] = None,
-                 graphs: bool = True, share_kv: Optional[bool] = None):
+                 graphs: bool = True, share_kv: Optional[bool] = None, key_layout: str = "groups"):
         if target.cfg.vocab_size != draft.cfg.vocab_size:
             raise ValueError("target and draft must share a vocabulary")
         self.target, self.draft, self.k = target, draft, k
@@ -526,9 +529,11 @@ class SpeculativeBatch:
         if share_kv and not shared:
             raise ValueError("share_kv needs an early-exit draft of the target (early_exit_draft)")
         self.shared = bool(shared) if share_kv is None else bool(share_kv)
-        self.pool_t = PagedKVPool(target.cfg, num_blocks, block_size, dtype=self.dtype, device=self.dev)
+        self.pool_t = PagedKVPool(target.cfg, num_blocks, block_size, dtype=self.dtype, device=self.dev,
+                                  key_layout=key_layout)
         self.pool_d = self.pool_t if self.shared else PagedKVPool(draft.cfg, draft_num_blocks or num_blocks,
-                                                                  block_size, dtype=self.dtype, device=self.dev)
+                                                                  block_size, dtype=self.dtype, device=self.dev,
+                                                                  key_layout=key_layout)
         self.block_size = block_size
         self.limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
         self.gen = generator

@@ -34,9 +34,13 @@ extern "C" {
 
 /* Layout of one layer of a paged KV pool.
  * Key element (block, head, slot, dim) lives at k[block*k_block + head*k_head + slot*k_slot + dim*k_dim],
- * value element likewise with the v_* strides. The fast attention path wants
- * k_slot == head_dim, k_dim == 1 (slot-major keys) and v_slot == 1, v_dim == block_size
- * (dim-major values, so a block's 16 keys of one dim are 32 contiguous bytes). */
+ * or, when k_group != 0 (then k_dim == 1 and head_dim % 8 == 0), at
+ * k[block*k_block + head*k_head + slot*k_slot + (dim/8)*k_group + dim%8]: keys stored as 8-dim groups.
+ * Value element likewise with the v_* strides. The fast attention path wants dim-major values
+ * (v_slot == 1, v_dim == block_size: a block's 16 keys of one dim are 32 contiguous bytes) and either
+ * slot-major keys (k_slot == head_dim, k_dim == 1, k_group == 0) or grouped keys (k_slot == 8,
+ * k_group == 8*block_size: a block's 16 keys of one 8-dim group are 256 contiguous bytes, so each
+ * 16-byte-per-lane load of a key tile is one contiguous 1 KB run). */
 typedef struct fs_kv_layout {
   void* k;
   void* v;
@@ -47,6 +51,7 @@ typedef struct fs_kv_layout {
   int32_t head_dim;
   int32_t dtype;
   int64_t num_blocks; /* block ids outside [0, num_blocks) are never dereferenced */
+  int64_t k_group;    /* 0: key dims at dim*k_dim; else the stride between 8-dim groups of a key */
 } fs_kv_layout;
 
 const char* fs_last_error(void);

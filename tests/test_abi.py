@@ -41,7 +41,7 @@ def test_python_binding_covers_the_header(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fs_abi_version() == 2
+    assert lib.fs_abi_version() == 3   # fs_kv_layout gained k_group
 
 
 def test_argument_errors_are_reported_not_launched(lib):
@@ -60,6 +60,12 @@ def test_argument_errors_are_reported_not_launched(lib):
     rc = lib.fs_paged_attention(None, 0, 0, 0, ctypes.byref(lay), None, 0, 1, None, 1, 1, 1, 1.0, None, 0, 0, 0, None,
                                 0, None)
     assert rc == -1 and b"paged_attention" in lib.fs_last_error()
+    # grouped keys need k_dim == 1: refused before anything is launched
+    bad = _lib.KVLayout(1, 1, 4096, 2048, 8, 2, 64, 16, 1, 16, 16, 2, 128, 1, 8, 128)
+    rc = lib.fs_paged_attention(1, 0, 0, 0, ctypes.byref(bad), 1, 1, 1, 1, 1, 1, 2, 1.0, 1, 0, 0, 0, 1, 1 << 30, None)
+    assert rc == -1 and b"grouped keys" in lib.fs_last_error()
+    rc = lib.fs_paged_kv_write(1, 1, 0, 0, 0, 1, 1, 1, 1, 1, 1, ctypes.byref(bad), None)
+    assert rc == -1 and b"grouped keys" in lib.fs_last_error()
 
 
 def test_workspace_sizes_are_positive(lib):

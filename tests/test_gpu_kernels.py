@@ -164,16 +164,22 @@ def test_embedding():
 
 
 # ---- KV write + rotary ----------------------------------------------------------------------------------
+def _keys(pool, layer=0):
+    """A pool layer's keys in the reference's (num_blocks, n_kv_heads, block_size, head_dim) shape."""
+    return pool.k[layer].flatten(-2) if pool.key_layout == "groups" else pool.k[layer]
+
+
+@pytest.mark.parametrize("key_layout", ["slots", "groups"])
 @pytest.mark.parametrize("dtype,d,bs", [(torch.float32, 8, 4), (torch.float32, 32, 16), (torch.bfloat16, 128, 16),
                                         (torch.bfloat16, 64, 16), (torch.bfloat16, 24, 16)])   # 24: element path
-def test_qkv_rope_write(dtype, d, bs):
-    case("qkv_rope_write", dtype, d, bs)
+def test_qkv_rope_write(dtype, d, bs, key_layout):
+    case("qkv_rope_write", dtype, d, bs, key_layout)
     from forgeserve_amd import PagedKVPool, ModelConfig
     h, hkv, b, t = 8, 2, 3, 5
     cfg = ModelConfig(vocab_size=10, d_model=h * d, n_layers=1, n_heads=h, n_kv_heads=hkv, max_seq_len=200)
     s = orc.Shape.of(cfg)
     cos, sin = orc.rope_tables(s)
-    pool = PagedKVPool(cfg, 40, bs, dtype=dtype, device=DEV)
+    pool = PagedKVPool(cfg, 40, bs, dtype=dtype, device=DEV, key_layout=key_layout)
     perm = torch.randperm(40, generator=torch.Generator().manual_seed(5))
     nbk = -(-44 // bs)                       # positions reach 43
     tables = perm[: b * nbk].reshape(b, nbk)
@@ -188,7 +194,7 @@ def test_qkv_rope_write(dtype, d, bs):
     v_ref = x[:, h + hkv:]
     ok = (pos >= 0).reshape(-1)
     assert torch.equal(q[ok], q_ref[ok])
-    kp, vp = pool.k[0].cpu(), pool.v[0].cpu()
+    kp, vp = _keys(pool).cpu(), pool.v[0].cpu()
     for bi in range(b):
         for ti in range(t):
             p = int(pos[bi, ti])
@@ -227,13 +233,13 @@ def _oracle_attention(q, k, v, tables, pos, rep):
     return out.transpose(1, 2)
 
 
-def _run_attention(q, k, v, tables, pos, dtype, bs, pool_layout=True):
+def _run_attention(q, k, v, tables, pos, dtype, bs, key_layout="slots"):
     from forgeserve_amd import PagedKVPool, ModelConfig
     nblocks, hkv, _, d = k.shape
     h = q.shape[2]
     cfg = ModelConfig(vocab_size=8, d_model=h * d, n_layers=1, n_heads=h, n_kv_heads=hkv, max_seq_len=8)
-    pool = PagedKVPool(cfg, nblocks, bs, dtype=dtype, device=DEV)
-    pool.k[0].copy_(k.to(DEV))
+    pool = PagedKVPool(cfg, nblocks, bs, dtype=dtype, device=DEV, key_layout=key_layout)
+    pool.k[0].copy_(k.to(DEV).view(pool.k[0].shape))
     pool.v[0].copy_(v.to(DEV))
     out = ops.paged_attention(q.to(DEV), pool.layout(0), tables.int().to(DEV), pos.int().to(DEV),
                               1.0 / math.sqrt(d))
@@ -343,6 +349,30 @@ def test_attention_prefill_kernel_equals_unit_kernel_bitwise(d, g, bs, lens, sta
         bad = (got != full[i, :n]).any(-1).any(-1).nonzero()
         assert bad.numel() == 0, f"row {i}: {bad.numel()} tokens differ, first {bad[:5].flatten().tolist()}"
         assert torch.count_nonzero(full[i, n:]) == 0   # padding tokens
+
+
+@pytest.mark.parametrize("d,g,bs,t,ctx,dtype", [
+    (128, 4, 16, 7, [2048, 5000, 8190, 8199, 12000], torch.bfloat16),   # verify windows; two chunks + combine
+    (128, 4, 16, 1, [300, 8193, 20000], torch.bfloat16),                 # decode
+    (64, 8, 32, 5, [700, 1500, 33], torch.bfloat16),                     # block size 32, head_dim 64
+    (128, 2, 48, 3, [8400, 100], torch.bfloat16),                        # blocks of 48 keys
+    (128, 4, 16, 600, [600, 1300], torch.bfloat16),                      # prompts: the prefill kernel
+    (64, 4, 32, 300, [300, 9000], torch.bfloat16),                       # prefill kernel, head_dim 64, 2 chunks
+    (32, 4, 16, 5, [9, 40, 300], torch.float32),                         # the generic kernel
+])
+def test_attention_grouped_keys_equal_slot_keys_bitwise(d, g, bs, t, ctx, dtype):
+    """Keys stored as 8-dim groups (key_layout="groups") change only the addresses the kernels read
+    them from: every output equals the slot-major pool's bit for bit (unit, prefill and generic
+    kernels), and the grouped pool holds the same keys."""
+    case("attention grouped keys", d, g, bs, t, ctx, dtype)
+    hkv = 2
+    nblocks = sum(-(-c // bs) for c in ctx) + 5
+    q, k, v, tables, pos = _paged_case(len(ctx), t, hkv * g, hkv, d, bs, ctx, nblocks, dtype, 7 * d + bs + t)
+    a, _ = _run_attention(q, k, v, tables, pos, dtype, bs)
+    b, pool = _run_attention(q, k, v, tables, pos, dtype, bs, key_layout="groups")
+    assert torch.equal(_keys(pool).cpu(), k)
+    bad = (a != b).any(-1).nonzero()
+    assert bad.numel() == 0, f"{bad.shape[0]} (row, token, head) outputs differ, first {bad[:3].tolist()}"
 
 
 def test_attention_padding_rows_are_zero():
@@ -493,7 +523,8 @@ def test_prefill_attention_matches_oracle(d):
 def test_qkv_rope_gemm_equals_gemm_then_rope(b, t, h, hkv, k):
     """The QKV projection reduced inside the rotary + pool write (split-K partials added by the rotary
     kernel) stores the same keys/values and returns the same queries as the projection followed by
-    fs_qkv_rope_write; a padding token (position -1) is neither rotated nor written either way."""
+    fs_qkv_rope_write; a padding token (position -1) is neither rotated nor written either way. A third
+    pool keeps its keys as 8-dim groups and receives the same keys."""
     case("qkv_rope_gemm", b, t, h, hkv, k)
     from forgeserve_amd import PagedKVPool, ModelConfig, _lib
     d, bs = 128, 16
@@ -515,6 +546,10 @@ def test_qkv_rope_gemm_equals_gemm_then_rope(b, t, h, hkv, k):
     assert torch.equal(q_one, q_two)
     assert torch.equal(pools[1].k_store, pools[0].k_store)
     assert torch.equal(pools[1].v_store, pools[0].v_store)
+    grouped = PagedKVPool(cfg, b * nb, bs, dtype=torch.bfloat16, device=DEV, key_layout="groups")
+    q_grp = ops.qkv_rope_gemm(x, w, pos, t, h, cos.to(DEV), sin.to(DEV), tables, grouped.layout(0))
+    assert torch.equal(q_grp, q_two)
+    assert torch.equal(_keys(grouped), pools[0].k[0]) and torch.equal(grouped.v_store, pools[0].v_store)
 
 
 @pytest.mark.parametrize("dtype,d,bs", [(torch.bfloat16, 128, 16), (torch.float32, 32, 4)])

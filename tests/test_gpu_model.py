@@ -67,19 +67,22 @@ def test_paged_forward_matches_reference(small):
     assert _max_abs(torch.cat(got, 1).cpu().numpy(), gold["paged_logits"]) <= 1e-4
 
 
-def test_paged_update_write_then_read_back():
-    """tests/test_paged.py:20-41 of the reference through PagedLayerView.update."""
-    case("paged update")
+@pytest.mark.parametrize("key_layout", ["slots", "groups"])
+def test_paged_update_write_then_read_back(key_layout):
+    """tests/test_paged.py:20-41 of the reference through PagedLayerView.update (keys slot-major, or
+    stored as 8-dim groups: the same values through the reference-shaped reads)."""
+    case("paged update", key_layout)
     cfg = fa.ModelConfig(vocab_size=64, d_model=64, n_layers=3, n_heads=8, n_kv_heads=4, max_seq_len=64)
-    pool = fa.PagedKVPool(cfg, num_blocks=10, block_size=4)
+    pool = fa.PagedKVPool(cfg, num_blocks=10, block_size=4, key_layout=key_layout)
     table = torch.tensor([[7, 2, 9]])
     k = torch.randn(1, 4, 10, 8, device="cuda")
     v = torch.randn_like(k)
     k_all, v_all = pool.views(table, torch.arange(10)[None])[0].update(k, v)
     assert k_all.shape == (1, 4, 12, 8)
     assert torch.equal(k_all[:, :, :10], k) and torch.equal(v_all[:, :, :10], v)
-    assert torch.equal(pool.k[0][2, :, 1], k[0, :, 5]) and torch.equal(pool.v[0][2, :, 1], v[0, :, 5])
-    pool = fa.PagedKVPool(cfg, num_blocks=8, block_size=4)
+    keys = pool.k[0].flatten(-2) if key_layout == "groups" else pool.k[0]
+    assert torch.equal(keys[2, :, 1], k[0, :, 5]) and torch.equal(pool.v[0][2, :, 1], v[0, :, 5])
+    pool = fa.PagedKVPool(cfg, num_blocks=8, block_size=4, key_layout=key_layout)
     k = torch.randn(2, 4, 6, 8, device="cuda")
     k_all, _ = pool.views(torch.tensor([[0, 1], [2, 3]]), torch.arange(6)[None].expand(2, 6))[0].update(k, k.clone())
     assert torch.equal(k_all[:, :, :6], k)
