@@ -135,7 +135,8 @@ class BlockAllocator:
 
 
 class PagedKVPool:
-    """The block pool of every layer (paged.py:42-58)."""
+    """The block pool of every layer (paged.py:42-58). key_layout: "slots" (the reference's key shape,
+    the default) or "groups" (keys as 8-dim groups of every slot; see the module docstring)."""
 
     def __init__(self, cfg: ModelConfig, num_blocks: int, block_size: int = 16, tp: TPContext = SINGLE,
                  dtype=torch.float32, device=None, key_layout: str = "slots"):

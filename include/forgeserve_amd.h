@@ -55,6 +55,7 @@ typedef struct fs_kv_layout {
 } fs_kv_layout;
 
 const char* fs_last_error(void);
+/* 3 since fs_kv_layout gained k_group (a caller built against an older layout struct must be rebuilt). */
 int fs_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------- */
