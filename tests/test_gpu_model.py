@@ -410,14 +410,17 @@ def test_graph_engine_equals_eager_engine(small):
 
 
 # ---- speculative engine (batched speculation inside Engine) ---------------------------------------------
-def test_spec_engine_greedy_matches_the_reference_engine(small):
+@pytest.mark.parametrize("key_layout", ["slots", "groups"])
+def test_spec_engine_greedy_matches_the_reference_engine(small, key_layout):
     """Greedy: the speculative engine emits the reference Engine's tokens exactly, through a pool small
-    enough to force recompute preemptions (engine_runs.json, run greedy_tight)."""
-    case("spec engine greedy")
+    enough to force recompute preemptions (engine_runs.json, run greedy_tight), whichever key layout
+    its pool uses."""
+    case("spec engine greedy", key_layout)
     gold = golden_json("engine_runs.json")
     run = gold["runs"]["greedy_tight"]
     draft = fa.early_exit_draft(small, 1)
-    e = fa.Engine(small, num_blocks=run["num_blocks"], block_size=4, max_batch=5, draft=draft, k=4)
+    e = fa.Engine(small, num_blocks=run["num_blocks"], block_size=4, max_batch=5, draft=draft, k=4,
+                  key_layout=key_layout)
     ids = [e.add_request(p, n) for p, n in gold["requests"]]
     out = e.run()
     assert [out[i] for i in ids] == run["outputs"]
@@ -426,13 +429,14 @@ def test_spec_engine_greedy_matches_the_reference_engine(small):
     assert e.stats["rounds"] > 0 and e.stats["accepted"] <= e.stats["proposed"]
 
 
-def test_spec_engine_bf16_greedy_equals_generate(bf_target):
-    case("spec engine bf16")
+@pytest.mark.parametrize("key_layout", ["slots", "groups"])
+def test_spec_engine_bf16_greedy_equals_generate(bf_target, key_layout):
+    case("spec engine bf16", key_layout)
     draft = fa.early_exit_draft(bf_target, 1)
     g = torch.Generator().manual_seed(11)
     reqs = [(torch.randint(0, 1000, (int(n),), generator=g).tolist(), int(m))
             for n, m in zip(torch.randint(2, 50, (7,), generator=g), torch.randint(3, 30, (7,), generator=g))]
-    e = fa.Engine(bf_target, num_blocks=200, block_size=16, max_batch=4, draft=draft, k=3)
+    e = fa.Engine(bf_target, num_blocks=200, block_size=16, max_batch=4, draft=draft, k=3, key_layout=key_layout)
     ids = [e.add_request(p, m) for p, m in reqs]
     out = e.run()
     for rid, (p, m) in zip(ids, reqs):
