@@ -578,7 +578,7 @@ attn_unit_kernel(AttnParams P) {
   typedef __attribute__((address_space(4))) const AttnItem ConstItem;   // read-only: scalar loads
   ConstItem* ep = (ConstItem*)(uintptr_t)(P.items + e_idx);
   const int b = ep->b, z = ep->z, s = ep->s, qmax = ep->qmax;
-  const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x & 63, l16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform, in a scalar register
   const int row0 = z * QTILE;
   const int nrows = min(QTILE, P.T * P.G - row0);

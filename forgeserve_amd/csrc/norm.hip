@@ -207,7 +207,6 @@ template <int DT>
 __global__ void __launch_bounds__(256) silu_mul_vec_kernel(const uint16_t* __restrict__ gu, int64_t ldgu,
                                                            uint16_t* __restrict__ h, int64_t ldh, int64_t M,
                                                            int64_t F) {
-  typedef Elem<DT> E;
   const int64_t groups = F / 8, total = M * groups;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = i / groups, c = 8 * (i - m * groups);

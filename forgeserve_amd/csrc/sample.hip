@@ -627,7 +627,7 @@ __global__ void __launch_bounds__(THREADS) accept_pair_kernel(AcceptArgs A) {
     A.cmax[2 * o + 1 - set] = bonus ? 0.f : INFINITY;      // rejection: p / E not collected, rescan
     A.ncand[2 * o + 1 - set] = bonus ? 0 : NCAND + 1;
   }
-  if (threadIdx.x < NCAND && threadIdx.x < sh_n[0]) A.cand[(2 * o + set) * NCAND + threadIdx.x] = sh_c[0][threadIdx.x];
+  if ((int)threadIdx.x < NCAND && (int)threadIdx.x < sh_n[0]) A.cand[(2 * o + set) * NCAND + threadIdx.x] = sh_c[0][threadIdx.x];
 }
 
 // launch 4: one wave per sampled sequence draws the extra token and writes the outputs and rollback:
