@@ -41,7 +41,6 @@ Kernel-only modes (one JSON line each, used for the rocprofv3 counter runs):
 
 import argparse
 import json
-import math
 import os
 import sys
 import time

@@ -17,13 +17,12 @@ Two entry points:
 """
 
 from collections import OrderedDict
-from typing import Dict, List, Optional, Sequence, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
 
 from . import ops
-from ._lib import to_device
 from .kv import new_contiguous_cache
 from .model import prefill_packed
 from .paged import BlockList, OutOfBlocks, PagedKVPool
