@@ -484,10 +484,14 @@ def run_rounds(torch, fa, ops, target, draft, args, temperature, timing):
            "proposed": sb.stats["proposed"] - acc0["proposed"], "accepted": sb.stats["accepted"] - acc0["accepted"]}
     if timing:
         out["attn_avg"], out["attn_bytes"] = time_verify_attention(torch, fa, ops, sb, last_lens)
-        past = sum(1 for n in last_lens for t in range(K + 1) if n - 1 + t >= 8192)
-        out["combine_note"] = (f"{past} of {len(last_lens) * (K + 1)} query positions of the measured round "
-                               f"reach past key 8191, so attn_combine_kernel also runs" if past else
-                               "every query of the measured round sees one chunk, so no combine launch")
+        from forgeserve_amd import _lib
+
+        split = int(_lib.load().fs_paged_attention_split())
+        past = sum(1 for n in last_lens for t in range(K + 1) if n - 1 + t >= split)
+        out["combine_note"] = (f"{split}-key chunks; {past} of {len(last_lens) * (K + 1)} query positions of the "
+                               f"measured round reach past key {split - 1}, so attn_combine_kernel also runs"
+                               if past else f"{split}-key chunks; every query of the measured round sees one "
+                               "chunk, so no combine launch")
         out["phases"] = phase_times(torch, sb)
     del sb
     torch.cuda.empty_cache()
@@ -666,7 +670,7 @@ def main():
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic("paged_attention_verify_8b.md"),
                      "kernel": "paged_attention verify: attn_unit_kernel<128,16>, one call per layer, after one "
-                               "attn_plan_kernel per pass (8192-key chunks); " + main_run["combine_note"],
+                               "attn_plan_kernel per pass; " + main_run["combine_note"],
                      "avg_launch_us": round(attn_avg * 1e6, 2),
                      "algorithmic_bytes_per_launch": int(attn_traffic)},
         "accept_kernel": {"avg_us": round(acc_avg * 1e6, 2), "achieved_GBs": round(acc_gbs, 1),

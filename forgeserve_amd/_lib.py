@@ -54,6 +54,7 @@ SIGNATURES = {
                                                      c_p, c_p, c_i32, c_i32, c_i32, c_f32, c_p, c_i64, c_i64, c_p,
                                                      c_i64, c_p]),
     "fs_paged_attention_workspace_size": (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "fs_paged_attention_split": (c_i32, []),
     "fs_gemm": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i32, c_p, c_i64,
                         c_p]),
     "fs_gemm_workspace_size": (c_i64, [c_i64, c_i64, c_i64, c_i32]),

@@ -5,7 +5,8 @@
 // key_pos <= query_pos mask, scaled_dot_product_attention with scale 1/sqrt(D)).
 //
 // Work split (both kernels): the keys of a row are cut into fixed chunks of `split` absolute positions
-// (512 unless FS_ATTN_SPLIT says otherwise; fixed for the life of the process); chunk s covers keys
+// (512 for the generic kernel, FS_ATTN_SPLIT (default 16384) for the MFMA kernels; fixed for the life
+// of the process); chunk s covers keys
 // [s*split, (s+1)*split). Each workgroup produces the softmax partial
 // (running max m, sum l, unnormalised output acc) of its chunk, and attn_combine merges the chunks of
 // a query in increasing chunk order. A query at position p only ever reads the chunks that hold
@@ -132,7 +133,8 @@ FS_DEVICE int tile_chunks(const AttnParams& P, int qmax) {
 }
 
 constexpr int UNIT_WAVES = 8;                  // waves per unit workgroup
-constexpr int MAX_SPLIT = 64 * 16 * UNIT_WAVES;   // keys per chunk, at most: a wave's tiles fit one wavefront
+constexpr int MAX_SPLIT = 2 * 64 * 16 * UNIT_WAVES;   // keys per chunk, at most: a wave's tiles fit two
+                                                       // table entries per lane
 
 // One workgroup lists every item: first the chunks that lie wholly below their tile's furthest
 // query (the full chunks), tile by tile, then the last chunk of each tile, longest first. Workgroups
@@ -426,16 +428,20 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, g = lane >> 4;
   const int ntiles = (kend - kbeg + 15) >> 4;
-  const int nt_w = ntiles > w ? (ntiles - w + UNIT_WAVES - 1) / UNIT_WAVES : 0;   // <= 64 tiles
+  const int nt_w = ntiles > w ? (ntiles - w + UNIT_WAVES - 1) / UNIT_WAVES : 0;   // <= 128 tiles
   const bool two = nrows > 16;
   const int BS = BSZ ? BSZ : P.kv.block_size;
   const int64_t v_dim = BSZ ? BSZ : P.kv.v_dim;   // == block_size (dim-major values)
 
-  // lane i: raw table entry of the block holding this wave's i-th tile (-1 past the table)
-  int my_phys = -1;
-  if (lane < nt_w) {
-    const int blk = (kbeg + 16 * (w + UNIT_WAVES * lane)) / BS;
-    if (blk < P.max_blocks) my_phys = P.table[(int64_t)b * P.table_stride + blk];
+  // lane i: raw table entries of the blocks holding this wave's tiles i and 64 + i (-1 past the table)
+  int my_phys[2] = {-1, -1};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int i = 64 * h + lane;
+    if (i < nt_w) {
+      const int blk = (kbeg + 16 * (w + UNIT_WAVES * i)) / BS;
+      if (blk < P.max_blocks) my_phys[h] = P.table[(int64_t)b * P.table_stride + blk];
+    }
   }
 
   typedef uint16_t u16;
@@ -455,8 +461,8 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
   short4_t vb0[MT], vb1[MT], vb2[MT];
 
   auto key0 = [&](int i) { return kbeg + 16 * (w + UNIT_WAVES * i); };
-  auto block_of = [&](int i) {   // physical block of the wave's i-th tile, -1 when unmapped
-    const int v = __builtin_amdgcn_readlane(my_phys, i);
+  auto block_of = [&](int i) {   // physical block of the wave's i-th tile, -1 when unmapped (i uniform)
+    const int v = __builtin_amdgcn_readlane(i < 64 ? my_phys[0] : my_phys[1], i & 63);
     return (v >= 0 && v < P.kv.num_blocks) ? v : -1;
   };
 
@@ -1039,16 +1045,18 @@ bool mfma_eligible(const fs_kv_layout& kv, const void* q, int64_t q_sb, int64_t 
   return true;
 }
 
-// Keys per chunk. The generic kernel uses 512. The MFMA path uses FS_ATTN_SPLIT (default 8192; a
-// multiple of 64 in [256, MAX_SPLIT]), read once: it must stay fixed for the life of the process, since
-// the chunk boundaries decide the rounding of every output.
+// Keys per chunk. The generic kernel uses 512. The MFMA path uses FS_ATTN_SPLIT (default 16384 =
+// MAX_SPLIT; a multiple of 64 in [256, MAX_SPLIT]), read once: it must stay fixed for the life of the
+// process, since the chunk boundaries decide the rounding of every output. A large chunk keeps batched
+// rows of up to 16K keys in one workgroup per KV head (no partials, no combine); few rows of much
+// longer contexts spread over more workgroups with a smaller one.
 constexpr int GENERIC_SPLIT = 512;
 
 int attn_split() {
   static const int split = [] {
     const char* e = getenv("FS_ATTN_SPLIT");
-    int v = e ? atoi(e) : 8192;
-    if (v < 256 || v > MAX_SPLIT || v % 64) v = 8192;
+    int v = e ? atoi(e) : MAX_SPLIT;
+    if (v < 256 || v > MAX_SPLIT || v % 64) v = MAX_SPLIT;
     return v;
   }();
   return split;
@@ -1068,6 +1076,8 @@ int64_t max_items(int32_t B, int32_t T, int32_t n_heads, int32_t max_blocks, int
 int min_split() { return attn_split() < GENERIC_SPLIT ? attn_split() : GENERIC_SPLIT; }
 
 }  // namespace
+
+extern "C" int32_t fs_paged_attention_split(void) { return attn_split(); }
 
 extern "C" int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32_t n_heads, int32_t head_dim,
                                                      int32_t max_blocks, int32_t block_size) {

@@ -134,6 +134,12 @@ int fs_paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, 
  * Each query's result is bit-identical to fs_paged_attention's for the same query, keys and position.
  * Replaces model.py:70-76 over paged.py:80-81 for a prefill (T = prompt length, engine.py:80-95) of
  * several prompts at once. workspace: fs_paged_attention_workspace_size(S, T, ...). */
+/* Keys per chunk of the MFMA attention path (FS_ATTN_SPLIT, default 16384), fixed for the life of the
+ * process: a query at position p reads chunks 0 .. p / split and, past the first, its output is merged
+ * from per-chunk partials. No counterpart in the reference (it gathers every key); for callers and
+ * benchmarks that report how a workload is split. */
+int32_t fs_paged_attention_split(void);
+
 int fs_paged_attention_varlen(const void* q, int64_t q_st, int64_t q_sh, const fs_kv_layout* kv,
                               const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
                               const int32_t* positions, const int32_t* cu_seqlens, int32_t S, int32_t T,

@@ -71,6 +71,7 @@ def test_argument_errors_are_reported_not_launched(lib):
 def test_workspace_sizes_are_positive(lib):
     assert lib.fs_paged_attention_workspace_size(64, 7, 32, 128, 600, 16) > 64 * 7 * 32 * 128 * 4
     assert lib.fs_spec_accept_workspace_size(64, 6, 128256) > 0
+    assert lib.fs_paged_attention_split() == int(os.environ.get("FS_ATTN_SPLIT", 16384))
     assert lib.fs_sampling_workspace_size(64, 128256) > 0
     assert lib.fs_paged_attention_workspace_size(0, 1, 1, 1, 1, 1) == 0
     # split-K partials: a function of (N, K) only, sized for M rows

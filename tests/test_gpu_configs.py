@@ -91,14 +91,15 @@ def _oracle_attention_rows(q, pool, tables, pos, ctx):
     return torch.cat(outs)
 
 
-@pytest.mark.parametrize("which", ["c5", "past_8192"])
+@pytest.mark.parametrize("which", ["c5", "past_chunk"])
 def test_attention_c5_shape(which):
     """B = 64, T = 7, 32/8 heads, head_dim 128, bf16, contexts U[2048, 8192] (seed 0), 16-token blocks
-    in random pool order; and 8 rows whose query windows reach or cross key position 8192."""
+    in random pool order; and 8 rows whose query windows reach or cross key positions 8192 and 16384
+    (the attention's key chunks are 16384 positions)."""
     if which == "c5":
         ctx = torch.randint(2048, 8193, (64,), generator=torch.Generator().manual_seed(0)).tolist()
     else:
-        ctx = [8190, 8192, 8193, 8196, 8199, 12000, 16390, 2048]
+        ctx = [8190, 8199, 16380, 16384, 16385, 16390, 20000, 2048]
     case("attention", which, len(ctx), "rows, max context", max(ctx))
     q, pool, tables, pos = _attention_case(ctx, 7, 0)
     out = ops.paged_attention(q, pool.layout(0), tables.to(DEV), pos.to(DEV), 128 ** -0.5).float().cpu()

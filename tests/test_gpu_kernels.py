@@ -309,11 +309,11 @@ def test_attention_prefill_equals_decode_bitwise(d):
 
 
 @pytest.mark.parametrize("d,g,bs,lens,starts,qscale", [
-    (128, 4, 16, [9000], [0], 1.0),              # the prompt crosses key 8192: two chunks and the combine
+    (128, 4, 16, [17000], [0], 1.0),             # the prompt crosses key 16384: two chunks and the combine
     (128, 4, 32, [700, 1500], [0, 300], 1.0),    # block size 32; row 0 has 800 padding tokens
     (64, 8, 16, [513, 90], [40, 0], 1.0),
     (128, 1, 16, [260], [3], 1.0),               # one head per KV head: 9 query tiles
-    (128, 2, 48, [8400], [0], 1.0),              # blocks of 48 keys: the 8192-key chunk starts mid-block
+    (128, 2, 48, [16500], [0], 1.0),             # blocks of 48 keys: the second chunk starts mid-block
     (128, 4, 16, [1100, 333], [0, 64], 12.0),    # scores spread over ~2^30: references move often
     (64, 4, 16, [700], [5], 12.0),
 ])
@@ -352,12 +352,12 @@ def test_attention_prefill_kernel_equals_unit_kernel_bitwise(d, g, bs, lens, sta
 
 
 @pytest.mark.parametrize("d,g,bs,t,ctx,dtype", [
-    (128, 4, 16, 7, [2048, 5000, 8190, 8199, 12000], torch.bfloat16),   # verify windows; two chunks + combine
-    (128, 4, 16, 1, [300, 8193, 20000], torch.bfloat16),                 # decode
+    (128, 4, 16, 7, [2048, 5000, 16380, 16389, 20000], torch.bfloat16),  # verify windows; two chunks + combine
+    (128, 4, 16, 1, [300, 16385, 34000], torch.bfloat16),                # decode, 2 and 3 chunks
     (64, 8, 32, 5, [700, 1500, 33], torch.bfloat16),                     # block size 32, head_dim 64
-    (128, 2, 48, 3, [8400, 100], torch.bfloat16),                        # blocks of 48 keys
+    (128, 2, 48, 3, [16500, 100], torch.bfloat16),                       # blocks of 48 keys, 2 chunks
     (128, 4, 16, 600, [600, 1300], torch.bfloat16),                      # prompts: the prefill kernel
-    (64, 4, 32, 300, [300, 9000], torch.bfloat16),                       # prefill kernel, head_dim 64, 2 chunks
+    (64, 4, 32, 300, [300, 17000], torch.bfloat16),                      # prefill kernel, head_dim 64, 2 chunks
     (32, 4, 16, 5, [9, 40, 300], torch.float32),                         # the generic kernel
 ])
 def test_attention_grouped_keys_equal_slot_keys_bitwise(d, g, bs, t, ctx, dtype):
@@ -386,14 +386,14 @@ def test_attention_padding_rows_are_zero():
     assert torch.count_nonzero(out[1, :2]) > 0
 
 
-LONG_CTX = [8, 8191, 8192, 8193, 8199, 20000]   # one, two and three 8192-key chunks
+LONG_CTX = [8, 8192, 16383, 16384, 16385, 16391, 33000]   # one, two and three 16384-key chunks
 
 
 def test_attention_long_contexts():
     """Contexts that span several key chunks: queries past the first chunk are merged from per-chunk
     partials, the others are finished by their chunk's workgroup."""
     case("attention long", LONG_CTX)
-    q, k, v, tables, pos = _paged_case(len(LONG_CTX), 7, 8, 2, 128, 16, LONG_CTX, 3400, torch.bfloat16, 12)
+    q, k, v, tables, pos = _paged_case(len(LONG_CTX), 7, 8, 2, 128, 16, LONG_CTX, 6700, torch.bfloat16, 12)
     out, _ = _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
     ref = _oracle_attention(q, k, v, tables, pos, 4)
     assert rel_err(out.cpu().float(), ref) < 2e-2
@@ -402,7 +402,7 @@ def test_attention_long_contexts():
 def test_attention_long_verify_equals_decode_bitwise():
     case("attention long invariance", LONG_CTX)
     t = 7
-    q, k, v, tables, pos = _paged_case(len(LONG_CTX), t, 8, 2, 128, 16, LONG_CTX, 3400, torch.bfloat16, 13)
+    q, k, v, tables, pos = _paged_case(len(LONG_CTX), t, 8, 2, 128, 16, LONG_CTX, 6700, torch.bfloat16, 13)
     full, pool = _run_attention(q, k, v, tables, pos, torch.bfloat16, 16)
     lay = pool.layout(0)
     tab = tables.int().to(DEV)
@@ -419,7 +419,7 @@ def test_attention_plan_reuse_equals_fresh_plan():
     case("attention plan reuse")
     from forgeserve_amd import PagedKVPool, ModelConfig, _lib
     h, hkv, d, bs, t = 8, 2, 128, 16, 7
-    ctx = [300, 9000, 40, 2100]   # 9000 keys span two chunks: the combine path runs too
+    ctx = [300, 17000, 40, 2100]   # 17000 keys span two chunks: the combine path runs too
     nblocks = sum(-(-c // bs) for c in ctx) + 2
     q, k, v, tables, pos = _paged_case(len(ctx), t, h, hkv, d, bs, ctx, nblocks, torch.bfloat16, 77)
     cfg = ModelConfig(vocab_size=8, d_model=h * d, n_layers=3, n_heads=h, n_kv_heads=hkv, max_seq_len=16)
