@@ -59,6 +59,7 @@ SIGNATURES = {
                         c_p]),
     "fs_gemm_workspace_size": (c_i64, [c_i64, c_i64, c_i64, c_i32]),
     "fs_gemm_splits": (c_i32, [c_i64, c_i64, c_i32]),
+    "fs_gemm_serial": (c_i32, [c_i64, c_i64, c_i64, c_i32]),
     "fs_gemm_partials": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i32, c_p, c_i64, c_p]),
     "fs_splitk_add_rmsnorm": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_f32, c_i32,
                                       c_p]),

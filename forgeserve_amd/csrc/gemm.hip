@@ -177,13 +177,18 @@ struct RowStatsOut {
 // SWIGLU: W holds [gate; up] (N/2 rows each) and the tile's output columns are interleaved, column
 // 2j = gate row j and 2j + 1 = up row j, so that each lane's four consecutive columns are two (gate, up)
 // pairs; the epilogue stores silu(gate) * up to C[row][j] (model.py:93) instead of the products.
-template <int BM, int BN, int NS, int WGM = 2, int WGN = 2, bool STATS = false, bool PRIO = false, bool SWIGLU = false>
+// SERIAL: the workgroup runs the `serial` K splits of its tile one after the other (gridDim.y == 1):
+// each split's chain starts from zero as a split-K workgroup's does, and its result is added to a
+// running f32 sum in increasing split order, the additions the split-K reduction makes, so the output
+// equals the split-K path's bit for bit with no partials written.
+template <int BM, int BN, int NS, int WGM = 2, int WGN = 2, bool STATS = false, bool PRIO = false, bool SWIGLU = false,
+          bool SERIAL = false>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uint16_t* __restrict__ X, int64_t ldx,
                                                             const uint16_t* __restrict__ W, int64_t ldw,
                                                             uint16_t* __restrict__ C, int64_t ldc,
                                                             const uint16_t* __restrict__ R, int64_t ldr, int64_t M,
                                                             int64_t N, int64_t K, int tiles_m, int ntiles,
-                                                            float* __restrict__ part, RowStatsOut rs) {
+                                                            float* __restrict__ part, RowStatsOut rs, int serial) {
   constexpr int KB = 64;                       // k per stage
   constexpr int ROWB = KB * 2;                 // bytes per stage row (128)
   constexpr int NW = WGM * WGN;                // waves: WGM along M, WGN along N
@@ -258,17 +263,30 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
     }
   };
 
-  float4_t acc[TM][TN];
+  float4_t acc[TM][TN], sum[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  // SERIAL: fold the finished split's chain into the running sum and restart the chain from zero
+  const int nks = SERIAL ? nk / serial : nk;
+  auto fold = [&](bool first) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum[i][j][r] = first ? acc[i][j][r] : sum[i][j][r] + acc[i][j][r];
+        acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+      }
+  };
 
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nk) issue(s);
 
   for (int kt = 0; kt < nk; ++kt) {
+    if (SERIAL && kt > 0 && kt % nks == 0) fold(kt == nks);
     // stages issued after kt and still allowed in flight: min(NS - 2, nk - 1 - kt)
     wait_stages(min(NS - 2, nk - 1 - kt));
     __syncthreads();  // stage kt has landed for every wave; stage kt-1 is no longer being read
@@ -295,6 +313,13 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
         for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], xf[i], acc[i][j], 0, 0, 0);
       if (PRIO) __builtin_amdgcn_s_setprio(0);
     }
+  }
+  if (SERIAL) {   // the last split, then the sum takes the accumulators' place in the epilogue
+    fold(nk == nks);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = sum[i][j];
   }
 
   // acc[i][j]: lane (l16, g) holds C[m = 16i + l16][n = 16j + 4g + r], r = 0..3 (wave-local)
@@ -565,7 +590,7 @@ void launch_lds(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, 
   const dim3 grid((unsigned)(8 * ((nt + 7) / 8)), (unsigned)splits);
 #define FS_LDS_LAUNCH(BM_, BN_, NS_, WGM_, WGN_, PRIO_)                                                       \
   gemm_bf16_lds_kernel<BM_, BN_, NS_, WGM_, WGN_, STATS, PRIO_, SWIGLU><<<grid, 64 * WGM_ * WGN_, 0, s>>>(      \
-      a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part, rs)
+      a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt, part, rs, 1)
   // 64 x 128 with a 3-stage ring (72 KB of LDS): two workgroups share a CU, so one's epilogue (the
   // head's statistics) overlaps the other's weight stream
   if (cf.bm == 64 && cf.bn == 128) FS_LDS_LAUNCH(64, 128, 3, 2, 4, false);
@@ -583,6 +608,25 @@ void launch_lds(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, 
 
 bool lds_ok(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t K) {
   return K % 64 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B);
+}
+
+// A split-K shape whose unsplit 256 x 128 tiles alone fill the GPU twice over (a long prefill) runs its
+// K splits one after the other inside each workgroup: the split-K arithmetic without the f32 partials.
+// Only for splits of at most 2048 k: there the partials' HBM traffic costs more than the narrower tile
+// the running sum forces (measured at M = 32768: the o projection 1.80 -> 1.38 ms, qkv even); with
+// 3584-k splits (the down projection) the 256 x 256 tiles and their partials are faster (3.9 vs 4.6 ms).
+constexpr int kSerialTiles = 512;
+bool serial_for(int64_t M, int64_t N, int64_t K, int splits) {
+  return splits > 1 && K / splits <= 2048 && ((M + 255) / 256) * ((N + 127) / 128) >= kSerialTiles;
+}
+
+void launch_serial(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c, int64_t ldc,
+                   const uint16_t* r, int64_t ldr, int64_t M, int64_t N, int64_t K, int splits, hipStream_t s) {
+  // 256 x 128 tiles, 8 waves of 64 x 64 (the running sum doubles the accumulators), 3-stage ring (144 KB)
+  const int tm = (int)((M + 255) / 256), nt = tm * (int)((N + 127) / 128);
+  gemm_bf16_lds_kernel<256, 128, 3, 4, 2, false, false, false, true>
+      <<<dim3((unsigned)(8 * ((nt + 7) / 8)), 1u), 512, 0, s>>>(a, lda, b, ldb, c, ldc, r, ldr, M, N, K, tm, nt,
+                                                                nullptr, RowStatsOut{}, splits);
 }
 
 }  // namespace
@@ -617,6 +661,11 @@ extern "C" int fs_gemm_row_stats(const void* A, int64_t lda, const void* B, int6
 extern "C" int32_t fs_gemm_splits(int64_t N, int64_t K, int32_t dtype) {
   if (N <= 0 || K <= 0 || dtype != FS_BF16 || N % 4) return 1;
   return split_for(N, K);
+}
+
+extern "C" int32_t fs_gemm_serial(int64_t M, int64_t N, int64_t K, int32_t dtype) {
+  if (M <= 0) return 0;
+  return serial_for(M, N, K, fs_gemm_splits(N, K, dtype)) ? 1 : 0;
 }
 
 extern "C" int fs_gemm_partials(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
@@ -656,7 +705,7 @@ extern "C" int fs_gemm_swiglu(const void* A, int64_t lda, const void* B, int64_t
 extern "C" int64_t fs_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int32_t dtype) {
   if (M <= 0 || N <= 0 || K <= 0 || dtype != FS_BF16) return 0;
   const int s = split_for(N, K);
-  return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
+  return s > 1 && !serial_for(M, N, K, s) ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
 }
 
 extern "C" int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, const void* R,
@@ -673,6 +722,10 @@ extern "C" int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, v
     const uint16_t* a = (const uint16_t*)A;
     const uint16_t* b = (const uint16_t*)B;
     const int splits = N % 4 == 0 ? split_for(N, K) : 1;
+    if (serial_for(M, N, K, splits)) {
+      launch_serial(a, lda, b, ldb, (uint16_t*)C, ldc, (const uint16_t*)R, ldr, M, N, K, splits, s);
+      return fs::launch_status("gemm_bf16_lds_serial");
+    }
     float* part = nullptr;
     if (splits > 1) {
       const int64_t need = (int64_t)splits * M * N * (int64_t)sizeof(float);

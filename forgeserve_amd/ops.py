@@ -107,9 +107,10 @@ def gemm(a: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
 def gemm_add_rmsnorm(a: torch.Tensor, w: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor,
                      eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
     """x = a @ w.T + residual (nn.Linear then the residual add, model.py:105-106) and y = RMSNorm(x)
-    with norm_weight (model.py:29-31): returns (x, y). When the GEMM splits K, the partials are added
-    by the norm kernel itself (no separate reduction pass); otherwise the GEMM adds the residual and
-    the norm runs on its output. The results are the same either way."""
+    with norm_weight (model.py:29-31): returns (x, y). When the GEMM splits K into partials, they are
+    added by the norm kernel itself (no separate reduction pass); otherwise (no split, or a long batch
+    whose workgroups run the splits one after the other) the GEMM adds the residual and the norm runs
+    on its output. The results are the same either way."""
     require_device(a, w, residual, norm_weight)
     m, lda = _rows(a)
     n, ldb = _rows(w)
@@ -117,6 +118,7 @@ def gemm_add_rmsnorm(a: torch.Tensor, w: torch.Tensor, residual: torch.Tensor, n
     lib = _lib.load()
     if (a.dtype in (torch.bfloat16,) and w.dtype == a.dtype and w.shape[1] == k and residual.shape == (m, n)
             and residual.dtype == a.dtype and n % 8 == 0 and n <= 8192 and lib.fs_gemm_splits(n, k, _dt(a)) > 1
+            and not lib.fs_gemm_serial(m, n, k, _dt(a))
             and k % 64 == 0 and lda % 8 == 0 and ldb % 8 == 0 and residual.stride(1) == 1
             and residual.stride(0) % 8 == 0 and norm_weight.is_contiguous() and norm_weight.dtype == a.dtype):
         splits = lib.fs_gemm_splits(n, k, _dt(a))
@@ -279,8 +281,8 @@ def qkv_rope_gemm(h: torch.Tensor, w: torch.Tensor, positions: torch.Tensor, T: 
                   rope_cos: torch.Tensor, rope_sin: torch.Tensor, tables: torch.Tensor, layout: KVLayout,
                   slots: Optional[torch.Tensor] = None) -> torch.Tensor:
     """qkv_rope_write(gemm(h, w), ...): the fused QKV projection (model.py:57-60, 64-66) followed by the
-    rotary + pool write. When the projection splits K, the rotary kernel adds the partials itself (no
-    separate reduction pass); the results are the same either way."""
+    rotary + pool write. When the projection splits K into partials, the rotary kernel adds them itself
+    (no separate reduction pass); the results are the same either way."""
     require_device(h, w, positions, tables)
     m, lda = _rows(h)
     n, ldb = _rows(w)
@@ -289,7 +291,8 @@ def qkv_rope_gemm(h: torch.Tensor, w: torch.Tensor, positions: torch.Tensor, T: 
     d = layout.head_dim
     if (h.dtype == torch.bfloat16 and w.dtype == h.dtype and w.shape[1] == k and layout.dtype == _dt(h)
             and k % 64 == 0 and lda % 8 == 0 and ldb % 8 == 0 and n % 8 == 0 and (d // 2) % 8 == 0
-            and lib.fs_gemm_splits(n, k, _dt(h)) > 1 and positions.dtype == I32 and tables.dtype == I32
+            and lib.fs_gemm_splits(n, k, _dt(h)) > 1 and not lib.fs_gemm_serial(m, n, k, _dt(h))
+            and positions.dtype == I32 and tables.dtype == I32
             and (slots is None or slots.dtype == I32)):
         splits = lib.fs_gemm_splits(n, k, _dt(h))
         ws = _persistent_ws("gemm", splits * m * n * 4, h.device)

@@ -185,6 +185,12 @@ int64_t fs_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int32_t dtype);
 /* How many ways fs_gemm splits K for an (N, K) bf16 product (1: not split). A function of N and K only. */
 int32_t fs_gemm_splits(int64_t N, int64_t K, int32_t dtype);
 
+/* 1 when fs_gemm runs a split shape's K ranges one after the other inside each workgroup (large M:
+ * same arithmetic, same bits, no f32 partials, fs_gemm_workspace_size 0), else 0. Such shapes are
+ * cheaper through fs_gemm than through fs_gemm_partials. Internal tuning, no counterpart in the
+ * reference. */
+int32_t fs_gemm_serial(int64_t M, int64_t N, int64_t K, int32_t dtype);
+
 /* The first half of a split-K fs_gemm: the f32 partial products of each K range, partials[s][M][N]
  * (s = 0 .. fs_gemm_splits(N, K) - 1), each the sum over its K range in increasing k. For consumers
  * that add them themselves (fs_splitk_add_rmsnorm). bf16, K % 64 == 0, N % 4 == 0, only for shapes

@@ -78,3 +78,9 @@ def test_workspace_sizes_are_positive(lib):
     assert lib.fs_gemm_workspace_size(448, 4096, 4096, 1) == 4 * 448 * 4096 * 4
     assert lib.fs_gemm_workspace_size(64, 28672, 4096, 1) == 0
     assert lib.fs_gemm_workspace_size(64, 4096, 4096, 0) == 0
+    # a long batch runs the splits one after the other in each workgroup: no partials
+    assert lib.fs_gemm_serial(448, 4096, 4096, 1) == 0 and lib.fs_gemm_serial(4096, 4096, 4096, 1) == 1
+    assert lib.fs_gemm_workspace_size(4096, 4096, 4096, 1) == 0
+    assert lib.fs_gemm_serial(32768, 28672, 4096, 1) == 0   # not split
+    assert lib.fs_gemm_serial(32768, 4096, 14336, 1) == 0   # 3584-k splits keep their partials
+    assert lib.fs_gemm_serial(4096, 4096, 4096, 0) == 0 and lib.fs_gemm_serial(0, 4096, 4096, 1) == 0

@@ -108,6 +108,37 @@ def test_splitk_add_rmsnorm_equals_gemm_then_norm(m, n, k):
     assert torch.equal(y, ops.add_rmsnorm(x_ref, nw, 1e-5))
 
 
+@pytest.mark.parametrize("m,n,k", [(4133, 4096, 4096), (8192, 4096, 8192), (2600, 6144, 4096)])
+def test_gemm_serial_splits_equal_short_batch_rows(m, n, k):
+    """A long batch whose workgroups run the K splits one after the other (no partials) gives every row
+    bit for bit as a short batch gives it through the partials and their reduction, residual included,
+    and gemm_add_rmsnorm at that length equals its short-batch rows too."""
+    case("gemm serial splits", m, n, k)
+    from forgeserve_amd import _lib
+    lib = _lib.load()
+    assert lib.fs_gemm_splits(n, k, _lib.BF16) > 1 and lib.fs_gemm_serial(m, n, k, _lib.BF16) == 1
+    assert lib.fs_gemm_workspace_size(m, n, k, _lib.BF16) == 0
+    assert lib.fs_gemm_serial(448, n, k, _lib.BF16) == 0   # the short batches below take the partials
+    g = torch.Generator().manual_seed(m + n)
+    a = torch.randn(m, k, generator=g).bfloat16().to(DEV)
+    w = (torch.randn(n, k, generator=g) * 0.03).bfloat16().to(DEV)
+    r = torch.randn(m, n, generator=g).bfloat16().to(DEV)
+    nw = (1 + 0.1 * torch.randn(n, generator=g)).bfloat16().to(DEV)
+    full = ops.gemm(a, w, residual=r)
+    x, y = ops.gemm_add_rmsnorm(a, w, r, nw, 1e-5)
+    assert torch.equal(x, full)
+    for lo in (0, 1000, m - 300):   # the last slice ends in the long batch's ragged last tile
+        hi = min(lo + 448, m)
+        assert torch.equal(ops.gemm(a[lo:hi], w, residual=r[lo:hi]), full[lo:hi])
+        _, ys = ops.gemm_add_rmsnorm(a[lo:hi], w, r[lo:hi], nw, 1e-5)
+        assert torch.equal(y[lo:hi], ys)
+    # and against float32 products on a few rows (bf16 output: half an ulp of the sum plus the rounding
+    # of the product before the residual is added)
+    ref = (a[-64:].float() @ w.float().T)
+    got = ops.gemm(a, w)[-64:].float()
+    assert ((got - ref).abs() <= ref.abs() * 2 ** -8 + 1e-3).all()
+
+
 # ---- row ops ------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_rmsnorm_and_residual(dtype):
