@@ -123,29 +123,44 @@ __global__ void __launch_bounds__(128) qkv_rope_write_vec_kernel(
     int32_t rope_len, const int32_t* __restrict__ table, int64_t table_stride, int32_t max_blocks, fs_kv_layout kv,
     uint16_t* __restrict__ q_out, int64_t q_stride) {
   const int64_t m = blockIdx.x;
+  const int D = kv.head_dim, half = D / 2, Hkv = kv.n_kv_heads;
+  const int ng = half / 8;
+  const int n_groups = (H + Hkv) * ng, nv = Hkv * D / 8;
+  const int64_t row0 = m * qkv_stride;   // the token's first element (of qkv, or of each partial)
+  const int gi = blockIdx.y * blockDim.x + threadIdx.x;
+  // The thread's inputs are loaded first: they depend on nothing the position decides, so they are in
+  // flight while the position, the rotary row and the pool slot are looked up.
+  const bool rot_thread = gi < n_groups, val_thread = !rot_thread && gi < n_groups + nv;
+  const int head = rot_thread ? gi / ng : 0, p0 = rot_thread ? 8 * (gi - head * ng) : 0;
+  const int e0 = val_thread ? 8 * (gi - n_groups) : 0;   // value group: element e0 of the kv heads' values
+  float x1[8], x2[8];
+  u32x4_t w = {0u, 0u, 0u, 0u};
+  if (rot_thread) {
+    load8<DT, PART>(qkv, pp, row0 + (int64_t)head * D + p0, x1);
+    load8<DT, PART>(qkv, pp, row0 + (int64_t)head * D + p0 + half, x2);
+  } else if (val_thread) {
+    const int64_t ve = row0 + (int64_t)(H + Hkv) * D + e0;
+    if (PART != 0) {
+      load8<DT, PART>(qkv, pp, ve, x1);
+      w = pack8<DT>(x1);
+    } else {
+      w = *reinterpret_cast<const u32x4_t*>(qkv + ve);
+    }
+  }
   int b = token_row ? token_row[m] : (int)(m / T);   // the token's table row
   const bool row_ok = token_row == nullptr || (b >= 0 && b < n_rows);
   b = row_ok ? b : 0;
-  const int D = kv.head_dim, half = D / 2, Hkv = kv.n_kv_heads;
   const int pos = row_ok ? positions[m] : -1;
   const bool rot_ok = pos >= 0 && pos < rope_len;
   int64_t blk = 0;
   int slot = 0;
   const int wpos = slots ? slots[m] : pos;
   const bool write_ok = rot_ok && slot_of(wpos, table, table_stride, b, max_blocks, kv, blk, slot);
-  const int64_t row0 = m * qkv_stride;   // the token's first element (of qkv, or of each partial)
   uint16_t* kp = reinterpret_cast<uint16_t*>(kv.k);
   uint16_t* vp = reinterpret_cast<uint16_t*>(kv.v);
-  const int ng = half / 8;
-  const int n_groups = (H + Hkv) * ng;
   const int64_t cs = rot_ok ? (int64_t)pos * half : 0;
-  const int gi = blockIdx.y * blockDim.x + threadIdx.x;
-  if (gi < n_groups) {
-    const int i = gi;
-    const int head = i / ng, p0 = 8 * (i - head * ng);
-    float x1[8], x2[8], c[8], sn[8], o1[8], o2[8];
-    load8<DT, PART>(qkv, pp, row0 + (int64_t)head * D + p0, x1);
-    load8<DT, PART>(qkv, pp, row0 + (int64_t)head * D + p0 + half, x2);
+  if (rot_thread) {
+    float c[8], sn[8], o1[8], o2[8];
     const float4_t c0 = *reinterpret_cast<const float4_t*>(rope_cos + cs + p0);
     const float4_t c1 = *reinterpret_cast<const float4_t*>(rope_cos + cs + p0 + 4);
     const float4_t s0 = *reinterpret_cast<const float4_t*>(rope_sin + cs + p0);
@@ -171,26 +186,13 @@ __global__ void __launch_bounds__(128) qkv_rope_write_vec_kernel(
       *reinterpret_cast<u32x4_t*>(ko + ((p0 + half) >> 3) * kgs) = pack8<DT>(o2);
     }
   }
-  const int nv = Hkv * D / 8;
-  if (write_ok && gi >= n_groups && gi < n_groups + nv) {
-    const int64_t vrow = row0 + (int64_t)(H + Hkv) * D;
-    {
-      const int i = gi - n_groups;
-      const int e0 = 8 * i, h = e0 / D, d0 = e0 - h * D;
-      u32x4_t w;
-      if (PART != 0) {
-        float x[8];
-        load8<DT, PART>(qkv, pp, vrow + e0, x);
-        w = pack8<DT>(x);
-      } else {
-        w = *reinterpret_cast<const u32x4_t*>(qkv + vrow + e0);
-      }
-      uint16_t* vo = vp + blk * kv.v_block + h * kv.v_head + slot * kv.v_slot + d0 * kv.v_dim;
+  if (write_ok && val_thread) {
+    const int h = e0 / D, d0 = e0 - h * D;
+    uint16_t* vo = vp + blk * kv.v_block + h * kv.v_head + slot * kv.v_slot + d0 * kv.v_dim;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vo[(2 * j) * kv.v_dim] = (uint16_t)(w[j] & 0xffffu);
-        vo[(2 * j + 1) * kv.v_dim] = (uint16_t)(w[j] >> 16);
-      }
+    for (int j = 0; j < 4; ++j) {
+      vo[(2 * j) * kv.v_dim] = (uint16_t)(w[j] & 0xffffu);
+      vo[(2 * j + 1) * kv.v_dim] = (uint16_t)(w[j] >> 16);
     }
   }
 }
