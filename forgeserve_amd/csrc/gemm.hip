@@ -206,12 +206,18 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_bf16_lds_kernel(const uin
   __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE];
 
   // XCD-aware order: workgroup ids go round-robin over the 8 XCDs; give each XCD a contiguous range
-  // of tiles, M fastest, so the M tiles that share a weight tile share that XCD's L2.
+  // of tiles, M fastest inside groups of at most 8 row tiles, so the tiles an XCD runs at once share
+  // both their activation and their weight k-slabs through its L2. (With all of M in one column of
+  // tiles, a long batch re-read its whole activation panel for every column of weight tiles.) With
+  // 8 row tiles or fewer this is plain M-fastest order.
   const int per_xcd = (ntiles + 7) / 8;
   const int tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (tile >= ntiles) return;
-  const int64_t m0 = (int64_t)(tile % tiles_m) * BM;
-  const int64_t n0 = (int64_t)(tile / tiles_m) * BN;
+  const int tiles_n = ntiles / tiles_m;
+  const int grp = tile / (8 * tiles_n), first = 8 * grp, gm = min(tiles_m - first, 8);
+  const int in_grp = tile - grp * 8 * tiles_n;
+  const int64_t m0 = (int64_t)(first + in_grp % gm) * BM;
+  const int64_t n0 = (int64_t)(in_grp / gm) * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g = lane >> 4;
