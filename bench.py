@@ -37,6 +37,9 @@ Kernel-only modes (one JSON line each, used for the rocprofv3 counter runs):
     python bench.py --kernel prefill_attention
                                          packed causal prefill attention: 8 prompts of 4096 tokens back to
                                          back, 32/8 heads, head_dim 128, bf16, block 16, TFLOP/s vs 2.5 PFLOP/s
+    python bench.py --kernel gemm_prefill
+                                         the 8B model's four layer GEMMs at M = 32768 (one packed prefill
+                                         forward), each call on the next layer's weights
 """
 
 import argparse
@@ -55,6 +58,7 @@ CFG = dict(vocab_size=128256, d_model=4096, n_layers=32, n_heads=32, n_kv_heads=
 DRAFT_LAYERS = 4
 BATCH, K, BLOCK = 64, 6, 16
 CTX_LO, CTX_HI = 2048, 8192
+PREFILL_TOKENS = 32768   # tokens per packed prefill forward (SpeculativeBatch.add_many's default)
 
 
 def log(*a):
@@ -304,14 +308,16 @@ def time_accept(torch, ops, reps, warmup, with_stats=False):
     return sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e-3
 
 
-def time_gemms(torch, ops, model, m, passes=3):
+def time_gemms(torch, ops, model, m, passes=3, head=True):
     """One layer's four GEMMs and the LM head at M rows (the verify pass: M = B*(k+1); a draft step:
-    M = B), each as the round runs it: qkv, wo and w_down as split-K partials where their (N, K)
-    splits K (the round adds the partials inside the rotary + KV write and the residual-add + RMSNorm
-    that follow, kernels counted apart), gate|up with the SwiGLU gate in its epilogue, the head with
-    its softmax-statistics epilogue. A shape's calls run back to back over successive layers' weights
-    (so that, as in a round, the weights stream from HBM rather than the 256 MB last-level cache),
-    `passes` times over the layers, between one pair of events: {name: (seconds per call, flops)}."""
+    M = B; a packed prefill forward: M = 32768, no head), each as the model runs it: qkv, wo and
+    w_down as split-K partials where their (N, K) splits K (the round adds the partials inside the
+    rotary + KV write and the residual-add + RMSNorm that follow, kernels counted apart) unless the
+    batch is long enough for the splits to run inside each workgroup (fs_gemm_serial), gate|up with the
+    SwiGLU gate in its epilogue, the head with its softmax-statistics epilogue. A shape's calls run back
+    to back over successive layers' weights (so that, as in a round, the weights stream from HBM rather
+    than the 256 MB last-level cache), `passes` times over the layers, between one pair of events:
+    {name: (seconds per call, flops)}."""
     from forgeserve_amd import _lib
     lib = _lib.load()
     layers = model.layers
@@ -319,8 +325,9 @@ def time_gemms(torch, ops, model, m, passes=3):
     shapes = {"qkv": (d, [b.attn.qkv_weight() for b in layers], "gemm"),
               "o": (d, [b.attn.wo.weight for b in layers], "gemm"),
               "gate_up": (d, [b.mlp.gate_up_weight() for b in layers], "swiglu"),
-              "down": (layers[0].mlp.w_down.weight.shape[1], [b.mlp.w_down.weight for b in layers], "gemm"),
-              "head": (d, [model.lm_head.weight], "head")}
+              "down": (layers[0].mlp.w_down.weight.shape[1], [b.mlp.w_down.weight for b in layers], "gemm")}
+    if head:
+        shapes["head"] = (d, [model.lm_head.weight], "head")
     out = {}
     for name, (kdim, ws, kind) in shapes.items():
         n = ws[0].shape[0]
@@ -334,7 +341,7 @@ def time_gemms(torch, ops, model, m, passes=3):
 
             def fn(w):
                 ops.gemm_row_stats(x, w, None, stats, out=logits)
-        elif lib.fs_gemm_splits(n, kdim, _lib.BF16) > 1:
+        elif lib.fs_gemm_splits(n, kdim, _lib.BF16) > 1 and not lib.fs_gemm_serial(m, n, kdim, _lib.BF16):
             part = torch.empty(lib.fs_gemm_splits(n, kdim, _lib.BF16) * m * n, dtype=torch.float32, device="cuda")
 
             def fn(w):
@@ -363,8 +370,9 @@ def time_gemms(torch, ops, model, m, passes=3):
 def gemm_summary(times, layers, peak_tflops):
     """Σ flops / Σ time over a pass's GEMMs (the layer GEMMs `layers` times, the head once; the verify
     pass runs blocks L_d..L-1 at M = B*(k+1), a draft step its L_d blocks at M = B)."""
-    t = sum(v[0] for k, v in times.items() if k != "head") * layers + times["head"][0]
-    f = sum(v[1] for k, v in times.items() if k != "head") * layers + times["head"][1]
+    hd = times.get("head", (0.0, 0))
+    t = sum(v[0] for k, v in times.items() if k != "head") * layers + hd[0]
+    f = sum(v[1] for k, v in times.items() if k != "head") * layers + hd[1]
     return {"tflops": round(f / t / 1e12, 1), "frac": round(f / t / 1e12 / peak_tflops, 4),
             "ms_per_pass": round(t * 1e3, 3),
             "per_gemm_us": {k: round(v[0] * 1e6, 1) for k, v in times.items()}}
@@ -534,6 +542,11 @@ def kernel_mode(args):
         out = {"kernel": "gemm", "m448": gemm_summary(time_gemms(torch, ops, target, BATCH * (K + 1)),
                                                       CFG["n_layers"] - draft.cfg.n_layers, MFMA_PEAK_TFLOPS),
                "m64": gemm_summary(time_gemms(torch, ops, draft, BATCH), draft.cfg.n_layers, MFMA_PEAK_TFLOPS)}
+    elif args.kernel == "gemm_prefill":
+        target, _ = build_models(torch, fa)
+        out = {"kernel": "gemm prefill (packed 32768-token forward, the 32 layers' four GEMMs)",
+               "m32768": gemm_summary(time_gemms(torch, ops, target, PREFILL_TOKENS, passes=1, head=False),
+                                      CFG["n_layers"], MFMA_PEAK_TFLOPS)}
     elif args.kernel == "prefill_attention":
         n_seq, L, h, hkv, d = 8, 4096, CFG["n_heads"], CFG["n_kv_heads"], 128
         g = torch.Generator(device="cuda").manual_seed(args.seed)
@@ -596,7 +609,7 @@ def main():
                     help="fill the pools with N(0,1) keys/values instead of prefilling the prompts")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kernel", choices=("round", "attention", "accept", "accept_stats", "copy", "engine_1b",
-                                         "prefill_attention", "gemm"),
+                                         "prefill_attention", "gemm", "gemm_prefill"),
                     default="round")
     args = ap.parse_args()
     if args.gpus != 1:
