@@ -139,6 +139,24 @@ def test_gemm_serial_splits_equal_short_batch_rows(m, n, k):
     assert ((got - ref).abs() <= ref.abs() * 2 ** -8 + 1e-3).all()
 
 
+@pytest.mark.parametrize("m,n,k,kind", [(4133, 28672, 1024, "swiglu"), (2600, 4096, 14336, "gemm"),
+                                        (3000, 1000, 256, "gemm")])
+def test_long_batch_rows_equal_short_batch_rows(m, n, k, kind):
+    """Long batches take 256-row tiles walked in groups of 8 row tiles (and, here, split-K partials or
+    the SwiGLU epilogue); every row equals the same row computed in a short batch, bit for bit."""
+    case("gemm long batch", m, n, k, kind)
+    from forgeserve_amd import _lib
+    assert not _lib.load().fs_gemm_serial(m, n, k, _lib.BF16)   # the partials / unsplit paths
+    g = torch.Generator().manual_seed(m + k)
+    a = torch.randn(m, k, generator=g).bfloat16().to(DEV)
+    w = (torch.randn(n, k, generator=g) * 0.03).bfloat16().to(DEV)
+    fn = ops.gemm_swiglu if kind == "swiglu" else ops.gemm
+    full = fn(a, w)
+    for lo in (0, 1111, m - 200):
+        hi = min(lo + 448, m)
+        assert torch.equal(fn(a[lo:hi], w), full[lo:hi])
+
+
 # ---- row ops ------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_rmsnorm_and_residual(dtype):
