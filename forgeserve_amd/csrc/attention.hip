@@ -71,11 +71,15 @@ struct AttnParams {
 // result is a normal float.
 FS_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// The maximum over the lanes l, l ^ 16, l ^ 32, l ^ 48. IEEE maximum (v_maximum3_f32, one instruction)
+// rather than fmaxf, which needs its permuted operands canonicalised first; the two agree on every
+// non-NaN input (the scores are finite or -inf) up to the sign of a zero maximum, which no result
+// depends on.
 FS_DEVICE float max_across_groups(float x) {
   auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
   auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 FS_DEVICE float sum_across_groups(float x) {

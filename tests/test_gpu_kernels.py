@@ -108,7 +108,8 @@ def test_splitk_add_rmsnorm_equals_gemm_then_norm(m, n, k):
     assert torch.equal(y, ops.add_rmsnorm(x_ref, nw, 1e-5))
 
 
-@pytest.mark.parametrize("m,n,k", [(4133, 4096, 4096), (8192, 4096, 8192), (2600, 6144, 4096)])
+@pytest.mark.parametrize("m,n,k", [(4133, 4096, 4096), (8192, 4096, 8192), (2600, 6144, 4096),
+                                   (3900, 4100, 4096)])   # a partial last column tile
 def test_gemm_serial_splits_equal_short_batch_rows(m, n, k):
     """A long batch whose workgroups run the K splits one after the other (no partials) gives every row
     bit for bit as a short batch gives it through the partials and their reduction, residual included,
