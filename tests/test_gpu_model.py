@@ -276,6 +276,45 @@ def test_packed_prefill_equals_per_sequence_prefill(which, bf_target, small):
     assert torch.equal(packed_pool.k_store, alone_pool.k_store) and torch.equal(packed_pool.v_store, alone_pool.v_store)
 
 
+def test_long_packed_prefill_equals_per_sequence_prefill():
+    """At the 8B layer shape (two blocks, d 4096, 32/8 heads, head_dim 128, ffn 14336), a 4400-token
+    packed forward runs the qkv and wo projections with their K splits inside each workgroup and the
+    long-batch tile order, the one-prompt prefills run them through split-K partials: the pool and the
+    last-token logits are the same bit for bit."""
+    case("long packed prefill")
+    from forgeserve_amd import _lib
+    lib = _lib.load()
+    assert lib.fs_gemm_serial(4400, 6144, 4096, _lib.BF16) and lib.fs_gemm_serial(4400, 4096, 4096, _lib.BF16)
+    assert not lib.fs_gemm_serial(1500, 6144, 4096, _lib.BF16)
+    cfg = fa.ModelConfig(vocab_size=32000, d_model=4096, n_layers=2, n_heads=32, n_kv_heads=8, ffn_dim=14336,
+                         max_seq_len=2048)
+    torch.manual_seed(5)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device("cuda"):
+            model = fa.ForgeModel(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    g = torch.Generator().manual_seed(32)
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in (1500, 1200, 1300, 400)]
+
+    def pool_and_lists():
+        pool = fa.PagedKVPool(cfg, 300, 16, dtype=model.dtype, device="cuda", key_layout="groups")
+        return pool, [pool.allocator.allocate(pool.blocks_for(len(p))) for p in prompts]
+
+    alone_pool, lists = pool_and_lists()
+    alone = []
+    for i, p in enumerate(prompts):
+        pos = torch.arange(len(p))[None]
+        alone.append(model(torch.tensor([p]), pos, alone_pool.views(torch.tensor([lists[i]]), pos))[0, -1])
+    packed_pool, lists2 = pool_and_lists()
+    assert lists2 == lists
+    got = fa.prefill_packed(model, packed_pool, prompts, lists)
+    assert torch.equal(got, torch.stack(alone))
+    assert torch.equal(packed_pool.k_store, alone_pool.k_store) and torch.equal(packed_pool.v_store, alone_pool.v_store)
+
+
 @pytest.mark.parametrize("which", ["bf16", "f32"])
 def test_shared_draft_cache_equals_separate_cache(which, bf_target, small):
     """An early-exit draft that reads and writes the target's cache for the blocks they share (and a
