@@ -247,6 +247,22 @@ __global__ void __launch_bounds__(256) embedding_kernel(const int64_t* __restric
   for (int64_t i = threadIdx.x; i < d; i += blockDim.x) o[i] = r[i];
 }
 
+// The same with 16-byte copies (rows of a multiple of 16 bytes, 16-byte aligned).
+__global__ void __launch_bounds__(256) embedding_vec_kernel(const int64_t* __restrict__ ids,
+                                                            const u32x4_t* __restrict__ w, int64_t d16,
+                                                            int64_t vocab, u32x4_t* __restrict__ out,
+                                                            int64_t ldo16) {
+  const int64_t m = blockIdx.x;
+  const int64_t id = ids[m];
+  u32x4_t* o = out + m * ldo16;
+  if (id < 0 || id >= vocab) {
+    for (int64_t i = threadIdx.x; i < d16; i += blockDim.x) o[i] = u32x4_t{0u, 0u, 0u, 0u};
+    return;
+  }
+  const u32x4_t* r = w + id * d16;
+  for (int64_t i = threadIdx.x; i < d16; i += blockDim.x) o[i] = r[i];
+}
+
 bool dtype_ok(int32_t dt) { return dt == FS_F32 || dt == FS_BF16 || dt == FS_F16; }
 
 }  // namespace
@@ -356,6 +372,13 @@ extern "C" int fs_embedding(const int64_t* ids, int64_t M, const void* weight, i
   FS_CHECK_ARG(M >= 0 && d_model > 0 && vocab > 0 && ldo >= d_model, "embedding: shapes");
   if (M == 0) return 0;
   hipStream_t s = fs::as_stream(stream);
+  const int64_t es = dtype == FS_F32 ? 4 : 2;   // bytes per element
+  if ((d_model * es) % 16 == 0 && (ldo * es) % 16 == 0 &&
+      ((reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(out)) & 15) == 0) {
+    embedding_vec_kernel<<<dim3((unsigned)M), 256, 0, s>>>(ids, (const u32x4_t*)weight, d_model * es / 16, vocab,
+                                                          (u32x4_t*)out, ldo * es / 16);
+    return fs::launch_status("embedding");
+  }
   if (dtype == FS_F32)
     embedding_kernel<float><<<dim3((unsigned)M), 256, 0, s>>>(ids, (const float*)weight, d_model, vocab,
                                                              (float*)out, ldo);

@@ -206,11 +206,16 @@ def test_rmsnorm_and_silu_general_paths_bf16():
     assert torch.equal(ops.silu_mul(strided), ops.silu_mul(packed))
 
 
-def test_embedding():
-    case("embedding")
-    w = torch.randn(100, 48).bfloat16()
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 48), (torch.bfloat16, 52), (torch.float32, 52),
+                                     (torch.float32, 4096)])   # 16-byte copies unless a row is 104 bytes
+def test_embedding(dtype, d):
+    case("embedding", dtype, d)
+    w = torch.randn(100, d).to(dtype)
     ids = torch.tensor([[3, 99, 0], [7, 7, 50]])
     assert torch.equal(ops.embedding(ids.to(DEV), w.to(DEV)).cpu(), w[ids.reshape(-1)])
+    # an id outside the vocabulary reads nothing and gives a zero row
+    got = ops.embedding(torch.tensor([5, -1, 100]).to(DEV), w.to(DEV)).cpu()
+    assert torch.equal(got[0], w[5]) and not got[1:].any()
 
 
 # ---- KV write + rotary ----------------------------------------------------------------------------------
