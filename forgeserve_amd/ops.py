@@ -14,12 +14,6 @@ from ._lib import DTYPE_CODE, KVLayout, check, ptr, require_device, stream_ptr
 
 I32 = torch.int32
 
-# Optional timing hook for benchmarks: when ATTN_EVENTS is a list, every paged_attention launch with
-# T == ATTN_EVENT_T appends a (start, end) pair of events recorded on the launching stream.
-ATTN_EVENTS = None
-ATTN_EVENT_T = None
-
-
 def _dt(t: torch.Tensor) -> int:
     try:
         return DTYPE_CODE[t.dtype]
@@ -390,17 +384,10 @@ def paged_attention(q: torch.Tensor, layout: KVLayout, tables: torch.Tensor, pos
     lib = _lib.load()
     need = lib.fs_paged_attention_workspace_size(b, t, h, d, nb, layout.block_size)
     ws = _persistent_ws("attention", need, q.device)
-    timing = ATTN_EVENTS is not None and t == ATTN_EVENT_T and not torch.cuda.is_current_stream_capturing()
-    if timing:
-        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-        ev[0].record()
     fn = lib.fs_paged_attention_reuse_plan if _reuse_plan(plan_key, positions) else lib.fs_paged_attention
     check(fn(ptr(q), q.stride(0), q.stride(1), q.stride(2), layout, ptr(tables), tables.stride(0), nb, ptr(positions),
              b, t, h, float(scale), ptr(out), out.stride(0), out.stride(1), out.stride(2), ptr(ws), ws.numel(),
              stream_ptr()), "paged_attention")
-    if timing:
-        ev[1].record()
-        ATTN_EVENTS.append(ev)
     return out
 
 

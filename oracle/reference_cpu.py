@@ -200,34 +200,67 @@ def attention_math(q, k_all, v_all, positions, rep):
     return torch.matmul(probs, v_all).to(q.dtype)
 
 
-def forward(w: Weights, s: Shape, idx, positions=None, kv=None, rope=None):
-    """model.py:141-159: logits (B, T, V) for token ids idx (B, T); kv: one cache view per layer."""
+def block(lw: Weights, s: Shape, x, positions, cache, rope):
+    """model.py:104-106 with Attention.forward (62-78) and SwiGLU (92-93): one pre-norm block on the
+    residual stream x (B, T, d). lw holds the block's weights under their names inside the block
+    ("attn_norm.weight", "attn.wq.weight", ...); cache is the block's cache view."""
+    b, t, _ = x.shape
+    cos, sin = rope
+    hd, nh, nkv = s.head_dim, s.n_heads, s.n_kv_heads
+    h = rms_norm(x, lw["attn_norm.weight"], s.norm_eps)
+    q = (h @ lw["attn.wq.weight"].T).view(b, t, nh, hd).transpose(1, 2)
+    k = (h @ lw["attn.wk.weight"].T).view(b, t, nkv, hd).transpose(1, 2)
+    v = (h @ lw["attn.wv.weight"].T).view(b, t, nkv, hd).transpose(1, 2)
+    q, k = rotate(q, cos, sin, positions), rotate(k, cos, sin, positions)
+    k_all, v_all = cache.update(k, v)
+    o = attention_math(q, k_all, v_all, positions, nh // nkv)
+    x = x + o.transpose(1, 2).reshape(b, t, nh * hd) @ lw["attn.wo.weight"].T
+    h = rms_norm(x, lw["mlp_norm.weight"], s.norm_eps)
+    g = h @ lw["mlp.w_gate.weight"].T
+    u = h @ lw["mlp.w_up.weight"].T
+    return x + (torch.nn.functional.silu(g) * u) @ lw["mlp.w_down.weight"].T
+
+
+def _positions(s: Shape, kv, idx, positions):
     b, t = idx.shape
-    if kv is None:
-        kv = contiguous_caches(s.n_layers)
     if positions is None:
         positions = (kv[0].length + torch.arange(t))[None].expand(b, t)
     positions = positions.long()
     if int(positions.max()) >= s.max_seq_len:
         raise ValueError("position exceeds max_seq_len")
-    cos, sin = rope if rope is not None else rope_tables(s)
-    hd, nh, nkv = s.head_dim, s.n_heads, s.n_kv_heads
+    return positions
+
+
+def forward(w: Weights, s: Shape, idx, positions=None, kv=None, rope=None):
+    """model.py:141-159: logits (B, T, V) for token ids idx (B, T); kv: one cache view per layer."""
+    if kv is None:
+        kv = contiguous_caches(s.n_layers)
+    positions = _positions(s, kv, idx, positions)
+    rope = rope if rope is not None else rope_tables(s)
     x = w["tok_emb.weight"][idx]
     for i in range(s.n_layers):
         p = f"layers.{i}."
-        h = rms_norm(x, w[p + "attn_norm.weight"], s.norm_eps)
-        q = (h @ w[p + "attn.wq.weight"].T).view(b, t, nh, hd).transpose(1, 2)
-        k = (h @ w[p + "attn.wk.weight"].T).view(b, t, nkv, hd).transpose(1, 2)
-        v = (h @ w[p + "attn.wv.weight"].T).view(b, t, nkv, hd).transpose(1, 2)
-        q, k = rotate(q, cos, sin, positions), rotate(k, cos, sin, positions)
-        k_all, v_all = kv[i].update(k, v)
-        o = attention_math(q, k_all, v_all, positions, nh // nkv)
-        x = x + o.transpose(1, 2).reshape(b, t, nh * hd) @ w[p + "attn.wo.weight"].T
-        h = rms_norm(x, w[p + "mlp_norm.weight"], s.norm_eps)
-        g = h @ w[p + "mlp.w_gate.weight"].T
-        u = h @ w[p + "mlp.w_up.weight"].T
-        x = x + (torch.nn.functional.silu(g) * u) @ w[p + "mlp.w_down.weight"].T
+        lw = {name[len(p):]: t for name, t in w.items() if name.startswith(p)}
+        x = block(lw, s, x, positions, kv[i], rope)
     return rms_norm(x, w["norm.weight"], s.norm_eps) @ w["tok_emb.weight"].T
+
+
+def forward_streamed(layer_weights, emb, norm_w, s: Shape, idx, positions=None, hidden=None):
+    """forward() (model.py:141-159) with one block's weights on the host at a time, for models too
+    large to hold whole in host memory: layer_weights(i) returns block i's weights (the names inside
+    the block, as block() takes them) and may build them on demand; emb is the tied embedding/head,
+    norm_w the final norm's weight. A fresh contiguous cache. hidden: optional list that receives the
+    residual stream after each block. Identical arithmetic to forward()."""
+    kv = contiguous_caches(s.n_layers)
+    positions = _positions(s, kv, idx, positions)
+    rope = rope_tables(s)
+    x = emb[idx]
+    for i in range(s.n_layers):
+        x = block(layer_weights(i), s, x, positions, kv[i], rope)
+        kv[i] = None
+        if hidden is not None:
+            hidden.append(x)
+    return rms_norm(x, norm_w, s.norm_eps) @ emb.T
 
 
 def draft_weights(w: Weights, n_layers: int) -> Weights:

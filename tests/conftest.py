@@ -28,3 +28,12 @@ def pytest_collection_modifyitems(config, items):
 @pytest.fixture(autouse=True)
 def _seed():
     torch.manual_seed(0)
+
+
+def pytest_terminal_summary(terminalreporter):
+    from helpers import RECORDS
+
+    if RECORDS:
+        terminalreporter.section("parity figures")
+        for line in RECORDS:
+            terminalreporter.write_line(line)

@@ -49,3 +49,13 @@ def product_model(cfg_kw, seed, std, dtype=torch.float32, n_layers=None, device=
     sd["lm_head.weight"] = w["tok_emb.weight"]
     m.load_state_dict(sd)
     return m.to(device=device, dtype=dtype)
+
+
+# Parity figures the GPU tests measure (errors, margins, near-tie counts). conftest.py prints them in
+# pytest's terminal summary, so a quiet (-q) run's output still carries them.
+RECORDS = []
+
+
+def record(line: str) -> None:
+    print(line, flush=True)
+    RECORDS.append(line)

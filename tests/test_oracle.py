@@ -171,6 +171,30 @@ def test_forward_c1_matches_reference_logits():
                                rtol=1e-5)
 
 
+def test_streamed_forward_matches_reference_logits():
+    """The layer-at-a-time forward (the full-depth GPU checks feed it one block's weights at a time)
+    gives the reference's logits, and the whole-dict forward's bit for bit, in float32 and in bf16."""
+    for cfg, seed, std, name in ((SMALL, 1, 0.25, "model_small.npz"), (C1, 0, 0.02, "model_c1.npz")):
+        w, s = oracle_model(cfg, seed, std)
+        gold = golden_npz(name)
+        idx = torch.from_numpy(gold["idx"]) if "idx" in gold else torch.tensor([golden_json("model_c1.json")["prompt"]])
+
+        def layer(i, w=w):
+            p = f"layers.{i}."
+            return {n[len(p):]: t for n, t in w.items() if n.startswith(p)}
+
+        hidden = []
+        got = orc.forward_streamed(layer, w["tok_emb.weight"], w["norm.weight"], s, idx, hidden=hidden)
+        assert len(hidden) == s.n_layers and hidden[-1].shape == (*idx.shape, s.d_model)
+        assert torch.equal(got, orc.forward(w, s, idx))
+        want = gold["logits"] if got.shape[0] > 1 or "idx" in gold else gold["logits"][None]
+        np.testing.assert_allclose(got.numpy(), want, atol=2e-5, rtol=1e-5)
+        wb = {n: t.bfloat16() for n, t in w.items()}
+        got_b = orc.forward_streamed(lambda i: {n: t.bfloat16() for n, t in layer(i).items()}, wb["tok_emb.weight"],
+                                     wb["norm.weight"], s, idx)
+        assert got_b.dtype == torch.bfloat16 and torch.equal(got_b, orc.forward(wb, s, idx))
+
+
 def test_paged_forward_matches_reference():
     w, s = oracle_model(SMALL, 1, 0.25)
     gold = golden_npz("model_small.npz")
