@@ -23,6 +23,12 @@ warm-up, then the median of three runs of each), scaled to a round.
 `t1_variant` = the same workload at temperature 1.0 (fresh prefill, same timing), whose acceptance
 exercises the residual draws; `verify_pass` = the target's verify pass alone (its k+1-token forward,
 head, statistics merge and fused acceptance) and one draft step, replayed from the round's graphs.
+`accept_kernel` = the fused acceptance alone at the 8B shape, standalone (every logit row read) and
+with the rows' statistics given as the round's LM heads emit them (achieved GB/s on the bytes that
+call reads, and the epilogue's marginal cost per head call).
+`c3_attention` / `c2_accept` = the paged verify attention (B=32, k+1=5, contexts U[512,4096], a random
+12,288-block pool) and the fused acceptance (B=64, k=5, V=32000, f32) alone, each with the CPU oracle
+timed at the same shape; `engine_1b` = the 1B-shape continuous-batching Engine over 48 requests.
 
     python bench.py [--gpus 1] [--steps 128] [--warmup 4] [--temperature 0.0] [--no-t1-variant]
 
@@ -37,6 +43,9 @@ Kernel-only modes (one JSON line each, used for the rocprofv3 counter runs):
     python bench.py --kernel prefill_attention
                                          packed causal prefill attention: 8 prompts of 4096 tokens back to
                                          back, 32/8 heads, head_dim 128, bf16, block 16, TFLOP/s vs 2.5 PFLOP/s
+    python bench.py --kernel c3          the attention configuration (see c3_attention), both key layouts
+    python bench.py --kernel c2          the acceptance configuration (see c2_accept)
+    python bench.py --kernel engine_1b   the 1B-shape Engine workload (see engine_1b)
     python bench.py --kernel gemm_prefill
                                          the 8B model's four layer GEMMs at M = 32768 (one packed prefill
                                          forward), each call on the next layer's weights
@@ -86,7 +95,7 @@ CFG_1B = dict(vocab_size=32000, d_model=2048, n_layers=16, n_heads=32, n_kv_head
 def engine_1b(args):
     """The 1B-shape continuous-batching workload: Engine(max_batch 16, k = 4, T = 0.7) with a 2-layer
     early-exit draft over 48 requests (prompts U[128, 1024], max_new_tokens U[64, 256]), the pool sized
-    below the peak demand so that recompute preemptions happen. Prints one JSON line."""
+    below the peak demand so that recompute preemptions happen. Returns the figures as a dict."""
     import torch
 
     import forgeserve_amd as fa
@@ -115,13 +124,19 @@ def engine_1b(args):
     el = time.perf_counter() - t0
     toks = sum(len(v) for v in out.values())
     assert all(len(out[i]) == n for i, (_, n) in enumerate(reqs))
-    print(json.dumps({"workload": "1B-shape continuous batching: 16L d2048 32/8 heads hd64 ffn8192 V32000 bf16, "
-                                  "2-layer early-exit draft, Engine max_batch 16, k=4, T=0.7, 48 requests, "
-                                  "prompts U[128,1024], max_new U[64,256], 600 blocks of 16 (keys in 8-dim groups)",
-                      "generated_tokens": toks, "seconds": round(el, 3), "tok_per_s": round(toks / el, 1),
-                      "engine_steps": eng.steps, "rounds": eng.stats["rounds"], "preemptions": eng.preemptions,
-                      "peak_running": eng.peak_running, "peak_blocks": eng.peak_blocks,
-                      "acceptance": round(eng.stats["accepted"] / max(eng.stats["proposed"], 1), 4)}), flush=True)
+    res = {"workload": "1B-shape continuous batching: 16L d2048 32/8 heads hd64 ffn8192 V32000 bf16, "
+                       "2-layer early-exit draft, Engine max_batch 16, k=4, T=0.7, 48 requests, "
+                       "prompts U[128,1024], max_new U[64,256], 600 blocks of 16 (keys in 8-dim groups)",
+           "generated_tokens": toks, "seconds": round(el, 3), "tok_per_s": round(toks / el, 1),
+           "engine_steps": eng.steps, "rounds": eng.stats["rounds"], "preemptions": eng.preemptions,
+           "peak_running": eng.peak_running, "peak_blocks": eng.peak_blocks,
+           "acceptance": round(eng.stats["accepted"] / max(eng.stats["proposed"], 1), 4),
+           "gpu_busy_fraction": profiled_figure("engine_1b_kernel_stats.md", "gpu_busy_fraction", float),
+           "gpu_busy_note": "kernel time / wall time of the same command under rocprofv3 --kernel-trace, "
+                            "from profiles/engine_1b_kernel_stats.md"}
+    del eng, target, draft
+    torch.cuda.empty_cache()
+    return res
 
 
 def attn_bytes(ctxs, t, h, hkv, d, bs):
@@ -255,24 +270,31 @@ def cpu_baseline(torch, committed_per_round):
     }
 
 
-def profiled_traffic(name):
-    """HBM bytes per call measured with rocprofv3 counters, from the summary committed under profiles/
-    (its line `traffic_bytes_per_call: N`), or None."""
+def profiled_figure(name, key, conv=int):
+    """A figure measured under rocprofv3 (counters or a kernel trace), from the summary committed under
+    profiles/ (its line `key: value`), or None."""
     import re
 
     path = os.path.join(ROOT, "profiles", name)
     try:
-        m = re.search(r"traffic_bytes_per_call:\s*(\d+)", open(path).read())
+        m = re.search(re.escape(key) + r":\s*([0-9.]+)", open(path).read())
     except OSError:
         return None
-    return int(m.group(1)) if m else None
+    return conv(m.group(1)) if m else None
+
+
+def profiled_traffic(name):
+    """HBM bytes per call measured with rocprofv3 counters (`traffic_bytes_per_call: N`), or None."""
+    return profiled_figure(name, "traffic_bytes_per_call")
 
 
 def time_accept(torch, ops, reps, warmup, with_stats=False):
-    """The acceptance kernel alone at the benchmark shape (bf16 logits, V = 128256): mean seconds per call.
-    The call is captured once into a graph and replayed, so the host's launch overhead is not timed.
-    with_stats: the rows' softmax statistics are given, as the LM head's epilogue emits them in the
-    round (they are computed here once, outside the timed calls)."""
+    """The acceptance kernel alone at the benchmark shape (bf16 logits, V = 128256): (mean seconds per
+    call, bytes the call reads). The call is captured once into a graph and replayed, so the host's
+    launch overhead is not timed. with_stats: the rows' softmax statistics are given, as the LM head's
+    epilogue emits them in the round (they are computed here once, outside the timed calls); the call
+    then reads only the rejected position's two logit rows (the target row alone for a bonus token),
+    the Exp(1) row, and per sequence the proposals, uniforms, statistics and 2k+1 proposal logits."""
     v = CFG["vocab_size"]
     g = torch.Generator(device="cuda").manual_seed(3)
     tl = torch.randn(BATCH, K + 1, v, device="cuda", generator=g).mul_(2).bfloat16()
@@ -305,7 +327,13 @@ def time_accept(torch, ops, reps, warmup, with_stats=False):
         graph.replay()
         b.record()
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e-3
+    sec = sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e-3
+    if not with_stats:
+        return sec, accept_bytes(BATCH, K, v)
+    _, n = ops.spec_accept(tl, dl, xs, None, temps, u, e, row_stats=st)
+    rows = sum(2 if int(x) < K else 1 for x in n.cpu())   # logit rows of the final draw
+    small = BATCH * (4 * K * 2 + 16 * (2 * K + 1) + 2 * (2 * K + 1) + 4 * (K + 2))
+    return sec, rows * v * 2 + BATCH * v * 4 + small
 
 
 def time_gemms(torch, ops, model, m, passes=3, head=True):
@@ -367,6 +395,22 @@ def time_gemms(torch, ops, model, m, passes=3, head=True):
     return out
 
 
+def head_epilogue_cost(torch, ops, model):
+    """Marginal cost of the LM head's softmax-statistics epilogue: graph-replayed head GEMMs with and
+    without it at M = B*(k+1) (a verify pass) and M = B (a draft step), in µs per call."""
+    w = model.lm_head.weight
+    n, d = w.shape
+    out = {}
+    for name, m in (("m448", BATCH * (K + 1)), ("m64", BATCH)):
+        x = torch.randn(m, d, device="cuda").to(w.dtype)
+        logits = torch.empty((m, n), dtype=w.dtype, device="cuda")
+        parts = torch.empty((m, ops.row_stats_parts(m, n, d), 4), dtype=torch.int32, device="cuda")
+        t_plain = graph_time(torch, lambda: ops.gemm(x, w, out=logits), 8)
+        t_stats = graph_time(torch, lambda: ops.gemm_row_stats(x, w, None, parts, out=logits), 8)
+        out[name] = round((t_stats - t_plain) * 1e6, 1)
+    return out
+
+
 def gemm_summary(times, layers, peak_tflops):
     """Σ flops / Σ time over a pass's GEMMs (the layer GEMMs `layers` times, the head once; the verify
     pass runs blocks L_d..L-1 at M = B*(k+1), a draft step its L_d blocks at M = B)."""
@@ -401,6 +445,185 @@ def attention_inputs(torch, fa, seed=0):
     q = torch.randn(BATCH, K + 1, CFG["n_heads"], 128, device="cuda").bfloat16()
     pos = torch.tensor([[c - (K + 1) + i for i in range(K + 1)] for c in ctxs], dtype=torch.int32).cuda()
     return ctxs, pool, q, pos, tables.cuda()
+
+
+def cpu_timed(fn, runs=3):
+    """One warm-up call, then the median of `runs` timed calls (seconds)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def graph_time(torch, fn, calls, reps=5):
+    """Mean seconds per fn() call: `calls` calls captured in one HIP graph, replayed `reps` times between
+    HIP events on the capturing stream (no host launch overhead in the figure)."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e-3 / (reps * calls)
+
+
+C3 = dict(batch=32, t=5, h=32, hkv=8, d=128, bs=16, pool=12288, lo=512, hi=4096, seed=6)
+
+
+def c3_attention(torch, fa, ops, cpu=True):
+    """The paged verify-attention kernel alone at the attention configuration: 32 sequences, k+1 = 5 query
+    tokens each (causal inside the window: the last 5 positions of each context), 32/8 heads, head_dim
+    128, bf16 N(0, 1) queries/keys/values (seed 6), contexts U[512, 4096], block 16, block tables the
+    first sum(ceil(ctx/16)) entries of a random permutation of a 12,288-block pool (paged.py:80-81,
+    model.py:70-76). Two layers' pools, alternated, so that a call does not find the previous call's
+    keys in the last-level cache. Per layout (keys slot-major as the reference's pool, and in 8-dim
+    groups as the speculative batches' pools): the attention per call with one work plan shared by 16
+    calls (a layer of a verify pass) and per standalone call (plan + attention). cpu: the oracle's
+    gather + masked softmax attention in f32 on this host (paged.py:80-81, model.py:70-76)."""
+    c = C3
+    g = torch.Generator().manual_seed(c["seed"])
+    ctxs = torch.randint(c["lo"], c["hi"] + 1, (c["batch"],), generator=g).tolist()
+    nb = [-(-x // c["bs"]) for x in ctxs]
+    perm = torch.randperm(c["pool"], generator=g)
+    tables = torch.zeros(c["batch"], max(nb), dtype=torch.int32)
+    at = 0
+    for i, n in enumerate(nb):
+        tables[i, :n] = perm[at:at + n].int()
+        at += n
+    cfg = fa.ModelConfig(vocab_size=8, d_model=c["h"] * c["d"], n_layers=2, n_heads=c["h"], n_kv_heads=c["hkv"],
+                         max_seq_len=16)
+    gd = torch.Generator(device="cuda").manual_seed(c["seed"])
+    q = torch.randn(c["batch"], c["t"], c["h"], c["d"], device="cuda", generator=gd).bfloat16()
+    pos = torch.tensor([[x - c["t"] + i for i in range(c["t"])] for x in ctxs], dtype=torch.int32).cuda()
+    tab = tables.cuda()
+    byts = attn_bytes(ctxs, c["t"], c["h"], c["hkv"], c["d"], c["bs"])
+    out = {"workload": "paged verify attention alone: B=32, k+1=5, 32/8 heads, hd128, bf16, ctx U[512,4096] "
+                       "(seed 6), block 16, tables a random permutation of a 12,288-block pool",
+           "algorithmic_bytes": byts}
+    o = torch.empty_like(q)
+    for layout in ("slots", "groups"):
+        pool = fa.PagedKVPool(cfg, c["pool"], c["bs"], dtype=torch.bfloat16, device="cuda", key_layout=layout)
+        pool.k_store.normal_(generator=gd)
+        pool.v_store.normal_(generator=gd)
+        lays = [pool.layout(0), pool.layout(1)]
+        state = {"i": 0, "key": object()}
+
+        def shared():
+            ops.paged_attention(q, lays[state["i"] % 2], tab, pos, c["d"] ** -0.5, out=o, plan_key=state["key"])
+            state["i"] += 1
+
+        def alone():
+            ops.paged_attention(q, lays[state["i"] % 2], tab, pos, c["d"] ** -0.5, out=o)
+            state["i"] += 1
+
+        t_shared = graph_time(torch, shared, 16)
+        t_alone = graph_time(torch, alone, 16)
+        out[layout] = {"avg_us": round(t_shared * 1e6, 2), "achieved_GBs": round(byts / t_shared / 1e9, 1),
+                       "frac": round(byts / t_shared / 1e9 / HBM_PEAK_GBS, 4),
+                       "standalone_us": round(t_alone * 1e6, 2)}
+        if layout == "slots" and cpu:
+            out["cpu"] = c3_cpu(torch, pool, q, tables, pos, ctxs)
+        del pool, lays
+        torch.cuda.empty_cache()
+    return out
+
+
+def c3_cpu(torch, pool, q, tables, pos, ctxs):
+    """The oracle's attention on the host at the attention configuration: the reference's gather of every
+    table block (paged.py:80-81), GQA repeat, key <= position mask and softmax attention in f32
+    (model.py:70-76), for the 32 rows at once."""
+    from oracle import reference_cpu as orc
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    c = C3
+    used = tables.unique().long()
+    kp = torch.zeros(c["pool"], c["hkv"], c["bs"], c["d"])
+    vp = torch.zeros(c["pool"], c["hkv"], c["bs"], c["d"])
+    kp[used] = pool.k[0][used.cuda()].float().cpu()
+    vp[used] = pool.v[0][used.cuda()].float().cpu()
+    qc = q.float().cpu().transpose(1, 2)
+    pc = pos.long().cpu()
+    tl = tables.long()
+    b = c["batch"]
+
+    def run():
+        k_all = kp[tl].permute(0, 2, 1, 3, 4).reshape(b, c["hkv"], -1, c["d"])
+        v_all = vp[tl].permute(0, 2, 1, 3, 4).reshape(b, c["hkv"], -1, c["d"])
+        return orc.attention_math(qc, k_all, v_all, pc, c["h"] // c["hkv"])
+
+    sec = cpu_timed(run)
+    byts = attn_bytes(ctxs, c["t"], c["h"], c["hkv"], c["d"], c["bs"])
+    return {"seconds": round(sec, 3), "GBs": round(byts / sec / 1e9, 2), "cores": threads, "kind": "port",
+            "sample": "the whole call (32 rows), one warm-up then the median of 3"}
+
+
+C2 = dict(batch=64, k=5, v=32000)
+
+
+def c2_inputs(torch):
+    """The acceptance configuration: target logits 2.0*N(0,1) (B, k+1, V) (seed 3), draft logits = the
+    target's first k positions + 0.5*N(0,1) (seed 4), f32, T = 1; draft tokens argmax(q_j / E_j), the
+    uniforms u (B, k) and the final Exp(1) row E (B, V) from seed 5."""
+    c = C2
+    b, k, v = c["batch"], c["k"], c["v"]
+    tl = torch.randn(b, k + 1, v, generator=torch.Generator().manual_seed(3)) * 2.0
+    dl = tl[:, :k] + torch.randn(b, k, v, generator=torch.Generator().manual_seed(4)) * 0.5
+    g5 = torch.Generator().manual_seed(5)
+    e_draft = torch.empty(b, k, v).exponential_(generator=g5)
+    xs = (torch.softmax(dl, -1) / e_draft).argmax(-1).int()
+    u = torch.rand(b, k, generator=g5)
+    e = torch.empty(b, v).exponential_(generator=g5)
+    return tl, dl, xs, u, e
+
+
+def c2_accept(torch, ops, cpu=True):
+    """The fused acceptance alone at the acceptance configuration (B = 64, k = 5, V = 32000, f32 logits,
+    T = 1): graph-replayed standalone calls, and, with cpu, the oracle's softmaxes and verify_draft on
+    the same injected randomness on this host (sampling.py:9-13, speculative.py:20-33)."""
+    c = C2
+    b, k, v = c["batch"], c["k"], c["v"]
+    tl, dl, xs, u, e = c2_inputs(torch)
+    args = (tl.cuda(), dl.cuda(), xs.cuda(), None, torch.ones(b, device="cuda"), u.cuda(), e.cuda())
+    sec = graph_time(torch, lambda: ops.spec_accept(*args), 16)
+    byts = accept_bytes(b, k, v, s_logit=4)
+    out = {"workload": "fused acceptance alone: B=64, k=5, V=32000, f32 logits, T=1, seeds 3/4/5",
+           "avg_us": round(sec * 1e6, 2), "algorithmic_bytes": byts, "achieved_GBs": round(byts / sec / 1e9, 1),
+           "frac": round(byts / sec / 1e9 / HBM_PEAK_GBS, 4)}
+    got, n = ops.spec_accept(*args)
+    out["mean_accepted"] = round(float(n.float().mean()), 3)
+    if cpu:
+        from oracle import reference_cpu as orc
+
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
+
+        def run():
+            res = []
+            for i in range(b):
+                p, q = orc.probs_from_logits(tl[i], 1.0), orc.probs_from_logits(dl[i], 1.0)
+                res.append(orc.verify_with_noise(p, q, xs[i].tolist(), u[i], e[i]))
+            return res
+
+        t = cpu_timed(run)
+        res = run()
+        out["cpu"] = {"seconds": round(t, 3), "GBs": round(byts / t / 1e9, 2), "cores": threads, "kind": "port",
+                      "sample": "the whole call (64 sequences), one warm-up then the median of 3"}
+        got, n = got.cpu(), n.cpu()
+        out["tokens_equal_oracle"] = all(got[i, : len(a) + 1].tolist() == a + [x] and int(n[i]) == len(a)
+                                         for i, (a, x) in enumerate(res))
+    return out
 
 
 def phase_times(torch, sb, reps=8):
@@ -533,10 +756,13 @@ def kernel_mode(args):
                "algorithmic_bytes": byts, "achieved_GBs": round(byts / sec / 1e9, 1)}
     elif args.kernel in ("accept", "accept_stats"):
         stats = args.kernel == "accept_stats"
-        sec = time_accept(torch, ops, steps, warmup, with_stats=stats)
-        byts = accept_bytes(BATCH, K, CFG["vocab_size"])
+        sec, byts = time_accept(torch, ops, steps, warmup, with_stats=stats)
         out = {"kernel": "spec_accept" + (" (row statistics given)" if stats else ""), "calls": steps,
-               "avg_us": round(sec * 1e6, 2), "algorithmic_bytes": byts, "achieved_GBs": round(byts / sec / 1e9, 1)}
+               "avg_us": round(sec * 1e6, 2), "bytes": byts, "achieved_GBs": round(byts / sec / 1e9, 1)}
+    elif args.kernel == "c3":
+        out = c3_attention(torch, fa, ops, cpu=False)
+    elif args.kernel == "c2":
+        out = c2_accept(torch, ops, cpu=False)
     elif args.kernel == "gemm":
         target, draft = build_models(torch, fa)
         out = {"kernel": "gemm", "m448": gemm_summary(time_gemms(torch, ops, target, BATCH * (K + 1)),
@@ -608,8 +834,9 @@ def main():
     ap.add_argument("--synthetic-kv", action="store_true",
                     help="fill the pools with N(0,1) keys/values instead of prefilling the prompts")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-engine-1b", action="store_true", help="skip the 1B-shape engine workload")
     ap.add_argument("--kernel", choices=("round", "attention", "accept", "accept_stats", "copy", "engine_1b",
-                                         "prefill_attention", "gemm", "gemm_prefill"),
+                                         "prefill_attention", "gemm", "gemm_prefill", "c2", "c3"),
                     default="round")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -617,7 +844,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.kernel == "engine_1b":
-        engine_1b(args)
+        print(json.dumps(engine_1b(args)), flush=True)
         return
     if args.kernel != "round":
         kernel_mode(args)
@@ -651,12 +878,22 @@ def main():
                              "committed_per_round": round(r["committed"] / args.steps, 2)}}
 
     v = CFG["vocab_size"]
-    acc_avg = time_accept(torch, ops, 20, 3)
+    acc_avg, _ = time_accept(torch, ops, 20, 3)
     acc_gbs = accept_bytes(BATCH, K, v) / acc_avg / 1e9
-    accs_avg = time_accept(torch, ops, 20, 3, with_stats=True)
+    accs_avg, accs_read = time_accept(torch, ops, 20, 3, with_stats=True)
+    head_ep = head_epilogue_cost(torch, ops, target)
     gemm_verify = gemm_summary(time_gemms(torch, ops, target, BATCH * (K + 1)), CFG["n_layers"] - draft.cfg.n_layers,
                                MFMA_PEAK_TFLOPS)
     gemm_draft = gemm_summary(time_gemms(torch, ops, draft, BATCH), draft.cfg.n_layers, MFMA_PEAK_TFLOPS)
+    log("timing the attention and acceptance configurations ...")
+    c3 = c3_attention(torch, fa, ops, cpu=not args.no_cpu_baseline)
+    c2 = c2_accept(torch, ops, cpu=not args.no_cpu_baseline)
+    eng = None
+    if not args.no_engine_1b:
+        del target, draft
+        torch.cuda.empty_cache()
+        log("running the 1B-shape engine workload ...")
+        eng = engine_1b(args)
 
     result = {
         "metric": "accepted tok/s (8B-shape, k=6, bs=64); verify-attn HBM GB/s vs peak",
@@ -689,9 +926,17 @@ def main():
         "accept_kernel": {"avg_us": round(acc_avg * 1e6, 2), "achieved_GBs": round(acc_gbs, 1),
                           "algorithmic_bytes": accept_bytes(BATCH, K, v),
                           "traffic": profiled_traffic("spec_accept_8b.md"),
-                          # as the round runs it: the rows' statistics come from the LM heads' epilogue
-                          "with_head_stats": {"avg_us": round(accs_avg * 1e6, 2),
-                                              "effective_GBs": round(accept_bytes(BATCH, K, v) / accs_avg / 1e9, 1)}},
+                          # as the round runs it: the rows' statistics come from the LM heads' epilogue,
+                          # so the call reads only what its bytes_read says; achieved_GBs is on those bytes
+                          "with_head_stats": {"avg_us": round(accs_avg * 1e6, 2), "bytes_read": accs_read,
+                                              "achieved_GBs": round(accs_read / accs_avg / 1e9, 1),
+                                              "head_epilogue_us": head_ep,
+                                              "note": "the statistics pass is not timed here: the LM head's "
+                                                      "epilogue computes it (head_epilogue_us: its marginal "
+                                                      "cost per head call, with statistics minus without)"}},
+        "c3_attention": c3,
+        "c2_accept": c2,
+        "engine_1b": eng,
         "prefill": prefill,
         "verify_pass": main_run["phases"],
         "t1_variant": t1,
