@@ -68,6 +68,7 @@ DRAFT_LAYERS = 4
 BATCH, K, BLOCK = 64, 6, 16
 CTX_LO, CTX_HI = 2048, 8192
 PREFILL_TOKENS = 32768   # tokens per packed prefill forward (SpeculativeBatch.add_many's default)
+ACCEPT_CALLS_PER_GRAPH = 10
 
 
 def log(*a):
@@ -290,8 +291,9 @@ def profiled_traffic(name):
 
 def time_accept(torch, ops, reps, warmup, with_stats=False):
     """The acceptance kernel alone at the benchmark shape (bf16 logits, V = 128256): (mean seconds per
-    call, bytes the call reads). The call is captured once into a graph and replayed, so the host's
-    launch overhead is not timed. with_stats: the rows' softmax statistics are given, as the LM head's
+    call, bytes the call reads). ACCEPT_CALLS_PER_GRAPH calls back to back are captured into a graph and
+    replayed between HIP events, so neither the host's launch overhead nor the events' own cost (about
+    10 µs per replay) is timed; the launch gaps between and inside the calls are. with_stats: the rows' softmax statistics are given, as the LM head's
     epilogue emits them in the round (they are computed here once, outside the timed calls); the call
     then reads only the rejected position's two logit rows (the target row alone for a bonus token),
     the Exp(1) row, and per sequence the proposals, uniforms, statistics and 2k+1 proposal logits."""
@@ -318,7 +320,8 @@ def time_accept(torch, ops, reps, warmup, with_stats=False):
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        ops.spec_accept(tl, dl, xs, None, temps, u, e, row_stats=st)
+        for _ in range(ACCEPT_CALLS_PER_GRAPH):
+            ops.spec_accept(tl, dl, xs, None, temps, u, e, row_stats=st)
     graph.replay()
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
@@ -327,7 +330,7 @@ def time_accept(torch, ops, reps, warmup, with_stats=False):
         graph.replay()
         b.record()
     torch.cuda.synchronize()
-    sec = sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e-3
+    sec = sum(a.elapsed_time(b) for a, b in ev) / len(ev) * 1e-3 / ACCEPT_CALLS_PER_GRAPH
     if not with_stats:
         return sec, accept_bytes(BATCH, K, v)
     _, n = ops.spec_accept(tl, dl, xs, None, temps, u, e, row_stats=st)

@@ -15,6 +15,7 @@
 // bit for bit with the CPU reference on the same noise.
 #include <math.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "common.h"
@@ -316,6 +317,29 @@ __global__ void sample_final_kernel(int R, int nch, const float* __restrict__ te
 // ------------------------------------------------------------------------------------------------
 // acceptance
 // ------------------------------------------------------------------------------------------------
+// Logits without given statistics take two launches: the statistics of every (row, 8K-column chunk)
+// (accept_stats_kernel), then accept_kernel; with the statistics given (from the LM head's epilogue),
+// or on probabilities, accept_kernel alone. In accept_kernel workgroup i takes work item i:
+//   items 0..B-1, step items: sequence b's step (merging its rows' chunk statistics when they come
+//     from the statistics launch); a greedy sequence is finished here;
+//   then pair items: one 4K-column chunk of a sampled sequence's draw each, sequence by sequence;
+//     a pair item loads its chunk of the Exp(1) row, waits until its sequence's step is published,
+//     then reads the rejected position's rows; the last pair item of a sequence to finish draws.
+// Workgroups are dispatched in increasing index order, so a pair item waits only for a step item
+// that has been dispatched before it and never waits itself: every wait ends. (Each wait is also
+// bounded by about a second of the constant clock, after which the error word is set and the item
+// gives up its work.)
+//
+// Results pass between workgroups (which may sit on different XCDs) through the workspace: records
+// are written with agent-scope relaxed stores (coherent across the XCDs without writing back an L2),
+// the writing wave waits until its stores have completed and then signals with an agent-scope store
+// or atomic; the reader reads the records with agent-scope loads. Atomics on one 256-byte line are
+// serialised (~12 ns each) and a polled line slows them further, so each sequence's counter and its
+// ready flag have lines of their own in the control words. The ready flag is set by the step and
+// cleared by the draw; the counter (the pair items) wraps to 0 with its last increment (atomic
+// increment with a limit); so each call leaves the control words as it found them: zero (the
+// workspace is zero-filled once, before its first use). They sit at the start of the workspace and
+// are sized for the largest batch, so that no call's records overlap them.
 struct AcceptArgs {
   RowSet rs;             // n0 = K+1 target rows, n1 = K draft rows
   int32_t K;
@@ -329,23 +353,79 @@ struct AcceptArgs {
   const float* u;        // [B, K]
   const float* E;        // [B, V]
   int64_t ldE;
+  unsigned* err;         // [1]   set if a wait ran out
+  unsigned* seqc;        // [1024 lines of 64] per sequence: its pair items counted in
+  unsigned* ready;       // [1024 lines of 64] per sequence: 1 from the step's publication to the draw
   Stat* stats;           // [B*(2K+1)][nch] chunk partials (logits mode)
-  Stat* mstats;          // [B*(2K+1)] merged row statistics (logits mode)
-  bool premerged;        // mstats are the caller's (from the LM head's epilogue): no statistics pass
+  Stat* mstats;          // [B*(2K+1)] merged row statistics (logits mode: the step's own)
+  bool premerged;        // mstats are the caller's (from the LM head's epilogue): no statistics launch
+  Stat* pairstat;        // [B][2] merged statistics of the step's target and draft rows j
   float* resid;          // [B][nchr] residual partial sums of the rejected row pair
-  float* cmax;           // [B][nchr][2] max of the cheap keys p/E and r/E per chunk (0: none positive)
-  int* ncand;            // [B][nchr][2] candidates of each draw (> NCAND: the list overflowed)
-  int* cand;             // [B][nchr][2][NCAND] their column indices, in no particular order
-  int* jpos;             // [B]
+  float* cmax;           // [B][nchr] max of the chunk's cheap keys (0: none positive; +inf: rescan)
+  int* ncand;            // [B][nchr] candidates of the chunk (> NCAND: the list overflowed)
+  int* cand;             // [B][nchr][NCAND] their column indices, in no particular order
+  int* jpos;             // [B]   the first rejected proposal, or k_eff
   int32_t* out_tokens;   // [B, K+1]
   int32_t* n_acc;        // [B]
   int32_t* seq_len;      // [B] or null
-  float* dbg_p;          // [B, K] or null: p_i(x_i) of the proposals i < k_eff (the accept test's p)
+  float* dbg_p;          // [B, K] or null: p_i(x_i) of the proposals the step tests (the accept test's p)
   float* dbg_q;          // [B, K] or null: q_i(x_i)
   float* dbg_s;          // [B] or null: the residual sum of the rejected position (0: none, or greedy)
 };
 
+constexpr int STEP_WAVES = THREADS / 64;
+constexpr int STEP_ROWS = 4;      // rows merged per wave and pass
+
+// agent-scope relaxed accesses: the records and flags that cross workgroups within the launch
+FS_DEVICE void st_ag(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+FS_DEVICE void st_ag(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+FS_DEVICE void st_ag(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+FS_DEVICE float ld_ag(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+FS_DEVICE int ld_ag(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+FS_DEVICE unsigned ld_ag(const unsigned* p) {
+  return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+FS_DEVICE void st_ag(Stat* p, const Stat& s) {
+  uint64_t* q = reinterpret_cast<uint64_t*>(p);
+  __hip_atomic_store(q, (uint64_t)__float_as_uint(s.m) | ((uint64_t)__float_as_uint(s.s) << 32), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, (uint64_t)__float_as_uint(s.av) | ((uint64_t)(uint32_t)s.ai << 32), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+FS_DEVICE Stat ld_ag(const Stat* p) {
+  uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<Stat*>(p));
+  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return Stat{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)), __uint_as_float((uint32_t)b),
+              (int)(uint32_t)(b >> 32)};
+}
+// This wave's stores have completed (vmcnt(0)), with no memory access moved across by the compiler.
+FS_DEVICE void stores_done() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Count one more completed item; true for the item that completes the count (the counter wraps to 0).
+FS_DEVICE bool count_in(unsigned* c, unsigned total) {
+  const unsigned old = __builtin_amdgcn_atomic_inc32(c, total - 1u, __ATOMIC_RELAXED, "agent");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return old == total - 1u;
+}
+
 FS_DEVICE int keff_of(const AcceptArgs& A, int b) { return A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K; }
+
+// Entry i of a region of 1024 lines of 64 words: word i / 1024 of line i % 1024.
+FS_DEVICE unsigned* ctl_word(unsigned* region, int64_t i) { return region + (i & 1023) * 64 + (i >> 10); }
+FS_DEVICE unsigned* seq_counter(const AcceptArgs& A, int b) { return ctl_word(A.seqc, b); }
+FS_DEVICE unsigned* ready_flag(const AcceptArgs& A, int b) { return ctl_word(A.ready, b); }
+
+
 
 FS_DEVICE void write_outputs(const AcceptArgs& A, int b, int j, int extra) {
   int32_t* o = A.out_tokens + (int64_t)b * (A.K + 1);
@@ -355,9 +435,6 @@ FS_DEVICE void write_outputs(const AcceptArgs& A, int b, int j, int extra) {
   A.n_acc[b] = j;
   if (A.seq_len) A.seq_len[b] = A.seq_len[b] + 1 + j;  // want = cached + 1 + len(accepted) (speculative.py:77)
 }
-
-constexpr int STEP_WAVES = 4;
-constexpr int STEP_ROWS = 4;    // rows merged per wave and pass
 
 // The chunk statistics of rows r (one wave, lane c holding chunk c) merged as merge_row does: the
 // max over the chunks, Σ s_c 2^(m_c - M) added in chunk order, the first argmax.
@@ -372,15 +449,16 @@ FS_DEVICE Stat merge_row_wave(const Stat& st, bool in, int nch) {
   return Stat{M, S, av, ai};
 }
 
-// The step of sequence b, run by one workgroup of STEP_WAVES waves: merge the row statistics
-// (logits mode: each wave takes STEP_ROWS rows at a time, one lane per chunk) into ms, then test
+// The step of sequence b, run by one whole workgroup: merge the row statistics (logits without given
+// statistics: each wave takes STEP_ROWS rows at a time, one lane per chunk) into ms, then test
 // every proposal at once, one lane each; the first rejection ends the walk (speculative.py:25-29).
-// The proposals and their logits are loaded before the merge, so the two latencies overlap. Writes
-// jpos (the first rejected proposal, or k_eff) and finishes a greedy sequence (the extra token is the
-// argmax of target row j).
+// The proposals and their logits are loaded before the merge, so the two latencies overlap. A greedy
+// sequence is finished here (the extra token is the argmax of target row j); for a sampled one the
+// rejected position j and its rows' statistics are published for the pair items.
 template <int DT, bool PROBS>
-FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* ms) {
+FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
   const int per = A.rs.n0 + A.rs.n1;
+  Stat* ms = A.mstats + (int64_t)b * per;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // No load waits for another: the proposals (wave 0, lane i: proposal i of the first 64) and the
   // chunk statistics are fetched for all K positions and rows, and k_eff only decides what is used.
@@ -397,14 +475,14 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* ms) {
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
   auto used = [&](int r) { return r < per && (r < A.rs.n0 ? r <= ke : (r - A.rs.n0) < ke); };
-  if (!PROBS && !A.premerged) {
+  if (!PROBS && !A.premerged) {   // the statistics launch's records
     if (A.nch <= 64) {
       for (int r0 = 0; r0 < per; r0 += STEP_WAVES * STEP_ROWS) {
         Stat st[STEP_ROWS];
 #pragma unroll
         for (int i = 0; i < STEP_ROWS; ++i) {
           const int r = r0 + w + STEP_WAVES * i;
-          if (r < per && lane < A.nch) st[i] = A.stats[((int64_t)b * per + r) * A.nch + lane];
+          if (used(r) && lane < A.nch) st[i] = A.stats[((int64_t)b * per + r) * A.nch + lane];
         }
 #pragma unroll
         for (int i = 0; i < STEP_ROWS; ++i) {
@@ -460,36 +538,19 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* ms) {
     if (rejected) j = i0 + __ffsll((unsigned long long)rejected) - 1;
   }
   if (threadIdx.x == 0) {
-    A.jpos[b] = j;
     if (!PROBS && T <= 0.f) {
       write_outputs(A, b, j, ms[j].ai);
       if (A.dbg_s) A.dbg_s[b] = 0.f;
+    } else {   // publish the outcome for the pair items
+      st_ag(A.jpos + b, j);
+      if (!PROBS) {
+        st_ag(A.pairstat + 2 * b, ms[j]);
+        if (j < ke) st_ag(A.pairstat + 2 * b + 1, ms[A.rs.n0 + j]);
+      }
+      stores_done();
+      st_ag(ready_flag(A, b), 1u);
     }
   }
-}
-
-// launch 1 (logits): per-(row, chunk) statistics of every row a sequence uses
-template <int DT>
-__global__ void __launch_bounds__(THREADS) accept_stats_kernel(AcceptArgs A) {
-  __shared__ float shf[THREADS / 64];
-  __shared__ int shi[THREADS / 64];
-  const int c = blockIdx.x;
-  const int rho = blockIdx.y;
-  const int per = A.rs.n0 + A.rs.n1;
-  const int b = rho / per, i = rho - b * per;
-  const int ke = keff_of(A, b);
-  if (i < A.rs.n0 ? i > ke : (i - A.rs.n0) >= ke) return;  // a row this sequence does not use
-  const float T = A.temps[b];
-  const auto* row = row_ptr<DT>(A.rs, b, i);
-  const Stat st = chunk_stat<DT>(row, c, A.V, T, shf, shi);
-  if (threadIdx.x == 0) A.stats[(int64_t)rho * A.nch + c] = st;
-}
-
-// launch 2: one workgroup per sequence runs its step (logits or probabilities)
-template <int DT, bool PROBS>
-__global__ void __launch_bounds__(64 * STEP_WAVES) accept_step_kernel(AcceptArgs A) {
-  const int b = blockIdx.x;
-  sequence_step<DT, PROBS>(A, b, A.mstats + (int64_t)b * (A.rs.n0 + A.rs.n1));
 }
 
 // The extra token is argmax_v fl(w_v / E_v) (multinomial as the argmax over Exp(1) noise), with
@@ -501,10 +562,10 @@ __global__ void __launch_bounds__(64 * STEP_WAVES) accept_step_kernel(AcceptArgs
 // p_v and q_v nearly cancel) plus, for bf16/f16 probabilities, the rounding of r / S to that dtype. A
 // column whose cheap key is below max · (1 - margin) cannot win, with the margin 8 or more times that
 // error (2^-18 for float32 arithmetic, 2^-6 for bf16 probabilities, 2^-8 for f16). Each chunk keeps the columns
-// within the margin of its own max (its candidates, nearly always one), and the final pass scores
-// them exactly. Chunks whose list overflowed, sequences whose max is too small for a relative bound,
-// and a rejection whose residual sums to 0 (its draw falls back to p / E, which the pass does not
-// rank) are rescanned exactly.
+// within the margin of its own max (its candidates, nearly always one), and the draw scores them
+// exactly. Chunks whose list overflowed, sequences whose max is too small for a relative bound, and a
+// rejection whose residual sums to 0 (its draw falls back to p / E, which the pass does not rank) are
+// rescanned exactly.
 constexpr int NCAND = 8;
 constexpr float CAND_MIN = 7.888609052210118e-31f;  // 2^-100: below it the bound is not relied on
 constexpr float MARGIN_F32 = 1.0f / 262144.0f;     // 2^-18
@@ -542,49 +603,76 @@ FS_DEVICE void collect(float key, int col, float th, int* n, int* list) {
   }
 }
 
-// launch 3: one pass over the rejected position's two rows and E, per chunk of CHR columns: the
-// residual partial sum and the max and candidates of the draw's keys (r / E at a rejection, p / E for
-// the bonus token)
+// What a pair item learns from its sequence's step (broadcast through LDS).
+struct PairCtx {
+  int j;
+  Stat sp, sq;
+  bool ok;   // false: the wait ran out (err is set; the item only counts itself in)
+};
+
+// Wait (thread 0) until sequence b's step is published, then read the outcome; bounded by ~1 s of
+// the constant 100 MHz clock. The step belongs to an item with a smaller index, which never waits.
+template <bool PROBS>
+FS_DEVICE void await_step(const AcceptArgs& A, int b, PairCtx* sh) {
+  if (threadIdx.x == 0) {
+    bool ok = true;
+    if (ld_ag(ready_flag(A, b)) == 0u) {
+      const uint64_t t0 = wall_clock64();
+      while (ld_ag(ready_flag(A, b)) == 0u) {
+        __builtin_amdgcn_s_sleep(16);
+        if (wall_clock64() - t0 > 100000000ull) {
+          ok = false;
+          st_ag(A.err, 1u);
+          break;
+        }
+      }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    sh->ok = ok;
+    if (ok) {
+      sh->j = ld_ag(A.jpos + b);
+      if (!PROBS) {
+        sh->sp = ld_ag(A.pairstat + 2 * b);
+        sh->sq = ld_ag(A.pairstat + 2 * b + 1);
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// One chunk of CHR columns of the draw of sequence b: the residual partial sum and the max and
+// candidates of the draw's keys (r / E at a rejection, p / E for the bonus token), written as records.
+// e: the chunk of the Exp(1) row, loaded before the wait for the step.
 template <int DT, bool PROBS>
-__global__ void __launch_bounds__(THREADS) accept_pair_kernel(AcceptArgs A) {
+FS_DEVICE void pair_chunk(const AcceptArgs& A, int b, int c, const PairCtx& pc, float (&e)[UNROLL_R][8], float* shf,
+                          int* sh_n, int* sh_c) {
   constexpr int PD = ProbType<DT, PROBS>::value;
-  __shared__ float shf[THREADS / 64];
-  __shared__ int sh_n[1];
-  __shared__ int sh_c[1][NCAND];
-  const int c = blockIdx.x, b = blockIdx.y;
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
-  if (!PROBS && T <= 0.f) return;  // greedy sequences were finished by the step
-  const int per = A.rs.n0 + A.rs.n1;
-  const Stat* ms = A.mstats + (int64_t)b * per;
-  const int j = A.jpos[b];
+  const int j = pc.j;
   const bool bonus = j >= ke;
   ProbFn sp, sq;
   if (!PROBS) {
-    sp = ProbFn(T, ms[j]);
-    if (!bonus) sq = ProbFn(T, ms[A.rs.n0 + j]);
+    sp = ProbFn(T, pc.sp);
+    if (!bonus) sq = ProbFn(T, pc.sq);
   }
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const auto* qr = bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j);
-  const float* er = A.E + (int64_t)b * A.ldE;
   const bool vec_ok = (A.V % VEC) == 0 &&
-                      (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr) |
-                         reinterpret_cast<uintptr_t>(er)) & 15) == 0);
-  float xp[UNROLL_R][8], xq[UNROLL_R][8], e[UNROLL_R][8];
+                      (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr)) & 15) == 0);
+  float xp[UNROLL_R][8], xq[UNROLL_R][8];
 #pragma unroll
   for (int u = 0; u < UNROLL_R; ++u) {   // every load of the chunk in flight before any arithmetic
     const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
     load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp[u]);
     if (!bonus) load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq[u]);
-    load8_f32(er, v0, A.V, vec_ok, e[u]);
   }
   if (!PROBS) {   // y = x / T once per element (the ProbFn arithmetic, divided ahead)
     divide_by_t(xp, T);
     if (!bonus) divide_by_t(xq, T);
   }
   // One set of cheap keys: p / E for the bonus token, r / E at a rejection. The p / E set of a
-  // rejection is needed only when the residual sums to 0; its chunks are then marked for an exact
-  // rescan instead of being collected here.
+  // rejection is needed only when the residual sums to 0; its chunks are then rescanned exactly.
   float ls = 0.f, mk = 0.f;
   float ak[UNROLL_R][8];   // cheap keys (0 past the row)
 #pragma unroll
@@ -615,68 +703,70 @@ __global__ void __launch_bounds__(THREADS) accept_pair_kernel(AcceptArgs A) {
   for (int u = 0; u < UNROLL_R; ++u) {
     const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) collect(ak[u][jj], (int)(v0 + jj), th, &sh_n[0], sh_c[0]);
+    for (int jj = 0; jj < 8; ++jj) collect(ak[u][jj], (int)(v0 + jj), th, &sh_n[0], sh_c);
   }
   __syncthreads();
   const int64_t o = (int64_t)b * A.nchr + c;
-  const int set = bonus ? 0 : 1;
-  if (threadIdx.x == 0) {
-    A.resid[o] = tot;
-    A.cmax[2 * o + set] = cm;
-    A.ncand[2 * o + set] = cm > 0.f ? sh_n[0] : 0;
-    A.cmax[2 * o + 1 - set] = bonus ? 0.f : INFINITY;      // rejection: p / E not collected, rescan
-    A.ncand[2 * o + 1 - set] = bonus ? 0 : NCAND + 1;
+  if (threadIdx.x < 64) {   // wave 0 writes the chunk's records
+    const int n = cm > 0.f ? sh_n[0] : 0;
+    if ((int)threadIdx.x < NCAND && (int)threadIdx.x < n) st_ag(A.cand + o * NCAND + threadIdx.x, sh_c[threadIdx.x]);
+    if (threadIdx.x == 0) {
+      st_ag(A.resid + o, tot);
+      st_ag(A.cmax + o, cm);
+      st_ag(A.ncand + o, n);
+    }
   }
-  if ((int)threadIdx.x < NCAND && (int)threadIdx.x < sh_n[0]) A.cand[(2 * o + set) * NCAND + threadIdx.x] = sh_c[0][threadIdx.x];
 }
 
-// launch 4: one wave per sampled sequence draws the extra token and writes the outputs and rollback:
-// the exact keys of the candidates of every chunk whose max reaches the margin (first index on ties),
-// with S summed over the chunks in increasing order.
+// The draw of sequence b, run by one wave once every pair item of b has written its records: S summed
+// over the chunks in increasing order, then the exact keys of the candidates of every chunk whose max
+// reaches the margin (first index on ties); writes the tokens, n_accepted and the rollback length.
 template <int DT, bool PROBS>
-__global__ void __launch_bounds__(64) accept_final_kernel(AcceptArgs A) {
+FS_DEVICE void final_draw(const AcceptArgs& A, int b, const PairCtx& pc) {
   constexpr int PD = ProbType<DT, PROBS>::value;
-  const int b = blockIdx.x, lane = threadIdx.x;
+  const int lane = threadIdx.x;
   const float T = PROBS ? 1.f : A.temps[b];
-  if (!PROBS && T <= 0.f) return;  // greedy sequences were finished by the step
   const int64_t o0 = (int64_t)b * A.nchr;
-  // the first 64 chunks' records are fetched together with the step's outcome; chunks past 64
-  // (vocabularies over 64 chunks) are fetched as they are needed
-  const bool in0 = lane < A.nchr;
-  const float rc0 = in0 ? A.resid[o0 + lane] : 0.f;
-  const float cm0[2] = {in0 ? A.cmax[2 * (o0 + lane)] : 0.f, in0 ? A.cmax[2 * (o0 + lane) + 1] : 0.f};
-  const int nc0[2] = {in0 ? A.ncand[2 * (o0 + lane)] : 0, in0 ? A.ncand[2 * (o0 + lane) + 1] : 0};
   const int ke = keff_of(A, b);
-  const int j = A.jpos[b];
+  const int j = pc.j;
   const bool bonus = j >= ke;
+  // the first 64 chunks' records are fetched together; chunks past 64 as they are needed
+  const bool in0 = lane < A.nchr;
+  const float rc0 = in0 ? ld_ag(A.resid + o0 + lane) : 0.f;
+  const float cmx0 = in0 ? ld_ag(A.cmax + o0 + lane) : 0.f;
+  const int nc0 = in0 ? ld_ag(A.ncand + o0 + lane) : 0;
   float s = 0.f;
   if (!bonus) {
     for (int c0 = 0; c0 < A.nchr; c0 += 64) {
-      const float rc = c0 == 0 ? rc0 : (c0 + lane < A.nchr ? A.resid[o0 + c0 + lane] : 0.f);
+      const float rc = c0 == 0 ? rc0 : (c0 + lane < A.nchr ? ld_ag(A.resid + o0 + c0 + lane) : 0.f);
       const int n = min(64, A.nchr - c0);
       for (int k = 0; k < n; ++k) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rc), k));
     }
     s = Elem<PD>::round(s);
   }
-  const int set = (bonus || !(s > 0.f)) ? 0 : 1;   // 0: w = p (speculative.py:31, 33), 1: w = r / S
+  // set p: w = p (speculative.py:31, 33): the bonus token, or a rejection whose residual sums to 0,
+  // whose chunks were not ranked for p / E and are all rescanned; set r: w = r / S
+  const bool set_r = !bonus && s > 0.f;
+  const bool rescan_all = !bonus && !set_r;
   auto cmax_at = [&](int c0) {
-    return c0 == 0 ? cm0[set] : (c0 + lane < A.nchr ? A.cmax[2 * (o0 + c0 + lane) + set] : 0.f);
+    return c0 == 0 ? cmx0 : (c0 + lane < A.nchr ? ld_ag(A.cmax + o0 + c0 + lane) : 0.f);
   };
   float gmax = 0.f;
-  for (int c0 = 0; c0 < A.nchr; c0 += 64) gmax = fmaxf(gmax, cmax_at(c0));
-  gmax = wave_max(gmax);
-  const bool trust = gmax >= CAND_MIN;
-  const float th = cand_threshold(gmax, set ? CandMargin<PD>::value : MARGIN_F32);
-  const int per = A.rs.n0 + A.rs.n1;
+  if (!rescan_all) {
+    for (int c0 = 0; c0 < A.nchr; c0 += 64) gmax = fmaxf(gmax, cmax_at(c0));
+    gmax = wave_max(gmax);
+  }
+  const bool trust = !rescan_all && gmax >= CAND_MIN;
+  const float th = cand_threshold(gmax, set_r ? CandMargin<PD>::value : MARGIN_F32);
   ProbFn sp, sq;
   if (!PROBS) {
-    sp = ProbFn(T, A.mstats[(int64_t)b * per + j]);
-    if (!bonus) sq = ProbFn(T, A.mstats[(int64_t)b * per + A.rs.n0 + j]);
+    sp = ProbFn(T, pc.sp);
+    if (!bonus) sq = ProbFn(T, pc.sq);
   }
   const auto* pr = row_ptr<DT>(A.rs, b, j);
   const PairRow<DT, PROBS> pair{pr, bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j), sp, sq};
   const float* er = A.E + (int64_t)b * A.ldE;
-  auto key = [&](int64_t col) { return set ? pair.key_r(col, s, er[col]) : pair.key_p(col, er[col]); };
+  auto key = [&](int64_t col) { return set_r ? pair.key_r(col, s, er[col]) : pair.key_p(col, er[col]); };
   float v = -INFINITY;
   int extra = 0x7fffffff;
   for (int c0 = 0; c0 < A.nchr; c0 += 64) {
@@ -684,7 +774,7 @@ __global__ void __launch_bounds__(64) accept_final_kernel(AcceptArgs A) {
     const int cl = c0 + lane;
     const bool in = cl < A.nchr;
     const bool keep = in && (!trust || cmax_at(c0) >= th);
-    const int ncl = c0 == 0 ? nc0[set] : (in ? A.ncand[2 * (o0 + cl) + set] : 0);
+    const int ncl = c0 == 0 ? nc0 : (in ? ld_ag(A.ncand + o0 + cl) : 0);
     uint64_t kept = __ballot(keep);
     while (kept) {
       const int k = __ffsll((unsigned long long)kept) - 1;
@@ -693,7 +783,7 @@ __global__ void __launch_bounds__(64) accept_final_kernel(AcceptArgs A) {
       const int n = __builtin_amdgcn_readlane(ncl, k);
       if (trust && n <= NCAND) {
         if (lane < n) {
-          const int col = A.cand[(2 * (o0 + c) + set) * NCAND + lane];
+          const int col = ld_ag(A.cand + (o0 + c) * NCAND + lane);
           argmax_merge(v, extra, key(col), col);
         }
       } else {   // exact rescan of the chunk
@@ -707,6 +797,62 @@ __global__ void __launch_bounds__(64) accept_final_kernel(AcceptArgs A) {
     write_outputs(A, b, j, extra);
     if (A.dbg_s) A.dbg_s[b] = s;
   }
+}
+
+// statistics launch (logits without given statistics): per-(row, chunk) statistics of every row a
+// sequence uses
+template <int DT>
+__global__ void __launch_bounds__(THREADS) accept_stats_kernel(AcceptArgs A) {
+  __shared__ float shf[THREADS / 64];
+  __shared__ int shi[THREADS / 64];
+  const int c = blockIdx.x;
+  const int rho = blockIdx.y;
+  const int per = A.rs.n0 + A.rs.n1;
+  const int b = rho / per, i = rho - b * per;
+  const int ke = keff_of(A, b);
+  if (i < A.rs.n0 ? i > ke : (i - A.rs.n0) >= ke) return;  // a row this sequence does not use
+  const float T = A.temps[b];
+  const auto* row = row_ptr<DT>(A.rs, b, i);
+  const Stat st = chunk_stat<DT>(row, c, A.V, T, shf, shi);
+  if (threadIdx.x == 0) A.stats[(int64_t)rho * A.nch + c] = st;
+}
+
+// B step items, then B * nchr pair items (sequence by sequence).
+template <int DT, bool PROBS>
+__global__ void __launch_bounds__(THREADS) accept_kernel(AcceptArgs A) {
+  __shared__ float shf[THREADS / 64];
+  __shared__ int sh_last;
+  __shared__ PairCtx sh_pc;
+  __shared__ int sh_n[1];
+  __shared__ int sh_c[NCAND];
+  if ((int)blockIdx.x < A.B) {
+    sequence_step<DT, PROBS>(A, blockIdx.x);
+    return;
+  }
+  const int item = blockIdx.x - A.B;
+  const int b = item / A.nchr, c = item - b * A.nchr;
+  // a pair item of a sampled sequence (greedy sequences were finished by their step)
+  const float T = PROBS ? 1.f : A.temps[b];
+  if (T <= 0.f) return;
+  float e[UNROLL_R][8];   // the chunk of the Exp(1) row does not depend on the step: loaded first
+  {
+    const float* er = A.E + (int64_t)b * A.ldE;
+    const bool vec_ok = (A.V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(er) & 15) == 0);
+#pragma unroll
+    for (int u = 0; u < UNROLL_R; ++u)
+      load8_f32(er, (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC, A.V, vec_ok, e[u]);
+  }
+  await_step<PROBS>(A, b, &sh_pc);
+  const PairCtx pc = sh_pc;
+  if (pc.ok) pair_chunk<DT, PROBS>(A, b, c, pc, e, shf, sh_n, sh_c);
+  if (threadIdx.x == 0) {
+    stores_done();
+    sh_last = count_in(seq_counter(A, b), (unsigned)A.nchr);   // the last pair item draws
+  }
+  __syncthreads();
+  if (!sh_last || threadIdx.x >= 64) return;
+  if (pc.ok) final_draw<DT, PROBS>(A, b, pc);
+  if (threadIdx.x == 0) st_ag(ready_flag(A, b), 0u);   // every pair item of b has passed its wait
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -784,41 +930,50 @@ int64_t nchunks(int64_t V) { return (V + CH - 1) / CH; }
 
 int64_t nchunks_r(int64_t V) { return (V + CHR - 1) / CHR; }
 
+// Control words at the start of the workspace (the error word; sequence counters and ready flags,
+// 1024 lines of 64 words each), so no call's records ever overlap them.
+constexpr int64_t CTL_REGION = 1024 * 64;
+constexpr int64_t CTL_BYTES = 256 + 2 * CTL_REGION * 4;
+
 int64_t accept_ws(int64_t B, int64_t K, int64_t V) {
   const int64_t nch = nchunks(V), nchr = nchunks_r(V);
   auto r = [](int64_t n) { return ((n + 255) / 256) * 256; };
-  return r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) + r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) +
-         r(B * nchr * 4) + 2 * r(B * nchr * 2 * 4) + r(B * nchr * 2 * NCAND * 4) + r(B * 4);
+  return CTL_BYTES + r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) + r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) +
+         r(B * 2 * (int64_t)sizeof(Stat)) + 3 * r(B * nchr * 4) + r(B * nchr * NCAND * 4) + r(B * 4);
 }
 
 void carve_accept(AcceptArgs& A, void* workspace, int64_t B, int64_t K, int nch, int nchr) {
   Carve cv{reinterpret_cast<char*>(workspace)};
+  unsigned* ctl = cv.take<unsigned>(64);
+  A.err = ctl + 1;
+  A.seqc = cv.take<unsigned>(CTL_REGION);
+  A.ready = cv.take<unsigned>(CTL_REGION);
   A.stats = cv.take<Stat>(B * (2 * K + 1) * nch);
   A.mstats = cv.take<Stat>(B * (2 * K + 1));
+  A.pairstat = cv.take<Stat>(B * 2);
   A.resid = cv.take<float>(B * nchr);
-  A.cmax = cv.take<float>(B * nchr * 2);
-  A.ncand = cv.take<int>(B * nchr * 2);
-  A.cand = cv.take<int>(B * nchr * 2 * NCAND);
+  A.cmax = cv.take<float>(B * nchr);
+  A.ncand = cv.take<int>(B * nchr);
+  A.cand = cv.take<int>(B * nchr * NCAND);
   A.jpos = cv.take<int>(B);
   A.premerged = false;
 }
 
 bool dtype_ok(int32_t dt) { return dt == FS_F32 || dt == FS_BF16 || dt == FS_F16; }
 
+// The statistics launch (logits without given statistics), then B step items and B * nchr pair items
+// in one launch.
 template <int DT>
 int launch_accept(const AcceptArgs& A, bool probs, hipStream_t s) {
-  const int per = A.rs.n0 + A.rs.n1;
-  const dim3 chunks((unsigned)A.nchr, (unsigned)A.B);
-  const dim3 finals((unsigned)A.B);
-  if (!probs) {
-    if (!A.premerged) accept_stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(A.B * per)), THREADS, 0, s>>>(A);
-    accept_step_kernel<DT, false><<<dim3((unsigned)A.B), 64 * STEP_WAVES, 0, s>>>(A);
-    accept_pair_kernel<DT, false><<<chunks, THREADS, 0, s>>>(A);
-    accept_final_kernel<DT, false><<<finals, 64, 0, s>>>(A);
+  const int64_t total = (int64_t)A.B * (1 + A.nchr);
+  if (total * THREADS >= ((int64_t)1 << 32))
+    return fs::arg_error("spec_accept: %lld work items exceed one launch", (long long)total);
+  if (probs) {
+    accept_kernel<DT, true><<<dim3((unsigned)total), THREADS, 0, s>>>(A);
   } else {
-    accept_step_kernel<DT, true><<<dim3((unsigned)A.B), 64 * STEP_WAVES, 0, s>>>(A);
-    accept_pair_kernel<DT, true><<<chunks, THREADS, 0, s>>>(A);
-    accept_final_kernel<DT, true><<<finals, 64, 0, s>>>(A);
+    const int per = A.rs.n0 + A.rs.n1;
+    if (!A.premerged) accept_stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(A.B * per)), THREADS, 0, s>>>(A);
+    accept_kernel<DT, false><<<dim3((unsigned)total), THREADS, 0, s>>>(A);
   }
   return fs::launch_status("spec_accept");
 }
@@ -997,9 +1152,11 @@ std::mutex scratch_mu;
 void* scratch_ptr[MAX_DEVICES] = {};   // the array's device address on each GPU, looked up once per device
 
 // The scratch address on the current device: hipGetSymbolAddress the first time a device calls, with
-// that device current; the cached pointer afterwards. In host code `scratch` only names a host-side
-// stand-in for the array, so kernels always receive this pointer.
-int scratch_on_current_device(void** out) {
+// that device current, then the acceptance's control words cleared on the caller's stream (the array
+// is zero when the code object loads; the clear makes that explicit); the cached pointer afterwards.
+// In host code `scratch` only names a host-side stand-in for the array, so kernels always receive this
+// pointer.
+int scratch_on_current_device(hipStream_t stream, void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
@@ -1009,11 +1166,25 @@ int scratch_on_current_device(void** out) {
   if (dev < 0 || dev >= MAX_DEVICES) return fs::arg_error("spec_accept_noalloc: device %d (at most %d)", dev, MAX_DEVICES);
   std::lock_guard<std::mutex> lock(scratch_mu);
   if (!scratch_ptr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) {
+      fs::set_error("spec_accept_noalloc: hipStreamIsCapturing: %s", hipGetErrorString(e));
+      return (int)e;
+    }
+    if (cs != hipStreamCaptureStatusNone)
+      return fs::arg_error("spec_accept_noalloc: the first call on device %d is being captured; make one call "
+                           "on this device before capturing", dev);
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr) {
       fs::set_error("spec_accept_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
       return e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+    }
+    e = hipMemsetAsync(p, 0, CTL_BYTES, stream);
+    if (e != hipSuccess) {
+      fs::set_error("spec_accept_noalloc: clearing the scratch: %s", hipGetErrorString(e));
+      return (int)e;
     }
     scratch_ptr[dev] = p;
   }
@@ -1035,8 +1206,8 @@ extern "C" int fs_spec_accept_noalloc(const void* tgt, int64_t tgt_sb, int64_t t
                "point holds per device; use fs_spec_accept with a workspace",
                B, K, (long long)V, (long long)need, (long long)NOALLOC_SCRATCH_BYTES);
   void* ws = nullptr;
-  if (int rc = scratch_on_current_device(&ws)) return rc;
-  // the acceptance rewrites every byte of its scratch that it reads later, so nothing is cleared
+  if (int rc = scratch_on_current_device(fs::as_stream(stream), &ws)) return rc;
+  // every call leaves the control words zero; the rest is rewritten before it is read
   return spec_accept_impl(tgt, tgt_sb, tgt_si, dft, dft_sb, dft_si, B, K, V, dtype, draft_tokens, k_eff, temperature, u,
                           E, ldE, out_tokens, n_accepted, seq_len, nullptr, nullptr, nullptr, row_stats, ws,
                           NOALLOC_SCRATCH_BYTES, stream);

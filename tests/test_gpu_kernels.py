@@ -867,6 +867,102 @@ def test_spec_accept_with_row_stats_bit_exact(temperature):
         assert out[bi, : len(acc) + 1].tolist() == acc + [extra], bi
 
 
+def _accept_control_words_zero():
+    """The acceptance's control words (the first 256 + 8 * 65536 bytes of its workspace) are zero."""
+    ws = [w for (name, _), w in ops._PERSISTENT.items() if name == "accept"]
+    assert ws and all(int(w[: 256 + 8 * 65536].count_nonzero()) == 0 for w in ws)
+
+
+def test_spec_accept_many_proposals_debug_outputs():
+    """K = 70 proposals, so the step tests them in two batches of 64 (f32 logits, T = 1): sequence 0
+    rejects proposal 10, sequence 1 accepts the first 64 and rejects proposal 66, sequence 2 accepts all
+    70 (bonus token), sequence 3 has an out-of-range proposal id at 3 (never accepted). Tokens and counts
+    against the oracle; the debug p(x), q(x) hold the oracle's values for every proposal the test
+    evaluated (all of the first 64 batch, the second batch only when the first was all accepted) and
+    stay untouched (NaN) for the others and for the out-of-range id; the residual sum. The workspace's
+    control words are zero again after the call."""
+    case("spec_accept K=70 debug")
+    b, k, v = 4, 70, 3001
+    g = torch.Generator().manual_seed(41)
+    tgt = torch.randn(b, k + 1, v, generator=g)
+    dft = tgt[:, :k] + 0.05 * torch.randn(b, k, v, generator=g)
+    p_all = [orc.probs_from_logits(tgt[i], 1.0) for i in range(b)]
+    q_all = [orc.probs_from_logits(dft[i], 1.0) for i in range(b)]
+    xs = torch.tensor([[orc.draw(q_all[i][j], orc.exp_noise(v, g)) for j in range(k)] for i in range(b)],
+                      dtype=torch.int32)
+    u = torch.zeros(b, k)          # u = 0 accepts any proposal with p(x) > 0
+    u[0, 10] = 1.0                 # u = 1 rejects whatever the ratio
+    u[1, 66] = 1.0
+    xs[3, 3] = v                   # out of range: never accepted
+    e = torch.empty(b, v).exponential_(generator=g)
+    temps = torch.ones(b)
+    out, n, dbg = ops.spec_accept(tgt.to(DEV), dft.to(DEV), xs.to(DEV), None, temps.to(DEV), u.to(DEV), e.to(DEV),
+                                  debug=True)
+    out, n = out.cpu(), n.cpu()
+    dbg = {key: val.cpu() for key, val in dbg.items()}
+    want_j = [10, 66, 70, 3]
+    for i in range(b):
+        xo, uo = xs[i].tolist(), u[i].clone()
+        if i == 3:
+            xo[3], uo[3] = 0, 1.0      # the same outcome: a rejection at 3
+        acc, extra = orc.verify_with_noise(p_all[i], q_all[i], xo, uo, e[i])
+        assert len(acc) == want_j[i] and int(n[i]) == len(acc), i
+        assert out[i, : len(acc) + 1].tolist() == acc + [extra], i
+        evaluated = set(range(64)) | (set(range(64, k)) if want_j[i] >= 64 else set())
+        for j in range(k):
+            x = int(xs[i, j])
+            if j in evaluated and x < v:
+                for key, ref in (("p_x", p_all[i][j, x]), ("q_x", q_all[i][j, x])):
+                    assert abs(float(dbg[key][i, j]) - float(ref)) <= 1e-5 * float(ref) + 1e-30, (i, j, key)
+            else:
+                assert math.isnan(float(dbg["p_x"][i, j])) and math.isnan(float(dbg["q_x"][i, j])), (i, j)
+        if want_j[i] < k:
+            tot = float(torch.clamp(p_all[i][want_j[i]] - q_all[i][want_j[i]], min=0).sum())
+            assert abs(float(dbg["res_sum"][i]) - tot) <= 1e-5 * tot, i
+        else:
+            assert float(dbg["res_sum"][i]) == 0.0
+    _accept_control_words_zero()
+
+
+def test_spec_accept_repeated_calls_leave_control_words_zero():
+    """Back-to-back calls of different shapes and modes on the one workspace (statistics pass, given
+    statistics, probabilities, greedy and sampled rows) each give the oracle's outcome, and the control
+    words are zero after each."""
+    case("spec_accept repeated calls")
+    g = torch.Generator().manual_seed(43)
+    for b, k, v, temp in ((3, 2, 700, 1.0), (9, 5, 9000, 0.0), (2, 0, 513, 0.8), (64, 6, 20000, 1.0)):
+        tgt = torch.randn(b, k + 1, v, generator=g) * 2
+        dft = tgt[:, :k] + torch.randn(b, k, v, generator=g)
+        xs = torch.randint(0, v, (b, k), generator=g, dtype=torch.int32)
+        u = torch.rand(b, k, generator=g)
+        e = torch.empty(b, v).exponential_(generator=g)
+        temps = torch.full((b,), temp)
+        for mode in ("logits", "stats"):
+            kw = {}
+            if mode == "stats":
+                rows = torch.cat([tgt, dft], 1)
+                y = rows / temp if temp > 0 else rows
+                mx = y.max(-1).values
+                kw["row_stats"] = _records(mx, torch.exp((y - mx[..., None]).double()).sum(-1).float(),
+                                           rows.max(-1).values, rows.argmax(-1)).to(DEV)
+            out, n = ops.spec_accept(tgt.to(DEV), dft.to(DEV), xs.to(DEV), None, temps.to(DEV), u.to(DEV), e.to(DEV),
+                                     **kw)
+            out, n = out.cpu(), n.cpu()
+            for i in range(b):
+                p = orc.probs_from_logits(tgt[i], temp)
+                q = orc.probs_from_logits(dft[i], temp)
+                acc, extra = orc.verify_with_noise(p, q, xs[i].tolist(), u[i], e[i])
+                assert int(n[i]) == len(acc) and out[i, : len(acc) + 1].tolist() == acc + [extra], (b, k, mode, i)
+            _accept_control_words_zero()
+        if k:
+            pr = torch.softmax(tgt[0], -1)
+            qr = torch.softmax(dft[0], -1)
+            got = _verify_probs_case(pr, qr, xs[0].tolist(), u[0], e[0])
+            want = orc.verify_with_noise(pr, qr, xs[0].tolist(), u[0], e[0])
+            assert got == (want[0] + [want[1]], len(want[0]))
+            _accept_control_words_zero()
+
+
 # ---- keyed random numbers (the speculative Engine's per-request streams) --------------------------------
 def test_keyed_noise_matches_the_philox_stream():
     """Uniforms bit-exact and Exp(1) variates within a few ulps of the numpy restatement of the Philox
