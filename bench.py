@@ -96,7 +96,8 @@ CFG_1B = dict(vocab_size=32000, d_model=2048, n_layers=16, n_heads=32, n_kv_head
 def engine_1b(args):
     """The 1B-shape continuous-batching workload: Engine(max_batch 16, k = 4, T = 0.7) with a 2-layer
     early-exit draft over 48 requests (prompts U[128, 1024], max_new_tokens U[64, 256]), the pool sized
-    below the peak demand so that recompute preemptions happen. Returns the figures as a dict."""
+    below the peak demand so that recompute preemptions happen, timed after a short warm-up run on
+    another Engine. Returns the figures as a dict."""
     import torch
 
     import forgeserve_amd as fa
@@ -114,6 +115,16 @@ def engine_1b(args):
     g = torch.Generator().manual_seed(args.seed + 1)
     reqs = [(torch.randint(0, cfg.vocab_size, (int(torch.randint(128, 1025, (1,), generator=g)),), generator=g).tolist(),
              int(torch.randint(64, 257, (1,), generator=g))) for _ in range(48)]
+    # warm-up: a short run of the same engine settings loads every kernel the run uses (the first launch
+    # of a kernel loads its code object); the timed engine then captures its own round graphs
+    warm = fa.Engine(target, num_blocks=600, block_size=16, max_batch=16, seed=args.seed + 7, draft=draft, k=4,
+                     key_layout="groups")
+    for p, _ in reqs[:20]:
+        warm.add_request(p, 12, temperature=0.7)
+    warm.run()
+    del warm
+    torch.cuda.synchronize()
+    time.sleep(0.25)   # an idle gap that marks where the timed run starts in a kernel trace
     eng = fa.Engine(target, num_blocks=600, block_size=16, max_batch=16, seed=args.seed, draft=draft, k=4,
                     key_layout="groups")
     for p, n in reqs:

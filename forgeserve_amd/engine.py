@@ -27,7 +27,7 @@ import torch
 
 from . import ops
 from ._lib import to_device
-from .model import ForgeModel
+from .model import ForgeModel, prefill_packed
 from .paged import BlockList, PagedKVPool, block_table
 from .sampling import exp_noise
 from .speculative import shared_layers, spec_round
@@ -47,6 +47,24 @@ class Request:
     blocks_d: List[int] = field(default_factory=BlockList)   # draft pool blocks (speculative engine)
     preempted: int = 0                                        # times this request was preempted
     stream: int = -1                                          # id of its random stream (speculative engine)
+
+
+class _TokenTail:
+    """What a round reads of a request's tokens (prompt + output): their number and the last two."""
+
+    __slots__ = ("n", "tail")
+
+    def __init__(self, req: "Request"):
+        self.n = len(req.prompt) + len(req.output)
+        self.tail = (req.prompt + req.output)[-2:] if len(req.output) < 2 else req.output[-2:]
+
+    def __len__(self) -> int:
+        return self.n
+
+    def __getitem__(self, i: int) -> int:
+        if not -len(self.tail) <= i < 0:
+            raise IndexError("only the last two tokens are kept")
+        return self.tail[i]
 
 
 def _stream_key(seed: int, rid: int, pos: int) -> int:
@@ -144,45 +162,80 @@ class Engine:
         return {rid: r.output for rid, r in self.requests.items()}
 
     def step(self) -> None:
+        """One engine step (engine.py:62-77); when the reference would prefill several waiting requests
+        in consecutive steps, those steps run here at once (_prefill_run)."""
+        if self.waiting and len(self.running) < self.max_batch and self._prefill_run():
+            return
         self.steps += 1
-        if self.waiting and len(self.running) < self.max_batch and self._try_prefill():
-            pass
-        elif self.running:
+        if self.running:
             if self.draft is not None:
                 self._spec_decode()
             else:
                 self._decode()
         elif self.waiting:
             raise RuntimeError("the head request cannot be scheduled: the block pool is too small")
-        used = self.pool.allocator.num_blocks - self.pool.allocator.num_free
+        self._note_peaks()
+
+    def _note_peaks(self, held_back: int = 0) -> None:
+        """Peak running requests and peak blocks in use after a step; held_back: blocks allocated ahead
+        for requests whose prefill steps come later."""
+        used = self.pool.allocator.num_blocks - self.pool.allocator.num_free - held_back
         self.peak_running, self.peak_blocks = max(self.peak_running, len(self.running)), max(self.peak_blocks, used)
 
     # ---- scheduling ---------------------------------------------------------------------------------
-    def _try_prefill(self) -> bool:
-        req = self.waiting[0]
-        tokens = req.prompt + req.output
-        need = self.pool.blocks_for(len(tokens))
+    PACK_TOKENS = 32768   # tokens per packed prefill forward
+
+    def _prefill_run(self) -> int:
+        """The prefill steps the reference would take one after another from here (engine.py:80-95): the
+        head request is prefilled while fewer than max_batch requests run and its blocks fit; each one
+        is a step of its own. They are admitted in the reference's order, computed in packed forwards
+        (model.prefill_packed, bit-identical to one forward per request), then each request's first
+        token is sampled in order and the step's counters updated as if it had run alone. Admission
+        counts every admitted request as running and its blocks as held, so a request the reference
+        would admit only because an earlier one finished at its first token is left to the next call.
+        Returns the number of steps taken (0: the head request does not fit)."""
         spec = self.draft is not None
-        need_d = self.pool_d.blocks_for(len(tokens)) if spec and not self.shared else 0
-        if need > self.pool.allocator.num_free or (spec and need_d > self.pool_d.allocator.num_free):
-            return False
-        self.waiting.popleft()
-        req.blocks = BlockList(self.pool.allocator.allocate(need))
-        positions = torch.arange(len(tokens))[None]
-        views = self.pool.views(torch.tensor([req.blocks]), positions)
-        logits = self.model(torch.tensor([tokens]), positions, views, last_only=True)
-        req.cached = len(tokens)
-        if spec:   # the draft's cache covers the same positions; the first token uses the request's stream
-            if not self.shared:   # (a shared draft's blocks were written by the model's prefill)
+        admitted = []
+        while self.waiting and len(self.running) + len(admitted) < self.max_batch:
+            req = self.waiting[0]
+            tokens = req.prompt + req.output
+            need = self.pool.blocks_for(len(tokens))
+            need_d = self.pool_d.blocks_for(len(tokens)) if spec and not self.shared else 0
+            if need > self.pool.allocator.num_free or (spec and need_d > self.pool_d.allocator.num_free):
+                break
+            self.waiting.popleft()
+            req.blocks = BlockList(self.pool.allocator.allocate(need))
+            if need_d:
                 req.blocks_d = BlockList(self.pool_d.allocator.allocate(need_d))
-                self.draft(torch.tensor([tokens]), positions,
-                           self.pool_d.views(torch.tensor([req.blocks_d]), positions), last_only=True)
-            self._append_keyed(req, logits[:, -1])
-        else:
-            self._append([req], logits[:, -1])
-        if not req.finished:
-            self.running.append(req)
-        return True
+            admitted.append((req, tokens))
+        if not admitted:
+            return 0
+        logits = []
+        i = 0
+        while i < len(admitted):   # packed forwards of up to PACK_TOKENS tokens
+            chunk, total = [], 0
+            while i < len(admitted) and (not chunk or total + len(admitted[i][1]) <= self.PACK_TOKENS):
+                chunk.append(admitted[i])
+                total += len(admitted[i][1])
+                i += 1
+            toks = [t for _, t in chunk]
+            logits.append(prefill_packed(self.model, self.pool, toks, [r.blocks for r, _ in chunk]))
+            if spec and not self.shared:   # (a shared draft's blocks were written by the model's prefill)
+                prefill_packed(self.draft, self.pool_d, toks, [r.blocks_d for r, _ in chunk])
+        logits = torch.cat(logits, 0)
+        held = sum(len(r.blocks) for r, _ in admitted)
+        for j, (req, tokens) in enumerate(admitted):
+            self.steps += 1
+            held -= len(req.blocks)
+            req.cached = len(tokens)
+            if spec:   # the first token uses the request's own stream
+                self._append_keyed(req, logits[j: j + 1])
+            else:
+                self._append([req], logits[j: j + 1])
+            if not req.finished:
+                self.running.append(req)
+            self._note_peaks(held)
+        return len(admitted)
 
     # ---- speculative decoding ---------------------------------------------------------------------
     def _remaining(self, req: Request) -> int:
@@ -227,12 +280,12 @@ class Engine:
             return
         batch = list(self.running)
         k_eff = [self._k_eff(r) for r in batch]
-        tokens = [r.prompt + r.output for r in batch]
+        tokens = [_TokenTail(r) for r in batch]
         temps = [float(r.temperature) for r in batch]
         draws = _KeyedDraws(batch, [len(t) for t in tokens], temps, self.seed, max(k_eff), self.cfg.vocab_size,
                             self.model.device)
         res = spec_round(self.model, self.draft, self.pool, self.pool_d, tokens, [r.blocks for r in batch],
-                         [r.blocks_d for r in batch], k_eff, temps, draws, graphs=self.graphs)
+                         [r.blocks_d for r in batch], k_eff, temps, draws, graphs=self.graphs, k=self.k)
         self.stats["rounds"] += 1
         for r, (req, row) in enumerate(zip(batch, res.tolist())):
             a = row[0]

@@ -452,7 +452,7 @@ def capture_phase_graphs(target, draft, pool_t, pool_d, st: "_RoundState") -> li
 @torch.no_grad()
 def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: List[List[int]],
                blocks_t: List[List[int]], blocks_d: List[List[int]], k_eff: List[int], temps: List[float],
-               draws, graphs: bool = True) -> torch.Tensor:
+               draws, graphs: bool = True, k: Optional[int] = None) -> torch.Tensor:
     """One draft-then-verify round (speculative.py:53-85) for b sequences whose caches hold positions
     0..n-2 (n = len(tokens[r])) and whose block lists cover positions up to n-1+k_eff[r].
 
@@ -463,9 +463,14 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     ignored, and a round with no sampled row draws nothing. With `graphs`, the round's kernels are
     captured in a HIP graph on the second round of a shape and replayed from then on (the same kernels
     on the same inputs: results are identical to running them one by one).
+    k: the round's number of draft steps (its graph shape), at least max(k_eff); default max(k_eff).
+    A caller whose rows' k_eff vary from round to round passes a fixed k so that its rounds share one
+    shape: rows with k_eff < k take no part in the steps past their k_eff.
     Returns (b, k+2) int32 on the host: n_accepted, then the committed tokens (-1 padded)."""
     b = len(tokens)
-    k = max(k_eff)
+    k = max(k_eff) if k is None else k
+    if k < max(k_eff):
+        raise ValueError(f"k = {k} < max(k_eff) = {max(k_eff)}")
     n = np.array([len(t) for t in tokens], dtype=np.int64)
     keff = np.array(k_eff, dtype=np.int64)
     limit = min(target.cfg.max_seq_len, draft.cfg.max_seq_len)
