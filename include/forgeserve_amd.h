@@ -174,12 +174,16 @@ int fs_paged_attention_varlen_reuse_plan(const void* q, int64_t q_st, int64_t q_
  * and, with R, a second rounding of the sum (nn.Linear then `x + ...`: model.py:77, 93, 105-106,
  * 119-120). Rows may be strided; columns are contiguous. A row of C does not depend on M (the
  * k-order, including any split of K, is a function of N and K only). workspace: at least
- * fs_gemm_workspace_size(M, N, K, dtype) bytes, 16-byte aligned, any contents (may be NULL when
- * that size is 0); calls that share a workspace must be ordered on one stream. */
+ * fs_gemm_workspace_size(M, N, K, dtype) bytes for this call's M, 16-byte aligned, any contents (may
+ * be NULL when that size is 0); calls that share a workspace must be ordered on one stream. */
 int fs_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, const void* R,
             int64_t ldr, int64_t M, int64_t N, int64_t K, int32_t dtype, void* workspace,
             int64_t workspace_bytes, void* stream);
 
+/* Workspace bytes fs_gemm needs for this M: splits * M * N * 4 for a shape that splits K, except that
+ * long batches (fs_gemm_serial) need none. The size therefore does not grow monotonically with M: a
+ * caller that keeps one workspace for calls of several M must query each M it uses (or the largest M
+ * for which fs_gemm_serial is 0) and keep the largest answer. */
 int64_t fs_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int32_t dtype);
 
 /* How many ways fs_gemm splits K for an (N, K) bf16 product (1: not split). A function of N and K only. */

@@ -1,8 +1,8 @@
 """fs_spec_accept_noalloc (the acceptance with its scratch in the library's fixed device array)
 against fs_spec_accept (the same kernels on a caller workspace): identical tokens, counts and
 rollback lengths, on two calls in a row, the second with a smaller batch, vocabulary and k, with and
-without the rows' statistics given; a shape whose scratch exceeds the array is refused before any
-launch."""
+without the rows' statistics given, and replayed from a HIP graph; a shape whose scratch exceeds the
+array is refused before any launch."""
 
 import pytest
 import torch
@@ -47,11 +47,12 @@ def _records(tgt, dft, temps):
     return torch.cat([f.contiguous().view(torch.int32), rows.argmax(-1).to(torch.int32)[..., None]], -1).contiguous()
 
 
-def _noalloc(tgt, dft, xs, k_eff, temps, u, e, seq, row_stats):
+def _noalloc(tgt, dft, xs, k_eff, temps, u, e, seq, row_stats, out=None, n=None):
     b, k1, v = tgt.shape
     k = k1 - 1
-    out = torch.full((b, k + 1), -7, dtype=torch.int32, device=DEV)
-    n = torch.full((b,), -7, dtype=torch.int32, device=DEV)
+    if out is None:
+        out = torch.full((b, k + 1), -7, dtype=torch.int32, device=DEV)
+        n = torch.full((b,), -7, dtype=torch.int32, device=DEV)
     rc = _lib.load().fs_spec_accept_noalloc(ptr(tgt), tgt.stride(0), tgt.stride(1), ptr(dft), dft.stride(0),
                                             dft.stride(1), b, k, v, DTYPE_CODE[tgt.dtype], ptr(xs), ptr(k_eff),
                                             ptr(temps), ptr(u), ptr(e), e.stride(0), ptr(row_stats), ptr(out), ptr(n),
@@ -73,6 +74,44 @@ def test_noalloc_acceptance_equals_the_workspace_entry_point(with_stats):
         assert torch.equal(got_out, want_out) and torch.equal(got_n, want_n)
         assert torch.equal(seq, seq_ref)
         assert int(want_n.sum()) > 0   # some proposals were accepted, so the accepted prefixes were compared
+
+
+@pytest.mark.parametrize("with_stats", [False, True])
+def test_noalloc_acceptance_under_graph_capture(with_stats):
+    """After an eager call (the first call on a device looks the scratch up and clears it, which must not
+    be captured), a call captured into a HIP graph and replayed three times, with eager work and
+    synchronisations between the replays, gives fs_spec_accept's outputs on every replay."""
+    case("spec_accept_noalloc graph", "row statistics" if with_stats else "statistics pass")
+    b, k, v = 16, 4, 32000
+    tgt, dft, xs, k_eff, temps, u, e, seq = _inputs(b, k, v, 5)
+    st = _records(tgt, dft, temps) if with_stats else None
+    seq0 = seq.clone()
+    seq_ref = seq0.clone()
+    want_out, want_n = ops.spec_accept(tgt, dft, xs, k_eff, temps, u, e, seq_len=seq_ref, row_stats=st)
+    out = torch.full((b, k + 1), -7, dtype=torch.int32, device=DEV)
+    n = torch.full((b,), -7, dtype=torch.int32, device=DEV)
+    _noalloc(tgt, dft, xs, k_eff, temps, u, e, seq, st, out, n)   # eager: the device's first call, if it is
+    torch.cuda.synchronize()
+    assert torch.equal(out, want_out) and torch.equal(n, want_n) and torch.equal(seq, seq_ref)
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g):
+            _noalloc(tgt, dft, xs, k_eff, temps, u, e, seq, st, out, n)
+    torch.cuda.current_stream().wait_stream(side)
+    x = torch.randn(512, 512, device=DEV)
+    for rep in range(3):
+        seq.copy_(seq0)
+        out.fill_(-7)
+        n.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        y = x @ x   # eager work between the replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, want_out) and torch.equal(n, want_n), rep
+        assert torch.equal(seq, seq_ref), rep
+        assert float(y.abs().sum()) > 0
 
 
 def test_noalloc_refuses_shapes_beyond_its_scratch():
