@@ -645,11 +645,12 @@ constexpr int PF_MIN_QTILES = 5; // a call with at least this many query tiles p
 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-// One 16-byte copy per lane straight into LDS (lane l lands at lds + 16 * l; the base is the same for
-// the whole wave). The copy is counted by vmcnt like any vector load; the waits below are explicit.
-FS_DEVICE void pf_dma16(const void* src, uint32_t lds) {
+// One 16-byte copy per lane straight into LDS from sbase + voff (a wave-uniform base in SGPRs and a
+// 32-bit unsigned per-lane byte offset; lane l lands at lds + 16 * l, the same base for the whole
+// wave). The copy is counted by vmcnt like any vector load; the waits below are explicit.
+FS_DEVICE void pf_dma16(const void* sbase, uint32_t voff, uint32_t lds) {
   const uint32_t l = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(l) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 template <int N>
@@ -662,6 +663,17 @@ FS_DEVICE void pf_wait_vm() {
 FS_DEVICE int pf_next_tile(int t, int n) {
   t += 8;
   return t < n ? t : (t & 7) + 1;
+}
+// The tile at ring position j (0 <= j < n): class v holds the n_v = ceil((n - v) / 8) tiles v, v + 8, ...
+FS_DEVICE int pf_ring_tile(int j, int n) {
+  int first = 0, t = 0;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const int nv = n > v ? ((n - 1 - v) >> 3) + 1 : 0;
+    if (j >= first && j < first + nv) t = v + 8 * (j - first);
+    first += nv;
+  }
+  return t;
 }
 
 template <int D, int BSZ>
@@ -767,9 +779,12 @@ attn_prefill_kernel(AttnParams P) {
       src_off = (int64_t)d * v_dim + 8 * h;
     }
   }
-  const u16* pool = reinterpret_cast<const u16*>(kpart ? P.kv.k : P.kv.v);
+  // copies read pool_h + (a tile's offset) + coff: the head's base is wave-uniform, the lane's part of
+  // a tile lies inside one block (a few KB), so it fits the 32-bit offset of the scalar-base form
+  const char* pool_h = reinterpret_cast<const char*>(kpart ? P.kv.k : P.kv.v) +
+                       2 * (int64_t)hkv * (kpart ? P.kv.k_head : P.kv.v_head);
+  const uint32_t coff = (uint32_t)(2 * src_off);
   const int64_t blk_stride = kpart ? P.kv.k_block : P.kv.v_block;
-  const int64_t lane_off = (int64_t)hkv * (kpart ? P.kv.k_head : P.kv.v_head) + src_off;
   const int64_t slot_mul = kpart ? P.kv.k_slot : 1;
   const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
   // this lane's operand reads inside a tile (bytes)
@@ -779,28 +794,33 @@ attn_prefill_kernel(AttnParams P) {
   for (int ks = 0; ks < KS; ++ks) koff[ks] = (kgrp ? (4 * ks + g) * 16 + l16 : l16 * CPR + ((4 * ks + g) ^ fk)) * 16;
   const int voff = TK + (2 * l16 + ((g >> 1) ^ ((l16 >> 3) & 1))) * 16 + 8 * (g & 1);
 
-  // copies walk the tiles PF_TILES at a time; a stage past the last tile copies the last tile again
-  int ct = 0, copied = 0;
+  // Copies walk the ring positions PF_TILES at a time; a position past the last tile copies the last
+  // tile again. Lane j holds the byte offset of the tile at ring position 64 * win + j (relative to
+  // pool_h), refreshed when a stage enters the next 64 positions, so a copy reads its tile's offset
+  // with two lane reads instead of walking the order and the table per copy.
+  static_assert(64 % PF_TILES == 0, "a stage's positions lie in one 64-position window");
+  uint32_t woff_lo = 0, woff_hi = 0;
+  auto refresh = [&](int win) {
+    const int t = pf_ring_tile(min(64 * win + lane, ntiles - 1), ntiles);
+    const int key0 = kbeg + 16 * t;
+    const int bi = key0 / BS;
+    const int ph = tbl[bi - blk0];
+    const int64_t pb = ph >= 0 ? ph : 0;         // unmapped: block 0, masked in attn_tile
+    const uint64_t o = (uint64_t)(2 * (pb * blk_stride + (int64_t)(key0 - bi * BS) * slot_mul));
+    woff_lo = (uint32_t)o;
+    woff_hi = (uint32_t)(o >> 32);
+  };
   auto issue = [&](int k) {
+    if ((k & (64 / PF_TILES - 1)) == 0) refresh(k / (64 / PF_TILES));
     const uint32_t base = ring0 + (uint32_t)((k % PF_NS) * STAGE) + (uint32_t)(p * 1024);
-    int tt[PF_TILES];
-#pragma unroll
-    for (int u = 0; u < PF_TILES; ++u) {
-      tt[u] = ct;
-      if (++copied < ntiles) ct = pf_next_tile(ct, ntiles);
-    }
-    // every table read of the stage before the first copy (each copy orders all memory accesses)
-    const u16* src[CPW];
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
-      const int key0 = kbeg + 16 * tt[(w + PF_WAVES * i) / CPT];
-      const int bi = key0 / BS;
-      const int ph = tbl[bi - blk0];
-      const int64_t pb = ph >= 0 ? ph : 0;       // unmapped: block 0, masked in attn_tile
-      src[i] = pool + pb * blk_stride + (int64_t)(key0 - bi * BS) * slot_mul;
+      const int u = (w + PF_WAVES * i) / CPT;   // the stage's tile this copy fills
+      const int j = (PF_TILES * k + u) & 63;
+      const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)woff_hi, j) << 32) |
+                         (uint32_t)__builtin_amdgcn_readlane((int)woff_lo, j);
+      pf_dma16(pool_h + o, coff, base + (uint32_t)(u * TB));
     }
-#pragma unroll
-    for (int i = 0; i < CPW; ++i) pf_dma16(src[i] + lane_off, base + (uint32_t)(((w + PF_WAVES * i) / CPT) * TB));
   };
   auto wait_stages = [&](int later) {
     if (later >= 2) pf_wait_vm<2 * CPW>();
