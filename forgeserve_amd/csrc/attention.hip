@@ -82,6 +82,21 @@ FS_DEVICE float max_across_groups(float x) {
   return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// max_across_groups of x0 and of x1 in three swaps: permlane16_swap of (x0, x1) yields {x0 rows
+// 0,1 ; x1 rows 0,1 ; x0 rows 2,3 ; x1 rows 2,3} as pairs, so one maximum leaves x0's groups 0/1 and
+// 2/3 in rows 0 and 2 and x1's in rows 1 and 3; permlane32_swap and a maximum complete both (x0's in
+// rows 0 and 2, x1's in rows 1 and 3), and a last permlane16_swap hands every lane both. The same
+// grouping, max(max(g0, g1), max(g2, g3)), as max_across_groups.
+FS_DEVICE void max_across_groups2(float x0, float x1, float& m0, float& m1) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x0), __float_as_uint(x1), false, false);
+  const float y = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  const float z = __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(z), __float_as_uint(z), false, false);
+  m0 = __uint_as_float(c[0]);
+  m1 = __uint_as_float(c[1]);
+}
+
 FS_DEVICE float sum_across_groups(float x) {
   auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
@@ -304,6 +319,62 @@ FS_DEVICE int rows_min_pos(const int (&rpos)[2], int nrows) {
 
 constexpr float REF_SLACK = 8.f;   // log2 units a tile's maximum may exceed the reference by
 
+// The softmax step of one tile for the lane's two rows: scores in log2 units (a key the row may not
+// see gets -inf; FULL: every row sees every key), the tile's row maxima, the references (a row's m
+// moves to the tile's maximum when that exceeds m by more than REF_SLACK), p = 2^(s - m) as bf16
+// MFMA operands, and l <- l * alpha + (the lane's sum of p), alpha = 2^(m_old - m_new) for a row
+// that moved, else 1. Returns whether any row of the wave moved; alpha is for the caller's rescale
+// of acc. LAZY: when no row moved, l <- l + sum, which is l * 1 + sum bit for bit.
+template <bool FULL, bool LAZY>
+FS_DEVICE bool tile_probs(const float4_t (&sc)[2], int j0, bool tile_valid, const int (&rpos)[2], float scale_log2,
+                          float (&m_run)[2], float (&l_run)[2], float (&alpha)[2], short4_t (&pf)[2]) {
+  const int g = (threadIdx.x & 63) >> 4;
+  float sv[2][4], x[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float v = sc[nt][e] * scale_log2;
+      sv[nt][e] = (FULL || (tile_valid && j0 + 4 * g + e <= rpos[nt])) ? v : -INFINITY;
+    }
+    x[nt] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sv[nt][0], sv[nt][1]),
+                                          __builtin_elementwise_maximum(sv[nt][2], sv[nt][3]));
+  }
+  float tmax[2];
+  max_across_groups2(x[0], x[1], tmax[0], tmax[1]);
+  bool mv[2];
+  float m_new[2], psum[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    // (-inf > x is false: a row that sees nothing here keeps its reference)
+    mv[nt] = tmax[nt] > m_run[nt] + REF_SLACK;
+    m_new[nt] = mv[nt] ? tmax[nt] : m_run[nt];
+    float pv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      pv[e] = (FULL || sv[nt][e] != -INFINITY) ? fast_exp2(sv[nt][e] - m_new[nt]) : 0.f;
+    pf[nt] = bf16_rne4(pv);
+    psum[nt] = (pv[0] + pv[1]) + (pv[2] + pv[3]);
+  }
+  const bool moved = __any(mv[0] || mv[1]);
+  if (!LAZY || moved) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      alpha[nt] = mv[nt] ? fast_exp2(m_run[nt] - m_new[nt]) : 1.f;
+      l_run[nt] = l_run[nt] * alpha[nt] + psum[nt];
+    }
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      alpha[nt] = 1.f;
+      l_run[nt] = l_run[nt] + psum[nt];
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) m_run[nt] = m_new[nt];
+  return moved;
+}
+
 template <int D, bool LAZY, bool BOTH = false>
 FS_DEVICE void attn_tile(const bf16x8_t (&kf)[D / 32], short4_t (&vf)[D / 16], int j0, bool tile_valid, int qmax,
                          const int (&rpos)[2], int rmin, bool two, const bf16x8_t (&qf)[2][D / 32],
@@ -345,52 +416,11 @@ FS_DEVICE void attn_tile(const bf16x8_t (&kf)[D / 32], short4_t (&vf)[D / 16], i
   }
   short4_t pf[2];
   float alpha[2];
-  bool moved = false;
-  if (full) {   // every key visible to every row: scores are finite, no masks
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      float sv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sv[e] = sc[nt][e] * scale_log2;
-      const float tmax = max_across_groups(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
-      const bool mv = tmax > m_run[nt] + REF_SLACK;
-      const float m_new = mv ? tmax : m_run[nt];
-      alpha[nt] = mv ? fast_exp2(m_run[nt] - m_new) : 1.f;
-      moved |= mv;
-      float pv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pv[e] = fast_exp2(sv[e] - m_new);
-      pf[nt] = bf16_rne4(pv);
-      l_run[nt] = l_run[nt] * alpha[nt] + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
-      m_run[nt] = m_new;
-    }
-  } else {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      float sv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = j0 + 4 * g + e;
-        const bool vis = tile_valid && key <= rpos[nt];
-        sv[e] = vis ? sc[nt][e] * scale_log2 : -INFINITY;
-      }
-      const float tmax = max_across_groups(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
-      // (-inf > x is false: a row that sees nothing here keeps its reference)
-      const bool mv = tmax > m_run[nt] + REF_SLACK;
-      const float m_new = mv ? tmax : m_run[nt];
-      alpha[nt] = mv ? fast_exp2(m_run[nt] - m_new) : 1.f;
-      moved |= mv;
-      float pv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pv[e] = (sv[e] == -INFINITY) ? 0.f : fast_exp2(sv[e] - m_new);
-      pf[nt] = bf16_rne4(pv);
-      l_run[nt] = l_run[nt] * alpha[nt] + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
-      m_run[nt] = m_new;
-    }
-  }
+  const bool moved = full ? tile_probs<true, LAZY>(sc, j0, tile_valid, rpos, scale_log2, m_run, l_run, alpha, pf)
+                          : tile_probs<false, LAZY>(sc, j0, tile_valid, rpos, scale_log2, m_run, l_run, alpha, pf);
   // The unit kernel rescales unconditionally (a branch there splits the accumulators' live ranges
-  // and spills at its register budget).
-  if (!LAZY || __any(moved)) {
+  // and spills at its register budget); alpha = 1 for every row that did not move.
+  if (!LAZY || moved) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
