@@ -1,8 +1,7 @@
 """Tensor-parallel context, kept as the size-1 case only (parallel.py:7-29 in the reference).
 
-This build runs the hot path on one GPU: a context of size 1 is a no-op, and larger sizes are
-refused rather than silently computing a partial result. How the path would shard across GPUs is
-described in DESIGN.md.
+The hot path runs on one GPU: a context of size 1 is a no-op, and larger sizes are refused rather
+than silently computing a partial result (no collective is implemented).
 """
 
 import torch

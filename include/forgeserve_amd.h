@@ -15,7 +15,7 @@
  * batches are this library's extension for batched speculation).
  *
  * The reference (forgeserve, pure PyTorch) has no C interface. Each entry point names the Python
- * function it replaces; INTEGRATION.md shows the ctypes binding a maintainer would add there.
+ * function it replaces; forgeserve_amd/_lib.py is a ctypes binding of every entry point.
  */
 #ifndef FORGESERVE_AMD_H
 #define FORGESERVE_AMD_H
