@@ -340,6 +340,22 @@ FS_DEVICE bool tile_probs(const float4_t (&sc)[2], int j0, bool tile_valid, cons
     x[nt] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sv[nt][0], sv[nt][1]),
                                           __builtin_elementwise_maximum(sv[nt][2], sv[nt][3]));
   }
+  // A row's tile maximum exceeds m + REF_SLACK exactly when one of its four lane groups' maxima does.
+  // LAZY: when no lane's does, no row moves (m_new = m, alpha = 1), and the reduction across the lane
+  // groups is skipped: the same values as the path below.
+  if (LAZY && !__any(x[0] > m_run[0] + REF_SLACK || x[1] > m_run[1] + REF_SLACK)) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      float pv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pv[e] = (FULL || sv[nt][e] != -INFINITY) ? fast_exp2(sv[nt][e] - m_run[nt]) : 0.f;
+      pf[nt] = bf16_rne4(pv);
+      alpha[nt] = 1.f;
+      l_run[nt] = l_run[nt] + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+    }
+    return false;
+  }
   float tmax[2];
   max_across_groups2(x[0], x[1], tmax[0], tmax[1]);
   bool mv[2];
