@@ -915,7 +915,7 @@ attn_prefill_kernel(AttnParams P) {
     __syncthreads();   // stage k has landed for every wave; stage k-1 is no longer being read
     if (k + PF_NS - 1 < nst) issue(k + PF_NS - 1);
     const char* st = ring + (k % PF_NS) * STAGE;
-#pragma unroll 1
+#pragma unroll
     for (int u = 0; u < PF_TILES; ++u) {
       if (k * PF_TILES + u >= ntiles) break;
       const int t = rt;
