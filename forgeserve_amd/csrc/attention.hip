@@ -71,22 +71,14 @@ struct AttnParams {
 // result is a normal float.
 FS_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// The maximum over the lanes l, l ^ 16, l ^ 32, l ^ 48. IEEE maximum (v_maximum3_f32, one instruction)
-// rather than fmaxf, which needs its permuted operands canonicalised first; the two agree on every
-// non-NaN input (the scores are finite or -inf) up to the sign of a zero maximum, which no result
-// depends on.
-FS_DEVICE float max_across_groups(float x) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
-// max_across_groups of x0 and of x1 in three swaps: permlane16_swap of (x0, x1) yields {x0 rows
-// 0,1 ; x1 rows 0,1 ; x0 rows 2,3 ; x1 rows 2,3} as pairs, so one maximum leaves x0's groups 0/1 and
-// 2/3 in rows 0 and 2 and x1's in rows 1 and 3; permlane32_swap and a maximum complete both (x0's in
-// rows 0 and 2, x1's in rows 1 and 3), and a last permlane16_swap hands every lane both. The same
-// grouping, max(max(g0, g1), max(g2, g3)), as max_across_groups.
+// The maxima over the lanes l, l ^ 16, l ^ 32, l ^ 48 of x0 and of x1, in three swaps:
+// permlane16_swap of (x0, x1) yields {x0 rows 0,1 ; x1 rows 0,1 ; x0 rows 2,3 ; x1 rows 2,3} as pairs,
+// so one maximum leaves x0's groups 0/1 and 2/3 in rows 0 and 2 and x1's in rows 1 and 3;
+// permlane32_swap and a maximum complete both (x0's in rows 0 and 2, x1's in rows 1 and 3), and a last
+// permlane16_swap hands every lane both. Every lane gets max(max(g0, g1), max(g2, g3)). IEEE maximum
+// (v_maximum3_f32, one instruction) rather than fmaxf, which needs its permuted operands canonicalised
+// first; the two agree on every non-NaN input (the scores are finite or -inf) up to the sign of a
+// zero maximum, which no result depends on.
 FS_DEVICE void max_across_groups2(float x0, float x1, float& m0, float& m1) {
   auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x0), __float_as_uint(x1), false, false);
   const float y = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
