@@ -30,7 +30,11 @@ namespace {
 
 constexpr int QTILE = 32;            // query rows per MFMA wave
 constexpr int PLAN_THREADS = 256;
-constexpr int64_t WS_HEADER = 256;    // workspace: item count, then the item list, then the partials
+constexpr int SPLIT_UNITS_MAX = 128;  // calls with at most this many units (half the CUs) split each in two
+// workspace: item count (bytes 0..255), the split units' arrival counters (one unsigned each), then
+// the item list, the chunk partials and the split units' published partials
+constexpr int64_t WS_COUNTERS = 256;
+constexpr int64_t WS_HEADER = WS_COUNTERS + 4 * SPLIT_UNITS_MAX;
 constexpr float LOG2E = 1.4426950408889634f;
 
 struct AttnParams {
@@ -61,6 +65,10 @@ struct AttnParams {
   // query tiles per plan item: 1 for the unit kernel, PF_WAVES for the prefill kernel (item.z is then
   // the index of a group of zgroup consecutive tiles, item.qmax the group's furthest query)
   int32_t zgroup;
+  // split units (attn_unit_half_kernel): one arrival counter per unit (zero between launches) and
+  // SPLIT_SLOTS published partials per unit
+  unsigned* split_cnt;
+  float* split_ws;
 };
 
 // Reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48) with the gfx950
@@ -144,6 +152,11 @@ FS_DEVICE int tile_chunks(const AttnParams& P, int qmax) {
 }
 
 constexpr int UNIT_WAVES = 8;                  // waves per unit workgroup
+constexpr int HALF_WAVES = UNIT_WAVES / 2;      // waves per workgroup of a split unit
+constexpr int SPLIT_SLOTS = 5;                  // published partials per split unit
+// floats of one published partial: m and l of the 32 rows, then acc as the LDS holds it (2 * D/16
+// (half, dim tile) pairs, 64 lanes, 4 values)
+constexpr int64_t split_slot_floats(int D) { return 2 * QTILE + (int64_t)QTILE * D; }
 constexpr int MAX_SPLIT = 2 * 64 * 16 * UNIT_WAVES;   // keys per chunk, at most: a wave's tiles fit two
                                                        // table entries per lane
 
@@ -174,6 +187,9 @@ FS_DEVICE int block_scan(int x, int* sh, int& tot) {
 }
 
 __global__ void __launch_bounds__(PLAN_THREADS) attn_plan_kernel(AttnParams P) {
+  // the split units' arrival counters start at zero (each unit's second half leaves its counter zero,
+  // so calls that reuse this plan find them so too)
+  for (int i = threadIdx.x; i < SPLIT_UNITS_MAX; i += PLAN_THREADS) st_ag(P.split_cnt + i, 0u);
   __shared__ int sh[PLAN_THREADS / 64];
   __shared__ int cursor[MAX_SPLIT / 16 + 1];   // last chunks by length in 16-key tiles
   const int tid = threadIdx.x;
@@ -665,6 +681,177 @@ attn_unit_kernel(AttnParams P) {
   }
 }
 
+// Device-coherent accesses to a split unit's published partials: buffer loads and stores with the sc1
+// cache policy (coherent at device scope, the encoding agent-scope atomics get), four floats at a time
+// where the data allows. Being plain accesses, the compiler issues a wave's loads together; the
+// barrier and the arrival count order them against the other half's stores.
+constexpr int CPOL_SC1 = 16;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+FS_DEVICE __amdgpu_buffer_rsrc_t slot_rsrc(float* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, bytes, 0x00020000);
+}
+FS_DEVICE void st4_dev(__amdgpu_buffer_rsrc_t r, int off, float4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, CPOL_SC1);
+}
+FS_DEVICE void st1_dev(__amdgpu_buffer_rsrc_t r, int off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, off, 0, CPOL_SC1);
+}
+FS_DEVICE float4_t ld4_dev(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_SC1));
+}
+FS_DEVICE float ld1_dev(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_SC1));
+}
+
+// A unit split in two: workgroup 2u + h (HALF_WAVES waves) builds classes HALF_WAVES*h + w of unit u,
+// each with the unit kernel's attn_wave_tiles, so that a call with few units keeps twice as many CUs
+// streaming. A row's result is the unit kernel's fold over classes 0..7 in increasing order: half 0
+// folds classes 0..3 and publishes that prefix (M, L, O), half 1 publishes its four class partials,
+// and the half that arrives second continues the fold through classes 4..7 and emits the rows. The
+// arrival is counted, never awaited; the published values cross XCDs through agent-scope accesses.
+template <int D, int BSZ>
+__global__ void __launch_bounds__(64 * HALF_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+attn_unit_half_kernel(AttnParams P) {
+  constexpr int MT = D / 16, NG = 2 * MT / HALF_WAVES;
+  constexpr int64_t SLOT = split_slot_floats(D);
+  __shared__ float4_t red_acc[HALF_WAVES][2 * MT][64];
+  __shared__ float red_m[HALF_WAVES][QTILE], red_l[HALF_WAVES][QTILE];
+  __shared__ int sh_last;
+  const int nkv = P.kv.n_kv_heads;
+  const int64_t unit = blockIdx.x >> 1;
+  const int h = blockIdx.x & 1;
+  const int64_t e_idx = unit / nkv;
+  const int hkv = (int)(unit - e_idx * nkv);
+  if (e_idx >= P.n_items[0]) return;   // uniform over the workgroup (and over both halves)
+  typedef __attribute__((address_space(4))) const AttnItem ConstItem;
+  ConstItem* ep = (ConstItem*)(uintptr_t)(P.items + e_idx);
+  const int b = ep->b, z = ep->z, s = ep->s, qmax = ep->qmax;
+  const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = z * QTILE;
+  const int nrows = min(QTILE, P.T * P.G - row0);
+  const int* posb = P.pos + (int64_t)b * P.T;
+  int rpos[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int r = 16 * nt + l16;
+    rpos[nt] = (r < nrows) ? posb[(row0 + r) / P.G] : -1;
+  }
+  const int kbeg = s * P.split;
+  const int kend = min(kbeg + P.split, qmax + 1);
+
+  attn_wave_tiles<D, BSZ>(P, b, kbeg, kend, qmax, row0, nrows, rpos, hkv, HALF_WAVES * h + w, red_acc[w], red_m[w],
+                          red_l[w]);
+  __syncthreads();
+
+  // this unit's published partials, SLOT floats each: slot 0 half 0's prefix, slots 1..4 classes 4..7
+  const __amdgpu_buffer_rsrc_t scr =
+      slot_rsrc(P.split_ws + unit * SPLIT_SLOTS * SLOT, (int)(SPLIT_SLOTS * SLOT * sizeof(float)));
+  auto m_at = [&](int slot, int r) { return (int)((slot * SLOT + r) * sizeof(float)); };
+  auto l_at = [&](int slot, int r) { return (int)((slot * SLOT + QTILE + r) * sizeof(float)); };
+  auto acc_at = [&](int slot, int gi) { return (int)((slot * SLOT + 2 * QTILE + (gi * 64 + lane) * 4) * sizeof(float)); };
+  float Mp[NG], Lp[NG];
+  float4_t op[NG];
+  if (h == 0) {   // classes 0..3 folded as the unit kernel folds them, then published
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int gi = w + HALF_WAVES * j, nt = gi / MT, mt = gi - nt * MT;
+      const int r = 16 * nt + l16;
+      float M = -INFINITY, L = 0.f;
+      float4_t o = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int v = 0; v < HALF_WAVES; ++v) {
+        float Mn, cM, cm;
+        if (!fold_weights(M, red_m[v][r], Mn, cM, cm)) continue;
+        L = fold_value(L, cM, red_l[v][r], cm);
+        const float4_t a = red_acc[v][gi][lane];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = fold_value(o[c], cM, a[c], cm);
+        M = Mn;
+      }
+      Mp[j] = M;
+      Lp[j] = L;
+      op[j] = o;
+      st4_dev(scr, acc_at(0, gi), o);
+      if (mt == 0 && g == 0) {
+        st1_dev(scr, m_at(0, r), M);
+        st1_dev(scr, l_at(0, r), L);
+      }
+    }
+  } else {   // this wave's class partial, as the unit kernel's LDS holds it
+#pragma unroll
+    for (int gi = 0; gi < 2 * MT; ++gi) st4_dev(scr, acc_at(1 + w, gi), red_acc[w][gi][lane]);
+    if (lane < QTILE) {
+      st1_dev(scr, m_at(1 + w, lane), red_m[w][lane]);
+      st1_dev(scr, l_at(1 + w, lane), red_l[w][lane]);
+    }
+  }
+  stores_done();
+  __syncthreads();   // every wave's published values have completed
+  if (threadIdx.x == 0) sh_last = count_in(P.split_cnt + unit, 2u);
+  __syncthreads();
+  if (!sh_last) return;
+
+  // the unit's second arrival: the fold continues through classes 4..7, then the rows are emitted
+  if (h == 0) {
+    float4_t a[NG][HALF_WAVES];   // every published value this wave needs, loaded at once
+    float m[NG][HALF_WAVES], l[NG][HALF_WAVES];
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int gi = w + HALF_WAVES * j, r = 16 * (gi / MT) + l16;
+#pragma unroll
+      for (int v = 0; v < HALF_WAVES; ++v) {
+        a[j][v] = ld4_dev(scr, acc_at(1 + v, gi));
+        m[j][v] = ld1_dev(scr, m_at(1 + v, r));
+        l[j][v] = ld1_dev(scr, l_at(1 + v, r));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int gi = w + HALF_WAVES * j, nt = gi / MT, mt = gi - nt * MT;
+      const int r = 16 * nt + l16;
+      float M = Mp[j], L = Lp[j];
+      float4_t o = op[j];
+#pragma unroll
+      for (int v = 0; v < HALF_WAVES; ++v) {
+        float Mn, cM, cm;
+        if (!fold_weights(M, m[j][v], Mn, cM, cm)) continue;
+        L = fold_value(L, cM, l[j][v], cm);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = fold_value(o[c], cM, a[j][v][c], cm);
+        M = Mn;
+      }
+      if (r < nrows) attn_emit<D>(P, b, s, kbeg, hkv, row0 + r, rpos[nt], mt, M, L, o);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int gi = w + HALF_WAVES * j, r = 16 * (gi / MT) + l16;
+      Mp[j] = ld1_dev(scr, m_at(0, r));
+      Lp[j] = ld1_dev(scr, l_at(0, r));
+      op[j] = ld4_dev(scr, acc_at(0, gi));
+    }
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int gi = w + HALF_WAVES * j, nt = gi / MT, mt = gi - nt * MT;
+      const int r = 16 * nt + l16;
+      float M = Mp[j], L = Lp[j];
+      float4_t o = op[j];
+#pragma unroll
+      for (int v = 0; v < HALF_WAVES; ++v) {
+        float Mn, cM, cm;
+        if (!fold_weights(M, red_m[v][r], Mn, cM, cm)) continue;
+        L = fold_value(L, cM, red_l[v][r], cm);
+        const float4_t av = red_acc[v][gi][lane];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = fold_value(o[c], cM, av[c], cm);
+        M = Mn;
+      }
+      if (r < nrows) attn_emit<D>(P, b, s, kbeg, hkv, row0 + r, rpos[nt], mt, M, L, o);
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------------
 // prefill kernel: one workgroup of PF_WAVES waves per (plan item of PF_WAVES query tiles, KV head)
 // ------------------------------------------------------------------------------------------------
@@ -1137,6 +1324,13 @@ int64_t max_items(int32_t B, int32_t T, int32_t n_heads, int32_t max_blocks, int
 
 int min_split() { return attn_split() < GENERIC_SPLIT ? attn_split() : GENERIC_SPLIT; }
 
+// Bytes of the split units' published partials for calls of at most `units` units (KV heads never
+// outnumber query heads, so items x n_heads bounds the units).
+int64_t split_bytes(int64_t units, int32_t head_dim) {
+  return (units < SPLIT_UNITS_MAX ? units : (int64_t)SPLIT_UNITS_MAX) * SPLIT_SLOTS * split_slot_floats(head_dim) *
+         (int64_t)sizeof(float);
+}
+
 }  // namespace
 
 extern "C" int32_t fs_paged_attention_split(void) { return attn_split(); }
@@ -1146,9 +1340,10 @@ extern "C" int64_t fs_paged_attention_workspace_size(int32_t B, int32_t T, int32
   if (B <= 0 || T <= 0 || n_heads <= 0 || head_dim <= 0 || max_blocks <= 0 || block_size <= 0) return 0;
   const int64_t rows = (int64_t)B * T * n_heads;
   const int64_t ns = nsplit_for(max_blocks, block_size, min_split());
-  const int64_t list =
-      (max_items(B, T, n_heads, max_blocks, block_size, min_split()) * (int64_t)sizeof(AttnItem) + 255) / 256 * 256;
-  return WS_HEADER + list + rows * ns * (head_dim + 2) * (int64_t)sizeof(float) + 256;
+  const int64_t items = max_items(B, T, n_heads, max_blocks, block_size, min_split());
+  const int64_t list = (items * (int64_t)sizeof(AttnItem) + 255) / 256 * 256;
+  const int64_t partials = (rows * ns * (head_dim + 2) * (int64_t)sizeof(float) + 255) / 256 * 256;
+  return WS_HEADER + list + partials + split_bytes(items * n_heads, head_dim) + 256;
 }
 
 namespace {
@@ -1212,12 +1407,16 @@ int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, con
   P.nsplit = (int32_t)nsplit_for(max_blocks, kv->block_size, P.split);
   const int64_t rows = (int64_t)B * T * n_heads;
   char* ws = reinterpret_cast<char*>(workspace);
-  const int64_t list =
-      (max_items(B, T, n_heads, max_blocks, kv->block_size, min_split()) * (int64_t)sizeof(AttnItem) + 255) / 256 * 256;
+  const int64_t items = max_items(B, T, n_heads, max_blocks, kv->block_size, min_split());
+  const int64_t list = (items * (int64_t)sizeof(AttnItem) + 255) / 256 * 256;
+  const int64_t ns_ws = nsplit_for(max_blocks, kv->block_size, min_split());   // >= P.nsplit
+  const int64_t partials = (rows * ns_ws * (kv->head_dim + 2) * (int64_t)sizeof(float) + 255) / 256 * 256;
   P.n_items = reinterpret_cast<int32_t*>(ws);
+  P.split_cnt = reinterpret_cast<unsigned*>(ws + WS_COUNTERS);
   P.items = reinterpret_cast<AttnItem*>(ws + WS_HEADER);
   P.ws_acc = reinterpret_cast<float*>(ws + WS_HEADER + list);
   P.ws_ml = P.ws_acc + rows * P.nsplit * kv->head_dim;
+  P.split_ws = reinterpret_cast<float*>(ws + WS_HEADER + list + partials);
   // direct outputs are stored 4 bf16 at a time
   P.direct = mfma && (reinterpret_cast<uintptr_t>(out) & 7) == 0 && o_sb % 4 == 0 && o_st % 4 == 0 && o_sh % 4 == 0;
   P.out = out;
@@ -1259,6 +1458,15 @@ int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, con
       } else {
         if (bs16) attn_prefill_kernel<64, 16><<<grid, threads, 0, st>>>(P);
         else attn_prefill_kernel<64, 0><<<grid, threads, 0, st>>>(P);
+      }
+    } else if (units <= SPLIT_UNITS_MAX) {   // few units: two workgroups each, to keep more CUs reading
+      const unsigned threads = 64 * HALF_WAVES;
+      if (kv->head_dim == 128) {
+        if (bs16) attn_unit_half_kernel<128, 16><<<2 * grid, threads, 0, st>>>(P);
+        else attn_unit_half_kernel<128, 0><<<2 * grid, threads, 0, st>>>(P);
+      } else {
+        if (bs16) attn_unit_half_kernel<64, 16><<<2 * grid, threads, 0, st>>>(P);
+        else attn_unit_half_kernel<64, 0><<<2 * grid, threads, 0, st>>>(P);
       }
     } else {
       const unsigned threads = 64 * UNIT_WAVES;

@@ -109,6 +109,36 @@ struct SoftmaxStat {
   int ai;
 };
 
+// Accesses that cross workgroups within one launch, whatever XCD each runs on: agent-scope relaxed
+// atomic stores and loads (global_store/global_load with the device-coherence bit: no L2 of one XCD
+// holds a value another XCD cannot see).
+FS_DEVICE void st_ag(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+FS_DEVICE void st_ag(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+FS_DEVICE void st_ag(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+FS_DEVICE float ld_ag(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+FS_DEVICE int ld_ag(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+FS_DEVICE unsigned ld_ag(const unsigned* p) {
+  return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// This wave's stores have completed (vmcnt(0)), with no memory access moved across by the compiler.
+FS_DEVICE void stores_done() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Count one more completed item; true for the item that completes the count (the counter wraps to 0).
+FS_DEVICE bool count_in(unsigned* c, unsigned total) {
+  const unsigned old = __builtin_amdgcn_atomic_inc32(c, total - 1u, __ATOMIC_RELAXED, "agent");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return old == total - 1u;
+}
+
 // ------------------------------------------------------------------------------------------------
 // host side: error reporting shared by every entry point
 // ------------------------------------------------------------------------------------------------

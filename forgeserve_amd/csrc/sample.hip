@@ -376,21 +376,9 @@ struct AcceptArgs {
 constexpr int STEP_WAVES = THREADS / 64;
 constexpr int STEP_ROWS = 4;      // rows merged per wave and pass
 
-// agent-scope relaxed accesses: the records and flags that cross workgroups within the launch
-FS_DEVICE void st_ag(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-FS_DEVICE void st_ag(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-FS_DEVICE void st_ag(unsigned* p, unsigned v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-FS_DEVICE float ld_ag(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-FS_DEVICE int ld_ag(const int* p) {
-  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-FS_DEVICE unsigned ld_ag(const unsigned* p) {
-  return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// agent-scope relaxed accesses (common.h) of the records that cross workgroups within the launch
+using ::ld_ag;
+using ::st_ag;
 FS_DEVICE void st_ag(Stat* p, const Stat& s) {
   uint64_t* q = reinterpret_cast<uint64_t*>(p);
   __hip_atomic_store(q, (uint64_t)__float_as_uint(s.m) | ((uint64_t)__float_as_uint(s.s) << 32), __ATOMIC_RELAXED,
@@ -404,18 +392,6 @@ FS_DEVICE Stat ld_ag(const Stat* p) {
   const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return Stat{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)), __uint_as_float((uint32_t)b),
               (int)(uint32_t)(b >> 32)};
-}
-// This wave's stores have completed (vmcnt(0)), with no memory access moved across by the compiler.
-FS_DEVICE void stores_done() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-// Count one more completed item; true for the item that completes the count (the counter wraps to 0).
-FS_DEVICE bool count_in(unsigned* c, unsigned total) {
-  const unsigned old = __builtin_amdgcn_atomic_inc32(c, total - 1u, __ATOMIC_RELAXED, "agent");
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  return old == total - 1u;
 }
 
 FS_DEVICE int keff_of(const AcceptArgs& A, int b) { return A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K; }

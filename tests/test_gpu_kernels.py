@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from forgeserve_amd import ops
+from forgeserve_amd import _lib, ops
 from oracle import reference_cpu as orc
 
 pytestmark = pytest.mark.gpu
@@ -404,6 +404,49 @@ def test_attention_prefill_kernel_equals_unit_kernel_bitwise(d, g, bs, lens, sta
         bad = (got != full[i, :n]).any(-1).any(-1).nonzero()
         assert bad.numel() == 0, f"row {i}: {bad.numel()} tokens differ, first {bad[:5].flatten().tolist()}"
         assert torch.count_nonzero(full[i, n:]) == 0   # padding tokens
+
+
+@pytest.mark.parametrize("d,g,bs,t,b,lo_ctx,hi_ctx,qscale", [
+    (128, 4, 16, 7, 200, 8, 2100, 1.0),       # verify windows, one chunk: outputs written directly
+    (128, 4, 16, 7, 200, 8, 2100, 12.0),      # scores spread over ~2^30: partial maxima far apart
+    (64, 8, 32, 5, 160, 3, 1500, 1.0),        # head_dim 64, block size 32
+    (128, 2, 48, 3, 140, 3, 1000, 1.0),       # blocks of 48 keys
+    (128, 4, 16, 1, 80, 16300, 16500, 1.0),   # decode over two chunks: partials for the combine
+])
+def test_attention_split_units_equal_unit_kernel_bitwise(d, g, bs, t, b, lo_ctx, hi_ctx, qscale):
+    """A call of at most 128 (item, KV head) units runs each unit as two workgroups of four waves (the
+    second to finish folds the other's partials in); a larger call runs one workgroup of eight waves per
+    unit. A row's outputs do not depend on which: the rows of one large call, recomputed in slices small
+    enough to split, give identical bits."""
+    case("attention split units == unit kernel", d, g, bs, t, b, qscale)
+    hkv = 2
+    gen = torch.Generator().manual_seed(d + g + bs + t + b)
+    ctx = torch.randint(lo_ctx, hi_ctx + 1, (b,), generator=gen)
+    ctx[: min(b, 4)] = torch.tensor([lo_ctx, hi_ctx, t, t + 1])[: min(b, 4)].clamp(min=t)
+    maxb = -(-int(ctx.max()) // bs)
+    nblocks = 2 * maxb + 7   # rows share blocks: tables draw from a small pool
+    tables = torch.randint(0, nblocks, (b, maxb), generator=gen)
+    k = torch.randn(nblocks, hkv, bs, d, generator=gen).bfloat16()
+    v = torch.randn(nblocks, hkv, bs, d, generator=gen).bfloat16()
+    q = (torch.randn(b, t, hkv * g, d, generator=gen) * qscale).bfloat16()
+    pos = ctx[:, None] - t + torch.arange(t)[None, :]
+    pos[1, 0] = -1   # a padding query
+    split = _lib.load().fs_paged_attention_split()
+    nsplit = -(-maxb * bs // split)
+    units = lambda rows: rows * (-(-t * g // 32)) * nsplit * hkv   # noqa: E731
+    step = max(r for r in range(1, b + 1) if units(r) <= 128)
+    assert units(b) > 128 and step < b
+    full, pool = _run_attention(q, k, v, tables, pos, torch.bfloat16, bs)
+    full = full.cpu()
+    lay, tab = pool.layout(0), tables.int().to(DEV)
+    for lo in range(0, b, step):
+        hi = min(b, lo + step)
+        part = ops.paged_attention(q[lo:hi].to(DEV), lay, tab[lo:hi], pos[lo:hi].int().to(DEV), 1.0 / math.sqrt(d))
+        bad = (part.cpu() != full[lo:hi]).any(-1).nonzero()
+        assert bad.numel() == 0, f"rows {lo}:{hi}: {bad.shape[0]} outputs differ, first {bad[:3].tolist()}"
+    assert torch.count_nonzero(full[1, 0]) == 0
+    ref = _oracle_attention(q[2:8], k, v, tables[2:8], pos[2:8], g)
+    assert rel_err(full[2:8].float(), ref) < 2e-2
 
 
 @pytest.mark.parametrize("d,g,bs,t,ctx,dtype", [
