@@ -30,7 +30,7 @@ from ._lib import to_device
 from .model import ForgeModel, prefill_packed
 from .paged import BlockList, PagedKVPool, block_table
 from .sampling import exp_noise
-from .speculative import shared_layers, spec_round
+from .speculative import _bucket, _launch_round, _round_state, shared_layers, spec_round
 
 
 @dataclass
@@ -92,10 +92,32 @@ class _KeyedDraws:
 
     def fill_round(self, noise_d, u, e):
         """noise_d (k, b, V) draft Exp(1) rows, u (b, >= k) uniforms, e (b, V) final Exp(1) rows."""
-        if noise_d.shape[0]:
-            ops.keyed_noise(self.keys, 0, noise_d, ops.RNG_EXP)
-        ops.keyed_noise(self.keys, SLOT_U, u, ops.RNG_UNIFORM)
-        ops.keyed_noise(self.keys, SLOT_FINAL, e, ops.RNG_EXP)
+        _fill_keyed(self.keys, noise_d, u, e)
+
+
+def _fill_keyed(keys, noise_d, u, e) -> None:
+    if noise_d.shape[0]:
+        ops.keyed_noise(keys, 0, noise_d, ops.RNG_EXP)
+    ops.keyed_noise(keys, SLOT_U, u, ops.RNG_UNIFORM)
+    ops.keyed_noise(keys, SLOT_FINAL, e, ops.RNG_EXP)
+
+
+class _DeviceKeyedDraws:
+    """_KeyedDraws for rounds queued before the host knows where they start. A request's key for the
+    round that starts at length n is its base (seed, request id) plus n, modulo 2^62; the lengths are
+    on the device (staged for the first round, advanced by fs_spec_advance after each), so each round's
+    keys are formed there just before its numbers are drawn: the keys _KeyedDraws would use."""
+
+    def __init__(self, reqs, seed, n_dev, dev):
+        base = [((seed * 1_000_003 + r.stream) * 1_000_033) % (1 << 62) for r in reqs]
+        self.base = to_device(torch.tensor(base, dtype=torch.int64), dev)
+        self.n = n_dev   # int32 (b,): the round state's lengths
+        self.keys = torch.empty_like(self.base)
+
+    def fill_round(self, noise_d, u, e):
+        torch.add(self.base, self.n, out=self.keys)
+        self.keys.bitwise_and_((1 << 62) - 1)
+        _fill_keyed(self.keys, noise_d, u, e)
 
 
 class Engine:
@@ -157,8 +179,12 @@ class Engine:
         return bool(self.waiting or self.running)
 
     def run(self) -> Dict[int, List[int]]:
+        """Steps until every request has finished (engine.py:57-60). With a draft, a run of speculative
+        rounds whose successors are known in advance is queued back to back (_queued_rounds): the same
+        steps, tokens, preemptions and counters as calling step() each time."""
         while self.has_work():
-            self.step()
+            if not (self.draft is not None and self._queued_rounds()):
+                self.step()
         return {rid: r.output for rid, r in self.requests.items()}
 
     def step(self) -> None:
@@ -298,6 +324,124 @@ class Engine:
             req.cached = len(req.prompt) + len(req.output) - 1
             if req.finished:
                 self.running.remove(req)
+
+    # ---- speculative rounds queued back to back ---------------------------------------------------
+    def _next_round_known(self, batch: List[Request]) -> bool:
+        """Whether, from the state at the start of a round over `batch`, the step after it is known to
+        be another round over the same requests: no row can finish in the round (each has at least
+        k + 2 tokens left and no EOS id; a round commits at most k + 1 tokens) and step() would not try
+        a prefill first (no request waits, or every batch slot is taken)."""
+        if self.waiting and len(self.running) < self.max_batch:
+            return False
+        return all(r.eos_id is None and self._remaining(r) >= self.k + 2 for r in batch)
+
+    def _reserve(self, batch: List[Request], spans: List[int]) -> Optional[int]:
+        """Blocks for `spans[i]` tokens of each request in both pools, taken in batch order, if they all
+        fit (else nothing is taken and None returned): the number taken from the model's pool."""
+        need_t = [max(0, self.pool.blocks_for(s) - len(r.blocks)) for r, s in zip(batch, spans)]
+        need_d = [] if self.shared else [max(0, self.pool_d.blocks_for(s) - len(r.blocks_d))
+                                         for r, s in zip(batch, spans)]
+        if sum(need_t) > self.pool.allocator.num_free or (need_d and sum(need_d) > self.pool_d.allocator.num_free):
+            return None
+        for r, n in zip(batch, need_t):
+            if n:
+                r.blocks += self.pool.allocator.allocate(n)
+        for r, n in zip(batch, need_d):
+            if n:
+                r.blocks_d += self.pool_d.allocator.allocate(n)
+        return sum(need_t)
+
+    def _trim(self, batch: List[Request], base: List[tuple]) -> None:
+        """Give back what a reservation took beyond the blocks _spec_decode would hold now: each
+        request keeps max(its blocks before the reservation, the blocks of its next window)."""
+        for r, (n_t, n_d) in zip(batch, base):
+            span = len(r.prompt) + len(r.output) + self._k_eff(r)
+            for pool, blocks, n0 in ((self.pool, r.blocks, n_t),) + (
+                    () if self.shared else ((self.pool_d, r.blocks_d, n_d),)):
+                keep = max(n0, pool.blocks_for(span))
+                if len(blocks) > keep:
+                    extra = blocks[keep:]
+                    del blocks[keep:]
+                    pool.allocator.release(extra)
+
+    def _queued_rounds(self) -> int:
+        """Speculative rounds queued back to back. While the step after the current round is known to
+        be another round over the same requests (_next_round_known), that round is launched before the
+        current one's tokens are read back: fs_spec_advance writes its inputs on the device and its keys
+        are formed there (_DeviceKeyedDraws), so the GPU does not wait for the host between rounds. A
+        queued round's blocks are reserved for the most tokens the round before it can commit; once
+        those are known the excess goes back (_trim), so each step leaves the pools' counts, the tokens
+        and the counters as step() leaves them (block ids may differ). Returns the steps taken; 0 when
+        the current step is not such a round (or its blocks would need a preemption): step() takes it."""
+        batch = list(self.running)
+        if not batch or not self._next_round_known(batch):
+            return 0
+        k, b = self.k, len(batch)
+        # the first round's blocks exactly as _spec_decode takes them (all fit: no preemption)
+        if self._reserve(batch, [len(r.prompt) + len(r.output) + k for r in batch]) is None:
+            return 0
+        blocks_t = [r.blocks for r in batch]
+        blocks_d = blocks_t if self.shared else [r.blocks_d for r in batch]
+        temps = [float(r.temperature) for r in batch]
+        st = _round_state(self.model, self.draft, self.pool, self.pool_d, b, k, blocks_t, blocks_d,
+                          any(t > 0 for t in temps))
+        st.stage([_TokenTail(r) for r in batch], [k] * b, temps, blocks_t, blocks_d, slot=0,
+                 budget=[self._remaining(r) for r in batch], eos=[-1] * b)
+        st.dev.copy_(st.hosts[0], non_blocking=True)
+        draws = _DeviceKeyedDraws(batch, self.seed, st.d["n"][:b], self.model.device)
+
+        def launch(j):
+            _launch_round(self.model, self.draft, self.pool, self.pool_d, st, b, draws, self.graphs, advance=True)
+            st.res_hosts[j % 2].copy_(st.res, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            return j, ev
+
+        pending = [launch(0)]
+        steps = 0
+        while pending:
+            j, ev = pending.pop(0)
+            held, base = 0, None
+            if self._next_round_known(batch):   # the host state is round j's start
+                # round j+1 starts at most k+1 tokens later and writes k past its start
+                spans = [min(len(r.prompt) + len(r.output) + 2 * k + 1, self.limit) for r in batch]
+                wt = _bucket(max(max(len(r.blocks), self.pool.blocks_for(x)) for r, x in zip(batch, spans)), 64)
+                wd = wt if self.shared else _bucket(
+                    max(max(len(r.blocks_d), self.pool_d.blocks_for(x)) for r, x in zip(batch, spans)), 64)
+                if (wt, wd) == (st.wt, st.wd):
+                    base = [(len(r.blocks), len(r.blocks_d)) for r in batch]
+                    held = self._reserve(batch, spans)
+                if held is not None and base is not None:
+                    slot = (j + 1) % 2
+                    st.stage_host(temps, blocks_t, blocks_d, slot)
+                    st.dev[st.host_off:].copy_(st.hosts[slot][st.host_off:], non_blocking=True)
+                    pending.append(launch(j + 1))
+                else:
+                    held, base = 0, None
+            # round j's tokens, as _spec_decode takes them (a request can finish only in a round with
+            # no successor queued)
+            ev.synchronize()
+            rows = st.res_hosts[j % 2][:b].tolist()
+            self.steps += 1
+            for req, row in zip(batch, rows):
+                a = row[0]
+                self.stats["proposed"] += self._k_eff(req)
+                self.stats["accepted"] += a
+                for token in row[1: a + 2]:
+                    self._push(req, token)
+                    if req.finished:
+                        break
+                req.cached = len(req.prompt) + len(req.output) - 1
+                if req.finished:
+                    if pending:
+                        raise RuntimeError("internal error: a request finished in a round with a successor queued")
+                    self.running.remove(req)
+            self.stats["rounds"] += 1
+            self._note_peaks(held)
+            if base is not None:
+                self._trim(batch, base)
+            steps += 1
+        return steps
 
     def _append_keyed(self, req: Request, logits: torch.Tensor) -> None:
         """Sample the token after a (re)prefill from the request's own stream."""

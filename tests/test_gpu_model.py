@@ -448,6 +448,63 @@ def test_graph_engine_equals_eager_engine(small):
     assert graph == eager
 
 
+def _engine_outcome(model, reqs, queued, **kw):
+    """Tokens, preemptions, steps, counters, peaks and free blocks of one Engine over `reqs`, driven by
+    run() (queued: it may queue rounds back to back) or by step() one call at a time (never queues);
+    also the steps run() took inside queued runs."""
+    e = fa.Engine(model, **kw)
+    ids = [e.add_request(p, n, temperature=t) for p, n, t in reqs]
+    taken = []
+    if queued:
+        inner = e._queued_rounds
+        e._queued_rounds = lambda: taken.append(inner()) or taken[-1]
+        out = e.run()
+    else:
+        while e.has_work():
+            e.step()
+        out = {rid: r.output for rid, r in e.requests.items()}
+    free = (e.pool.allocator.num_free, e.pool_d.allocator.num_free)
+    return ([out[i] for i in ids], e.preemptions, e.steps, dict(e.stats), e.peak_blocks, e.peak_running, free), taken
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_engine_run_queued_rounds_equal_single_steps(small, graphs):
+    """Engine.run() queues a speculative round behind the current one when the step after it is known
+    to be another round (no request can finish in it, none is admitted first, the blocks fit). It gives
+    what step() called once at a time gives: tokens (greedy and sampled), preemptions, steps, rounds,
+    proposals, peaks and free blocks, through a roomy pool, one tight enough to preempt, and a separate
+    draft pool; one request runs into max_seq_len."""
+    case("engine queued rounds", graphs)
+    draft = fa.early_exit_draft(small, 1)
+    reqs = [([1, 2, 3], 40, 0.8), ([9, 8, 7, 6], 35, 0.0), ([5, 5], 38, 1.0), ([30, 31, 32, 33, 34], 30, 0.6),
+            ([7] * 9, 36, 0.9), ([4, 4, 2], 33, 0.0), (list(range(20)), 60, 0.7)]
+    for num_blocks, share in ((96, None), (26, None), (96, False)):
+        kw = dict(num_blocks=num_blocks, block_size=4, max_batch=4, seed=5, draft=draft, k=3, graphs=graphs,
+                  share_kv=share)
+        got, taken = _engine_outcome(small, reqs, True, **kw)
+        want, _ = _engine_outcome(small, reqs, False, **kw)
+        assert got == want, num_blocks
+        assert max(taken) >= 3, taken   # runs of queued rounds did happen
+        if num_blocks == 26:
+            assert got[1] > 0
+
+
+def test_engine_run_queued_rounds_equal_single_steps_bf16(bf_target):
+    """The same on the bf16 kernels (fused head statistics, grouped keys, a 2-layer draft on the target's
+    cache), sampled and greedy requests through a pool that forces preemptions."""
+    case("engine queued rounds bf16")
+    draft = fa.early_exit_draft(bf_target, 2)
+    g = torch.Generator().manual_seed(21)
+    reqs = [(torch.randint(0, 1000, (int(n),), generator=g).tolist(), int(m), t)
+            for n, m, t in zip(torch.randint(2, 60, (9,), generator=g), torch.randint(20, 70, (9,), generator=g),
+                               [0.0, 0.7, 1.0, 0.0, 0.9, 0.5, 0.0, 0.8, 1.0])]
+    kw = dict(num_blocks=22, block_size=16, max_batch=5, seed=9, draft=draft, k=4, key_layout="groups")
+    got, taken = _engine_outcome(bf_target, reqs, True, **kw)
+    want, _ = _engine_outcome(bf_target, reqs, False, **kw)
+    assert got == want
+    assert max(taken) >= 3 and got[1] > 0, (taken, got[1])
+
+
 # ---- speculative engine (batched speculation inside Engine) ---------------------------------------------
 @pytest.mark.parametrize("key_layout", ["slots", "groups"])
 def test_spec_engine_greedy_matches_the_reference_engine(small, key_layout):
