@@ -30,7 +30,9 @@ namespace {
 
 constexpr int QTILE = 32;            // query rows per MFMA wave
 constexpr int PLAN_THREADS = 256;
-constexpr int SPLIT_UNITS_MAX = 128;  // calls with at most this many units (half the CUs) split each in two
+constexpr int SPLIT_UNITS_MAX = 128;  // calls with at most this many units (half the CUs) split each in two,
+constexpr int SPLIT_MIN_KEYS = 3072;  // when their tables can hold this many keys (shorter units do not repay
+                                      // the exchange)
 // workspace: item count (bytes 0..255), the split units' arrival counters (one unsigned each), then
 // the item list, the chunk partials and the split units' published partials
 constexpr int64_t WS_COUNTERS = 256;
@@ -1459,7 +1461,8 @@ int paged_attention(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, con
         if (bs16) attn_prefill_kernel<64, 16><<<grid, threads, 0, st>>>(P);
         else attn_prefill_kernel<64, 0><<<grid, threads, 0, st>>>(P);
       }
-    } else if (units <= SPLIT_UNITS_MAX) {   // few units: two workgroups each, to keep more CUs reading
+    } else if (units <= SPLIT_UNITS_MAX && (int64_t)max_blocks * kv->block_size >= SPLIT_MIN_KEYS) {
+      // few, possibly long units: two workgroups each, to keep more CUs reading
       const unsigned threads = 64 * HALF_WAVES;
       if (kv->head_dim == 128) {
         if (bs16) attn_unit_half_kernel<128, 16><<<2 * grid, threads, 0, st>>>(P);

@@ -407,17 +407,17 @@ def test_attention_prefill_kernel_equals_unit_kernel_bitwise(d, g, bs, lens, sta
 
 
 @pytest.mark.parametrize("d,g,bs,t,b,lo_ctx,hi_ctx,qscale", [
-    (128, 4, 16, 7, 200, 8, 2100, 1.0),       # verify windows, one chunk: outputs written directly
-    (128, 4, 16, 7, 200, 8, 2100, 12.0),      # scores spread over ~2^30: partial maxima far apart
-    (64, 8, 32, 5, 160, 3, 1500, 1.0),        # head_dim 64, block size 32
-    (128, 2, 48, 3, 140, 3, 1000, 1.0),       # blocks of 48 keys
+    (128, 4, 16, 7, 200, 8, 4200, 1.0),       # verify windows, one chunk: outputs written directly
+    (128, 4, 16, 7, 200, 8, 4200, 12.0),      # scores spread over ~2^30: partial maxima far apart
+    (64, 8, 32, 5, 160, 3, 4100, 1.0),        # head_dim 64, block size 32
+    (128, 2, 48, 3, 140, 3, 4100, 1.0),       # blocks of 48 keys
     (128, 4, 16, 1, 80, 16300, 16500, 1.0),   # decode over two chunks: partials for the combine
 ])
 def test_attention_split_units_equal_unit_kernel_bitwise(d, g, bs, t, b, lo_ctx, hi_ctx, qscale):
-    """A call of at most 128 (item, KV head) units runs each unit as two workgroups of four waves (the
-    second to finish folds the other's partials in); a larger call runs one workgroup of eight waves per
-    unit. A row's outputs do not depend on which: the rows of one large call, recomputed in slices small
-    enough to split, give identical bits."""
+    """A call of at most 128 (item, KV head) units whose tables hold at least 3072 keys runs each unit as
+    two workgroups of four waves (the second to finish folds the other's partials in); any other call
+    runs one workgroup of eight waves per unit. A row's outputs do not depend on which: the rows of one
+    large call, recomputed in slices small enough to split, give identical bits."""
     case("attention split units == unit kernel", d, g, bs, t, b, qscale)
     hkv = 2
     gen = torch.Generator().manual_seed(d + g + bs + t + b)
@@ -435,7 +435,7 @@ def test_attention_split_units_equal_unit_kernel_bitwise(d, g, bs, t, b, lo_ctx,
     nsplit = -(-maxb * bs // split)
     units = lambda rows: rows * (-(-t * g // 32)) * nsplit * hkv   # noqa: E731
     step = max(r for r in range(1, b + 1) if units(r) <= 128)
-    assert units(b) > 128 and step < b
+    assert units(b) > 128 and step < b and maxb * bs >= 3072
     full, pool = _run_attention(q, k, v, tables, pos, torch.bfloat16, bs)
     full = full.cpu()
     lay, tab = pool.layout(0), tables.int().to(DEV)
