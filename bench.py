@@ -144,7 +144,10 @@ def engine_1b(args):
            "peak_running": eng.peak_running, "peak_blocks": eng.peak_blocks,
            "acceptance": round(eng.stats["accepted"] / max(eng.stats["proposed"], 1), 4),
            "gpu_busy_fraction": profiled_figure("engine_1b_kernel_stats.md", "gpu_busy_fraction", float),
-           "gpu_busy_note": "kernel time / wall time of the same command under rocprofv3 --kernel-trace, "
+           "gpu_busy_fraction_unprofiled_wall": profiled_figure("engine_1b_kernel_stats.md",
+                                                                "gpu_busy_fraction_unprofiled_wall", float),
+           "gpu_busy_note": "kernel time / wall time of the same command under rocprofv3 --kernel-trace "
+                            "(and kernel time / the wall time without the profiler), "
                             "from profiles/engine_1b_kernel_stats.md"}
     del eng, target, draft
     torch.cuda.empty_cache()
