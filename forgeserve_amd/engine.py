@@ -79,45 +79,27 @@ SLOT_U, SLOT_FINAL, SLOT_PREFILL = 1 << 20, (1 << 20) + 1, (1 << 20) + 2
 
 class _KeyedDraws:
     """A speculative round's random numbers, one stream per request keyed by (seed, request id,
-    position), drawn on the device (ops.keyed_noise) straight into the round's buffers: the draft
-    steps' Exp(1) rows (slot i for step i), the uniforms u (slot SLOT_U, column i for proposal i) and
-    the final Exp(1) row (SLOT_FINAL). Every value depends only on the request's key, the slot and
-    the column, never on the batch or the round's k. Greedy requests get numbers too; the kernels
-    ignore them."""
+    position): the draft steps' Exp(1) rows (slot i for step i), the uniforms u (slot SLOT_U, column i
+    for proposal i) and the final Exp(1) row (SLOT_FINAL). Every value depends only on the request's
+    key, the slot and the column, never on the batch or the round's k. Greedy requests get numbers too;
+    the kernels ignore them. The round draws them on the device in its own kernels (and so inside its
+    HIP graph): the key of a round that starts at length n is base(seed, request id) + n modulo 2^62
+    (_stream_key), formed from the bases staged with the round's tables and the lengths the round
+    holds, staged by the host or advanced on the device (fs_spec_advance) for a queued round."""
 
-    def __init__(self, reqs, n, temps, seed, k, v, dev):
-        self.k, self.v, self.dev = k, v, dev
-        keys = torch.tensor([_stream_key(seed, r.stream, ni) for r, ni in zip(reqs, n)], dtype=torch.int64)
-        self.keys = to_device(keys, dev)
+    def __init__(self, reqs, seed):
+        self.kbase = [_stream_key(seed, r.stream, 0) for r in reqs]
 
-    def fill_round(self, noise_d, u, e):
-        """noise_d (k, b, V) draft Exp(1) rows, u (b, >= k) uniforms, e (b, V) final Exp(1) rows."""
-        _fill_keyed(self.keys, noise_d, u, e)
-
-
-def _fill_keyed(keys, noise_d, u, e) -> None:
-    if noise_d.shape[0]:
-        ops.keyed_noise(keys, 0, noise_d, ops.RNG_EXP)
-    ops.keyed_noise(keys, SLOT_U, u, ops.RNG_UNIFORM)
-    ops.keyed_noise(keys, SLOT_FINAL, e, ops.RNG_EXP)
-
-
-class _DeviceKeyedDraws:
-    """_KeyedDraws for rounds queued before the host knows where they start. A request's key for the
-    round that starts at length n is its base (seed, request id) plus n, modulo 2^62; the lengths are
-    on the device (staged for the first round, advanced by fs_spec_advance after each), so each round's
-    keys are formed there just before its numbers are drawn: the keys _KeyedDraws would use."""
-
-    def __init__(self, reqs, seed, n_dev, dev):
-        base = [((seed * 1_000_003 + r.stream) * 1_000_033) % (1 << 62) for r in reqs]
-        self.base = to_device(torch.tensor(base, dtype=torch.int64), dev)
-        self.n = n_dev   # int32 (b,): the round state's lengths
-        self.keys = torch.empty_like(self.base)
-
-    def fill_round(self, noise_d, u, e):
-        torch.add(self.base, self.n, out=self.keys)
-        self.keys.bitwise_and_((1 << 62) - 1)
-        _fill_keyed(self.keys, noise_d, u, e)
+    @staticmethod
+    def fill_in_round(st) -> None:
+        """Keys of st's rows from their staged bases and lengths, then their numbers (rows past the
+        batch have base 0 and length 0; the kernels ignore their numbers)."""
+        torch.add(st.d["kbase"], st.d["n"], out=st.keys)
+        st.keys.bitwise_and_((1 << 62) - 1)
+        if st.k:
+            ops.keyed_noise(st.keys, 0, st.noise_d[: st.k], ops.RNG_EXP)
+        ops.keyed_noise(st.keys, SLOT_U, st.u, ops.RNG_UNIFORM)
+        ops.keyed_noise(st.keys, SLOT_FINAL, st.e, ops.RNG_EXP)
 
 
 class Engine:
@@ -308,8 +290,7 @@ class Engine:
         k_eff = [self._k_eff(r) for r in batch]
         tokens = [_TokenTail(r) for r in batch]
         temps = [float(r.temperature) for r in batch]
-        draws = _KeyedDraws(batch, [len(t) for t in tokens], temps, self.seed, max(k_eff), self.cfg.vocab_size,
-                            self.model.device)
+        draws = _KeyedDraws(batch, self.seed)
         res = spec_round(self.model, self.draft, self.pool, self.pool_d, tokens, [r.blocks for r in batch],
                          [r.blocks_d for r in batch], k_eff, temps, draws, graphs=self.graphs, k=self.k)
         self.stats["rounds"] += 1
@@ -367,8 +348,8 @@ class Engine:
     def _queued_rounds(self) -> int:
         """Speculative rounds queued back to back. While the step after the current round is known to
         be another round over the same requests (_next_round_known), that round is launched before the
-        current one's tokens are read back: fs_spec_advance writes its inputs on the device and its keys
-        are formed there (_DeviceKeyedDraws), so the GPU does not wait for the host between rounds. A
+        current one's tokens are read back: fs_spec_advance writes its inputs on the device, where its
+        keys are formed too (_KeyedDraws), so the GPU does not wait for the host between rounds. A
         queued round's blocks are reserved for the most tokens the round before it can commit; once
         those are known the excess goes back (_trim), so each step leaves the pools' counts, the tokens
         and the counters as step() leaves them (block ids may differ). Returns the steps taken; 0 when
@@ -383,12 +364,12 @@ class Engine:
         blocks_t = [r.blocks for r in batch]
         blocks_d = blocks_t if self.shared else [r.blocks_d for r in batch]
         temps = [float(r.temperature) for r in batch]
+        draws = _KeyedDraws(batch, self.seed)
         st = _round_state(self.model, self.draft, self.pool, self.pool_d, b, k, blocks_t, blocks_d,
-                          any(t > 0 for t in temps))
+                          any(t > 0 for t in temps), keyed=True)
         st.stage([_TokenTail(r) for r in batch], [k] * b, temps, blocks_t, blocks_d, slot=0,
-                 budget=[self._remaining(r) for r in batch], eos=[-1] * b)
+                 budget=[self._remaining(r) for r in batch], eos=[-1] * b, kbase=draws.kbase)
         st.dev.copy_(st.hosts[0], non_blocking=True)
-        draws = _DeviceKeyedDraws(batch, self.seed, st.d["n"][:b], self.model.device)
 
         def launch(j):
             _launch_round(self.model, self.draft, self.pool, self.pool_d, st, b, draws, self.graphs, advance=True)
@@ -413,7 +394,7 @@ class Engine:
                     held = self._reserve(batch, spans)
                 if held is not None and base is not None:
                     slot = (j + 1) % 2
-                    st.stage_host(temps, blocks_t, blocks_d, slot)
+                    st.stage_host(temps, blocks_t, blocks_d, slot, draws.kbase)
                     st.dev[st.host_off:].copy_(st.hosts[slot][st.host_off:], non_blocking=True)
                     pending.append(launch(j + 1))
                 else:

@@ -172,9 +172,13 @@ class _RoundState:
     few graphs. Padding rows have k_eff 0 and only -1 positions (no KV write, no keys), temperature
     0, and their results are dropped."""
 
-    def __init__(self, dev, dtype, b, k, wt, wd, v, sampling, fused, parts_d, parts_t, n_shared=0, d_model=0):
+    def __init__(self, dev, dtype, b, k, wt, wd, v, sampling, fused, parts_d, parts_t, n_shared=0, d_model=0,
+                 keyed=False):
         self.b, self.k, self.wt, self.wd, self.v = b, k, wt, wd, v
         self.sampling, self.fused = sampling, fused
+        # keyed: the round's random numbers are drawn inside its kernels (and graph) from per-row key
+        # bases staged with the tables and the rows' lengths (the Engine's keyed streams)
+        self.keyed = keyed
         # a draft sharing the target's first n_shared blocks and their cache leaves its residual
         # streams after them here, one per fed token (the verify pass continues from them)
         self.n_shared = n_shared
@@ -182,7 +186,7 @@ class _RoundState:
         # staging: int64 ids [b, 2] (prev, last) and last [b]; int32 k_eff [b], draft positions [b, 2] (step 0)
         # then [k-1, b] (steps 1..k-1; [k, b], steps 0..k-1, with a shared cache), verify positions
         # [b, k+1], tables [b, wt] and [b, wd];
-        # float32 temperatures [b]
+        # float32 temperatures [b]; int64 key bases [b] (keyed rounds)
         # a draft on the target's cache feeds only `last` in step 0 (the verify pass has cached every
         # position before it), so its step 0 is staged with the others
         km = k if n_shared else max(k - 1, 0)
@@ -195,7 +199,7 @@ class _RoundState:
         spans = [("ids", np.int64, (b, 2)), ("last", np.int64, (b,)), ("keff", np.int32, (b,)), ("pos0", np.int32, (b, 2)),
                  ("posd", np.int32, (km, b)), ("posv", np.int32, (b, k + 1)), ("n", np.int32, (b,)),
                  ("budget", np.int32, (b,)), ("eos", np.int32, (b,)), ("done", np.int32, (b,)),
-                 ("temps", np.float32, (b,)), ("tab_t", np.int32, (b, wt))]
+                 ("temps", np.float32, (b,)), ("kbase", np.int64, (b,)), ("tab_t", np.int32, (b, wt))]
         if not n_shared:   # a draft on the target's cache reads the target's table
             spans.append(("tab_d", np.int32, (b, wd)))
         off, lay = 0, {}
@@ -221,6 +225,7 @@ class _RoundState:
         # what each table row of each host buffer holds: (block list, its version, entries copied)
         self._staged = [{}, {}]
         kk = max(k, 1)
+        self.keys = torch.zeros((b,), dtype=torch.int64, device=dev)
         self.u = torch.zeros((b, kk), dtype=torch.float32, device=dev)
         self.e = torch.ones((b, v), dtype=torch.float32, device=dev)
         self.noise_d = torch.ones((kk, b, v), dtype=torch.float32, device=dev) if sampling else None
@@ -238,10 +243,10 @@ class _RoundState:
         self.phase_graphs = None   # one graph per phase, captured on request (phase timing)
         self.uses = 0
 
-    def stage(self, tokens, k_eff, temps, blocks_t, blocks_d, slot=0, budget=None, eos=None) -> None:
+    def stage(self, tokens, k_eff, temps, blocks_t, blocks_d, slot=0, budget=None, eos=None, kbase=None) -> None:
         """Write one round's inputs into pinned staging buffer `slot` (rows past len(tokens) are padding,
         and done). budget, eos: each row's remaining tokens and EOS id (-1: none), for rounds whose
-        successors are advanced on the device."""
+        successors are advanced on the device. kbase: each row's key base (keyed rounds)."""
         b, k = len(tokens), self.k
         h = self.hs[slot]
         n = np.array([len(t) for t in tokens], dtype=np.int64)
@@ -272,13 +277,16 @@ class _RoundState:
         h["eos"][:b] = eos if eos is not None else -1
         h["done"].fill(1)
         h["done"][:b] = 0
-        self.stage_host(temps, blocks_t, blocks_d, slot)
+        self.stage_host(temps, blocks_t, blocks_d, slot, kbase)
 
-    def stage_host(self, temps, blocks_t, blocks_d, slot) -> None:
-        """The host-owned spans of staging buffer `slot`: temperatures and block tables."""
+    def stage_host(self, temps, blocks_t, blocks_d, slot, kbase=None) -> None:
+        """The host-owned spans of staging buffer `slot`: temperatures, key bases and block tables."""
         h, b = self.hs[slot], len(temps)
         h["temps"].fill(0)
         h["temps"][:b] = temps
+        h["kbase"].fill(0)
+        if kbase is not None:
+            h["kbase"][:b] = kbase
         tables = (("tab_t", blocks_t),) if self.n_shared else (("tab_t", blocks_t), ("tab_d", blocks_d))
         for name, lists in tables:
             # rows keep last round's entries: a row whose block list only grew gets its new blocks
@@ -358,8 +366,9 @@ _MAX_GRAPHS = 8
 
 
 def _round_state(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, b: int, k: int, blocks_t, blocks_d,
-                 sampling: bool) -> "_RoundState":
-    """The _RoundState of a round's shape (created on first use; at most _MAX_GRAPHS kept per pool)."""
+                 sampling: bool, keyed: bool = False) -> "_RoundState":
+    """The _RoundState of a round's shape (created on first use; at most _MAX_GRAPHS kept per pool).
+    keyed: the round draws its random numbers in its own kernels from staged key bases."""
     dev, dtype = target.device, target.dtype
     v = target.cfg.vocab_size
     n_shared = 0
@@ -377,10 +386,11 @@ def _round_state(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, b: int
     pd, pt = ops.row_stats_parts(bp, v, d), ops.row_stats_parts(bp * (k + 1), v, d)
     fused = dtype == torch.bfloat16 and k > 0 and pd > 0 and pt > 0
     cache = pool_t.__dict__.setdefault("_rounds", OrderedDict())
-    key = (bp, k, wt, wd, sampling, fused, _graph_key(target), _graph_key(draft), id(pool_d))
+    keyed = bool(keyed and sampling)
+    key = (bp, k, wt, wd, sampling, fused, keyed, _graph_key(target), _graph_key(draft), id(pool_d))
     st = cache.get(key)
     if st is None:
-        st = _RoundState(dev, dtype, bp, k, wt, wd, v, sampling, fused, pd, pt, n_shared, target.cfg.d_model)
+        st = _RoundState(dev, dtype, bp, k, wt, wd, v, sampling, fused, pd, pt, n_shared, target.cfg.d_model, keyed)
         cache[key] = st
         while len(cache) > _MAX_GRAPHS:
             cache.popitem(last=False)
@@ -391,16 +401,15 @@ def _round_state(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, b: int
 
 def _launch_round(target, draft, pool_t, pool_d, st: "_RoundState", b: int, draws, graphs: bool,
                   advance: bool = False) -> None:
-    """Queue one round on the current stream: the random numbers (drawn in the reference loop's order),
-    then the k+1 phases and, with `advance`, fs_spec_advance, which writes the next round's inputs from
-    this round's acceptance into the same device buffers. The kernels run eagerly on the shape's first
-    round and are captured in one graph on its second (one graph per value of `advance`), replayed after.
-    The round's result is st.res: (b, k+2) int32, n_accepted then the committed tokens."""
+    """Queue one round on the current stream: the random numbers (drawn in the reference loop's order,
+    or, for a keyed round, by its own first kernels), then the k+1 phases and, with `advance`,
+    fs_spec_advance, which writes the next round's inputs from this round's acceptance into the same
+    device buffers. The kernels run eagerly on the shape's first round and are captured in one graph on
+    its second (one graph per value of `advance`), replayed after. The round's result is st.res:
+    (b, k+2) int32, n_accepted then the committed tokens."""
     k = st.k
-    if st.sampling:
-        if hasattr(draws, "fill_round"):   # every row's numbers in one launch per kind
-            draws.fill_round(st.noise_d[:k, :b], st.u[:b], st.e[:b])
-        elif hasattr(draws, "draft_into"):
+    if st.sampling and not st.keyed:
+        if hasattr(draws, "draft_into"):
             for i in range(k):
                 draws.draft_into(i, st.noise_d[i, :b])
             draws.accept_into(st.u[:b], st.e[:b])
@@ -412,6 +421,8 @@ def _launch_round(target, draft, pool_t, pool_d, st: "_RoundState", b: int, draw
             st.e[:b].copy_(e)
 
     def kernels():
+        if st.keyed:   # the round's numbers from the staged key bases and the rows' lengths
+            draws.fill_in_round(st)
         for phase in range(k + 1):
             _round_phase(target, draft, pool_t, pool_d, st, phase)
         if advance:
@@ -460,7 +471,9 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     accepted round needs no catch-up forward; step i feeds x_{i-1} at n-1+i), one target verify pass
     over the k+1 window, one fused acceptance. `draws` supplies the randomness: draft(i) -> (b, V)
     Exp(1) noise of draft step i, accept() -> (u (b, k), E (b, V)); rows of greedy sequences are
-    ignored, and a round with no sampled row draws nothing. With `graphs`, the round's kernels are
+    ignored, and a round with no sampled row draws nothing. Draws with a `kbase` list instead have the
+    round draw its numbers in its own kernels: the bases are staged with the tables and
+    `draws.fill_in_round(st)` runs first in the round (captured with it). With `graphs`, the round's kernels are
     captured in a HIP graph on the second round of a shape and replayed from then on (the same kernels
     on the same inputs: results are identical to running them one by one).
     k: the round's number of draft steps (its graph shape), at least max(k_eff); default max(k_eff).
@@ -477,11 +490,12 @@ def spec_round(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, tokens: 
     if int((n - 1 + keff).max()) >= limit:
         raise ValueError(f"a round would write position {int((n - 1 + keff).max())} >= max_seq_len {limit}")
     sampling = any(t > 0 for t in temps)
-    st = _round_state(target, draft, pool_t, pool_d, b, k, blocks_t, blocks_d, sampling)
+    kbase = getattr(draws, "kbase", None)   # draws made inside the round from staged key bases
+    st = _round_state(target, draft, pool_t, pool_d, b, k, blocks_t, blocks_d, sampling, keyed=kbase is not None)
     if st.n_shared:
         blocks_d = blocks_t
     # host staging -> one copy, then the round
-    st.stage(tokens, k_eff, temps, blocks_t, blocks_d)
+    st.stage(tokens, k_eff, temps, blocks_t, blocks_d, kbase=kbase)
     st.dev.copy_(st.hosts[0], non_blocking=True)
     _launch_round(target, draft, pool_t, pool_d, st, b, draws, graphs)
     st.res_hosts[0].copy_(st.res, non_blocking=True)
