@@ -710,7 +710,8 @@ FS_DEVICE float ld1_dev(__amdgpu_buffer_rsrc_t r, int off) {
 // streaming. A row's result is the unit kernel's fold over classes 0..7 in increasing order: half 0
 // folds classes 0..3 and publishes that prefix (M, L, O), half 1 publishes its four class partials,
 // and the half that arrives second continues the fold through classes 4..7 and emits the rows. The
-// arrival is counted, never awaited; the published values cross XCDs through agent-scope accesses.
+// arrival is counted (an agent-scope atomic), never awaited; the published values cross XCDs through
+// device-coherent accesses.
 template <int D, int BSZ>
 __global__ void __launch_bounds__(64 * HALF_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 attn_unit_half_kernel(AttnParams P) {
