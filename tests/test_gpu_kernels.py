@@ -449,6 +449,47 @@ def test_attention_split_units_equal_unit_kernel_bitwise(d, g, bs, t, b, lo_ctx,
     assert rel_err(full[2:8].float(), ref) < 2e-2
 
 
+def test_attention_split_units_replayed_from_a_graph():
+    """The split-unit kernel captured in a HIP graph: each replay, with new queries copied in and other
+    attention calls run eagerly between replays, gives the eager call's bits (the arrival counters
+    are left at zero by every call, so a replay finds them as a fresh call does)."""
+    case("attention split units in a graph")
+    hkv, g, d, bs, t, b = 2, 4, 128, 16, 5, 8
+    gen = torch.Generator().manual_seed(77)
+    ctx = torch.randint(3000, 4201, (b,), generator=gen)
+    maxb = -(-int(ctx.max()) // bs)
+    assert maxb * bs >= 3072 and b * hkv <= 128   # the split kernel's conditions
+    nblocks = 2 * maxb + 7
+    tables = torch.randint(0, nblocks, (b, maxb), generator=gen)
+    k = torch.randn(nblocks, hkv, bs, d, generator=gen).bfloat16()
+    v = torch.randn(nblocks, hkv, bs, d, generator=gen).bfloat16()
+    qs = [torch.randn(b, t, hkv * g, d, generator=gen).bfloat16().to(DEV) for _ in range(3)]
+    pos = (ctx[:, None] - t + torch.arange(t)[None, :]).int().to(DEV)
+    _, pool = _run_attention(qs[0].cpu(), k, v, tables, pos.cpu(), torch.bfloat16, bs)
+    lay, tab = pool.layout(0), tables.int().to(DEV)
+    sc = 1.0 / math.sqrt(d)
+    want = [ops.paged_attention(q, lay, tab, pos, sc).clone() for q in qs]
+    q_in = qs[0].clone()
+    out = torch.empty_like(q_in)
+    ops.paged_attention(q_in, lay, tab, pos, sc, out=out)   # sizes the workspace before the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.paged_attention(q_in, lay, tab, pos, sc, out=out)
+    for rep in range(6):
+        i = rep % 3
+        q_in.copy_(qs[i])
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want[i]), rep
+        # eager calls between replays: a split call on other rows, and an unsplit one (a table of
+        # 2400 keys)
+        ops.paged_attention(qs[(i + 1) % 3][:3], lay, tab[:3], pos[:3], sc)
+        short = torch.full((b, 1), 2000 + rep, dtype=torch.int32, device=DEV)
+        ops.paged_attention(qs[i][:, :1].contiguous(), lay, tab[:, :150].contiguous(), short, sc)
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("d,g,bs,t,ctx,dtype", [
     (128, 4, 16, 7, [2048, 5000, 16380, 16389, 20000], torch.bfloat16),  # verify windows; two chunks + combine
     (128, 4, 16, 1, [300, 16385, 34000], torch.bfloat16),                # decode, 2 and 3 chunks
