@@ -1096,7 +1096,12 @@ attn_prefill_kernel(AttnParams P) {
     wait_stages(min(PF_NS - 2, nst - 1 - k));
     __syncthreads();   // stage k has landed for every wave; stage k-1 is no longer being read
     if (k + PF_NS - 1 < nst) issue(k + PF_NS - 1);
-    const char* st = ring + (k % PF_NS) * STAGE;
+    // the stage's operand addresses, once per stage: each tile's reads add only its constant offset
+    const uint32_t st_lds = ring0 + (uint32_t)((k % PF_NS) * STAGE);
+    uint32_t kad[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kad[ks] = st_lds + (uint32_t)koff[ks];
+    const uint32_t vad = st_lds + (uint32_t)voff;
 #pragma unroll
     for (int u = 0; u < PF_TILES; ++u) {
       if (k * PF_TILES + u >= ntiles) break;
@@ -1108,13 +1113,14 @@ attn_prefill_kernel(AttnParams P) {
         cur_v = t & 7;
       }
       if (t >= ntiles_w) continue;   // wholly above every query of the wave
-      const char* tk = st + u * TB;
+      typedef __attribute__((address_space(3))) const bf16x8_t LdsK;
+      typedef __attribute__((address_space(3))) const short4_t LdsV;
       bf16x8_t kf[KS];
       short4_t vf[MT];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const bf16x8_t*>(tk + koff[ks]);
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *(LdsK*)(uintptr_t)(kad[ks] + (uint32_t)(u * TB));
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) vf[mt] = *reinterpret_cast<const short4_t*>(tk + voff + mt * 16 * 32);
+      for (int mt = 0; mt < MT; ++mt) vf[mt] = *(LdsV*)(uintptr_t)(vad + (uint32_t)(u * TB + mt * 16 * 32));
       const int key0 = kbeg + 16 * t;
       const bool tv = all_mapped || tbl[key0 / BS - blk0] >= 0;
       attn_tile<D, true, true>(kf, vf, key0, tv, qmax, rpos, rmin, two, qf, P.scale_log2, acc, m_run, l_run);
