@@ -444,8 +444,7 @@ FS_DEVICE void attn_tile(const bf16x8_t (&kf)[D / 32], short4_t (&vf)[D / 16], i
   float alpha[2];
   const bool moved = full ? tile_probs<true, LAZY>(sc, j0, tile_valid, rpos, scale_log2, m_run, l_run, alpha, pf)
                           : tile_probs<false, LAZY>(sc, j0, tile_valid, rpos, scale_log2, m_run, l_run, alpha, pf);
-  // The unit kernel rescales unconditionally (a branch there splits the accumulators' live ranges
-  // and spills at its register budget); alpha = 1 for every row that did not move.
+  // LAZY: only when a row moved (alpha = 1 for every row that did not, so skipping it is exact)
   if (!LAZY || moved) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -576,7 +575,7 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
 
   const int rmin = rows_min_pos(rpos, nrows);
   auto consume = [&](int i, const bf16x8_t (&kf)[KS], short4_t (&vf)[MT]) {
-    attn_tile<D, false>(kf, vf, key0(i), block_of(i) >= 0, qmax, rpos, rmin, two, qf, P.scale_log2, acc, m_run,
+    attn_tile<D, true>(kf, vf, key0(i), block_of(i) >= 0, qmax, rpos, rmin, two, qf, P.scale_log2, acc, m_run,
                         l_run);
   };
 
