@@ -525,20 +525,23 @@ __device__ __attribute__((always_inline)) inline void attn_wave_tiles(const Attn
     return (v >= 0 && v < P.kv.num_blocks) ? v : -1;
   };
 
+  // the lane's element offsets inside a tile, fixed for the launch; a tile adds its wave-uniform base
+  const int64_t k_lane = (int64_t)l16 * k_slot + g * kgs;
+  const int64_t v_lane = (int64_t)l16 * v_dim + 4 * g;
   auto load_tile = [&](int i, bf16x8_t (&kd)[KS], short4_t (&vd)[MT]) {
     const int ic = max(min(i, nt_w - 1), 0);   // a wave without tiles reads block 0 and consumes nothing
     const int j0 = key0(ic);
     const int phys = block_of(ic);
     const int64_t pb = phys >= 0 ? phys : 0;
     const int slot0 = j0 - (j0 / BS) * BS;
-    const u16* kt_ = kpool + pb * P.kv.k_block + k_head_off + (int64_t)(slot0 + l16) * k_slot + g * kgs;
+    const u16* kt_ = kpool + (pb * P.kv.k_block + k_head_off + (int64_t)slot0 * k_slot) + k_lane;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)   // read once per launch: nontemporal
       kd[ks] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(kt_ + 4 * ks * kgs));
-    const u16* vt_ = vpool + pb * P.kv.v_block + v_head_off + slot0 + 4 * g;
+    const u16* vt_ = vpool + (pb * P.kv.v_block + v_head_off + slot0) + v_lane;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
-      vd[mt] = __builtin_nontemporal_load(reinterpret_cast<const short4_t*>(vt_ + (int64_t)(16 * mt + l16) * v_dim));
+      vd[mt] = __builtin_nontemporal_load(reinterpret_cast<const short4_t*>(vt_ + (int64_t)(16 * mt) * v_dim));
   };
 
   load_tile(0, kb0, vb0);
