@@ -232,12 +232,15 @@ class Engine:
                 prefill_packed(self.draft, self.pool_d, toks, [r.blocks_d for r, _ in chunk])
         logits = torch.cat(logits, 0)
         held = sum(len(r.blocks) for r, _ in admitted)
+        # the first tokens of a speculative engine's requests come from their own streams: drawn for all
+        # of them at once (each row's numbers depend only on its key)
+        firsts = self._first_tokens([r for r, _ in admitted], logits) if spec else None
         for j, (req, tokens) in enumerate(admitted):
             self.steps += 1
             held -= len(req.blocks)
             req.cached = len(tokens)
-            if spec:   # the first token uses the request's own stream
-                self._append_keyed(req, logits[j: j + 1])
+            if spec:
+                self._push(req, firsts[j])
             else:
                 self._append([req], logits[j: j + 1])
             if not req.finished:
@@ -424,17 +427,18 @@ class Engine:
             steps += 1
         return steps
 
-    def _append_keyed(self, req: Request, logits: torch.Tensor) -> None:
-        """Sample the token after a (re)prefill from the request's own stream."""
-        v = logits.shape[-1]
-        t = float(req.temperature)
+    def _first_tokens(self, reqs: List[Request], logits: torch.Tensor) -> List[int]:
+        """The token after each request's (re)prefill (logits row i for reqs[i]), from the request's own
+        stream at its current length (slot SLOT_PREFILL), in one launch; greedy rows take the argmax."""
+        v, dev = logits.shape[-1], logits.device
+        temps = [float(r.temperature) for r in reqs]
         noise = None
-        if t > 0:
-            pos = len(req.prompt) + len(req.output)
-            key = to_device(torch.tensor([_stream_key(self.seed, req.stream, pos)], dtype=torch.int64), logits.device)
-            noise = ops.keyed_noise(key, SLOT_PREFILL, torch.empty((1, v), device=logits.device), ops.RNG_EXP)
-        t_dev = to_device(torch.tensor([t], dtype=torch.float32), logits.device)
-        self._push(req, int(ops.sample_logits(logits, t_dev, noise).tolist()[0]))
+        if any(t > 0 for t in temps):
+            keys = [_stream_key(self.seed, r.stream, len(r.prompt) + len(r.output)) for r in reqs]
+            noise = ops.keyed_noise(to_device(torch.tensor(keys, dtype=torch.int64), dev), SLOT_PREFILL,
+                                    torch.empty((len(reqs), v), device=dev), ops.RNG_EXP)
+        t_dev = to_device(torch.tensor(temps, dtype=torch.float32), dev)
+        return ops.sample_logits(logits, t_dev, noise).tolist()
 
     def _push(self, req: Request, token: int) -> None:
         """Append one token; finish the request at max_new_tokens, EOS or max_seq_len (engine.py:132-139)."""
