@@ -649,7 +649,7 @@ def phase_times(torch, sb, reps=8):
     LM head with its statistics epilogue, statistics merges, fused acceptance) and the draft steps. The
     replays rewrite what the last round wrote (same keys, values, logits and outputs)."""
     st = next(reversed(sb.pool_t.__dict__.get("_rounds", {}).values()), None)
-    if st is None or not st.graphs:
+    if st is None or st.graph is None:
         return None
     from forgeserve_amd.speculative import capture_phase_graphs
     graphs = capture_phase_graphs(sb.target, sb.draft, sb.pool_t, sb.pool_d, st)

@@ -375,7 +375,7 @@ class Engine:
         st.dev.copy_(st.hosts[0], non_blocking=True)
 
         def launch(j):
-            _launch_round(self.model, self.draft, self.pool, self.pool_d, st, b, draws, self.graphs, advance=True)
+            _launch_round(self.model, self.draft, self.pool, self.pool_d, st, b, draws, self.graphs)
             st.res_hosts[j % 2].copy_(st.res, non_blocking=True)
             ev = torch.cuda.Event()
             ev.record()

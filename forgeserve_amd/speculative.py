@@ -239,7 +239,7 @@ class _RoundState:
             self.row_stats = torch.empty((b, 2 * k + 1, 4), dtype=I32, device=dev)
         self.res_hosts = [torch.empty((b, k + 2), dtype=torch.int32, pin_memory=True) for _ in range(2)]
         self.res = torch.empty((b, k + 2), dtype=I32, device=dev)   # the verify phase's output
-        self.graphs = {}           # the round's k+1 phases (and, keyed True, fs_spec_advance) in one graph
+        self.graph = None          # the round's kernels (k+1 phases, fs_spec_advance) in one graph
         self.phase_graphs = None   # one graph per phase, captured on request (phase timing)
         self.uses = 0
 
@@ -271,8 +271,10 @@ class _RoundState:
         h["posv"][:b] = np.where(t_ <= keff[:, None], n[:, None] - 1 + t_, -1)
         h["n"].fill(0)
         h["n"][:b] = n
+        # (without a budget the rows stay live in the round's device-side advance: its next-round
+        # inputs are then the real round's successor, which a host-staged next round overwrites)
         h["budget"].fill(0)
-        h["budget"][:b] = budget if budget is not None else 0
+        h["budget"][:b] = budget if budget is not None else 1 << 30
         h["eos"].fill(-1)
         h["eos"][:b] = eos if eos is not None else -1
         h["done"].fill(1)
@@ -399,14 +401,13 @@ def _round_state(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, b: int
     return st
 
 
-def _launch_round(target, draft, pool_t, pool_d, st: "_RoundState", b: int, draws, graphs: bool,
-                  advance: bool = False) -> None:
+def _launch_round(target, draft, pool_t, pool_d, st: "_RoundState", b: int, draws, graphs: bool) -> None:
     """Queue one round on the current stream: the random numbers (drawn in the reference loop's order,
-    or, for a keyed round, by its own first kernels), then the k+1 phases and, with `advance`,
-    fs_spec_advance, which writes the next round's inputs from this round's acceptance into the same
-    device buffers. The kernels run eagerly on the shape's first round and are captured in one graph on
-    its second (one graph per value of `advance`), replayed after. The round's result is st.res:
-    (b, k+2) int32, n_accepted then the committed tokens."""
+    or, for a keyed round, by its own first kernels), then the k+1 phases and fs_spec_advance, which
+    writes the next round's inputs from this round's acceptance into the same device buffers (used by
+    a round queued behind this one; a round staged by the host overwrites them). The kernels run
+    eagerly on the shape's first round and are captured in one graph on its second, replayed after.
+    The round's result is st.res: (b, k+2) int32, n_accepted then the committed tokens."""
     k = st.k
     if st.sampling and not st.keyed:
         if hasattr(draws, "draft_into"):
@@ -425,22 +426,20 @@ def _launch_round(target, draft, pool_t, pool_d, st: "_RoundState", b: int, draw
             draws.fill_in_round(st)
         for phase in range(k + 1):
             _round_phase(target, draft, pool_t, pool_d, st, phase)
-        if advance:
-            d = st.d
-            ops.spec_advance(st.res, st.b, k, 0 if st.n_shared else 1, d["n"], d["budget"], d["eos"], d["done"],
-                             d["ids"], d["last"], d["keff"], d["pos0"], d["posd"], d["posv"])
+        d = st.d
+        ops.spec_advance(st.res, st.b, k, 0 if st.n_shared else 1, d["n"], d["budget"], d["eos"], d["done"],
+                         d["ids"], d["last"], d["keff"], d["pos0"], d["posd"], d["posv"])
 
     if not graphs or st.uses == 0:
         kernels()
     else:
-        g = st.graphs.get(advance)
-        if g is None:   # the whole round in one graph: no launch gap between its phases
+        if st.graph is None:   # the whole round in one graph: no launch gap between its phases
             torch.cuda.current_stream().synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 kernels()
-            st.graphs[advance] = g
-        g.replay()
+            st.graph = g
+        st.graph.replay()
     st.uses += 1
 
 
@@ -756,7 +755,7 @@ class SpeculativeBatch:
                 o = st.host_off
                 st.dev[o:].copy_(st.hosts[slot][o:], non_blocking=True)
             draws = _GeneratorDraws(self.gen, b, k, self.target.cfg.vocab_size, self.dev) if sampled else None
-            _launch_round(self.target, self.draft, self.pool_t, self.pool_d, st, b, draws, True, advance=True)
+            _launch_round(self.target, self.draft, self.pool_t, self.pool_d, st, b, draws, True)
             st.res_hosts[j % 2].copy_(st.res, non_blocking=True)
             ev = torch.cuda.Event()
             ev.record()
