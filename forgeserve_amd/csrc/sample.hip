@@ -83,15 +83,56 @@ FS_DEVICE void load8(const typename Elem<DT>::T* row, int64_t v, int64_t V, bool
   }
 }
 
-FS_DEVICE void load8_f32(const float* row, int64_t v, int64_t V, bool vec_ok, float (&x)[8]) {
-  if (vec_ok && v + 8 <= V) {
-    const float4_t a = *reinterpret_cast<const float4_t*>(row + v);
-    const float4_t c = *reinterpret_cast<const float4_t*>(row + v + 4);
-    x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
-    x[4] = c[0]; x[5] = c[1]; x[6] = c[2]; x[7] = c[3];
+// Raw registers of 8 consecutive columns (two 16-byte loads for f32, one for bf16/f16), loaded
+// without bounds checks, then converted to f32 apart from the load. A block of loads is issued
+// first and converted after a scheduling barrier: a conversion between two loads makes the second
+// wait for the first (the compiler places the wait before the conversion).
+template <int DT>
+struct Raw8 {
+  typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+  u32x4 w[DT == FS_F32 ? 2 : 1];
+  FS_DEVICE void load(const typename Elem<DT>::T* row, int64_t v) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(row + v);
+    w[0] = q[0];
+    if (DT == FS_F32) w[DT == FS_F32 ? 1 : 0] = q[1];
+  }
+  FS_DEVICE void to_f32(float (&x)[8]) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (DT == FS_F32) {
+        x[j] = __uint_as_float(w[0][j]);
+        x[4 + j] = __uint_as_float(w[DT == FS_F32 ? 1 : 0][j]);
+      } else {
+        x[2 * j] = Elem<DT>::to_f32((uint16_t)(w[0][j] & 0xffffu));
+        x[2 * j + 1] = Elem<DT>::to_f32((uint16_t)(w[0][j] >> 16));
+      }
+    }
+  }
+};
+
+// Every group u (columns v0 + u * THREADS * VEC .. + 7) of a U-group block is in range and 16-byte
+// loadable: false only in a row's last chunk (or for unaligned rows).
+template <int U>
+FS_DEVICE bool block_in_range(int64_t v0, int64_t V, bool vec_ok) {
+  return vec_ok && v0 + (int64_t)(U - 1) * THREADS * VEC + VEC <= V;
+}
+
+// U groups of 8 consecutive columns per thread, group u at column v0 + u * THREADS * VEC, as f32;
+// columns >= V read as `fill`. In range, the U loads are issued back to back before any conversion.
+template <int DT, int U>
+FS_DEVICE void load_block(const typename Elem<DT>::T* row, int64_t v0, int64_t V, bool vec_ok, float fill,
+                          float (&x)[U][8]) {
+  constexpr int64_t STRIDE = (int64_t)THREADS * VEC;
+  if (block_in_range<U>(v0, V, vec_ok)) {
+    Raw8<DT> r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) r[u].load(row, v0 + u * STRIDE);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) r[u].to_f32(x[u]);
   } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = (v + j < V) ? row[v + j] : 1.f;
+    for (int u = 0; u < U; ++u) load8<DT>(row, v0 + u * STRIDE, V, vec_ok, fill, x[u]);
   }
 }
 
@@ -180,9 +221,7 @@ template <int DT>
 FS_DEVICE Stat chunk_stat(const typename Elem<DT>::T* row, int c, int64_t V, float T, float* shf, int* shi) {
   const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
   float x[UNROLL][8];
-#pragma unroll
-  for (int u = 0; u < UNROLL; ++u)
-    load8<DT>(row, (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC, V, vec_ok, -INFINITY, x[u]);
+  load_block<DT, UNROLL>(row, (int64_t)c * CH + (int64_t)threadIdx.x * VEC, V, vec_ok, -INFINITY, x);
   Stat st;
   if (T <= 0.f) {
     float amv = -INFINITY;
@@ -263,22 +302,35 @@ __global__ void __launch_bounds__(THREADS) sample_argmax_kernel(RowSet rs, int64
   const int c = blockIdx.x, r = blockIdx.y;
   const float T = temps ? temps[r] : t_all;
   if (T <= 0.f) return;
-  if (threadIdx.x == 0) shs = merge_row(stats + (int64_t)r * nch, nch);
-  __syncthreads();
-  const ProbFn fs(T, shs);
   const auto* row = row_ptr<DT>(rs, r, 0);
   const float* er = E + (int64_t)r * ldE;
   const bool vec_ok = (V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0) &&
                       ((reinterpret_cast<uintptr_t>(er) & 15) == 0);
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  float x[UNROLL][8], e[UNROLL][8];
+  float x[UNROLL][8], e[UNROLL][8];   // the chunk's loads go out before the row's statistics are merged
+  const int64_t vb = (int64_t)c * CH + (int64_t)threadIdx.x * VEC;
+  if (block_in_range<UNROLL>(vb, V, vec_ok)) {
+    Raw8<DT> rx[UNROLL];
+    Raw8<FS_F32> re[UNROLL];
 #pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v0 = (int64_t)c * CH + (int64_t)(threadIdx.x + THREADS * u) * VEC;
-    load8<DT>(row, v0, V, vec_ok, -INFINITY, x[u]);
-    load8_f32(er, v0, V, vec_ok, e[u]);
+    for (int u = 0; u < UNROLL; ++u) {
+      rx[u].load(row, vb + u * THREADS * VEC);
+      re[u].load(er, vb + u * THREADS * VEC);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      rx[u].to_f32(x[u]);
+      re[u].to_f32(e[u]);
+    }
+  } else {
+    load_block<DT, UNROLL>(row, vb, V, vec_ok, -INFINITY, x);
+    load_block<FS_F32, UNROLL>(er, vb, V, vec_ok, 1.f, e);
   }
+  if (threadIdx.x == 0) shs = merge_row(stats + (int64_t)r * nch, nch);
+  __syncthreads();
+  const ProbFn fs(T, shs);
   divide_by_t(x, T);
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
@@ -317,29 +369,19 @@ __global__ void sample_final_kernel(int R, int nch, const float* __restrict__ te
 // ------------------------------------------------------------------------------------------------
 // acceptance
 // ------------------------------------------------------------------------------------------------
-// Logits without given statistics take two launches: the statistics of every (row, 8K-column chunk)
-// (accept_stats_kernel), then accept_kernel; with the statistics given (from the LM head's epilogue),
-// or on probabilities, accept_kernel alone. In accept_kernel workgroup i takes work item i:
-//   items 0..B-1, step items: sequence b's step (merging its rows' chunk statistics when they come
-//     from the statistics launch); a greedy sequence is finished here;
-//   then pair items: one 4K-column chunk of a sampled sequence's draw each, sequence by sequence;
-//     a pair item loads its chunk of the Exp(1) row, waits until its sequence's step is published,
-//     then reads the rejected position's rows; the last pair item of a sequence to finish draws.
-// Workgroups are dispatched in increasing index order, so a pair item waits only for a step item
-// that has been dispatched before it and never waits itself: every wait ends. (Each wait is also
-// bounded by about a second of the constant clock, after which the error word is set and the item
-// gives up its work.)
-//
-// Results pass between workgroups (which may sit on different XCDs) through the workspace: records
-// are written with agent-scope relaxed stores (coherent across the XCDs without writing back an L2),
-// the writing wave waits until its stores have completed and then signals with an agent-scope store
-// or atomic; the reader reads the records with agent-scope loads. Atomics on one 256-byte line are
-// serialised (~12 ns each) and a polled line slows them further, so each sequence's counter and its
-// ready flag have lines of their own in the control words. The ready flag is set by the step and
-// cleared by the draw; the counter (the pair items) wraps to 0 with its last increment (atomic
-// increment with a limit); so each call leaves the control words as it found them: zero (the
-// workspace is zero-filled once, before its first use). They sit at the start of the workspace and
-// are sized for the largest batch, so that no call's records overlap them.
+// Logits without given statistics take four launches: the statistics of every (row, 8K-column
+// chunk) (accept_stats_kernel), the steps (accept_step_kernel), the draws' chunks (accept_kernel),
+// then the draws (accept_draw_kernel); with the statistics given (from the LM head's epilogue), or on
+// probabilities, the last three alone.
+//   accept_step_kernel, one workgroup per sequence: sequence b's step (merging its rows' chunk
+//     statistics when they come from the statistics launch); a greedy sequence is finished here, a
+//     sampled one records its first rejected position and that position's row statistics;
+//   accept_kernel, one workgroup per (sampled sequence, 4K-column chunk): reads its sequence's step,
+//     then its chunk of the Exp(1) row and of the rejected position's rows, all at once, and records
+//     the chunk's residual sum and the candidates of the draw;
+//   accept_draw_kernel, one wave per sampled sequence: the draw from the chunks' records.
+// Every record is read by a later launch than the one that wrote it, so no workgroup waits for
+// another and the workspace needs no initial contents.
 struct AcceptArgs {
   RowSet rs;             // n0 = K+1 target rows, n1 = K draft rows
   int32_t K;
@@ -353,9 +395,6 @@ struct AcceptArgs {
   const float* u;        // [B, K]
   const float* E;        // [B, V]
   int64_t ldE;
-  unsigned* err;         // [1]   set if a wait ran out
-  unsigned* seqc;        // [1024 lines of 64] per sequence: its pair items counted in
-  unsigned* ready;       // [1024 lines of 64] per sequence: 1 from the step's publication to the draw
   Stat* stats;           // [B*(2K+1)][nch] chunk partials (logits mode)
   Stat* mstats;          // [B*(2K+1)] merged row statistics (logits mode: the step's own)
   bool premerged;        // mstats are the caller's (from the LM head's epilogue): no statistics launch
@@ -364,6 +403,8 @@ struct AcceptArgs {
   float* cmax;           // [B][nchr] max of the chunk's cheap keys (0: none positive; +inf: rescan)
   int* ncand;            // [B][nchr] candidates of the chunk (> NCAND: the list overflowed)
   int* cand;             // [B][nchr][NCAND] their column indices, in no particular order
+  float* candw;          // [B][nchr][NCAND] their weights: r_v at a rejection, p_v for the bonus token
+  float* cande;          // [B][nchr][NCAND] their Exp(1) values E_v
   int* jpos;             // [B]   the first rejected proposal, or k_eff
   int32_t* out_tokens;   // [B, K+1]
   int32_t* n_acc;        // [B]
@@ -376,70 +417,118 @@ struct AcceptArgs {
 constexpr int STEP_WAVES = THREADS / 64;
 constexpr int STEP_ROWS = 4;      // rows merged per wave and pass
 
-// agent-scope relaxed accesses (common.h) of the records that cross workgroups within the launch
-using ::ld_ag;
-using ::st_ag;
-FS_DEVICE void st_ag(Stat* p, const Stat& s) {
-  uint64_t* q = reinterpret_cast<uint64_t*>(p);
-  __hip_atomic_store(q, (uint64_t)__float_as_uint(s.m) | ((uint64_t)__float_as_uint(s.s) << 32), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(q + 1, (uint64_t)__float_as_uint(s.av) | ((uint64_t)(uint32_t)s.ai << 32), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-FS_DEVICE Stat ld_ag(const Stat* p) {
-  uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<Stat*>(p));
-  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return Stat{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)), __uint_as_float((uint32_t)b),
-              (int)(uint32_t)(b >> 32)};
-}
-
 FS_DEVICE int keff_of(const AcceptArgs& A, int b) { return A.k_eff ? min(max(A.k_eff[b], 0), A.K) : A.K; }
 
-// Entry i of a region of 1024 lines of 64 words: word i / 1024 of line i % 1024.
-FS_DEVICE unsigned* ctl_word(unsigned* region, int64_t i) { return region + (i & 1023) * 64 + (i >> 10); }
-FS_DEVICE unsigned* seq_counter(const AcceptArgs& A, int b) { return ctl_word(A.seqc, b); }
-FS_DEVICE unsigned* ready_flag(const AcceptArgs& A, int b) { return ctl_word(A.ready, b); }
 
 
+// What the outputs need that does not depend on the outcome, loaded by the caller up front (one
+// wave): proposal `lane` of sequence b (lane < K) and seq_len[b].
+struct OutPre {
+  int d0, len0;
+};
+FS_DEVICE OutPre out_pre(const AcceptArgs& A, int b) {
+  const int lane = threadIdx.x & 63;
+  return OutPre{lane < A.K ? A.draft[(int64_t)b * A.K + lane] : 0, A.seq_len ? A.seq_len[b] : 0};
+}
 
-FS_DEVICE void write_outputs(const AcceptArgs& A, int b, int j, int extra) {
+// The outputs of sequence b, written by one whole wave (lane i: token i, i + 64, ...): the j accepted
+// proposals, the extra token, then -1.
+FS_DEVICE void write_outputs(const AcceptArgs& A, int b, int j, int extra, const OutPre& pre) {
+  const int lane = threadIdx.x & 63;
   int32_t* o = A.out_tokens + (int64_t)b * (A.K + 1);
-  for (int i = 0; i < j; ++i) o[i] = A.draft[(int64_t)b * A.K + i];
-  o[j] = extra;
-  for (int i = j + 1; i <= A.K; ++i) o[i] = -1;
-  A.n_acc[b] = j;
-  if (A.seq_len) A.seq_len[b] = A.seq_len[b] + 1 + j;  // want = cached + 1 + len(accepted) (speculative.py:77)
+  for (int i = lane; i <= A.K; i += 64) {
+    const int d = i < 64 ? pre.d0 : (i < j ? A.draft[(int64_t)b * A.K + i] : 0);
+    o[i] = i < j ? d : (i == j ? extra : -1);
+  }
+  if (lane == 0) {
+    A.n_acc[b] = j;
+    if (A.seq_len) A.seq_len[b] = pre.len0 + 1 + j;  // want = cached + 1 + len(accepted) (speculative.py:77)
+  }
 }
 
-// The chunk statistics of rows r (one wave, lane c holding chunk c) merged as merge_row does: the
-// max over the chunks, Σ s_c 2^(m_c - M) added in chunk order, the first argmax.
-FS_DEVICE Stat merge_row_wave(const Stat& st, bool in, int nch) {
-  float M = wave_max(in ? st.m : -INFINITY);
-  const float term = (!in || st.m == -INFINITY) ? 0.f : st.s * __builtin_amdgcn_exp2f((st.m - M) * LOG2E_F);
-  float S = 0.f;
-  for (int c = 0; c < nch; ++c) S += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(term), c));
-  float av = in ? st.av : -INFINITY;
-  int ai = in ? st.ai : 0x7fffffff;
-  wave_argmax(av, ai);
-  return Stat{M, S, av, ai};
+// The chunk statistics of R rows (one wave, lane c holding chunk c of each) merged as merge_row does:
+// the max over the chunks, Σ s_c 2^(m_c - M) added in chunk order, the first argmax. The rows'
+// reductions are interleaved step by step, so their cross-lane latencies overlap.
+template <int R>
+FS_DEVICE void merge_rows_wave(const Stat (&st)[R], bool in, int nch, Stat (&out)[R]) {
+  float M[R], S[R], term[R], av[R];
+  int ai[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    M[i] = in ? st[i].m : -INFINITY;
+    av[i] = in ? st[i].av : -INFINITY;
+    ai[i] = in ? st[i].ai : 0x7fffffff;
+    S[i] = 0.f;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float oa[R], om[R];
+    int oi[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      om[i] = __shfl_xor(M[i], o, 64);
+      oa[i] = __shfl_xor(av[i], o, 64);
+      oi[i] = __shfl_xor(ai[i], o, 64);
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      M[i] = fmaxf(M[i], om[i]);
+      argmax_merge(av[i], ai[i], oa[i], oi[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    term[i] = (!in || st[i].m == -INFINITY) ? 0.f : st[i].s * __builtin_amdgcn_exp2f((st[i].m - M[i]) * LOG2E_F);
+  for (int c = 0; c < nch; ++c)
+#pragma unroll
+    for (int i = 0; i < R; ++i) S[i] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(term[i]), c));
+#pragma unroll
+  for (int i = 0; i < R; ++i) out[i] = Stat{M[i], S[i], av[i], ai[i]};
 }
 
-// The step of sequence b, run by one whole workgroup: merge the row statistics (logits without given
-// statistics: each wave takes STEP_ROWS rows at a time, one lane per chunk) into ms, then test
-// every proposal at once, one lane each; the first rejection ends the walk (speculative.py:25-29).
-// The proposals and their logits are loaded before the merge, so the two latencies overlap. A greedy
-// sequence is finished here (the extra token is the argmax of target row j); for a sampled one the
-// rejected position j and its rows' statistics are published for the pair items.
+// The step of sequence b, run by one whole workgroup. Wave 0 tests every proposal at once, one lane
+// each; the first rejection ends the walk (speculative.py:25-29). The rows' statistics it needs, those
+// of the first STEP_LDS proposals' rows, are staged in LDS meanwhile: merged from the statistics
+// launch's chunk records (each wave takes STEP_ROWS rows at a time, one lane per chunk; every row is
+// also written to the workspace), or, given, loaded by waves 1-3 while wave 0 waits for its proposals'
+// logits. A greedy sequence is finished here (the extra token is the argmax of target row j); for a
+// sampled one the rejected position j and its rows' statistics are recorded for the next launches.
+constexpr int STEP_LDS = 64;
+
 template <int DT, bool PROBS>
-FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
+FS_DEVICE void sequence_step(const AcceptArgs& A, int b, Stat* sh_ms) {
+  // sh_ms: target rows 0..STEP_LDS at [r], draft rows 0..STEP_LDS-1 at [STEP_LDS + 1 + r]
   const int per = A.rs.n0 + A.rs.n1;
-  Stat* ms = A.mstats + (int64_t)b * per;
+  const Stat* ms = A.mstats + (int64_t)b * per;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // No load waits for another: the proposals (wave 0, lane i: proposal i of the first 64) and the
-  // chunk statistics are fetched for all K positions and rows, and k_eff only decides what is used.
+  auto slot_of = [&](int r) {   // the LDS slot of row r, or -1
+    return r < A.rs.n0 ? (r <= STEP_LDS ? r : -1) : (r - A.rs.n0 < STEP_LDS ? STEP_LDS + 1 + r - A.rs.n0 : -1);
+  };
+  const int ke = keff_of(A, b);
+  const float T = PROBS ? 1.f : A.temps[b];
+  auto used = [&](int r) { return r < per && (r < A.rs.n0 ? r <= ke : (r - A.rs.n0) < ke); };
+  if (!PROBS && A.premerged && w > 0) {   // the given statistics of the staged rows (waves 1-3)
+    for (int t = threadIdx.x - 64; t < 2 * STEP_LDS + 1; t += blockDim.x - 64) {
+      const int r = t <= STEP_LDS ? t : A.rs.n0 + t - (STEP_LDS + 1);
+      if (used(r)) sh_ms[t] = ms[r];
+    }
+  }
+  // the statistics launch's chunk records of the first STEP_WAVES * STEP_ROWS rows, fetched before
+  // wave 0 waits for its proposals
+  const bool merge = !PROBS && !A.premerged && A.nch <= 64;
+  const Stat none{-INFINITY, 0.f, -INFINITY, 0x7fffffff};
+  Stat st0[STEP_ROWS];
+  if (merge) {
+#pragma unroll
+    for (int i = 0; i < STEP_ROWS; ++i) {
+      const int r = w + STEP_WAVES * i;
+      st0[i] = used(r) && lane < A.nch ? A.stats[((int64_t)b * per + r) * A.nch + lane] : none;
+    }
+  }
+  // wave 0, lane i: proposal i of the first 64 and its logits in the target and draft rows
   int x0 = -1;
   float u0 = 0.f, xp0 = 0.f, xq0 = 0.f;
+  const int len0 = A.seq_len && w == 0 ? A.seq_len[b] : 0;
   if (w == 0 && lane < A.K) {
     x0 = A.draft[(int64_t)b * A.K + lane];
     u0 = A.u[(int64_t)b * A.K + lane];
@@ -448,38 +537,51 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
       xq0 = Elem<DT>::load(row_ptr<DT>(A.rs, b, A.rs.n0 + lane), x0);
     }
   }
-  const int ke = keff_of(A, b);
-  const float T = PROBS ? 1.f : A.temps[b];
-  auto used = [&](int r) { return r < per && (r < A.rs.n0 ? r <= ke : (r - A.rs.n0) < ke); };
   if (!PROBS && !A.premerged) {   // the statistics launch's records
-    if (A.nch <= 64) {
+    Stat* mw = A.mstats + (int64_t)b * per;
+    if (merge) {
       for (int r0 = 0; r0 < per; r0 += STEP_WAVES * STEP_ROWS) {
         Stat st[STEP_ROWS];
 #pragma unroll
         for (int i = 0; i < STEP_ROWS; ++i) {
           const int r = r0 + w + STEP_WAVES * i;
-          if (used(r) && lane < A.nch) st[i] = A.stats[((int64_t)b * per + r) * A.nch + lane];
+          if (r0 == 0) {
+            st[i] = st0[i];
+          } else {
+            st[i] = used(r) && lane < A.nch ? A.stats[((int64_t)b * per + r) * A.nch + lane] : none;
+          }
         }
+        Stat mg[STEP_ROWS];   // rows the sequence does not use merge to `none`, never stored
+        merge_rows_wave<STEP_ROWS>(st, lane < A.nch, A.nch, mg);
 #pragma unroll
         for (int i = 0; i < STEP_ROWS; ++i) {
           const int r = r0 + w + STEP_WAVES * i;
-          if (!used(r)) continue;   // uniform over the wave
-          const Stat m = merge_row_wave(st[i], lane < A.nch, A.nch);
-          if (lane == 0) ms[r] = m;
+          if (lane == 0 && used(r)) {
+            mw[r] = mg[i];
+            if (slot_of(r) >= 0) sh_ms[slot_of(r)] = mg[i];
+          }
         }
       }
     } else {
       for (int r = threadIdx.x; r < per; r += blockDim.x)
-        if (used(r)) ms[r] = merge_row(A.stats + ((int64_t)b * per + r) * A.nch, A.nch);
+        if (used(r)) {
+          const Stat m = merge_row(A.stats + ((int64_t)b * per + r) * A.nch, A.nch);
+          mw[r] = m;
+          if (slot_of(r) >= 0) sh_ms[slot_of(r)] = m;
+        }
     }
     __threadfence_block();
-    __syncthreads();
   }
+  __syncthreads();
+  // the statistics of target row r (r <= ke) and of draft row r (r < ke)
+  auto tstat = [&](int r) { return r <= STEP_LDS ? sh_ms[r] : ms[r]; };
+  auto dstat = [&](int r) { return r < STEP_LDS ? sh_ms[STEP_LDS + 1 + r] : ms[A.rs.n0 + r]; };
+  if (w != 0) return;
   int j = ke;
   for (int i0 = 0; i0 < ke && j == ke; i0 += 64) {
     const int i = i0 + lane;
     bool accept = false;
-    if (w == 0 && i < ke) {
+    if (i < ke) {
       int x = x0;
       float u = u0, xp = xp0, xq = xq0;
       if (i0 > 0) {   // proposals past the first 64
@@ -496,11 +598,11 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
           px = xp;
           qx = xq;
         } else if (T > 0.f) {
-          px = ProbFn(T, ms[i])(xp);
-          qx = ProbFn(T, ms[A.rs.n0 + i])(xq);
+          px = ProbFn(T, tstat(i))(xp);
+          qx = ProbFn(T, dstat(i))(xq);
         } else {  // one-hot rows of the first argmax (sampling.py:11-12)
-          px = ms[i].ai == x ? 1.f : 0.f;
-          qx = ms[A.rs.n0 + i].ai == x ? 1.f : 0.f;
+          px = tstat(i).ai == x ? 1.f : 0.f;
+          qx = dstat(i).ai == x ? 1.f : 0.f;
         }
         const float ratio = qx > 0.f ? Elem<ProbType<DT, PROBS>::value>::round(px / qx) : 1.0f;  // speculative.py:26
         accept = u < fminf(1.0f, ratio);
@@ -510,21 +612,17 @@ FS_DEVICE void sequence_step(const AcceptArgs& A, int b) {
         }
       }
     }
-    const uint64_t rejected = __ballot(w == 0 && i < ke && !accept);
+    const uint64_t rejected = __ballot(i < ke && !accept);
     if (rejected) j = i0 + __ffsll((unsigned long long)rejected) - 1;
   }
-  if (threadIdx.x == 0) {
-    if (!PROBS && T <= 0.f) {
-      write_outputs(A, b, j, ms[j].ai);
-      if (A.dbg_s) A.dbg_s[b] = 0.f;
-    } else {   // publish the outcome for the pair items
-      st_ag(A.jpos + b, j);
-      if (!PROBS) {
-        st_ag(A.pairstat + 2 * b, ms[j]);
-        if (j < ke) st_ag(A.pairstat + 2 * b + 1, ms[A.rs.n0 + j]);
-      }
-      stores_done();
-      st_ag(ready_flag(A, b), 1u);
+  if (!PROBS && T <= 0.f) {
+    write_outputs(A, b, j, tstat(j).ai, OutPre{x0, len0});
+    if (lane == 0 && A.dbg_s) A.dbg_s[b] = 0.f;
+  } else if (lane == 0) {   // the outcome for the next launches
+    A.jpos[b] = j;
+    if (!PROBS) {
+      A.pairstat[2 * b] = tstat(j);
+      if (j < ke) A.pairstat[2 * b + 1] = dstat(j);
     }
   }
 }
@@ -571,57 +669,43 @@ struct PairRow {
   }
 };
 
-// Candidates of one set: the columns whose cheap key reaches the threshold (LDS list, first NCAND kept)
-FS_DEVICE void collect(float key, int col, float th, int* n, int* list) {
+// Candidates of one set: the columns whose cheap key reaches the threshold, with the weight and
+// Exp(1) value their exact key is computed from (LDS lists, first NCAND kept)
+FS_DEVICE void collect(float key, int col, float w, float e, float th, int* n, int* list, float* wl, float* el) {
   if (key >= th) {
     const int k = atomicAdd(n, 1);
-    if (k < NCAND) list[k] = col;
+    if (k < NCAND) {
+      list[k] = col;
+      wl[k] = w;
+      el[k] = e;
+    }
   }
 }
 
-// What a pair item learns from its sequence's step (broadcast through LDS).
+// What a pair item learns from its sequence's step (written by the step launch).
 struct PairCtx {
   int j;
   Stat sp, sq;
-  bool ok;   // false: the wait ran out (err is set; the item only counts itself in)
 };
 
-// Wait (thread 0) until sequence b's step is published, then read the outcome; bounded by ~1 s of
-// the constant 100 MHz clock. The step belongs to an item with a smaller index, which never waits.
 template <bool PROBS>
-FS_DEVICE void await_step(const AcceptArgs& A, int b, PairCtx* sh) {
-  if (threadIdx.x == 0) {
-    bool ok = true;
-    if (ld_ag(ready_flag(A, b)) == 0u) {
-      const uint64_t t0 = wall_clock64();
-      while (ld_ag(ready_flag(A, b)) == 0u) {
-        __builtin_amdgcn_s_sleep(16);
-        if (wall_clock64() - t0 > 100000000ull) {
-          ok = false;
-          st_ag(A.err, 1u);
-          break;
-        }
-      }
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    sh->ok = ok;
-    if (ok) {
-      sh->j = ld_ag(A.jpos + b);
-      if (!PROBS) {
-        sh->sp = ld_ag(A.pairstat + 2 * b);
-        sh->sq = ld_ag(A.pairstat + 2 * b + 1);
-      }
-    }
+FS_DEVICE PairCtx read_step(const AcceptArgs& A, int b) {
+  PairCtx pc;
+  pc.j = A.jpos[b];
+  if (!PROBS) {
+    pc.sp = A.pairstat[2 * b];
+    pc.sq = A.pairstat[2 * b + 1];
   }
-  __syncthreads();
+  return pc;
 }
 
 // One chunk of CHR columns of the draw of sequence b: the residual partial sum and the max and
 // candidates of the draw's keys (r / E at a rejection, p / E for the bonus token), written as records.
-// e: the chunk of the Exp(1) row, loaded before the wait for the step.
+// The rows' addresses depend on the step's outcome, so it is read first and waited for before any
+// load of the chunk is issued: issued after them it would queue behind every item's chunk stream.
 template <int DT, bool PROBS>
-FS_DEVICE void pair_chunk(const AcceptArgs& A, int b, int c, const PairCtx& pc, float (&e)[UNROLL_R][8], float* shf,
-                          int* sh_n, int* sh_c) {
+FS_DEVICE void pair_chunk(const AcceptArgs& A, int b, int c, const PairCtx& pc, float* shf, int* sh_n, int* sh_c,
+                          float* sh_w, float* sh_e) {
   constexpr int PD = ProbType<DT, PROBS>::value;
   const int ke = keff_of(A, b);
   const float T = PROBS ? 1.f : A.temps[b];
@@ -636,12 +720,31 @@ FS_DEVICE void pair_chunk(const AcceptArgs& A, int b, int c, const PairCtx& pc, 
   const auto* qr = bonus ? pr : row_ptr<DT>(A.rs, b, A.rs.n0 + j);
   const bool vec_ok = (A.V % VEC) == 0 &&
                       (((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(qr)) & 15) == 0);
-  float xp[UNROLL_R][8], xq[UNROLL_R][8];
+  const float* er = A.E + (int64_t)b * A.ldE;
+  const bool evec_ok = (A.V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(er) & 15) == 0);
+  __builtin_amdgcn_sched_barrier(0);   // j is in hand before the first load below is issued
+  float xp[UNROLL_R][8], xq[UNROLL_R][8], e[UNROLL_R][8];   // every load in flight before any arithmetic
+  const int64_t vb = (int64_t)c * CHR + (int64_t)threadIdx.x * VEC;
+  if (block_in_range<UNROLL_R>(vb, A.V, vec_ok && evec_ok)) {
+    Raw8<DT> rp[UNROLL_R], rq[UNROLL_R];
+    Raw8<FS_F32> re[UNROLL_R];
 #pragma unroll
-  for (int u = 0; u < UNROLL_R; ++u) {   // every load of the chunk in flight before any arithmetic
-    const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
-    load8<DT>(pr, v0, A.V, vec_ok, 0.f, xp[u]);
-    if (!bonus) load8<DT>(qr, v0, A.V, vec_ok, 0.f, xq[u]);
+    for (int u = 0; u < UNROLL_R; ++u) {   // for the bonus token qr is pr: a second read of the same lines
+      rp[u].load(pr, vb + u * THREADS * VEC);
+      rq[u].load(qr, vb + u * THREADS * VEC);
+      re[u].load(er, vb + u * THREADS * VEC);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < UNROLL_R; ++u) {
+      rp[u].to_f32(xp[u]);
+      rq[u].to_f32(xq[u]);
+      re[u].to_f32(e[u]);
+    }
+  } else {
+    load_block<DT, UNROLL_R>(pr, vb, A.V, vec_ok, 0.f, xp);
+    if (!bonus) load_block<DT, UNROLL_R>(qr, vb, A.V, vec_ok, 0.f, xq);
+    load_block<FS_F32, UNROLL_R>(er, vb, A.V, evec_ok, 1.f, e);
   }
   if (!PROBS) {   // y = x / T once per element (the ProbFn arithmetic, divided ahead)
     divide_by_t(xp, T);
@@ -651,6 +754,7 @@ FS_DEVICE void pair_chunk(const AcceptArgs& A, int b, int c, const PairCtx& pc, 
   // rejection is needed only when the residual sums to 0; its chunks are then rescanned exactly.
   float ls = 0.f, mk = 0.f;
   float ak[UNROLL_R][8];   // cheap keys (0 past the row)
+  float wv[UNROLL_R][8];   // the exact keys' weights: p_v for the bonus token, r_v at a rejection
 #pragma unroll
   for (int u = 0; u < UNROLL_R; ++u) {
     const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
@@ -660,11 +764,13 @@ FS_DEVICE void pair_chunk(const AcceptArgs& A, int b, int c, const PairCtx& pc, 
       const float re = __builtin_amdgcn_rcpf(e[u][jj]);
       const float p = PROBS ? xp[u][jj] : sp.of_y(xp[u][jj]);
       if (bonus) {
+        wv[u][jj] = p;
         ak[u][jj] = in ? p * re : 0.f;
       } else {   // (p - q).clamp(min=0), rounded to the probability dtype
         const float q = PROBS ? xq[u][jj] : sq.of_y(xq[u][jj]);
         const float r = in ? fmaxf(Elem<PD>::round(p - q), 0.f) : 0.f;
         ls += r;
+        wv[u][jj] = r;
         ak[u][jj] = r * re;
       }
       mk = fmaxf(mk, ak[u][jj]);
@@ -679,43 +785,78 @@ FS_DEVICE void pair_chunk(const AcceptArgs& A, int b, int c, const PairCtx& pc, 
   for (int u = 0; u < UNROLL_R; ++u) {
     const int64_t v0 = (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC;
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) collect(ak[u][jj], (int)(v0 + jj), th, &sh_n[0], sh_c);
+    for (int jj = 0; jj < 8; ++jj)
+      collect(ak[u][jj], (int)(v0 + jj), wv[u][jj], e[u][jj], th, &sh_n[0], sh_c, sh_w, sh_e);
   }
   __syncthreads();
   const int64_t o = (int64_t)b * A.nchr + c;
   if (threadIdx.x < 64) {   // wave 0 writes the chunk's records
     const int n = cm > 0.f ? sh_n[0] : 0;
-    if ((int)threadIdx.x < NCAND && (int)threadIdx.x < n) st_ag(A.cand + o * NCAND + threadIdx.x, sh_c[threadIdx.x]);
+    if ((int)threadIdx.x < NCAND && (int)threadIdx.x < n) {
+      A.cand[o * NCAND + threadIdx.x] = sh_c[threadIdx.x];
+      A.candw[o * NCAND + threadIdx.x] = sh_w[threadIdx.x];
+      A.cande[o * NCAND + threadIdx.x] = sh_e[threadIdx.x];
+    }
     if (threadIdx.x == 0) {
-      st_ag(A.resid + o, tot);
-      st_ag(A.cmax + o, cm);
-      st_ag(A.ncand + o, n);
+      A.resid[o] = tot;
+      A.cmax[o] = cm;
+      A.ncand[o] = n;
     }
   }
 }
 
-// The draw of sequence b, run by one wave once every pair item of b has written its records: S summed
+// The draw of sequence b, run by one wave from the records of its chunks: S summed
 // over the chunks in increasing order, then the exact keys of the candidates of every chunk whose max
 // reaches the margin (first index on ties); writes the tokens, n_accepted and the rollback length.
+// Chunks are taken 32 at a time, lanes l and l + 32 on chunk l: both fetch its records, each half of
+// its candidates' (column, weight, E), all at once, so a draw waits for one round trip; only a chunk
+// that is rescanned (its list overflowed, or the bound is not relied on) reads the logits and E again.
+constexpr int DRAW_CHUNKS = 32;
+constexpr int CAND_HALF = NCAND / 2;
+
 template <int DT, bool PROBS>
-FS_DEVICE void final_draw(const AcceptArgs& A, int b, const PairCtx& pc) {
+FS_DEVICE void final_draw(const AcceptArgs& A, int b) {
   constexpr int PD = ProbType<DT, PROBS>::value;
   const int lane = threadIdx.x;
-  const float T = PROBS ? 1.f : A.temps[b];
+  const int cl = lane & (DRAW_CHUNKS - 1), half = lane / DRAW_CHUNKS;
   const int64_t o0 = (int64_t)b * A.nchr;
+  struct Chunk {
+    float rc, cmx;
+    int n;
+    int col[CAND_HALF];
+    float w[CAND_HALF], e[CAND_HALF];
+  };
+  auto fetch = [&](int c0) {   // chunk c0 + cl, candidates half * CAND_HALF .. (zeros past the last chunk)
+    Chunk k;
+    const bool in = c0 + cl < A.nchr;
+    const int64_t o = o0 + (in ? c0 + cl : 0);
+    k.rc = in ? A.resid[o] : 0.f;
+    k.cmx = in ? A.cmax[o] : 0.f;
+    k.n = in ? A.ncand[o] : 0;
+#pragma unroll
+    for (int i = 0; i < CAND_HALF; ++i) {
+      const int64_t q = o * NCAND + half * CAND_HALF + i;
+      k.col[i] = in ? A.cand[q] : 0;
+      k.w[i] = in ? A.candw[q] : 0.f;
+      k.e[i] = in ? A.cande[q] : 1.f;
+    }
+    return k;
+  };
+  // every load that depends on nothing goes out before the first is used (a greedy sequence, finished
+  // by its step, reads stale records and returns)
+  const Chunk k0 = fetch(0);
+  const OutPre pre = out_pre(A, b);
+  const PairCtx pc = read_step<PROBS>(A, b);
+  const float T = PROBS ? 1.f : A.temps[b];
   const int ke = keff_of(A, b);
+  if (T <= 0.f) return;
   const int j = pc.j;
   const bool bonus = j >= ke;
-  // the first 64 chunks' records are fetched together; chunks past 64 as they are needed
-  const bool in0 = lane < A.nchr;
-  const float rc0 = in0 ? ld_ag(A.resid + o0 + lane) : 0.f;
-  const float cmx0 = in0 ? ld_ag(A.cmax + o0 + lane) : 0.f;
-  const int nc0 = in0 ? ld_ag(A.ncand + o0 + lane) : 0;
   float s = 0.f;
   if (!bonus) {
-    for (int c0 = 0; c0 < A.nchr; c0 += 64) {
-      const float rc = c0 == 0 ? rc0 : (c0 + lane < A.nchr ? ld_ag(A.resid + o0 + c0 + lane) : 0.f);
-      const int n = min(64, A.nchr - c0);
+    for (int c0 = 0; c0 < A.nchr; c0 += DRAW_CHUNKS) {
+      const float rc = c0 == 0 ? k0.rc : (c0 + cl < A.nchr ? A.resid[o0 + c0 + cl] : 0.f);
+      const int n = min(DRAW_CHUNKS, A.nchr - c0);
       for (int k = 0; k < n; ++k) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rc), k));
     }
     s = Elem<PD>::round(s);
@@ -724,12 +865,10 @@ FS_DEVICE void final_draw(const AcceptArgs& A, int b, const PairCtx& pc) {
   // whose chunks were not ranked for p / E and are all rescanned; set r: w = r / S
   const bool set_r = !bonus && s > 0.f;
   const bool rescan_all = !bonus && !set_r;
-  auto cmax_at = [&](int c0) {
-    return c0 == 0 ? cmx0 : (c0 + lane < A.nchr ? ld_ag(A.cmax + o0 + c0 + lane) : 0.f);
-  };
   float gmax = 0.f;
   if (!rescan_all) {
-    for (int c0 = 0; c0 < A.nchr; c0 += 64) gmax = fmaxf(gmax, cmax_at(c0));
+    for (int c0 = 0; c0 < A.nchr; c0 += DRAW_CHUNKS)
+      gmax = fmaxf(gmax, c0 == 0 ? k0.cmx : (c0 + cl < A.nchr ? A.cmax[o0 + c0 + cl] : 0.f));
     gmax = wave_max(gmax);
   }
   const bool trust = !rescan_all && gmax >= CAND_MIN;
@@ -745,34 +884,28 @@ FS_DEVICE void final_draw(const AcceptArgs& A, int b, const PairCtx& pc) {
   auto key = [&](int64_t col) { return set_r ? pair.key_r(col, s, er[col]) : pair.key_p(col, er[col]); };
   float v = -INFINITY;
   int extra = 0x7fffffff;
-  for (int c0 = 0; c0 < A.nchr; c0 += 64) {
-    // lane l: chunk c0 + l, kept if its max reaches the margin; the kept chunks are then taken in turn
-    const int cl = c0 + lane;
-    const bool in = cl < A.nchr;
-    const bool keep = in && (!trust || cmax_at(c0) >= th);
-    const int ncl = c0 == 0 ? nc0 : (in ? ld_ag(A.ncand + o0 + cl) : 0);
-    uint64_t kept = __ballot(keep);
-    while (kept) {
-      const int k = __ffsll((unsigned long long)kept) - 1;
-      kept &= kept - 1;
-      const int c = c0 + k;
-      const int n = __builtin_amdgcn_readlane(ncl, k);
-      if (trust && n <= NCAND) {
-        if (lane < n) {
-          const int col = ld_ag(A.cand + (o0 + c) * NCAND + lane);
-          argmax_merge(v, extra, key(col), col);
-        }
-      } else {   // exact rescan of the chunk
-        const int64_t hi = min((int64_t)(c + 1) * CHR, A.V);
-        for (int64_t col = (int64_t)c * CHR + lane; col < hi; col += 64) argmax_merge(v, extra, key(col), (int)col);
-      }
+  for (int c0 = 0; c0 < A.nchr; c0 += DRAW_CHUNKS) {
+    const Chunk k = c0 == 0 ? k0 : fetch(c0);
+    const bool keep = c0 + cl < A.nchr && (!trust || k.cmx >= th);
+    const bool listed = keep && trust && k.n <= NCAND;
+    if (listed) {   // this half of the chunk's candidates, scored from their records (the exact keys)
+#pragma unroll
+      for (int i = 0; i < CAND_HALF; ++i)
+        if (half * CAND_HALF + i < k.n)
+          argmax_merge(v, extra, set_r ? Elem<PD>::round(k.w[i] / s) / k.e[i] : k.w[i] / k.e[i], k.col[i]);
+    }
+    uint64_t rescan = __ballot(keep && !listed && half == 0);
+    while (rescan) {   // exact rescan of the chunk by the whole wave
+      const int l = __ffsll((unsigned long long)rescan) - 1;
+      rescan &= rescan - 1;
+      const int c = c0 + l;
+      const int64_t hi = min((int64_t)(c + 1) * CHR, A.V);
+      for (int64_t col = (int64_t)c * CHR + lane; col < hi; col += 64) argmax_merge(v, extra, key(col), (int)col);
     }
   }
   wave_argmax(v, extra);
-  if (lane == 0) {
-    write_outputs(A, b, j, extra);
-    if (A.dbg_s) A.dbg_s[b] = s;
-  }
+  write_outputs(A, b, j, extra, pre);
+  if (lane == 0 && A.dbg_s) A.dbg_s[b] = s;
 }
 
 // statistics launch (logits without given statistics): per-(row, chunk) statistics of every row a
@@ -793,42 +926,33 @@ __global__ void __launch_bounds__(THREADS) accept_stats_kernel(AcceptArgs A) {
   if (threadIdx.x == 0) A.stats[(int64_t)rho * A.nch + c] = st;
 }
 
-// B step items, then B * nchr pair items (sequence by sequence).
+// B step items, one sequence each.
+template <int DT, bool PROBS>
+__global__ void __launch_bounds__(THREADS) accept_step_kernel(AcceptArgs A) {
+  __shared__ Stat sh_ms[2 * STEP_LDS + 1];
+  sequence_step<DT, PROBS>(A, blockIdx.x, sh_ms);
+}
+
+// B * nchr pair items (sequence by sequence).
 template <int DT, bool PROBS>
 __global__ void __launch_bounds__(THREADS) accept_kernel(AcceptArgs A) {
   __shared__ float shf[THREADS / 64];
-  __shared__ int sh_last;
-  __shared__ PairCtx sh_pc;
   __shared__ int sh_n[1];
   __shared__ int sh_c[NCAND];
-  if ((int)blockIdx.x < A.B) {
-    sequence_step<DT, PROBS>(A, blockIdx.x);
-    return;
-  }
-  const int item = blockIdx.x - A.B;
+  __shared__ float sh_w[NCAND], sh_e[NCAND];
+  const int item = blockIdx.x;
   const int b = item / A.nchr, c = item - b * A.nchr;
   // a pair item of a sampled sequence (greedy sequences were finished by their step)
   const float T = PROBS ? 1.f : A.temps[b];
+  const PairCtx pc = read_step<PROBS>(A, b);   // loaded with T (stale for a greedy sequence, unused)
   if (T <= 0.f) return;
-  float e[UNROLL_R][8];   // the chunk of the Exp(1) row does not depend on the step: loaded first
-  {
-    const float* er = A.E + (int64_t)b * A.ldE;
-    const bool vec_ok = (A.V % VEC) == 0 && ((reinterpret_cast<uintptr_t>(er) & 15) == 0);
-#pragma unroll
-    for (int u = 0; u < UNROLL_R; ++u)
-      load8_f32(er, (int64_t)c * CHR + (int64_t)(threadIdx.x + THREADS * u) * VEC, A.V, vec_ok, e[u]);
-  }
-  await_step<PROBS>(A, b, &sh_pc);
-  const PairCtx pc = sh_pc;
-  if (pc.ok) pair_chunk<DT, PROBS>(A, b, c, pc, e, shf, sh_n, sh_c);
-  if (threadIdx.x == 0) {
-    stores_done();
-    sh_last = count_in(seq_counter(A, b), (unsigned)A.nchr);   // the last pair item draws
-  }
-  __syncthreads();
-  if (!sh_last || threadIdx.x >= 64) return;
-  if (pc.ok) final_draw<DT, PROBS>(A, b, pc);
-  if (threadIdx.x == 0) st_ag(ready_flag(A, b), 0u);   // every pair item of b has passed its wait
+  pair_chunk<DT, PROBS>(A, b, c, pc, shf, sh_n, sh_c, sh_w, sh_e);
+}
+
+// B draws, one wave each.
+template <int DT, bool PROBS>
+__global__ void __launch_bounds__(64) accept_draw_kernel(AcceptArgs A) {
+  final_draw<DT, PROBS>(A, blockIdx.x);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -906,24 +1030,15 @@ int64_t nchunks(int64_t V) { return (V + CH - 1) / CH; }
 
 int64_t nchunks_r(int64_t V) { return (V + CHR - 1) / CHR; }
 
-// Control words at the start of the workspace (the error word; sequence counters and ready flags,
-// 1024 lines of 64 words each), so no call's records ever overlap them.
-constexpr int64_t CTL_REGION = 1024 * 64;
-constexpr int64_t CTL_BYTES = 256 + 2 * CTL_REGION * 4;
-
 int64_t accept_ws(int64_t B, int64_t K, int64_t V) {
   const int64_t nch = nchunks(V), nchr = nchunks_r(V);
   auto r = [](int64_t n) { return ((n + 255) / 256) * 256; };
-  return CTL_BYTES + r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) + r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) +
-         r(B * 2 * (int64_t)sizeof(Stat)) + 3 * r(B * nchr * 4) + r(B * nchr * NCAND * 4) + r(B * 4);
+  return r(B * (2 * K + 1) * nch * (int64_t)sizeof(Stat)) + r(B * (2 * K + 1) * (int64_t)sizeof(Stat)) +
+         r(B * 2 * (int64_t)sizeof(Stat)) + 3 * r(B * nchr * 4) + 3 * r(B * nchr * NCAND * 4) + r(B * 4);
 }
 
 void carve_accept(AcceptArgs& A, void* workspace, int64_t B, int64_t K, int nch, int nchr) {
   Carve cv{reinterpret_cast<char*>(workspace)};
-  unsigned* ctl = cv.take<unsigned>(64);
-  A.err = ctl + 1;
-  A.seqc = cv.take<unsigned>(CTL_REGION);
-  A.ready = cv.take<unsigned>(CTL_REGION);
   A.stats = cv.take<Stat>(B * (2 * K + 1) * nch);
   A.mstats = cv.take<Stat>(B * (2 * K + 1));
   A.pairstat = cv.take<Stat>(B * 2);
@@ -931,25 +1046,31 @@ void carve_accept(AcceptArgs& A, void* workspace, int64_t B, int64_t K, int nch,
   A.cmax = cv.take<float>(B * nchr);
   A.ncand = cv.take<int>(B * nchr);
   A.cand = cv.take<int>(B * nchr * NCAND);
+  A.candw = cv.take<float>(B * nchr * NCAND);
+  A.cande = cv.take<float>(B * nchr * NCAND);
   A.jpos = cv.take<int>(B);
   A.premerged = false;
 }
 
 bool dtype_ok(int32_t dt) { return dt == FS_F32 || dt == FS_BF16 || dt == FS_F16; }
 
-// The statistics launch (logits without given statistics), then B step items and B * nchr pair items
-// in one launch.
+// The statistics launch (logits without given statistics), then B step items, B * nchr pair items
+// and B draws.
 template <int DT>
 int launch_accept(const AcceptArgs& A, bool probs, hipStream_t s) {
-  const int64_t total = (int64_t)A.B * (1 + A.nchr);
+  const int64_t total = (int64_t)A.B * A.nchr;
   if (total * THREADS >= ((int64_t)1 << 32))
     return fs::arg_error("spec_accept: %lld work items exceed one launch", (long long)total);
   if (probs) {
+    accept_step_kernel<DT, true><<<dim3((unsigned)A.B), THREADS, 0, s>>>(A);
     accept_kernel<DT, true><<<dim3((unsigned)total), THREADS, 0, s>>>(A);
+    accept_draw_kernel<DT, true><<<dim3((unsigned)A.B), 64, 0, s>>>(A);
   } else {
     const int per = A.rs.n0 + A.rs.n1;
     if (!A.premerged) accept_stats_kernel<DT><<<dim3((unsigned)A.nch, (unsigned)(A.B * per)), THREADS, 0, s>>>(A);
+    accept_step_kernel<DT, false><<<dim3((unsigned)A.B), THREADS, 0, s>>>(A);
     accept_kernel<DT, false><<<dim3((unsigned)total), THREADS, 0, s>>>(A);
+    accept_draw_kernel<DT, false><<<dim3((unsigned)A.B), 64, 0, s>>>(A);
   }
   return fs::launch_status("spec_accept");
 }
@@ -1118,7 +1239,7 @@ extern "C" int fs_spec_accept_stats(const void* tgt, int64_t tgt_sb, int64_t tgt
 // ------------------------------------------------------------------------------------------------
 // Scratch of fs_spec_accept_noalloc: a fixed device array that each GPU holds for the life of the
 // process. Its size bounds the shapes that entry point takes (batch 512 at k = 8 and a 128256-token
-// vocabulary needs 3.6 MiB). Calls on one GPU share it: calls that overlap on one device race.
+// vocabulary needs 3.96 MiB). Calls on one GPU share it: calls that overlap on one device race.
 constexpr int64_t NOALLOC_SCRATCH_BYTES = (int64_t)4 << 20;
 static __device__ __align__(256) char scratch[NOALLOC_SCRATCH_BYTES];
 
@@ -1128,10 +1249,9 @@ std::mutex scratch_mu;
 void* scratch_ptr[MAX_DEVICES] = {};   // the array's device address on each GPU, looked up once per device
 
 // The scratch address on the current device: hipGetSymbolAddress the first time a device calls, with
-// that device current, then the acceptance's control words cleared on the caller's stream (the array
-// is zero when the code object loads; the clear makes that explicit); the cached pointer afterwards.
-// In host code `scratch` only names a host-side stand-in for the array, so kernels always receive this
-// pointer.
+// that device current (outside any stream capture), the cached pointer afterwards. The acceptance
+// needs no initial contents in its workspace. In host code `scratch` only names a host-side stand-in
+// for the array, so kernels always receive this pointer.
 int scratch_on_current_device(hipStream_t stream, void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
@@ -1157,11 +1277,6 @@ int scratch_on_current_device(hipStream_t stream, void** out) {
       fs::set_error("spec_accept_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
       return e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
     }
-    e = hipMemsetAsync(p, 0, CTL_BYTES, stream);
-    if (e != hipSuccess) {
-      fs::set_error("spec_accept_noalloc: clearing the scratch: %s", hipGetErrorString(e));
-      return (int)e;
-    }
     scratch_ptr[dev] = p;
   }
   *out = scratch_ptr[dev];
@@ -1183,7 +1298,6 @@ extern "C" int fs_spec_accept_noalloc(const void* tgt, int64_t tgt_sb, int64_t t
                B, K, (long long)V, (long long)need, (long long)NOALLOC_SCRATCH_BYTES);
   void* ws = nullptr;
   if (int rc = scratch_on_current_device(fs::as_stream(stream), &ws)) return rc;
-  // every call leaves the control words zero; the rest is rewritten before it is read
   return spec_accept_impl(tgt, tgt_sb, tgt_si, dft, dft_sb, dft_si, B, K, V, dtype, draft_tokens, k_eff, temperature, u,
                           E, ldE, out_tokens, n_accepted, seq_len, nullptr, nullptr, nullptr, row_stats, ws,
                           NOALLOC_SCRATCH_BYTES, stream);

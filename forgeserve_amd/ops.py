@@ -29,19 +29,16 @@ _PERSISTENT = {}
 _RETIRED = []   # outgrown scratch buffers: a captured HIP graph may still hold their addresses
 
 
-def _persistent_ws(name: str, nbytes: int, device, zero: bool = False) -> torch.Tensor:
+def _persistent_ws(name: str, nbytes: int, device) -> torch.Tensor:
     """A per-device scratch buffer reused across calls (calls are ordered on torch's current stream,
     so consecutive users never overlap); grown when a call needs more. An outgrown buffer is kept
-    alive for the life of the process, since graphs captured earlier launch kernels on it. zero: the
-    buffer is zero-filled when it is allocated (the acceptance's control words; its calls leave them
-    zero)."""
+    alive for the life of the process, since graphs captured earlier launch kernels on it."""
     key = (name, torch.device(device))
     ws = _PERSISTENT.get(key)
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
             _RETIRED.append(ws)
-        ws = (torch.zeros if zero else torch.empty)(max(int(nbytes * 1.25), 1 << 20), dtype=torch.uint8,
-                                                     device=key[1])
+        ws = torch.empty(max(int(nbytes * 1.25), 1 << 20), dtype=torch.uint8, device=key[1])
         _PERSISTENT[key] = ws
     return ws
 
@@ -522,7 +519,7 @@ def spec_accept(tgt: torch.Tensor, dft: torch.Tensor, draft_tokens: torch.Tensor
     if n_accepted is None:
         n_accepted = torch.empty((b,), dtype=I32, device=tgt.device)
     lib = _lib.load()
-    ws = _persistent_ws("accept", lib.fs_spec_accept_workspace_size(b, k, v), tgt.device, zero=True)
+    ws = _persistent_ws("accept", lib.fs_spec_accept_workspace_size(b, k, v), tgt.device)
     dbg = None
     if debug:
         dbg = {"p_x": torch.full((b, k), float("nan"), dtype=torch.float32, device=tgt.device),
@@ -560,7 +557,7 @@ def verify_probs(p: torch.Tensor, q: torch.Tensor, draft_tokens: torch.Tensor, u
     out = torch.empty((k + 1,), dtype=I32, device=p.device)
     n = torch.empty((1,), dtype=I32, device=p.device)
     lib = _lib.load()
-    ws = _persistent_ws("accept", lib.fs_spec_accept_workspace_size(1, k, v), p.device, zero=True)
+    ws = _persistent_ws("accept", lib.fs_spec_accept_workspace_size(1, k, v), p.device)
     check(lib.fs_verify_probs(ptr(p), p.stride(0), ptr(q), q.stride(0) if k else 0, k, v, _dt(p),
                               ptr(draft_tokens.contiguous()), ptr(u.contiguous()), ptr(noise.contiguous()), ptr(out),
                               ptr(n), ptr(ws), ws.numel(), stream_ptr()), "verify_probs")

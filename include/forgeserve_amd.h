@@ -306,10 +306,10 @@ int64_t fs_sampling_workspace_size(int64_t R, int64_t V);
  * untouched. res_sum [B] the sum of the residual max(p_j - q_j, 0) at the first rejection j
  * (speculative.py:30), 0 when every proposal was accepted or the row is greedy. They let a caller
  * measure how near a decision was to a tie.
- * The call is one kernel launch whose workgroups pass results to each other through the workspace:
- * its first 256 + 8 * 65536 bytes are control words that must be zero before the first call on a
- * workspace (zero-fill it once after allocating it); every call leaves them zero again. Calls that
- * share a workspace must not overlap (order them on one stream). */
+ * The call is four kernel launches (statistics, steps, chunks of the draws, draws; three with the
+ * statistics given) that pass records through the workspace; each launch reads only what an earlier
+ * one of the same call wrote, so the workspace needs no initial contents. Calls that share a
+ * workspace must not overlap (order them on one stream). */
 int fs_spec_accept(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
                    int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype, const int32_t* draft_tokens,
                    const int32_t* k_eff, const float* temperature, const float* u, const float* E,
@@ -336,8 +336,8 @@ int fs_spec_accept_stats(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const 
  * 128256-token vocabulary fits) are refused with FS_ERR_ARG before anything is launched. Every call on
  * one GPU shares that GPU's scratch, so calls that overlap on one device (different streams, or host
  * threads) race; calls ordered on one stream do not. No debug outputs. The first call on a device
- * looks the array up and clears its control words on `stream`; it must not be made while that stream
- * is being captured into a HIP graph (it then fails with FS_ERR_ARG): make one call before capturing. */
+ * looks the array up (a host API call); it must not be made while `stream` is being captured into a
+ * HIP graph (it then fails with FS_ERR_ARG): make one call before capturing. */
 int fs_spec_accept_noalloc(const void* tgt, int64_t tgt_sb, int64_t tgt_si, const void* dft, int64_t dft_sb,
                            int64_t dft_si, int32_t B, int32_t K, int64_t V, int32_t dtype, const int32_t* draft_tokens,
                            const int32_t* k_eff, const float* temperature, const float* u, const float* E,
@@ -366,8 +366,7 @@ int fs_verify_probs(const void* p, int64_t ldp, const void* q, int64_t ldq, int3
                     int32_t* out_tokens, int32_t* n_accepted, void* workspace, int64_t workspace_bytes,
                     void* stream);
 
-/* Workspace of fs_spec_accept / fs_verify_probs (256-byte aligned; zero-filled before its first use,
- * and left with its control words zero by every call: see fs_spec_accept). */
+/* Workspace of fs_spec_accept / fs_verify_probs (256-byte aligned, any contents). */
 int64_t fs_spec_accept_workspace_size(int32_t B, int32_t K, int64_t V);
 
 /* ---------------------------------------------------------------------------------------------- */
