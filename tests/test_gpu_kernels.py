@@ -1008,6 +1008,43 @@ def test_spec_accept_many_proposals_debug_outputs():
             assert float(dbg["res_sum"][i]) == 0.0
 
 
+def test_spec_accept_vocab_past_32_chunks():
+    """A vocabulary of 140,003 columns: 35 chunks of 4096, so the draw takes its chunks in two passes of
+    32, and V is not a multiple of 8, so every row ends in a partial 16-byte group (the bounds-checked
+    loads). f32 and bf16 logits, statistics computed or given; one sequence's residual is planted in
+    the last chunk and one's in the first, against the oracle."""
+    case("spec_accept V=140003")
+    g = torch.Generator().manual_seed(44)
+    b, k, v = 4, 3, 140003
+    tgt = torch.randn(b, k + 1, v, generator=g) * 2
+    dft = tgt[:, :k] + torch.randn(b, k, v, generator=g)
+    xs = torch.randint(0, v, (b, k), generator=g, dtype=torch.int32)
+    u = torch.rand(b, k, generator=g)
+    u[0, 0] = u[1, 0] = 1.0          # sequences 0 and 1 reject their first proposal
+    tgt[0, 0, v - 5] = dft[0, 0, v - 5] + 20.0   # ... with the residual's mass in the last chunk
+    tgt[1, 0, 3] = dft[1, 0, 3] + 20.0
+    e = torch.empty(b, v).exponential_(generator=g)
+    temps = torch.ones(b)
+    for dtype in (torch.float32, torch.bfloat16):
+        t_, d_ = tgt.to(dtype), dft.to(dtype)
+        for mode in ("logits", "stats"):
+            kw = {}
+            if mode == "stats":
+                rows = torch.cat([t_, d_], 1).float()
+                mx = rows.max(-1).values
+                kw["row_stats"] = _records(mx, torch.exp((rows - mx[..., None]).double()).sum(-1).float(),
+                                           mx, rows.argmax(-1)).to(DEV)
+            out, n = ops.spec_accept(t_.to(DEV), d_.to(DEV), xs.to(DEV), None, temps.to(DEV), u.to(DEV), e.to(DEV),
+                                     **kw)
+            out, n = out.cpu(), n.cpu()
+            for i in range(b):
+                p = orc.probs_from_logits(t_[i].float(), 1.0)
+                q = orc.probs_from_logits(d_[i].float(), 1.0)
+                acc, extra = orc.verify_with_noise(p, q, xs[i].tolist(), u[i], e[i])
+                assert int(n[i]) == len(acc) and out[i, : len(acc) + 1].tolist() == acc + [extra], (dtype, mode, i)
+            assert int(out[0, 0]) >= 32 * 4096 and int(out[1, 0]) < 4096, (dtype, mode)
+
+
 def test_spec_accept_repeated_calls_on_a_dirty_workspace():
     """Back-to-back calls of different shapes and modes on the one workspace (statistics pass, given
     statistics, probabilities, greedy and sampled rows), each after the workspace was filled with 0xFF
