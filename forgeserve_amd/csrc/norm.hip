@@ -126,7 +126,10 @@ __global__ void __launch_bounds__(NORM_THREADS) add_rmsnorm_vec_kernel(
 // order), then the residual: x_out = round(x + residual), y = rmsnorm(x_out) * w. This is the GEMM's
 // reduction (gemm_splitk_reduce_kernel) followed by add_rmsnorm_vec_kernel on its output, in one pass.
 // SPLITS > 0: that many partials, all loaded before the first add; 0: `splits` of them, one at a time.
-template <int DT, int SPLITS>
+// G > 0: the row is exactly G groups per thread (N = NORM_THREADS * 8 * G): every group's loads are
+// issued before the first is used (with a bounds branch around each group, the compiler waits for a
+// group's loads before issuing the next group's); G == 0: any N up to NORM_VEC_MAX, group by group.
+template <int DT, int SPLITS, int G>
 __global__ void __launch_bounds__(NORM_THREADS) splitk_add_rmsnorm_kernel(
     const float* __restrict__ parts, int splits, int64_t part_stride, const uint16_t* __restrict__ residual,
     int64_t ldr, uint16_t* __restrict__ x_out, int64_t ldxo, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
@@ -136,6 +139,45 @@ __global__ void __launch_bounds__(NORM_THREADS) splitk_add_rmsnorm_kernel(
   const int ng = (int)(N / 8);
   float v[NORM_VEC_GROUPS][8];
   float sq = 0.f;
+  if constexpr (G > 0 && SPLITS > 0) {
+    static_assert(G <= NORM_VEC_GROUPS, "at most NORM_VEC_GROUPS groups per thread");
+    float4_t q0[G][SPLITS], q1[G][SPLITS];
+    u32x4_t rr[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int gi = threadIdx.x + NORM_THREADS * u;
+      const float* p0 = parts + m * N + 8 * gi;
+#pragma unroll
+      for (int sp = 0; sp < SPLITS; ++sp) {
+        q0[u][sp] = *reinterpret_cast<const float4_t*>(p0 + sp * part_stride);
+        q1[u][sp] = *reinterpret_cast<const float4_t*>(p0 + sp * part_stride + 4);
+      }
+      rr[u] = *reinterpret_cast<const u32x4_t*>(residual + m * ldr + 8 * gi);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int gi = threadIdx.x + NORM_THREADS * u;
+      float4_t a0 = q0[u][0], a1 = q1[u][0];
+#pragma unroll
+      for (int sp = 1; sp < SPLITS; ++sp)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          a0[j] += q0[u][sp][j];
+          a1[j] += q1[u][sp][j];
+        }
+      float d[8];
+      unpack8<DT>(rr[u], d);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[u][j] = Elem<DT>::round(Elem<DT>::round(a0[j]) + d[j]);
+        v[u][j + 4] = Elem<DT>::round(Elem<DT>::round(a1[j]) + d[j + 4]);
+      }
+      *reinterpret_cast<u32x4_t*>(x_out + m * ldxo + 8 * gi) = pack8<DT>(v[u]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sq += v[u][j] * v[u][j];
+    }
+  } else {
 #pragma unroll
   for (int u = 0; u < NORM_VEC_GROUPS; ++u) {
     const int gi = threadIdx.x + NORM_THREADS * u;
@@ -182,6 +224,7 @@ __global__ void __launch_bounds__(NORM_THREADS) splitk_add_rmsnorm_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) sq += v[u][j] * v[u][j];
   }
+  }
   sq = wave_sum(sq);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
   __syncthreads();
@@ -190,7 +233,7 @@ __global__ void __launch_bounds__(NORM_THREADS) splitk_add_rmsnorm_kernel(
   for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[i];
   const float r = 1.0f / sqrtf(tot / (float)N + eps);
 #pragma unroll
-  for (int u = 0; u < NORM_VEC_GROUPS; ++u) {
+  for (int u = 0; u < (G > 0 && SPLITS > 0 ? G : NORM_VEC_GROUPS); ++u) {
     const int gi = threadIdx.x + NORM_THREADS * u;
     if (gi >= ng) continue;
     float wv[8], o[8];
@@ -280,20 +323,32 @@ extern "C" int fs_splitk_add_rmsnorm(const float* parts, int32_t splits, const v
                "splitk_add_rmsnorm: 16-byte aligned rows");
   if (M == 0) return 0;
   hipStream_t s = fs::as_stream(stream);
-#define FS_LAUNCH_PARTS(DT, S)                                                                                  \
-  splitk_add_rmsnorm_kernel<DT, S><<<dim3((unsigned)M), NORM_THREADS, 0, s>>>(                               \
+  // Short batches (latency-bound: a decode step's rows) take whole groups per thread with every load
+  // issued up front, at most 8 partial groups in registers per thread; long ones (bandwidth-bound,
+  // where issuing every load at once measured slower: 448 rows 9.4 -> 10.2 us) go group by group. The
+  // two forms do the same arithmetic in the same order, so a row's bits do not depend on M.
+  const int64_t gpt = N % (NORM_THREADS * 8) == 0 ? N / (NORM_THREADS * 8) : 0;
+  const int g = M <= 128 && (gpt == 1 || gpt == 2 || gpt == 4) && gpt * splits <= 8 ? (int)gpt : 0;
+#define FS_LAUNCH_PARTS(DT, S, G)                                                                               \
+  splitk_add_rmsnorm_kernel<DT, S, G><<<dim3((unsigned)M), NORM_THREADS, 0, s>>>(                            \
       parts, splits, M * N, (const uint16_t*)residual, ldr, (uint16_t*)x_out, ldxo, (const uint16_t*)weight,      \
       (uint16_t*)y, ldy, N, eps)
+#define FS_LAUNCH_G(DT, S)                                                                                      \
+  if (g == 1) FS_LAUNCH_PARTS(DT, S, 1);                                                                      \
+  else if (g == 2 && (S) <= 4) FS_LAUNCH_PARTS(DT, S, (S) <= 4 ? 2 : 0);                                     \
+  else if (g == 4 && (S) <= 2) FS_LAUNCH_PARTS(DT, S, (S) <= 2 ? 4 : 0);                                     \
+  else FS_LAUNCH_PARTS(DT, S, 0);
 #define FS_LAUNCH_DT(DT)                                                                                        \
   switch (splits) {                                                                                           \
-    case 2: FS_LAUNCH_PARTS(DT, 2); break;                                                                    \
-    case 4: FS_LAUNCH_PARTS(DT, 4); break;                                                                    \
-    case 8: FS_LAUNCH_PARTS(DT, 8); break;                                                                    \
-    default: FS_LAUNCH_PARTS(DT, 0); break;                                                                   \
+    case 2: FS_LAUNCH_G(DT, 2); break;                                                                        \
+    case 4: FS_LAUNCH_G(DT, 4); break;                                                                        \
+    case 8: FS_LAUNCH_G(DT, 8); break;                                                                        \
+    default: FS_LAUNCH_PARTS(DT, 0, 0); break;                                                                \
   }
   if (dtype == FS_BF16) FS_LAUNCH_DT(FS_BF16)
   else FS_LAUNCH_DT(FS_F16)
 #undef FS_LAUNCH_DT
+#undef FS_LAUNCH_G
 #undef FS_LAUNCH_PARTS
   return fs::launch_status("splitk_add_rmsnorm");
 }

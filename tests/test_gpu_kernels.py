@@ -108,6 +108,32 @@ def test_splitk_add_rmsnorm_equals_gemm_then_norm(m, n, k):
     assert torch.equal(y, ops.add_rmsnorm(x_ref, nw, 1e-5))
 
 
+@pytest.mark.parametrize("n,splits", [(4096, 4), (2048, 8), (2048, 2), (1024, 4)])
+def test_splitk_add_rmsnorm_rows_do_not_depend_on_the_batch(n, splits):
+    """The split-K residual-add + RMSNorm gives a row the same bits in a 448-row call (loads group by
+    group) as in a 64-row call (every load issued up front), for the row widths of the 8B and 1B
+    models and one that takes the general path."""
+    case("splitk add_rmsnorm rows", n, splits)
+    from forgeserve_amd import _lib
+    from forgeserve_amd._lib import ptr, stream_ptr
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(n + splits)
+    big, small = 448, 64
+    parts = torch.randn(splits, big, n, generator=g).to(DEV)
+    resid = torch.randn(big, n, generator=g).bfloat16().to(DEV)
+    w = (1 + 0.1 * torch.randn(n, generator=g)).bfloat16().to(DEV)
+    outs = {}
+    for m in (big, small):
+        p = parts[:, :m].contiguous()
+        x = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+        y = torch.empty_like(x)
+        assert lib.fs_splitk_add_rmsnorm(ptr(p), splits, ptr(resid), n, ptr(x), n, ptr(w), ptr(y), n, m, n, 1e-5,
+                                         _lib.BF16, stream_ptr()) == 0
+        outs[m] = (x, y)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[big][0][:small], outs[small][0]) and torch.equal(outs[big][1][:small], outs[small][1])
+
+
 @pytest.mark.parametrize("m,n,k", [(4133, 4096, 4096), (8192, 4096, 8192), (2600, 6144, 4096),
                                    (3900, 4100, 4096)])   # a partial last column tile
 def test_gemm_serial_splits_equal_short_batch_rows(m, n, k):
