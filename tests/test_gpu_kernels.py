@@ -777,7 +777,7 @@ def _c2_inputs(b=64, k=5, v=32000, seed=3, dtype=torch.float32):
 
 
 @pytest.mark.parametrize("temperature", [1.0, 0.0, 0.7])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_spec_accept_c2_bit_exact(temperature, dtype):
     """Batch 64, k=5, V=32000: accepted lengths, replacement and bonus tokens identical to the oracle's
     verify_draft on the same injected uniforms and Exp(1) noise."""
@@ -1037,7 +1037,7 @@ def test_spec_accept_many_proposals_debug_outputs():
 def test_spec_accept_vocab_past_32_chunks():
     """A vocabulary of 140,003 columns: 35 chunks of 4096, so the draw takes its chunks in two passes of
     32, and V is not a multiple of 8, so every row ends in a partial 16-byte group (the bounds-checked
-    loads). f32 and bf16 logits, statistics computed or given; one sequence's residual is planted in
+    loads). f32, bf16 and f16 logits, statistics computed or given; one sequence's residual is planted in
     the last chunk and one's in the first, against the oracle."""
     case("spec_accept V=140003")
     g = torch.Generator().manual_seed(44)
@@ -1051,7 +1051,7 @@ def test_spec_accept_vocab_past_32_chunks():
     tgt[1, 0, 3] = dft[1, 0, 3] + 20.0
     e = torch.empty(b, v).exponential_(generator=g)
     temps = torch.ones(b)
-    for dtype in (torch.float32, torch.bfloat16):
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
         t_, d_ = tgt.to(dtype), dft.to(dtype)
         for mode in ("logits", "stats"):
             kw = {}
