@@ -826,6 +826,22 @@ def test_sample_logits(temperature):
     assert got == want
 
 
+@pytest.mark.parametrize("temperature", [0.0, 0.7, 1.0])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_sample_logits_whole_groups(temperature, dtype):
+    """Rows whose columns fill whole 16-byte groups (V = 32000 and 20000: the loads issued together, a
+    partial last chunk for 20000), against the oracle's draw on the same noise."""
+    case("sample_logits whole groups", temperature, dtype)
+    g = torch.Generator().manual_seed(9)
+    for v in (32000, 20000):
+        x = (torch.randn(23, v, generator=g) * 3).to(dtype)
+        e = torch.empty(23, v).exponential_(generator=g)
+        got = ops.sample_logits(x.to(DEV), temperature, e.to(DEV) if temperature else None).cpu().tolist()
+        want = [orc.draw(orc.probs_from_logits(x[r].float(), temperature), e[r]) if temperature
+                else int(x[r].float().argmax()) for r in range(23)]
+        assert got == want, v
+
+
 def test_probs_from_logits():
     case("probs_from_logits")
     x = torch.randn(5, 20000) * 4
