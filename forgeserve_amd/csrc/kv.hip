@@ -111,9 +111,23 @@ FS_DEVICE void load8(const uint16_t* qkv, const QkvPart& pp, int64_t e, float (&
   }
 }
 
+// Verify windows: T consecutive tokens of a table row (rows back to back, T <= VWIN_MAX_T) sit in
+// consecutive pool slots, so a dim's values of the window are one short run of the dim-major value
+// tile. Their values are written by the grid's last row of workgroups through LDS, lanes taking
+// consecutive tokens of one dim; written per token, every lane of a store would hit its own 32-byte
+// run (the 8B verify shape, 448 tokens from two K splits: 12.8 -> 10.6 us per call).
+// A window workgroup stages the values of all its heads (at most ceil(n_kv_heads / T) of them) at once.
+constexpr int VWIN_MAX_T = 16;
+constexpr int VWIN_LDS = 8192;   // 16-bit elements
+__host__ __device__ inline bool value_window(int T, const int32_t* token_row, int n_kv_heads, int head_dim) {
+  return T > 1 && T <= VWIN_MAX_T && token_row == nullptr && (n_kv_heads + T) * head_dim <= VWIN_LDS;
+}
+
 // Grid (token, group block): each thread takes one 8-pair rotation group of a q or k head, or one
 // 8-element group of the values (grid.y blocks of blockDim.x groups cover both), so a token's work is
-// spread over several workgroups and every thread issues its loads at once.
+// spread over several workgroups and every thread issues its loads at once. For a verify window
+// (value_window) the per-token blocks take only the rotation groups, and workgroup (token m, last
+// grid row) writes the values of KV heads m % T, m % T + T, ... for every token of m's row.
 template <int DT, int PART = 0>
 __global__ void __launch_bounds__(128) qkv_rope_write_vec_kernel(
     const uint16_t* __restrict__ qkv, QkvPart pp, int64_t qkv_stride, int32_t T, int32_t H,
@@ -126,11 +140,73 @@ __global__ void __launch_bounds__(128) qkv_rope_write_vec_kernel(
   const int D = kv.head_dim, half = D / 2, Hkv = kv.n_kv_heads;
   const int ng = half / 8;
   const int n_groups = (H + Hkv) * ng, nv = Hkv * D / 8;
+  const bool vwin = value_window(T, token_row, Hkv, D);
+  if (vwin && blockIdx.y == gridDim.y - 1) {
+    __shared__ uint16_t vt[VWIN_LDS];   // the window's values of the workgroup's heads, [head][dim][token]
+    __shared__ int64_t sblk[VWIN_MAX_T];
+    __shared__ int sslot[VWIN_MAX_T], sok[VWIN_MAX_T];
+    const int b = (int)(m / T), t0 = (int)(m - (int64_t)b * T);
+    const int64_t mrow = (int64_t)b * T;
+    if ((int)threadIdx.x < T) {   // each token's pool slot, found as the per-token path finds it
+      const int64_t mt = mrow + threadIdx.x;
+      const int pos = positions[mt];
+      int64_t blk = 0;
+      int slot = 0;
+      const int wpos = slots ? slots[mt] : pos;
+      const bool ok = pos >= 0 && pos < rope_len && slot_of(wpos, table, table_stride, b, max_blocks, kv, blk, slot);
+      sblk[threadIdx.x] = blk;
+      sslot[threadIdx.x] = slot;
+      sok[threadIdx.x] = ok ? 1 : 0;
+    }
+    uint16_t* vp = reinterpret_cast<uint16_t*>(kv.v);
+    const int gpt = D / 8, nh = t0 < Hkv ? (Hkv - t0 + T - 1) / T : 0;   // heads t0, t0 + T, ...
+    for (int i = threadIdx.x; i < T * gpt; i += blockDim.x) {   // token i / gpt, dims 8 (i % gpt) ..
+      const int t = i / gpt, c = i - t * gpt;
+      const int64_t e0 = (mrow + t) * qkv_stride + (int64_t)(H + Hkv + t0) * D + 8 * c;
+      for (int h0 = 0; h0 < nh; h0 += 2) {   // two heads' loads in flight together
+        u32x4_t w[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int64_t e = e0 + (int64_t)min(h0 + u, nh - 1) * T * D;
+          if (PART != 0) {
+            float x[8];
+            load8<DT, PART>(qkv, pp, e, x);
+            w[u] = pack8<DT>(x);
+          } else {
+            w[u] = *reinterpret_cast<const u32x4_t*>(qkv + e);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          if (h0 + u >= nh) break;
+          uint16_t* row = vt + ((h0 + u) * D + 8 * c) * T + t;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            row[(2 * j) * T] = (uint16_t)(w[u][j] & 0xffffu);
+            row[(2 * j + 1) * T] = (uint16_t)(w[u][j] >> 16);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // thread k stores token k % T of dims k / T, k / T + dstep, ...: a store's lanes run along the
+    // tokens of one dim, then to the next dim
+    const int tq = (int)threadIdx.x % T, dq = (int)threadIdx.x / T, dstep = (int)blockDim.x / T;
+    if (dq < dstep && sok[tq]) {
+      uint16_t* vq = vp + sblk[tq] * kv.v_block + (int64_t)t0 * kv.v_head + (int64_t)sslot[tq] * kv.v_slot;
+      for (int hi = 0; hi < nh; ++hi) {
+        uint16_t* vh = vq + (int64_t)hi * T * kv.v_head;
+        const uint16_t* src = vt + hi * D * T + tq;
+        for (int d = dq; d < D; d += dstep) vh[(int64_t)d * kv.v_dim] = src[d * T];
+      }
+    }
+    return;
+  }
   const int64_t row0 = m * qkv_stride;   // the token's first element (of qkv, or of each partial)
   const int gi = blockIdx.y * blockDim.x + threadIdx.x;
   // The thread's inputs are loaded first: they depend on nothing the position decides, so they are in
   // flight while the position, the rotary row and the pool slot are looked up.
-  const bool rot_thread = gi < n_groups, val_thread = !rot_thread && gi < n_groups + nv;
+  const bool rot_thread = gi < n_groups, val_thread = !vwin && !rot_thread && gi < n_groups + nv;
   const int head = rot_thread ? gi / ng : 0, p0 = rot_thread ? 8 * (gi - head * ng) : 0;
   const int e0 = val_thread ? 8 * (gi - n_groups) : 0;   // value group: element e0 of the kv heads' values
   float x1[8], x2[8];
@@ -349,8 +425,12 @@ int qkv_rope_write(const void* qkv, int64_t qkv_stride, int64_t n_tokens, int32_
                    kv->k_head % 8 == 0 && kv->k_block % 8 == 0 && al16(pp.part ? (const void*)pp.part : qkv) &&
                    al16(q_out) && al16(kv->k) && al16(rope_cos) && al16(rope_sin);
   // the vectorised kernel: one thread per 8-element group (q/k rotation groups, then value groups)
-  const int vec_groups = (n_heads + kv->n_kv_heads) * (kv->head_dim / 16) + kv->n_kv_heads * kv->head_dim / 8;
-  const dim3 vgrid((unsigned)n_tokens, (unsigned)((vec_groups + 127) / 128));
+  // (a verify window: the rotation groups' blocks, then one row of value workgroups)
+  const int rot_groups = (n_heads + kv->n_kv_heads) * (kv->head_dim / 16);
+  const int vec_groups = rot_groups + kv->n_kv_heads * kv->head_dim / 8;
+  const dim3 vgrid((unsigned)n_tokens, value_window(T, token_row, kv->n_kv_heads, kv->head_dim)
+                                           ? (unsigned)((rot_groups + 127) / 128 + 1)
+                                           : (unsigned)((vec_groups + 127) / 128));
   if (pp.part) {   // the partials are read by the vectorised kernel only
     FS_CHECK_ARG(vec && pp.splits >= 1 && pp.stride >= n_tokens * qkv_stride,
                  "qkv_rope_write_partials: needs 16-bit data, head_dim/2 %% 8 == 0, 16-byte aligned rows");

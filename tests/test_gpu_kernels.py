@@ -286,6 +286,65 @@ def test_qkv_rope_write(dtype, d, bs, key_layout):
             assert torch.equal(vp[blk, :, p % bs], v_ref[bi, :, ti])
 
 
+@pytest.mark.parametrize("t,d,partials", [(7, 128, False), (7, 128, True), (2, 64, False), (16, 128, True)])
+def test_qkv_rope_write_window_across_blocks(t, d, partials):
+    """A verify window's values are written by the window workgroups (tokens of a row in consecutive
+    slots, lanes taking consecutive tokens of one dim): windows that cross a block boundary, a padding
+    token, T = 2 (a workgroup writes several KV heads) and T = 16 (more tokens than KV heads). Keys and
+    values equal the oracle's, and the pool equals the one written token by token (T = 1, each token
+    through its row's table)."""
+    case("qkv_rope_write window", t, d, partials)
+    from forgeserve_amd import PagedKVPool, ModelConfig
+    h, hkv, b, bs = 32, 8, 6, 16
+    cfg = ModelConfig(vocab_size=10, d_model=h * d, n_layers=1, n_heads=h, n_kv_heads=hkv, max_seq_len=256)
+    cos, sin = orc.rope_tables(orc.Shape.of(cfg))
+    g = torch.Generator().manual_seed(40 + t)
+    nb = 8
+    tables = torch.randperm(b * nb, generator=g).reshape(b, nb)
+    starts = torch.tensor([14, 31, 0, 60, 95, 47])          # windows across slots 15|16, 31|32, 63|64 ...
+    pos = starts[:, None] + torch.arange(t)
+    pos[1, -1] = -1                                          # a padding token
+    n = (h + 2 * hkv) * d
+    qkv = torch.randn(b * t, n, generator=g).bfloat16()
+    pools = [PagedKVPool(cfg, b * nb, bs, dtype=torch.bfloat16, device=DEV, key_layout="groups") for _ in range(2)]
+    args = (cos.to(DEV), sin.to(DEV))
+    flat_pos = pos.reshape(-1).int().to(DEV)
+    if partials:   # two split-K partials whose sum rounds to qkv's values
+        p0 = torch.randn(b * t, n, generator=g)
+        part = torch.stack([p0, qkv.float() - p0]).to(DEV).contiguous()
+        lib = _lib.load()
+        q = torch.empty((b * t, h * d), dtype=torch.bfloat16, device=DEV)
+        tab = tables.int().to(DEV)
+        ops.check(lib.fs_qkv_rope_write_partials(part.data_ptr(), 2, b * t, n, t, h, flat_pos.data_ptr(), 0,
+                                                 args[0].data_ptr(), args[1].data_ptr(), args[0].shape[0],
+                                                 tab.data_ptr(), tab.stride(0), tab.shape[1], pools[0].layout(0),
+                                                 q.data_ptr(), q.stride(0), ops.stream_ptr()), "partials")
+        qkv = (part[0] + part[1]).bfloat16().cpu()   # the values the kernel adds and rounds
+    else:
+        q = ops.qkv_rope_write(qkv.to(DEV), flat_pos, t, h, *args, tables.int().to(DEV), pools[0].layout(0))
+    q_one = ops.qkv_rope_write(qkv.to(DEV), flat_pos, 1, h, *args, tables.repeat_interleave(t, 0).int().to(DEV),
+                               pools[1].layout(0))
+    ok = (pos >= 0).reshape(-1).to(DEV)
+    assert torch.equal(q[ok], q_one[ok])
+    assert torch.equal(pools[0].k_store, pools[1].k_store)
+    assert torch.equal(pools[0].v_store, pools[1].v_store)
+    x = qkv.view(b, t, h + 2 * hkv, d).transpose(1, 2)
+    k_ref = orc.rotate(x[:, h:h + hkv], cos, sin, pos.clamp(min=0))
+    v_ref = x[:, h + hkv:]
+    kp, vp = _keys(pools[0]).cpu(), pools[0].v[0].cpu()
+    nonzero = 0
+    for bi in range(b):
+        for ti in range(t):
+            p = int(pos[bi, ti])
+            if p < 0:
+                continue
+            blk = int(tables[bi, p // bs])
+            assert torch.equal(kp[blk, :, p % bs], k_ref[bi, :, ti])
+            assert torch.equal(vp[blk, :, p % bs], v_ref[bi, :, ti])
+            nonzero += int(v_ref[bi, :, ti].ne(0).sum())
+    assert int(pools[0].v_store.ne(0).sum()) == nonzero   # no other slot of the pool was written
+
+
 # ---- paged attention --------------------------------------------------------------------------------------
 def _paged_case(b, t, h, hkv, d, bs, ctx, nblocks, dtype, seed):
     g = torch.Generator().manual_seed(seed)
