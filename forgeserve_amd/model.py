@@ -143,18 +143,20 @@ class Block(nn.Module):
         self.mlp_norm = RMSNorm(cfg.d_model, cfg.norm_eps)
         self.mlp = SwiGLU(cfg, tp)
 
-    def step(self, x: torch.Tensor, b: int, t: int, pos32: torch.Tensor, view, rope, h=None, next_norm=None):
+    def step(self, x: torch.Tensor, b: int, t: int, pos32: torch.Tensor, view, rope, h=None, next_norm=None,
+             x_out=None):
         """x (B*T, d) -> x + attn(norm(x)), then + mlp(norm(.)) (model.py:104-106). h: norm(x) by this
         block's attention norm when the caller has it. Returns (x_out, next_norm(x_out) or None): a
-        projection that splits K is reduced inside the residual-add + norm kernel that follows it."""
+        projection that splits K is reduced inside the residual-add + norm kernel that follows it. x_out:
+        where the block's output goes (a new tensor when None)."""
         if h is None:
             h = ops.add_rmsnorm(x, self.attn_norm.weight, self.attn_norm.eps)
         a = self.attn.attend(h, b, t, pos32, view, rope)
         x1, h2 = ops.gemm_add_rmsnorm(a, self.attn.wo.weight, x, self.mlp_norm.weight, self.mlp_norm.eps)
         g = ops.gemm_swiglu(h2, self.mlp.gate_up_weight())
         if next_norm is None:
-            return ops.gemm(g, self.mlp.w_down.weight, residual=x1), None
-        return ops.gemm_add_rmsnorm(g, self.mlp.w_down.weight, x1, next_norm.weight, next_norm.eps)
+            return ops.gemm(g, self.mlp.w_down.weight, out=x_out, residual=x1), None
+        return ops.gemm_add_rmsnorm(g, self.mlp.w_down.weight, x1, next_norm.weight, next_norm.eps, x_out=x_out)
 
 
 class ForgeModel(nn.Module):
@@ -253,10 +255,11 @@ class ForgeModel(nn.Module):
         receive the logits (then it is returned as is) and `hidden_out` (B, d_model) the last
         position's residual stream after the last layer (the head's input before its norm)."""
         b, t = idx.shape
+        direct = last_only and t == 1 and hidden_out is not None   # the last block writes hidden_out
         x, y = self._layers(ops.embedding(idx, self.tok_emb.weight), 0, len(self.layers), b, t, pos32, kv,
-                            last_norm=self.norm)
+                            last_norm=self.norm, x_out=hidden_out if direct else None)
         if last_only:
-            if hidden_out is not None:
+            if hidden_out is not None and x is not hidden_out:
                 hidden_out.copy_(x.view(b, t, -1)[:, -1])
             y = y.view(b, t, -1)[:, -1].contiguous()
             if out is not None:
@@ -265,16 +268,17 @@ class ForgeModel(nn.Module):
         return self.head_normed(y, head_stats).view(b, t, -1)
 
     def _layers(self, x: torch.Tensor, start: int, stop: int, b: int, t: int, pos32: torch.Tensor, kv: List,
-                last_norm=None):
+                last_norm=None, x_out=None):
         """Blocks start..stop-1 on the residual stream x (B*T, d); kv[i] is block i's cache view.
         Returns (x, last_norm(x)): each block's output is normalised by the next block's attention
         norm in the same kernel as its last projection's reduction; after block stop-1 by last_norm
-        (None: not normalised)."""
+        (None: not normalised). x_out: where block stop-1 writes its output (then returned as x)."""
         rope = self._rope()
         h = None
         for i in range(start, stop):
             nxt = self.layers[i + 1].attn_norm if i + 1 < stop else last_norm
-            x, h = self.layers[i].step(x, b, t, pos32, kv[i], rope, h=h, next_norm=nxt)
+            x, h = self.layers[i].step(x, b, t, pos32, kv[i], rope, h=h, next_norm=nxt,
+                                       x_out=x_out if i == stop - 1 else None)
         if start >= stop and last_norm is not None:   # no block ran (a draft that is the whole model)
             h = ops.add_rmsnorm(x, last_norm.weight, last_norm.eps)
         return x, h

@@ -99,12 +99,13 @@ def gemm(a: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
 
 
 def gemm_add_rmsnorm(a: torch.Tensor, w: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor,
-                     eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+                     eps: float, x_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """x = a @ w.T + residual (nn.Linear then the residual add, model.py:105-106) and y = RMSNorm(x)
     with norm_weight (model.py:29-31): returns (x, y). When the GEMM splits K into partials, they are
     added by the norm kernel itself (no separate reduction pass); otherwise (no split, or a long batch
     whose workgroups run the splits one after the other) the GEMM adds the residual and the norm runs
-    on its output. The results are the same either way."""
+    on its output. The results are the same either way. x_out: an (m, n) tensor with unit column stride
+    that receives x (returned as x)."""
     require_device(a, w, residual, norm_weight)
     m, lda = _rows(a)
     n, ldb = _rows(w)
@@ -120,14 +121,19 @@ def gemm_add_rmsnorm(a: torch.Tensor, w: torch.Tensor, residual: torch.Tensor, n
         ws = _persistent_ws("gemm", need, a.device)
         check(lib.fs_gemm_partials(ptr(a), lda, ptr(w), ldb, m, n, k, _dt(a), ptr(ws), ws.numel(), stream_ptr()),
               "gemm_partials")
-        x = torch.empty((m, n), dtype=a.dtype, device=a.device)
+        direct = (x_out is not None and x_out.shape == (m, n) and x_out.dtype == a.dtype and x_out.stride(1) == 1
+                  and x_out.stride(0) % 8 == 0 and x_out.data_ptr() % 16 == 0)
+        x = x_out if direct else torch.empty((m, n), dtype=a.dtype, device=a.device)
         y = torch.empty((m, n), dtype=a.dtype, device=a.device)
-        check(lib.fs_splitk_add_rmsnorm(ptr(ws), splits, ptr(residual), residual.stride(0), ptr(x), n,
+        check(lib.fs_splitk_add_rmsnorm(ptr(ws), splits, ptr(residual), residual.stride(0), ptr(x), x.stride(0),
                                         ptr(norm_weight), ptr(y), n, m, n, float(eps), _dt(a), stream_ptr()),
               "splitk_add_rmsnorm")
+        if x_out is not None and not direct:
+            x = x_out.copy_(x)
         return x, y
     x = gemm(a, w, residual=residual)
-    return x, add_rmsnorm(x, norm_weight, eps)
+    y = add_rmsnorm(x, norm_weight, eps)
+    return (x if x_out is None else x_out.copy_(x)), y
 
 
 def row_stats_parts(m: int, n: int, k: int) -> int:
@@ -443,12 +449,14 @@ def probs_from_logits(logits: torch.Tensor, temperature: float) -> torch.Tensor:
 
 
 def sample_logits(logits: torch.Tensor, temperature, noise: Optional[torch.Tensor] = None,
-                  out32: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  out32: Optional[torch.Tensor] = None, out64: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Token ids (int64, logits.shape[:-1]) for logits (..., V) (sampling.py:16-21).
 
     temperature: a float for every row, or a float32 device tensor with one value per row.
     noise: float32 Exp(1) noise with the logits' shape (the categorical draw is argmax(p / noise));
-    None makes every row greedy. out32: optional int32 view that also receives the tokens."""
+    None makes every row greedy. out32: optional int32 view that also receives the tokens; out64: an
+    optional contiguous int64 tensor of one element per row that receives them as the result does (and
+    is returned, reshaped)."""
     require_device(logits)
     shape = logits.shape
     x = logits.reshape(-1, shape[-1])
@@ -456,7 +464,9 @@ def sample_logits(logits: torch.Tensor, temperature, noise: Optional[torch.Tenso
         x = x.contiguous()
     r, ld = x.shape[0], x.stride(0)
     v = shape[-1]
-    tok = torch.empty((r,), dtype=torch.int64, device=logits.device)
+    if out64 is not None and (out64.dtype != torch.int64 or out64.numel() != r or not out64.is_contiguous()):
+        raise ValueError("sample_logits: out64 must be a contiguous int64 tensor of one element per row")
+    tok = out64.view(-1) if out64 is not None else torch.empty((r,), dtype=torch.int64, device=logits.device)
     t_ptr, t_all = 0, 0.0
     if isinstance(temperature, torch.Tensor):
         require_device(temperature)

@@ -232,6 +232,7 @@ class _RoundState:
         # results passed between phases
         self.dft_logits = torch.empty((b, k, v), dtype=dtype, device=dev)
         self.draft_tok = torch.empty((b, k), dtype=I32, device=dev)
+        self.tok64 = torch.empty((max(k, 1), b), dtype=torch.int64, device=dev)   # step i's tokens, as ids
         if fused:
             # draft step i writes its rows' records into parts_d[:, i]; one merge after the last step
             self.parts_d = torch.empty((b, k, parts_d, 4), dtype=I32, device=dev)
@@ -330,17 +331,18 @@ def _round_phase(target, draft, pool_t: PagedKVPool, pool_d: PagedKVPool, st: _R
         elif i == 0:                  # re-feed (prev, last): the draft's own cache may lack prev
             idx, pos = d["ids"], d["pos0"]
         else:
-            idx = st.draft_tok[:, i - 1].to(torch.int64)[:, None]
+            idx = st.tok64[i - 1][:, None]
             pos = d["posd"][i if st.n_shared else i - 1][:, None]
         logits = draft._run(idx, pos, pool_d.views(d["tab_d"], pos), last_only=True,
                             head_stats=(temps, st.parts_d[:, i]) if st.fused else None, out=st.dft_logits[:, i],
                             hidden_out=st.hidden[:, i] if st.n_shared else None)
-        ops.sample_logits(logits, temps, st.noise_d[i] if st.sampling else None, out32=st.draft_tok[:, i])
+        ops.sample_logits(logits, temps, st.noise_d[i] if st.sampling else None, out32=st.draft_tok[:, i],
+                          out64=st.tok64[i])
         if st.fused and i == k - 1:   # draft row (b, i) is record b*k + i: sequence b's draft rows k+1 .. 2k
             ops.row_stats_merge(st.parts_d.view(b * k, -1, 4), st.row_stats, k, 2 * k + 1, k + 1)
         return None
     last = d["last"]
-    idx = torch.cat([last[:, None], st.draft_tok.to(torch.int64)], 1) if k else last[:, None]
+    idx = torch.cat([last[:, None], st.tok64[:k].t()], 1) if k else last[:, None]
     pos = d["posv"]
     temps_t = temps.repeat_interleave(k + 1) if st.fused else None
     views = pool_t.views(d["tab_t"], pos)
