@@ -228,19 +228,23 @@ __global__ void __launch_bounds__(128) qkv_rope_write_vec_kernel(
   b = row_ok ? b : 0;
   const int pos = row_ok ? positions[m] : -1;
   const bool rot_ok = pos >= 0 && pos < rope_len;
+  // the rotary row is loaded before the slot lookup: both depend only on the position
+  const int64_t cs = rot_ok ? (int64_t)pos * half : 0;
+  float4_t c0 = {}, c1 = {}, s0 = {}, s1 = {};
+  if (rot_thread) {
+    c0 = *reinterpret_cast<const float4_t*>(rope_cos + cs + p0);
+    c1 = *reinterpret_cast<const float4_t*>(rope_cos + cs + p0 + 4);
+    s0 = *reinterpret_cast<const float4_t*>(rope_sin + cs + p0);
+    s1 = *reinterpret_cast<const float4_t*>(rope_sin + cs + p0 + 4);
+  }
   int64_t blk = 0;
   int slot = 0;
   const int wpos = slots ? slots[m] : pos;
   const bool write_ok = rot_ok && slot_of(wpos, table, table_stride, b, max_blocks, kv, blk, slot);
   uint16_t* kp = reinterpret_cast<uint16_t*>(kv.k);
   uint16_t* vp = reinterpret_cast<uint16_t*>(kv.v);
-  const int64_t cs = rot_ok ? (int64_t)pos * half : 0;
   if (rot_thread) {
     float c[8], sn[8], o1[8], o2[8];
-    const float4_t c0 = *reinterpret_cast<const float4_t*>(rope_cos + cs + p0);
-    const float4_t c1 = *reinterpret_cast<const float4_t*>(rope_cos + cs + p0 + 4);
-    const float4_t s0 = *reinterpret_cast<const float4_t*>(rope_sin + cs + p0);
-    const float4_t s1 = *reinterpret_cast<const float4_t*>(rope_sin + cs + p0 + 4);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       c[j] = c0[j]; c[j + 4] = c1[j];
